@@ -1,0 +1,63 @@
+"""The C-ABI library builds, loads, and exports what include/*.h declares.
+
+CPU-only: loading libthundersync_hip.so and calling the version/error
+entry points touches no GPU.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+
+from tests.conftest import ROOT
+from thundersync_amd import _lib
+
+
+def declared_symbols() -> set[str]:
+    names = set()
+    for header in (ROOT / "include").glob("*.h"):
+        text = header.read_text()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        names.update(re.findall(r"\b(ts_[a-z0-9_]+)\s*\(", text))
+    return names
+
+
+def test_every_declared_symbol_has_a_binding():
+    assert declared_symbols() == set(_lib.SIGNATURES)
+
+
+def test_the_library_loads_and_exports_every_symbol():
+    assert _lib.LIB_PATH.exists(), "build the library first (__graft_entry__.build())"
+    lib = ctypes.CDLL(str(_lib.LIB_PATH))
+    for name in declared_symbols():
+        assert hasattr(lib, name), name
+
+
+def test_version_and_empty_error(monkeypatch):
+    monkeypatch.setenv(_lib.HIP_ENV, "auto")
+    _lib.reset()
+    try:
+        lib = _lib.require_library()
+        assert lib.ts_hip_version().decode().startswith("thundersync_hip")
+        assert "gfx950" in _lib.hip_build()
+    finally:
+        _lib.reset()
+
+
+def test_argument_errors_are_reported_without_a_device(monkeypatch):
+    """A null pointer is refused before any launch; the message names the call."""
+    monkeypatch.setenv(_lib.HIP_ENV, "auto")
+    _lib.reset()
+    try:
+        lib = _lib.require_library()
+        status = lib.ts_rmsnorm_fwd(None, None, None, None, 4, 8, 1e-6, _lib.TS_BF16, None)
+        assert status != 0
+        assert "ts_rmsnorm_fwd" in lib.ts_hip_last_error().decode()
+        try:
+            _lib.check(status, "ts_rmsnorm_fwd(test)")
+        except RuntimeError as error:
+            assert "null pointer" in str(error)
+        else:  # pragma: no cover
+            raise AssertionError("check() did not raise")
+    finally:
+        _lib.reset()

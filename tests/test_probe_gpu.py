@@ -1,0 +1,74 @@
+"""Pin the MFMA and register-transpose lane layouts the kernels assume.
+
+One wave runs v_mfma_f32_16x16x32_bf16, v_mfma_f32_32x32x16_bf16 and the
+8x8 16-bit register transpose on integer-valued bf16 operands (exact in
+fp32), and the result is compared with the layouts written in
+thundersync_amd/csrc/common.h, computed here with numpy.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from thundersync_amd import _lib
+
+pytestmark = pytest.mark.gpu
+
+
+def expected_16(a, b):
+    # a, b: [64 lanes, 8 slots]; A[row=l%16][k=8*(l//16)+j], B[k][col=l%16]
+    A = np.zeros((16, 32))
+    B = np.zeros((32, 16))
+    for l in range(64):
+        for j in range(8):
+            A[l % 16, 8 * (l // 16) + j] = a[l, j]
+            B[8 * (l // 16) + j, l % 16] = b[l, j]
+    D = A @ B
+    out = np.zeros((64, 4))
+    for l in range(64):
+        for i in range(4):
+            out[l, i] = D[4 * (l // 16) + i, l % 16]
+    return out
+
+
+def expected_32(a, b):
+    A = np.zeros((32, 16))
+    B = np.zeros((16, 32))
+    for l in range(64):
+        for j in range(8):
+            A[l % 32, 8 * (l // 32) + j] = a[l, j]
+            B[8 * (l // 32) + j, l % 32] = b[l, j]
+    D = A @ B
+    out = np.zeros((64, 16))
+    for l in range(64):
+        for i in range(16):
+            out[l, i] = D[8 * (i // 4) + 4 * (l // 32) + (i % 4), l % 32]
+    return out
+
+
+def test_mfma_and_transpose_layouts(cuda):
+    lib = _lib.require_library()
+    rng = np.random.default_rng(0)
+    a = rng.integers(-4, 5, size=(64, 8)).astype(np.float32)
+    b = rng.integers(-4, 5, size=(64, 8)).astype(np.float32)
+    t_in = rng.integers(-100, 100, size=(64, 8, 8)).astype(np.float32)
+    da = torch.tensor(a, dtype=torch.bfloat16, device=cuda)
+    db = torch.tensor(b, dtype=torch.bfloat16, device=cuda)
+    dt = torch.tensor(t_in, dtype=torch.bfloat16, device=cuda)
+    d16 = torch.empty(64, 4, dtype=torch.float32, device=cuda)
+    d32 = torch.empty(64, 16, dtype=torch.float32, device=cuda)
+    t_out = torch.empty(64, 8, 8, dtype=torch.bfloat16, device=cuda)
+    print("probe: ts_probe_layouts", flush=True)
+    _lib.check(
+        lib.ts_probe_layouts(da.data_ptr(), db.data_ptr(), d16.data_ptr(), d32.data_ptr(),
+                             dt.data_ptr(), t_out.data_ptr(), _lib.stream_of(da)),
+        "ts_probe_layouts",
+    )
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(d16.cpu().numpy(), expected_16(a, b))
+    np.testing.assert_array_equal(d32.cpu().numpy(), expected_32(a, b))
+    np.testing.assert_array_equal(
+        t_out.float().cpu().numpy(), np.transpose(t_in, (0, 2, 1))
+    )

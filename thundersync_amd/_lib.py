@@ -1,0 +1,150 @@
+"""Loading libthundersync_hip.so and the ``THUNDERSYNC_HIP`` switch.
+
+The switch has the semantics of the reference's ``THUNDERSYNC_FA4``
+(src/thundersync/engine/streaming.py:395-505):
+
+* ``require`` -- every resolution that cannot load the library raises, and
+  the failure is not cached, so every later dispatch raises again;
+* ``off`` -- the library is never loaded; the resolution returns None;
+* ``auto`` (also the value when the variable is unset) -- the library is
+  loaded when it can be; otherwise the resolution returns None.
+
+The resolution happens once, under a lock, and is cached until
+:func:`reset` clears it.  :func:`library` is what the integration point (the
+reference's attention dispatch, or a test) consults; the operators in this
+package call :func:`require_library`, which raises whenever the library is
+not available -- there is no host fallback inside this package.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from pathlib import Path
+
+HIP_ENV = "THUNDERSYNC_HIP"
+HIP_SETTINGS = ("require", "off", "auto")
+LIB_NAME = "libthundersync_hip.so"
+LIB_PATH = Path(__file__).resolve().parent / LIB_NAME
+
+# Every symbol include/thundersync_hip.h declares, with its ctypes signature.
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_INT = ctypes.c_int
+_F = ctypes.c_float
+SIGNATURES: dict[str, tuple[object, list[object]]] = {
+    "ts_hip_version": (ctypes.c_char_p, []),
+    "ts_hip_last_error": (ctypes.c_char_p, []),
+    "ts_rmsnorm_fwd": (_INT, [_P, _P, _P, _P, _I64, _I64, _F, _INT, _P]),
+    "ts_rmsnorm_bwd_workspace": (_I64, [_I64, _I64]),
+    "ts_rmsnorm_bwd": (_INT, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _INT, _P]),
+    "ts_probe_layouts": (_INT, [_P, _P, _P, _P, _P, _P, _P]),
+}
+
+TS_OK = 0
+TS_F32, TS_F16, TS_BF16 = 0, 1, 2
+
+_LOCK = threading.Lock()
+_LIB: ctypes.CDLL | None = None
+_RESOLVED = False
+_SETTING: str | None = None
+
+
+def hip_setting() -> str:
+    """The ``THUNDERSYNC_HIP`` setting: ``require``, ``off`` or ``auto``."""
+    value = os.environ.get(HIP_ENV, "auto").strip().lower() or "auto"
+    if value not in HIP_SETTINGS:
+        raise ValueError(f"{HIP_ENV} must be one of {', '.join(HIP_SETTINGS)}, not {value!r}")
+    return value
+
+
+def _load() -> ctypes.CDLL:
+    if not LIB_PATH.exists():
+        raise OSError(f"{LIB_PATH} is not built (run __graft_entry__.build())")
+    lib = ctypes.CDLL(str(LIB_PATH))
+    for name, (restype, argtypes) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = restype
+        fn.argtypes = argtypes
+    return lib
+
+
+def library() -> ctypes.CDLL | None:
+    """The library, resolved once under ``THUNDERSYNC_HIP``, or None."""
+    global _LIB, _RESOLVED, _SETTING
+    if _RESOLVED:
+        return _LIB
+    with _LOCK:
+        if _RESOLVED:
+            return _LIB
+        setting = hip_setting()
+        if setting == "off":
+            _LIB, _SETTING, _RESOLVED = None, setting, True
+            return None
+        try:
+            lib = _load()
+        except Exception as error:
+            if setting == "require":
+                raise RuntimeError(
+                    f"{HIP_ENV}=require but {LIB_NAME} cannot be loaded: {error!r}"
+                ) from error
+            lib = None
+        _LIB, _SETTING, _RESOLVED = lib, setting, True
+        return lib
+
+
+def hip_build() -> str | None:
+    """Diagnostic: the loaded library's version string, or None. Never raises."""
+    try:
+        lib = library()
+    except RuntimeError:
+        return None
+    return None if lib is None else lib.ts_hip_version().decode()
+
+
+def reset() -> None:
+    """Forget the resolution; the next call re-reads the setting."""
+    global _LIB, _RESOLVED, _SETTING
+    with _LOCK:
+        _LIB, _RESOLVED, _SETTING = None, False, None
+
+
+def require_library() -> ctypes.CDLL:
+    """The library, or an error that says why it is not available."""
+    lib = library()
+    if lib is None:
+        if _SETTING == "off":
+            raise RuntimeError(f"the HIP kernels are switched off ({HIP_ENV}=off)")
+        raise RuntimeError(
+            f"{LIB_NAME} is not available; build it with __graft_entry__.build()"
+        )
+    return lib
+
+
+def check(status: int, what: str) -> None:
+    """Raise RuntimeError naming the kernel call when a status is not TS_OK."""
+    if status != TS_OK:
+        lib = require_library()
+        message = lib.ts_hip_last_error().decode()
+        raise RuntimeError(f"{what} failed (status {status}): {message}")
+
+
+def dtype_code(dtype) -> int:
+    import torch
+
+    codes = {torch.float32: TS_F32, torch.float16: TS_F16, torch.bfloat16: TS_BF16}
+    if dtype not in codes:
+        raise TypeError(f"unsupported dtype {dtype}")
+    return codes[dtype]
+
+
+def stream_of(tensor) -> int:
+    """The current HIP stream of ``tensor``'s device, as an integer handle."""
+    import torch
+
+    return torch.cuda.current_stream(tensor.device).cuda_stream
+
+
+def ptr(tensor) -> int | None:
+    return None if tensor is None else tensor.data_ptr()

@@ -1,0 +1,145 @@
+// Shared device helpers for the gfx950 kernels of libthundersync_hip.
+//
+// Everything here is written for CDNA4 (gfx950): 64-lane wavefronts, the
+// bf16 MFMA instructions v_mfma_f32_16x16x32_bf16 / v_mfma_f32_32x32x16_bf16,
+// and 160 KB of LDS per CU.  No other target is built.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <string.h>
+#include <stdio.h>
+#include <stdarg.h>
+
+namespace ts {
+
+typedef __bf16 bf16;
+typedef _Float16 f16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kWave = 64;
+
+// dtype codes shared with the host (include/thundersync_hip.h).
+enum DType : int { kF32 = 0, kF16 = 1, kBF16 = 2 };
+
+// ---------------------------------------------------------------------------
+// scalar conversions.  bf16 rounding is round-to-nearest-even, the rounding
+// torch applies in `.to(torch.bfloat16)`.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float bf_bits_to_f(uint32_t h) {
+  return __uint_as_float(h << 16);
+}
+__device__ __forceinline__ uint32_t f_to_bf_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;  // NaN stays NaN
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+__device__ __forceinline__ float to_f(float x) { return x; }
+__device__ __forceinline__ float to_f(bf16 x) { return (float)x; }
+__device__ __forceinline__ float to_f(f16 x) { return (float)x; }
+
+template <typename T> __device__ __forceinline__ T from_f(float x);
+template <> __device__ __forceinline__ float from_f<float>(float x) { return x; }
+template <> __device__ __forceinline__ bf16 from_f<bf16>(float x) {
+  uint16_t b = (uint16_t)f_to_bf_bits(x);
+  bf16 r;
+  __builtin_memcpy(&r, &b, 2);
+  return r;
+}
+template <> __device__ __forceinline__ f16 from_f<f16>(float x) { return (f16)x; }
+
+// pack two floats into one dword of two bf16 (lo = a, hi = b)
+__device__ __forceinline__ uint32_t pack_bf2(float a, float b) {
+  return f_to_bf_bits(a) | (f_to_bf_bits(b) << 16);
+}
+
+// ---------------------------------------------------------------------------
+// MFMA wrappers (gfx950).
+//
+// v_mfma_f32_16x16x32_bf16:  D[16x16] += A[16x32] * B[32x16]
+//   A: lane l holds row (l & 15), eight k values of k-group (l >> 4)
+//   B: lane l holds col (l & 15), eight k values of k-group (l >> 4)
+//   D: lane l holds col (l & 15), rows 4*(l >> 4) + i, i = 0..3
+// The contraction pairs A and B through the same (k-group, slot) position,
+// so callers may assign any permutation of their contraction index to the
+// slots provided A and B use the same one.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+// v_mfma_f32_32x32x16_bf16:  D[32x32] += A[32x16] * B[16x32]
+//   A: lane l holds row (l & 31), eight k values of k-group (l >> 5)
+//   B: lane l holds col (l & 31), eight k values of k-group (l >> 5)
+//   D: lane l holds col (l & 31), rows 8*(i >> 2) + 4*(l >> 5) + (i & 3)
+__device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) {
+  bf16x8 r;
+  __builtin_memcpy(&r, &v, 16);
+  return r;
+}
+__device__ __forceinline__ u32x4 as_u32x4(bf16x8 v) {
+  u32x4 r;
+  __builtin_memcpy(&r, &v, 16);
+  return r;
+}
+
+// Transpose an 8x8 block of 16-bit values held as eight 16-byte rows.
+// in[j] holds row j (8 columns); out[e] receives column e (8 rows).
+__device__ __forceinline__ void transpose8x8(const u32x4 in[8], u32x4 out[8]) {
+#pragma unroll
+  for (int p = 0; p < 4; ++p) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t x = in[2 * q][p];
+      const uint32_t y = in[2 * q + 1][p];
+      // column 2p is the low halves, column 2p+1 the high halves
+      out[2 * p][q] = __builtin_amdgcn_perm(y, x, 0x05040100u);
+      out[2 * p + 1][q] = __builtin_amdgcn_perm(y, x, 0x07060302u);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// wave reductions over lanes that differ in the given xor masks
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float shfl_xor(float v, int mask) {
+  return __shfl_xor(v, mask, kWave);
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += shfl_xor(v, m);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, shfl_xor(v, m));
+  return v;
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
+
+// ---------------------------------------------------------------------------
+// host-side error state
+// ---------------------------------------------------------------------------
+void set_error(const char* fmt, ...);
+int check_launch(const char* what);
+
+}  // namespace ts
+
+#define TS_CHECK_ARG(cond, ...)            \
+  do {                                     \
+    if (!(cond)) {                         \
+      ::ts::set_error(__VA_ARGS__);        \
+      return TS_ERR_INVALID;               \
+    }                                      \
+  } while (0)

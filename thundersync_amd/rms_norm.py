@@ -1,0 +1,131 @@
+"""RMSNorm with the FP32 VJP, on the gfx950 kernels.
+
+Drop-in for the reference's ``accel/rms_norm.py:7-70``: the forward keeps
+the replaced ``Qwen3RMSNorm``'s primal operation order and both casts
+(``w * T(float(x) * rstd)``) and saves ``(hidden, weight, rstd)``; the
+backward is the FP32 VJP from that saved statistic, with ``dx`` cast to the
+hidden dtype and ``dw`` to the weight dtype.  Both directions run in
+``ts_rmsnorm_fwd`` / ``ts_rmsnorm_bwd`` (include/thundersync_hip.h); there is
+no host path -- a CPU tensor raises.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+try:  # the module swap targets transformers' Qwen3 norm when it is importable
+    from transformers.models.qwen3.modeling_qwen3 import Qwen3RMSNorm
+except Exception:  # pragma: no cover - transformers absent
+    Qwen3RMSNorm = None
+
+
+def _check_device(hidden: torch.Tensor, weight: torch.Tensor) -> None:
+    if not hidden.is_cuda or not weight.is_cuda:
+        raise RuntimeError("thundersync_amd RMSNorm runs on the GPU only; got a CPU tensor")
+    if hidden.dtype != weight.dtype:
+        raise TypeError(
+            f"hidden ({hidden.dtype}) and weight ({weight.dtype}) must share a dtype"
+        )
+    if weight.dim() != 1 or hidden.shape[-1] != weight.shape[0]:
+        raise ValueError(
+            f"weight {tuple(weight.shape)} does not match hidden {tuple(hidden.shape)}"
+        )
+
+
+def rms_norm_forward(hidden: torch.Tensor, weight: torch.Tensor, eps: float):
+    """``(w * T(x * rstd), rstd)`` with ``rstd`` fp32 of shape ``[..., 1]``."""
+    _check_device(hidden, weight)
+    lib = _lib.require_library()
+    x = hidden.contiguous()
+    w = weight.contiguous()
+    width = x.shape[-1]
+    rows = x.numel() // width if width else 0
+    y = torch.empty_like(x)
+    rstd = torch.empty((*x.shape[:-1], 1), dtype=torch.float32, device=x.device)
+    _lib.check(
+        lib.ts_rmsnorm_fwd(
+            x.data_ptr(), w.data_ptr(), y.data_ptr(), rstd.data_ptr(), rows, width,
+            float(eps), _lib.dtype_code(x.dtype), _lib.stream_of(x),
+        ),
+        f"ts_rmsnorm_fwd(rows={rows}, width={width}, dtype={x.dtype})",
+    )
+    return y, rstd
+
+
+def rms_norm_backward(gradient, hidden, weight, rstd, needs=(True, True)):
+    """``(dx, dw)`` of the FP32 VJP; either may be None when not needed."""
+    _check_device(hidden, weight)
+    lib = _lib.require_library()
+    x = hidden.contiguous()
+    w = weight.contiguous()
+    dy = gradient.to(x.dtype).contiguous()
+    width = x.shape[-1]
+    rows = x.numel() // width if width else 0
+    rs = rstd.contiguous().to(torch.float32)
+    dx = torch.empty_like(x) if needs[0] else None
+    dw = torch.empty_like(w) if needs[1] else None
+    if dx is None and dw is None:
+        return None, None
+    ws_bytes = int(lib.ts_rmsnorm_bwd_workspace(rows, width)) if dw is not None else 0
+    workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=x.device)
+    _lib.check(
+        lib.ts_rmsnorm_bwd(
+            dy.data_ptr(), x.data_ptr(), w.data_ptr(), rs.data_ptr(),
+            _lib.ptr(dx), _lib.ptr(dw), workspace.data_ptr(), ws_bytes, rows, width,
+            _lib.dtype_code(x.dtype), _lib.stream_of(x),
+        ),
+        f"ts_rmsnorm_bwd(rows={rows}, width={width}, dtype={x.dtype})",
+    )
+    return dx, dw
+
+
+class FP32RMSNormVJP(torch.autograd.Function):
+    """``FP32RMSNormVJP.apply(hidden, weight, eps)`` as in accel/rms_norm.py:7-43."""
+
+    @staticmethod
+    def forward(ctx, hidden, weight, eps):
+        primal, rstd = rms_norm_forward(hidden, weight, eps)
+        ctx.save_for_backward(hidden, weight, rstd)
+        ctx.eps = eps
+        return primal
+
+    @staticmethod
+    @torch.autograd.function.once_differentiable
+    def backward(ctx, gradient):
+        hidden, weight, rstd = ctx.saved_tensors
+        need = ctx.needs_input_grad
+        dx, dw = rms_norm_backward(gradient, hidden, weight, rstd, (need[0], need[1]))
+        return dx, dw, None
+
+
+if Qwen3RMSNorm is not None:
+
+    class StableQwen3RMSNorm(Qwen3RMSNorm):
+        """Qwen3RMSNorm whose low-precision training forward runs FP32RMSNormVJP.
+
+        Dispatch rule of accel/rms_norm.py:46-52: bf16/fp16 inputs under grad
+        take the HIP op; everything else is the stock module's forward.
+        """
+
+        def forward(self, hidden):
+            if hidden.dtype not in (torch.bfloat16, torch.float16) or not torch.is_grad_enabled():
+                return super().forward(hidden)
+            return FP32RMSNormVJP.apply(hidden, self.weight, self.variance_epsilon)
+
+    def use_stable_qwen3_rms_norm(model: torch.nn.Module) -> int:
+        """Swap every Qwen3RMSNorm, keeping Parameter identity (accel/rms_norm.py:55-70)."""
+        count = 0
+        for name, module in list(model.named_modules()):
+            if not name or not isinstance(module, Qwen3RMSNorm):
+                continue
+            if isinstance(module, StableQwen3RMSNorm):
+                continue
+            with torch.device("meta"):
+                replacement = StableQwen3RMSNorm(module.weight.numel(), eps=module.variance_epsilon)
+            replacement.weight = module.weight
+            replacement.train(module.training)
+            model.set_submodule(name, replacement)
+            count += 1
+        return count
