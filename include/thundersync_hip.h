@@ -74,6 +74,112 @@ int ts_rmsnorm_bwd(const void* dy, const void* x, const void* w,
                    int dtype, void* stream);
 
 /* ------------------------------------------------------------------------
+ * Forest / packed bottom-right-causal GQA attention (bf16, head_dim 128)
+ *
+ * A problem is a set of query SEGMENTS and key RUNS.  Segment s owns query
+ * rows [q_row0, q_row0 + q_len) of the packed Q/O/dO/dQ tensors
+ * ([rows, Hq, 128], any row/head stride) and attends to a virtual key
+ * sequence of kv_len keys assembled from runs: seg_spans[span0 .. span0 +
+ * nspan) lists (run, kpos) -- run `index` supplies keys [kpos, kpos + len)
+ * of that sequence.  Visibility is bottom-right causal over the sequence:
+ * query row i sees key position j iff j <= kv_len - q_len + i.  A run is
+ * one contiguous [len, Hkv, 128] block of K/V rows (a retained chunk, a
+ * forest node, a prefix), read in place through its own pointers and
+ * strides, never concatenated; run_visits[visit0 .. visit0 + nvisit) lists
+ * (segment, kpos) -- every segment that reads it -- and the backward writes
+ * the run's dK/dV, summed over those visits, through its dk/dv pointers.
+ *
+ * This one description covers:
+ *   - _causal_sdpa(query, ks, vs, scale) with ks/vs a chunk list: one
+ *     segment, one run per chunk (engine/streaming.py:1080-1162);
+ *   - _ChunkedCausalSDPA (retained per-chunk K/V, :1314-1423);
+ *   - _PackedFlashSplit over a plain turn pack (:1704-1836): one segment per
+ *     turn, its ancestor chunks and its own K/V as runs;
+ *   - _ragged_causal_sdpa cohorts (:1165-1297);
+ *   - forest_attention(q, k, v, plan) (engine/attention.py:186-231): one
+ *     segment per node, one run per node, key_ranges as the span lists.
+ * The split-at-the-prefix-plus-LSE-merge of the reference's flash/cuDNN
+ * paths (:614-803, :939-1077) is not needed: each segment's softmax runs
+ * over its whole key sequence in one pass.
+ * ------------------------------------------------------------------------ */
+
+typedef struct ts_attn_ref {
+  int32_t index; /* run (in seg_spans) or segment (in run_visits) */
+  int32_t kpos;  /* position of the run's first key in the segment's keys */
+} ts_attn_ref;
+
+typedef struct ts_attn_segment {
+  int64_t q_row0;
+  int32_t q_len;
+  int32_t kv_len;
+  int32_t span0;
+  int32_t nspan;
+} ts_attn_segment;
+
+typedef struct ts_attn_run {
+  uint64_t k, v;   /* device address of key 0, kv-head 0 */
+  uint64_t dk, dv; /* gradient destinations (backward only; may be 0) */
+  int64_t k_row_stride, k_head_stride, v_row_stride, v_head_stride;
+  int64_t dk_row_stride, dk_head_stride, dv_row_stride, dv_head_stride;
+  int32_t len;
+  int32_t visit0;
+  int32_t nvisit;
+  int32_t reserved;
+} ts_attn_run;
+
+typedef struct ts_attn_problem {
+  const ts_attn_segment* segs; /* device arrays */
+  const ts_attn_ref* seg_spans;
+  const ts_attn_run* runs;
+  const ts_attn_ref* run_visits;
+  const int32_t* q_work;  /* pairs (segment, first row): one per 32-row block */
+  const int32_t* kv_work; /* pairs (run, first key): one per 64-key block */
+  int32_t n_q_work;
+  int32_t n_kv_work;
+  int32_t n_segs;
+  int32_t n_runs;
+  int32_t hq;
+  int32_t hkv;
+  int32_t head_dim;
+  float scale;
+  int32_t q_block;  /* rows per q_work item: 32 * 4 / ts_attn_heads_per_block */
+  int32_t kv_block; /* keys per kv_work item: 64 */
+  int64_t q_rows;   /* rows of Q/O/dO/dQ */
+} ts_attn_problem;
+
+/* Query heads one forward/dQ work-group processes for a GQA group size
+ * (hq / hkv): 4 when it divides the group, else 2, else 1.  The rows per
+ * q_work item are 32 * 4 / that value. */
+int ts_attn_heads_per_block(int group);
+
+typedef struct ts_attn_rows {
+  uint64_t ptr; /* device address of row 0, head 0 */
+  int64_t row_stride;
+  int64_t head_stride;
+} ts_attn_rows;
+
+/* Forward: out (bf16) and lse (fp32, natural log, [hq, lse_ld]).
+ * Replaces the dispatch of _causal_sdpa (engine/streaming.py:1080-1162),
+ * _flash_split_grouped_forward (:710-731), _PackedFlashSplit.forward
+ * (:1727-1775), _ragged_causal_sdpa (:1165-1226), forest_attention
+ * (engine/attention.py:186-231) and FA4's flash_attn_func(causal=True)
+ * (:508-529). */
+int ts_attn_fwd(const ts_attn_problem* problem, ts_attn_rows q, ts_attn_rows out,
+                float* lse, int64_t lse_ld, void* stream);
+
+/* Backward: dq (bf16, same row layout contract as q) and each run's dK/dV
+ * (bf16, written through the run's dk/dv, summed over the run's visits in a
+ * fixed order -- no atomics).  `delta` is a caller-provided fp32 workspace of
+ * hq * lse_ld floats (rowsum(dO * O)).
+ * Replaces _flash_split_grouped_backward (engine/streaming.py:734-768),
+ * _ChunkedCausalSDPA.backward (:1378-1423), _PackedFlashSplit.backward and
+ * its two varlen flash backward calls (:1777-1836), the per-segment
+ * recompute of _RaggedAttentionIndependentVJP.backward (:1273-1297). */
+int ts_attn_bwd(const ts_attn_problem* problem, ts_attn_rows q, ts_attn_rows out,
+                ts_attn_rows dout, const float* lse, int64_t lse_ld, float* delta,
+                ts_attn_rows dq, void* stream);
+
+/* ------------------------------------------------------------------------
  * Diagnostics
  * ------------------------------------------------------------------------ */
 

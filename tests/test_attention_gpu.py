@@ -1,0 +1,179 @@
+"""HIP attention against the CPU oracle (bottom-right causal GQA, fp32).
+
+Bar: outputs and input gradients within 2e-2 max-abs
+of the fp32 oracle on identical bf16 inputs.  Where a tensor's magnitude
+exceeds 1 (summed key gradients of a long shared prefix), the bar scales with
+max|ref| -- the bf16 rounding of the stored result alone is 2^-9 relative --
+which is the reference's own drift metric (tests/test_fa4_bottom_right.py:
+66-70 of the reference).  Kernels use no atomics: repeated runs are
+bit-identical.
+"""
+
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+from oracle import attention as ref
+from thundersync_amd import attention as hip
+
+pytestmark = pytest.mark.gpu
+
+D = 128
+
+
+def close(got, want, what, bar=2e-2):
+    got = got.detach().float().cpu()
+    want = want.detach().float().cpu()
+    assert got.shape == want.shape, (what, got.shape, want.shape)
+    err = (got - want).abs().max().item() if got.numel() else 0.0
+    scale = max(1.0, want.abs().max().item() if want.numel() else 0.0)
+    assert err <= bar * scale, f"{what}: max-abs {err:.4g} > {bar} x {scale:.3g}"
+    return err
+
+
+def make(t, chunks, hq, hkv, seed):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(1, t, hq, D, generator=g).to(torch.bfloat16)
+    ks = [torch.randn(n, hkv, D, generator=g).to(torch.bfloat16) for n in chunks]
+    vs = [torch.randn(n, hkv, D, generator=g).to(torch.bfloat16) for n in chunks]
+    dout = torch.randn(1, t, hq, D, generator=g).to(torch.bfloat16)
+    return q, ks, vs, dout
+
+
+CHAINS = [
+    (64, [64], 4, 4),
+    (37, [100, 37], 8, 2),
+    (128, [7, 64, 130, 128], 32, 8),
+    (1, [9], 4, 2),
+    (2, [5, 3], 4, 2),
+    (200, [300, 17, 200], 40, 8),
+    (96, [96], 2, 1),
+    (513, [1024, 513], 32, 8),
+    (70, [33, 70], 8, 8),
+]
+
+
+@pytest.mark.parametrize("t,chunks,hq,hkv", CHAINS)
+def test_chain_matches_oracle(cuda, t, chunks, hq, hkv):
+    print(f"attention chain t={t} chunks={chunks} hq={hq} hkv={hkv}", flush=True)
+    q, ks, vs, dout = make(t, chunks, hq, hkv, seed=t + sum(chunks) + hq)
+    scale = D ** -0.5
+    want, wq, wks, wvs = ref.attention_with_grads(q[0], ks, vs, dout[0], scale)
+    qc = q.to(cuda).requires_grad_()
+    kc = [k.to(cuda).requires_grad_() for k in ks]
+    vc = [v.to(cuda).requires_grad_() for v in vs]
+    out = hip.causal_attention(qc.transpose(1, 2), kc, vc, scale)
+    assert out.shape == (1, hq, t, D)
+    out.transpose(1, 2).backward(dout.to(cuda))
+    torch.cuda.synchronize()
+    close(out[0].transpose(0, 1), want, "out")
+    close(qc.grad[0], wq, "dq")
+    for i, (k, v) in enumerate(zip(kc, vc)):
+        close(k.grad, wks[i], f"dk[{i}]")
+        close(v.grad, wvs[i], f"dv[{i}]")
+
+
+def test_lse_and_determinism(cuda):
+    t, chunks, hq, hkv = 300, [512, 300], 32, 8
+    q, ks, vs, dout = make(t, chunks, hq, hkv, seed=3)
+    scale = D ** -0.5
+    _, want_lse = ref.chained_attention(q[0], ks, vs, scale)
+    layout = hip.chain_layout(t, chunks, hq, hkv)
+    runs = []
+    for _ in range(2):
+        qc = q[0].to(cuda).requires_grad_()
+        kc = [k.to(cuda).requires_grad_() for k in ks]
+        vc = [v.to(cuda).requires_grad_() for v in vs]
+        out, lse = hip.attention(qc, layout, kc, vc, scale)
+        out.backward(dout[0].to(cuda))
+        torch.cuda.synchronize()
+        runs.append((out.detach(), lse, qc.grad, [k.grad for k in kc], [v.grad for v in vc]))
+    torch.testing.assert_close(runs[0][1].cpu(), want_lse, rtol=0, atol=1e-3)
+    a, b = runs
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1]) and torch.equal(a[2], b[2])
+    for x, y in zip(a[3] + a[4], b[3] + b[4]):
+        assert torch.equal(x, y)
+
+
+# per segment: (own tokens, turn chunks after the shared prompt), as the
+# reference's packed-split test (tests/test_packed_flash_split.py:194-200)
+PACKS = [
+    [(157, [157, 157]), (157, [42, 157, 68]), (42, []), (157, [157])],
+    [(64, [8000]), (512, [1000, 157]), (1024, [])],
+    [(2, [5]), (3, [])],
+]
+PROMPT = 492
+
+
+@pytest.mark.parametrize("hq,hkv", [(32, 8), (40, 8)])
+@pytest.mark.parametrize("pack", PACKS)
+def test_packed_matches_per_segment_oracle(cuda, pack, hq, hkv):
+    print(f"packed pack={pack} hq={hq}", flush=True)
+    g = torch.Generator().manual_seed(sum(n for n, _ in pack))
+    total = sum(n for n, _ in pack)
+
+    def leaf(*shape):
+        return torch.randn(*shape, generator=g).to(torch.bfloat16)
+
+    query = leaf(1, total, hq, D)
+    key, value = leaf(total, hkv, D), leaf(total, hkv, D)
+    prompt = (leaf(PROMPT, hkv, D), leaf(PROMPT, hkv, D))
+    turns = [[(leaf(n, hkv, D), leaf(n, hkv, D)) for n in chunks] for _n, chunks in pack]
+    dout = leaf(1, total, hq, D)
+    scale = D ** -0.5
+
+    # device leaves (the shared prompt is ONE object passed once per segment)
+    qd = query.to(cuda).requires_grad_()
+    kd, vd = key.to(cuda).requires_grad_(), value.to(cuda).requires_grad_()
+    pk, pv = prompt[0].to(cuda).requires_grad_(), prompt[1].to(cuda).requires_grad_()
+    td = [[(a.to(cuda).requires_grad_(), b.to(cuda).requires_grad_()) for a, b in segs] for segs in turns]
+    ancestors = [([pk] + [a for a, _ in segs], [pv] + [b for _, b in segs]) for segs in td]
+    lengths = [n for n, _ in pack]
+    layout = hip.pack_layout(lengths, ancestors, device=cuda)
+    out = hip.PackedAttention.apply(qd.transpose(1, 2), kd, vd, scale, layout, *layout.inputs(ancestors))
+    out.transpose(1, 2).backward(dout.to(cuda))
+    torch.cuda.synchronize()
+    assert out.transpose(1, 2).is_contiguous()
+
+    # oracle: each segment on its own over prompt + turns + own
+    row0 = 0
+    want_pk = torch.zeros(PROMPT, hkv, D)
+    want_pv = torch.zeros(PROMPT, hkv, D)
+    for s, (n, _chunks) in enumerate(pack):
+        ks = [prompt[0]] + [a for a, _ in turns[s]] + [key[row0 : row0 + n]]
+        vs = [prompt[1]] + [b for _, b in turns[s]] + [value[row0 : row0 + n]]
+        o, dq, dks, dvs = ref.attention_with_grads(query[0, row0 : row0 + n], ks, vs, dout[0, row0 : row0 + n], scale)
+        close(out[0, :, row0 : row0 + n].transpose(0, 1), o, f"seg {s} out")
+        close(qd.grad[0, row0 : row0 + n], dq, f"seg {s} dq")
+        close(kd.grad[row0 : row0 + n], dks[-1], f"seg {s} own dk")
+        close(vd.grad[row0 : row0 + n], dvs[-1], f"seg {s} own dv")
+        for j, (a, b) in enumerate(td[s]):
+            close(a.grad, dks[1 + j], f"seg {s} turn {j} dk")
+            close(b.grad, dvs[1 + j], f"seg {s} turn {j} dv")
+        want_pk += dks[0]
+        want_pv += dvs[0]
+        row0 += n
+    close(pk.grad, want_pk, "shared prompt dk")
+    close(pv.grad, want_pv, "shared prompt dv")
+
+
+def test_ragged_cohort(cuda):
+    g = torch.Generator().manual_seed(7)
+    qs = [torch.randn(1, 8, n, D, generator=g).to(torch.bfloat16) for n in (4, 8, 33)]
+    ks = [torch.randn(n, 2, D, generator=g).to(torch.bfloat16) for n in (12, 16, 40)]
+    vs = [torch.randn(n, 2, D, generator=g).to(torch.bfloat16) for n in (12, 16, 40)]
+    outs = hip.ragged_causal_attention([q.to(cuda) for q in qs], [k.to(cuda) for k in ks],
+                                       [v.to(cuda) for v in vs], D ** -0.5)
+    for q, k, v, o in zip(qs, ks, vs, outs):
+        want, _ = ref.bottom_right_attention(q[0].transpose(0, 1), k, v, D ** -0.5)
+        close(o[0].transpose(0, 1), want, "ragged out")
+
+
+def test_cpu_and_dtype_refused():
+    q = torch.randn(1, 4, 8, D, dtype=torch.bfloat16)
+    k = torch.randn(8, 2, D, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        hip.causal_attention(q, [k], [k], 0.1)

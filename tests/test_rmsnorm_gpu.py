@@ -42,9 +42,12 @@ def test_forward_matches_oracle(cuda, rows, width, dtype):
     got, rstd = rms_norm_forward(x.to(cuda), w.to(cuda), 1e-6)
     torch.cuda.synchronize()
     torch.testing.assert_close(rstd.cpu(), want_rstd, rtol=2e-6, atol=0)
-    # |y| <= |w| * |xhat|: one output ulp relative to the value
-    tol = (want.float().abs() * ulp(dtype) * 1.01 + 1e-30)
-    assert bool(((got.cpu().float() - want.float()).abs() <= tol).all())
+    # one output ulp for 16-bit outputs; fp32 outputs carry rstd's own
+    # reduction-order difference (a few fp32 ulps)
+    units = 1.01 if dtype != torch.float32 else 8.0
+    tol = want.float().abs() * ulp(dtype) * units + 1e-30
+    err = (got.cpu().float() - want.float()).abs()
+    assert bool((err <= tol).all()), float((err / tol).max())
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])

@@ -23,6 +23,8 @@ import os
 import threading
 from pathlib import Path
 
+from ._abi import AttnProblem, AttnRows
+
 HIP_ENV = "THUNDERSYNC_HIP"
 HIP_SETTINGS = ("require", "off", "auto")
 LIB_NAME = "libthundersync_hip.so"
@@ -40,6 +42,12 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "ts_rmsnorm_bwd_workspace": (_I64, [_I64, _I64]),
     "ts_rmsnorm_bwd": (_INT, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _INT, _P]),
     "ts_probe_layouts": (_INT, [_P, _P, _P, _P, _P, _P, _P]),
+    "ts_attn_heads_per_block": (_INT, [_INT]),
+    "ts_attn_fwd": (_INT, [ctypes.POINTER(AttnProblem), AttnRows, AttnRows, _P, _I64, _P]),
+    "ts_attn_bwd": (
+        _INT,
+        [ctypes.POINTER(AttnProblem), AttnRows, AttnRows, AttnRows, _P, _I64, _P, AttnRows, _P],
+    ),
 }
 
 TS_OK = 0

@@ -1,0 +1,735 @@
+"""Forest / packed bottom-right-causal GQA attention on the gfx950 kernels.
+
+One differentiable core op, :func:`attention`, serves every shape the
+reference's streaming engine produces.  A call is described by an
+:class:`AttnLayout`:
+
+* **key sources** -- the K/V tensors the call reads, each ``[N, Hkv, 128]``
+  (a retained chunk, a pack's own K/V, a forest's whole K/V), read in place;
+* **runs** -- contiguous row ranges of a source (a whole chunk, one forest
+  node);
+* **segments** -- blocks of query rows of the packed ``[R, Hq, 128]`` query,
+  each attending bottom-right-causally to the concatenation of its runs.
+
+The layout is integer metadata only (no pointers), so one layout serves every
+layer of a model call, as the reference's ``_PackLayout`` does
+(src/thundersync/engine/streaming.py:1613-1698).  The pointer table is
+rebuilt per call from the tensors themselves.
+
+Reference entry points mirrored here (same argument meaning):
+
+* :func:`causal_attention` -- the callable-backend form ``(query, ks, vs,
+  scale) -> out`` that ``_causal_sdpa(..., backend=)`` dispatches to
+  (engine/streaming.py:1094-1095) and ``grpo/attention.py:148-172`` provides;
+* :class:`ChunkedCausalAttention` -- ``_ChunkedCausalSDPA.apply(query, scale,
+  n_chunks, keep_state, backend, *ks, *vs)`` (engine/streaming.py:1314-1423);
+* :class:`PackLayout` / :class:`PackedAttention` -- ``_PackedFlashSplit.apply(
+  query, key, value, scale, layout, *ancestors)`` (engine/streaming.py:
+  1613-1836), with ancestors in the reference's "last segment first" order;
+* :func:`ragged_causal_attention` -- ``_ragged_causal_sdpa`` (:1165-1226);
+* :func:`forest_attention` -- ``forest_attention(q, k, v, plan, *, scale)``
+  (engine/attention.py:186-231).
+
+There is no host path: CPU tensors, unsupported dtypes or head dims raise.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+import threading
+from collections.abc import Sequence
+from dataclasses import dataclass, field
+
+import numpy as np
+import torch
+
+from . import _lib
+from ._abi import REF_DTYPE, RUN_DTYPE, SEG_DTYPE, AttnProblem, AttnRows
+from .operator_profiling import operator_range
+
+HEAD_DIM = 128
+KV_BLOCK = 64
+
+
+def heads_per_block(group: int) -> int:
+    """Query heads per forward/dQ work-group (mirror of ts_attn_heads_per_block)."""
+    if group % 4 == 0:
+        return 4
+    if group % 2 == 0:
+        return 2
+    return 1
+
+
+def q_block_rows(hq: int, hkv: int) -> int:
+    return 32 * 4 // heads_per_block(hq // hkv)
+
+
+# ---------------------------------------------------------------------------
+# layout
+# ---------------------------------------------------------------------------
+@dataclass(frozen=True)
+class Run:
+    source: int  # index into the call's key sources
+    offset: int  # first row within the source
+    length: int
+
+
+@dataclass(eq=False)
+class AttnLayout:
+    """Integer description of one attention call (see the module docstring)."""
+
+    q_rows: int
+    hq: int
+    hkv: int
+    source_rows: tuple[int, ...]
+    runs: tuple[Run, ...]
+    seg_q: tuple[tuple[int, int], ...]  # (q_row0, q_len) per segment
+    seg_spans: tuple[tuple[tuple[int, int], ...], ...]  # per segment: (run, kpos)
+    seg_kv: tuple[int, ...] = field(init=False)
+    _tables: dict = field(default_factory=dict, init=False, repr=False)
+    _lock: threading.Lock = field(default_factory=threading.Lock, init=False, repr=False)
+
+    def __post_init__(self):
+        if self.hq <= 0 or self.hkv <= 0 or self.hq % self.hkv:
+            raise ValueError(f"query heads {self.hq} are not a multiple of KV heads {self.hkv}")
+        kv = []
+        for s, spans in enumerate(self.seg_spans):
+            pos = 0
+            for run, kpos in spans:
+                if not 0 <= run < len(self.runs):
+                    raise ValueError(f"segment {s} names run {run} of {len(self.runs)}")
+                if kpos != pos:
+                    raise ValueError(f"segment {s}: spans must tile its keys in order (kpos {kpos} != {pos})")
+                pos += self.runs[run].length
+            kv.append(pos)
+        object.__setattr__(self, "seg_kv", tuple(kv))
+        if len(self.seg_q) != len(self.seg_spans):
+            raise ValueError("one span list per segment")
+        for s, (row0, length) in enumerate(self.seg_q):
+            if length < 0 or row0 < 0 or row0 + length > self.q_rows:
+                raise ValueError(f"segment {s} rows [{row0}, {row0 + length}) outside [0, {self.q_rows})")
+            if length > 0 and self.seg_kv[s] < length:
+                raise ValueError(
+                    f"segment {s} has {length} query rows but only {self.seg_kv[s]} keys; "
+                    "bottom-right causal attention needs kv_len >= q_len"
+                )
+        for r, run in enumerate(self.runs):
+            if not 0 <= run.source < len(self.source_rows):
+                raise ValueError(f"run {r} names source {run.source}")
+            if run.length <= 0 or run.offset < 0 or run.offset + run.length > self.source_rows[run.source]:
+                raise ValueError(f"run {r} rows outside its source")
+        if max([*self.seg_kv, 0]) >= 2**31 or self.q_rows >= 2**40:
+            raise ValueError("attention problem too large")
+
+    # -- work lists ---------------------------------------------------------
+    def _host_tables(self):
+        qb = q_block_rows(self.hq, self.hkv)
+        segs = np.zeros(len(self.seg_q), SEG_DTYPE)
+        spans, visits_of = [], [[] for _ in self.runs]
+        q_items = []
+        for s, ((row0, length), sp) in enumerate(zip(self.seg_q, self.seg_spans)):
+            segs[s] = (row0, length, self.seg_kv[s], len(spans), len(sp))
+            for run, kpos in sp:
+                spans.append((run, kpos))
+                visits_of[run].append((s, kpos))
+            off = self.seg_kv[s] - length
+            for q0 in range(0, length, qb):
+                # visible keys of the block's last row: the block's cost
+                last = min(q0 + qb, length) - 1
+                q_items.append((-(off + last + 1), s, q0))
+        visit_rows, visit0 = [], []
+        for run, vis in enumerate(visits_of):
+            visit0.append(len(visit_rows))
+            visit_rows.extend(vis)
+        kv_items = []
+        for run, vis in enumerate(visits_of):
+            if not vis:
+                continue
+            length = self.runs[run].length
+            for k0 in range(0, length, KV_BLOCK):
+                cost = 0
+                for s, kpos in vis:
+                    off = self.seg_kv[s] - self.seg_q[s][1]
+                    first_row = max(0, kpos + k0 - off)
+                    cost += max(0, self.seg_q[s][1] - first_row)
+                kv_items.append((-cost, run, k0))
+        # longest first; ties keep a deterministic order
+        q_items.sort()
+        kv_items.sort()
+        q_work = np.array([(s, q0) for _, s, q0 in q_items], np.int32).reshape(-1, 2)
+        kv_work = np.array([(r, k0) for _, r, k0 in kv_items], np.int32).reshape(-1, 2)
+        seg_spans = np.array(spans, REF_DTYPE) if spans else np.zeros(0, REF_DTYPE)
+        run_visits = np.array(visit_rows, REF_DTYPE) if visit_rows else np.zeros(0, REF_DTYPE)
+        return segs, seg_spans, run_visits, q_work, kv_work, visit0, [len(v) for v in visits_of]
+
+    def device_tables(self, device: torch.device):
+        """Upload the layout's integer tables once per device (pinned, non-blocking)."""
+        key = (device.type, device.index)
+        hit = self._tables.get(key)
+        if hit is not None:
+            return hit
+        with self._lock:
+            hit = self._tables.get(key)
+            if hit is None:
+                segs, spans, visits, q_work, kv_work, visit0, nvisit = self._host_tables()
+                parts = [segs.view(np.uint8), spans.view(np.uint8), visits.view(np.uint8),
+                         q_work.view(np.uint8).reshape(-1), kv_work.view(np.uint8).reshape(-1)]
+                offsets, total = [], 0
+                for p in parts:
+                    offsets.append(total)
+                    total += (p.size + 255) // 256 * 256
+                blob = np.zeros(max(total, 256), np.uint8)
+                for o, p in zip(offsets, parts):
+                    blob[o : o + p.size] = p
+                host = torch.from_numpy(blob).pin_memory() if device.type == "cuda" else torch.from_numpy(blob)
+                dev = host.to(device, non_blocking=True)
+                base = dev.data_ptr()
+                hit = {
+                    "blob": dev,
+                    "host": host,
+                    "segs": base + offsets[0],
+                    "seg_spans": base + offsets[1],
+                    "run_visits": base + offsets[2],
+                    "q_work": base + offsets[3],
+                    "kv_work": base + offsets[4],
+                    "n_q_work": int(q_work.shape[0]),
+                    "n_kv_work": int(kv_work.shape[0]),
+                    "visit0": visit0,
+                    "nvisit": nvisit,
+                }
+                self._tables[key] = hit
+        return hit
+
+    def problem(self, device, runs_ptr: int, scale: float) -> AttnProblem:
+        t = self.device_tables(device)
+        return AttnProblem(
+            t["segs"], t["seg_spans"], runs_ptr, t["run_visits"], t["q_work"], t["kv_work"],
+            t["n_q_work"], t["n_kv_work"], len(self.seg_q), len(self.runs), self.hq, self.hkv,
+            HEAD_DIM, float(scale), q_block_rows(self.hq, self.hkv), KV_BLOCK, self.q_rows,
+        )
+
+    # -- reference diagnostics ---------------------------------------------
+    def visible_pairs(self) -> int:
+        """Exactly visible (query, key) pairs, per head: sum over segments."""
+        total = 0
+        for (_, t), s in zip(self.seg_q, self.seg_kv):
+            total += t * (s - t) + t * (t + 1) // 2
+        return total
+
+
+def _check_rows_tensor(t: torch.Tensor, name: str, heads: int) -> None:
+    if t.dim() != 3 or t.shape[1] != heads or t.shape[2] != HEAD_DIM:
+        raise ValueError(f"{name} must be [rows, {heads}, {HEAD_DIM}], got {tuple(t.shape)}")
+    if t.stride(2) != 1 or t.stride(0) % 8 or t.stride(1) % 8 or t.data_ptr() % 16:
+        raise ValueError(f"{name} needs a contiguous head dim, 16-byte alignment and 8-element strides")
+
+
+def _rows(t: torch.Tensor) -> AttnRows:
+    return AttnRows(t.data_ptr(), t.stride(0), t.stride(1))
+
+
+def _run_table(layout: AttnLayout, keys, values, dkeys=None, dvalues=None) -> torch.Tensor:
+    visit = layout.device_tables(keys[0].device)
+    table = np.zeros(len(layout.runs), RUN_DTYPE)
+    esz = 2
+    for r, run in enumerate(layout.runs):
+        k, v = keys[run.source], values[run.source]
+        row = table[r]
+        row["k"] = k.data_ptr() + run.offset * k.stride(0) * esz
+        row["v"] = v.data_ptr() + run.offset * v.stride(0) * esz
+        row["k_row_stride"], row["k_head_stride"] = k.stride(0), k.stride(1)
+        row["v_row_stride"], row["v_head_stride"] = v.stride(0), v.stride(1)
+        if dkeys is not None:
+            dk, dv = dkeys[run.source], dvalues[run.source]
+            row["dk"] = dk.data_ptr() + run.offset * dk.stride(0) * esz
+            row["dv"] = dv.data_ptr() + run.offset * dv.stride(0) * esz
+            row["dk_row_stride"], row["dk_head_stride"] = dk.stride(0), dk.stride(1)
+            row["dv_row_stride"], row["dv_head_stride"] = dv.stride(0), dv.stride(1)
+        row["len"] = run.length
+        row["visit0"] = visit["visit0"][r]
+        row["nvisit"] = visit["nvisit"][r]
+    host = torch.from_numpy(table.view(np.uint8)).pin_memory()
+    return host.to(keys[0].device, non_blocking=True), host
+
+
+def _validate_call(layout: AttnLayout, query: torch.Tensor, keys, values) -> None:
+    if not query.is_cuda:
+        raise RuntimeError("thundersync_amd attention runs on the GPU only; got a CPU tensor")
+    if query.dtype != torch.bfloat16:
+        raise TypeError(f"thundersync_amd attention takes bf16, got {query.dtype}")
+    _check_rows_tensor(query, "query", layout.hq)
+    if query.shape[0] != layout.q_rows:
+        raise ValueError(f"query has {query.shape[0]} rows, layout {layout.q_rows}")
+    if len(keys) != len(layout.source_rows) or len(values) != len(layout.source_rows):
+        raise ValueError("one K and one V tensor per key source")
+    for i, (k, v) in enumerate(zip(keys, values)):
+        for name, t in (("key", k), ("value", v)):
+            if t.device != query.device or t.dtype != query.dtype:
+                raise ValueError(f"{name} source {i} must be {query.dtype} on {query.device}")
+            _check_rows_tensor(t, f"{name} source {i}", layout.hkv)
+            if t.shape[0] != layout.source_rows[i]:
+                raise ValueError(f"{name} source {i} has {t.shape[0]} rows, layout {layout.source_rows[i]}")
+
+
+class _Attention(torch.autograd.Function):
+    """out, lse = attention over `layout`; grads to query and every key source."""
+
+    @staticmethod
+    def forward(ctx, query, layout, scale, n_sources, *kv):
+        keys, values = list(kv[:n_sources]), list(kv[n_sources:])
+        _validate_call(layout, query, keys, values)
+        lib = _lib.require_library()
+        out = torch.empty(query.shape, dtype=query.dtype, device=query.device)
+        lse = torch.empty(layout.hq, max(layout.q_rows, 1), dtype=torch.float32, device=query.device)
+        runs, host = _run_table(layout, keys, values)
+        problem = layout.problem(query.device, runs.data_ptr(), scale)
+        with operator_range("hip_attention_forward", rows=layout.q_rows, segments=len(layout.seg_q)):
+            _lib.check(
+                lib.ts_attn_fwd(ctypes.byref(problem), _rows(query), _rows(out), lse.data_ptr(),
+                                lse.shape[1], _lib.stream_of(query)),
+                f"ts_attn_fwd(rows={layout.q_rows}, hq={layout.hq}, hkv={layout.hkv})",
+            )
+        ctx.layout, ctx.scale, ctx.n_sources = layout, scale, n_sources
+        ctx.keep = (runs, host)
+        ctx.save_for_backward(query, out, lse, *kv)
+        ctx.mark_non_differentiable(lse)
+        return out, lse
+
+    @staticmethod
+    @torch.autograd.function.once_differentiable
+    def backward(ctx, dout, _dlse):
+        query, out, lse, *kv = ctx.saved_tensors
+        layout, n = ctx.layout, ctx.n_sources
+        keys, values = kv[:n], kv[n:]
+        lib = _lib.require_library()
+        dout = dout.contiguous() if dout.stride(2) != 1 or dout.stride(0) % 8 or dout.stride(1) % 8 else dout
+        dq = torch.empty(query.shape, dtype=query.dtype, device=query.device)
+        covered = sum(t for _, t in layout.seg_q)
+        if covered != layout.q_rows:
+            dq.zero_()
+        dkeys = [torch.empty(k.shape, dtype=k.dtype, device=k.device) for k in keys]
+        dvalues = [torch.empty(v.shape, dtype=v.dtype, device=v.device) for v in values]
+        # rows of a source that no run covers, or runs nobody reads, get zeros
+        visit = layout.device_tables(query.device)
+        covered_rows = [0] * n
+        for r, run in enumerate(layout.runs):
+            if visit["nvisit"][r]:
+                covered_rows[run.source] += run.length
+        for i in range(n):
+            if covered_rows[i] != layout.source_rows[i]:
+                dkeys[i].zero_()
+                dvalues[i].zero_()
+        runs, host = _run_table(layout, keys, values, dkeys, dvalues)
+        delta = torch.empty(layout.hq, max(layout.q_rows, 1), dtype=torch.float32, device=query.device)
+        problem = layout.problem(query.device, runs.data_ptr(), ctx.scale)
+        with operator_range("hip_attention_backward", rows=layout.q_rows, segments=len(layout.seg_q)):
+            _lib.check(
+                lib.ts_attn_bwd(ctypes.byref(problem), _rows(query), _rows(out), _rows(dout),
+                                lse.data_ptr(), lse.shape[1], delta.data_ptr(), _rows(dq),
+                                _lib.stream_of(query)),
+                f"ts_attn_bwd(rows={layout.q_rows}, hq={layout.hq}, hkv={layout.hkv})",
+            )
+        ctx.keep_bwd = (runs, host)
+        return (dq, None, None, None, *dkeys, *dvalues)
+
+
+def attention(query: torch.Tensor, layout: AttnLayout, keys: Sequence[torch.Tensor],
+              values: Sequence[torch.Tensor], scale: float) -> tuple[torch.Tensor, torch.Tensor]:
+    """Core op: query ``[R, Hq, 128]`` bf16 -> (out ``[R, Hq, 128]``, lse ``[Hq, R]`` fp32)."""
+    return _Attention.apply(query, layout, float(scale), len(keys), *keys, *values)
+
+
+# ---------------------------------------------------------------------------
+# layouts for the reference's call shapes
+# ---------------------------------------------------------------------------
+def _dedupe(tensors: Sequence[torch.Tensor]):
+    """Distinct tensors (by identity) and, per input position, its source index."""
+    sources, index, where = [], {}, []
+    for t in tensors:
+        key = id(t)
+        if key not in index:
+            index[key] = len(sources)
+            sources.append(t)
+        where.append(index[key])
+    return sources, where
+
+
+def chain_layout(query_len: int, chunk_lengths: Sequence[int], hq: int, hkv: int) -> AttnLayout:
+    """One segment of `query_len` rows over the concatenation of chunks."""
+    runs = tuple(Run(i, 0, n) for i, n in enumerate(chunk_lengths) if n > 0)
+    spans, pos = [], 0
+    run_index = 0
+    for i, n in enumerate(chunk_lengths):
+        if n > 0:
+            spans.append((run_index, pos))
+            run_index += 1
+            pos += n
+    return AttnLayout(
+        q_rows=query_len, hq=hq, hkv=hkv, source_rows=tuple(chunk_lengths), runs=runs,
+        seg_q=((0, query_len),), seg_spans=(tuple(spans),),
+    )
+
+
+def _query_rows(query: torch.Tensor) -> torch.Tensor:
+    """``[1, Hq, T, D]`` (any strides) -> ``[T, Hq, D]`` view."""
+    if query.dim() != 4 or query.shape[0] != 1:
+        raise ValueError(f"query must be [1, Hq, T, D], got {tuple(query.shape)}")
+    return query[0].transpose(0, 1)
+
+
+def _as_rows(t: torch.Tensor) -> torch.Tensor:
+    """A [rows, heads, D] view usable by the kernels (copy only if it must)."""
+    if t.stride(2) == 1 and t.stride(0) % 8 == 0 and t.stride(1) % 8 == 0 and t.data_ptr() % 16 == 0:
+        return t
+    return t.contiguous()
+
+
+def causal_attention(query: torch.Tensor, ks: Sequence[torch.Tensor], vs: Sequence[torch.Tensor],
+                     scale: float) -> torch.Tensor:
+    """Backend callable ``(query [1,Hq,T,D], ks, vs, scale) -> [1,Hq,T,D]``.
+
+    ``ks``/``vs`` are chunk lists ``[S_c, Hkv, D]`` in chronological order;
+    query row i sees keys ``0 .. S - T + i`` of their concatenation, which is
+    never materialised (engine/streaming.py:1080-1162).
+    """
+    q = _as_rows(_query_rows(query))
+    keys, kw = _dedupe(ks)
+    values, vw = _dedupe(vs)
+    if kw != vw or len(keys) != len(ks):
+        # distinct chunk objects per position keep one run per chunk
+        keys, values = list(ks), list(vs)
+    keys = [_as_rows(k) for k in keys]
+    values = [_as_rows(v) for v in values]
+    layout = chain_layout(q.shape[0], [k.shape[0] for k in keys], q.shape[1], keys[0].shape[1])
+    out, _ = attention(q, layout, keys, values, scale)
+    return out.transpose(0, 1).unsqueeze(0)
+
+
+class ChunkedCausalAttention(torch.autograd.Function):
+    """``apply(query, scale, n_chunks, keep_state, backend, *ks, *vs)``.
+
+    Argument order of ``_ChunkedCausalSDPA`` (engine/streaming.py:1354): the
+    op keeps only the query, its output and log-sum-exp plus references to the
+    per-chunk K/V (never a concatenated copy) and returns one dK/dV per chunk
+    in input order.  ``keep_state`` and ``backend`` are accepted for
+    signature compatibility; this op always keeps the output and LSE, which
+    is what the reference's saved-state mode keeps.
+    """
+
+    @staticmethod
+    def forward(ctx, query, scale, n_chunks, keep_state, backend, *chunks):
+        ks, vs = chunks[:n_chunks], chunks[n_chunks:]
+        with torch.enable_grad():
+            leaves = [c.detach().requires_grad_(c.requires_grad) for c in chunks]
+            q = query.detach().requires_grad_(query.requires_grad)
+            out = causal_attention(q, leaves[:n_chunks], leaves[n_chunks:], scale)
+        ctx.graph = (q, leaves, out)
+        return out.detach()
+
+    @staticmethod
+    @torch.autograd.function.once_differentiable
+    def backward(ctx, grad_out):
+        q, leaves, out = ctx.graph
+        inputs = [t for t in (q, *leaves) if t.requires_grad]
+        grads = torch.autograd.grad(out, inputs, grad_out, allow_unused=True) if inputs else []
+        it = iter(grads)
+        dq = next(it) if q.requires_grad else None
+        rest = [next(it) if c.requires_grad else None for c in leaves]
+        return (dq, None, None, None, None, *rest)
+
+
+@dataclass(eq=False)
+class PackLayout:
+    """Where each segment of a plain turn pack sits (engine/streaming.py:1613-1650).
+
+    ``lengths``: query rows per segment; ``prefixes``: ancestor tokens per
+    segment; ``counts``: ancestor chunks per segment.  ``cu_lengths`` and
+    ``cu_prefixes`` are the int32 cumulative sums ``[0, *accumulate(...)]``.
+    The op's ancestor inputs are grouped by segment, LAST segment first.
+    """
+
+    lengths: list[int]
+    prefixes: list[int]
+    counts: list[int]
+    cu_lengths: torch.Tensor
+    cu_prefixes: torch.Tensor
+    counted: bool = True
+
+    def inputs(self, ancestors):
+        ks = [c for ks, _vs in reversed(ancestors) for c in ks]
+        vs = [c for _ks, vs in reversed(ancestors) for c in vs]
+        return ks + vs
+
+    def by_segment(self, chunks):
+        grouped, offset = [], 0
+        for count in reversed(self.counts):
+            grouped.append(list(chunks[offset : offset + count]))
+            offset += count
+        return grouped[::-1]
+
+
+def pack_layout(lengths: Sequence[int], ancestors, device=None) -> PackLayout:
+    """Build a PackLayout from per-segment lengths and ancestor chunk lists."""
+    from itertools import accumulate
+
+    prefixes = [sum(c.shape[0] for c in ks) for ks, _vs in ancestors]
+    counts = [len(ks) for ks, _vs in ancestors]
+    cu_l = torch.tensor([0, *accumulate(lengths)], dtype=torch.int32)
+    cu_p = torch.tensor([0, *accumulate(prefixes)], dtype=torch.int32)
+    if device is not None and torch.device(device).type == "cuda":
+        cu_l = cu_l.pin_memory().to(device, non_blocking=True)
+        cu_p = cu_p.pin_memory().to(device, non_blocking=True)
+    return PackLayout(list(lengths), prefixes, counts, cu_l, cu_p)
+
+
+class PackedAttention(torch.autograd.Function):
+    """``apply(query, key, value, scale, layout, *ancestors)``, as _PackedFlashSplit.
+
+    ``query [1, Hq, sum(T), D]``, the pack's own ``key``/``value`` ``[sum(T),
+    Hkv, D]``, then the ancestor chunks in ``PackLayout.inputs`` order.  Each
+    segment attends to its ancestors (fully) then its own rows (causally);
+    one forward and one backward launch serve the whole pack.  A chunk object
+    passed for several segments (the shared prompt) is one key run visited
+    by each of them, so its gradient is summed inside the kernel.
+    """
+
+    @staticmethod
+    def forward(ctx, query, key, value, scale, layout, *ancestors):
+        total = sum(layout.counts)
+        a_keys = layout.by_segment(ancestors[:total])
+        a_vals = layout.by_segment(ancestors[total:])
+        q = _as_rows(_query_rows(query))
+        own_k, own_v = _as_rows(key), _as_rows(value)
+        srcs_k, srcs_v, src_index = [own_k], [own_v], {}
+        runs: list[Run] = []
+        seg_q, seg_spans = [], []
+        row0 = 0
+        # own-K/V runs, one per segment (source 0)
+        own_runs = []
+        for length in layout.lengths:
+            own_runs.append(len(runs))
+            runs.append(Run(0, row0, length))
+            row0 += length
+        chunk_run = {}
+        for s, (length, ks, vs) in enumerate(zip(layout.lengths, a_keys, a_vals)):
+            spans, pos = [], 0
+            for kc, vc in zip(ks, vs):
+                if kc.shape[0] == 0:
+                    continue
+                ident = (id(kc), id(vc))
+                if ident not in chunk_run:
+                    if ident not in src_index:
+                        src_index[ident] = len(srcs_k)
+                        srcs_k.append(_as_rows(kc))
+                        srcs_v.append(_as_rows(vc))
+                    chunk_run[ident] = len(runs)
+                    runs.append(Run(src_index[ident], 0, kc.shape[0]))
+                spans.append((chunk_run[ident], pos))
+                pos += kc.shape[0]
+            if length > 0:
+                spans.append((own_runs[s], pos))
+            seg_q.append((sum(layout.lengths[:s]), length))
+            seg_spans.append(tuple(spans))
+        att_layout = AttnLayout(
+            q_rows=q.shape[0], hq=q.shape[1], hkv=own_k.shape[1],
+            source_rows=tuple(t.shape[0] for t in srcs_k), runs=tuple(runs),
+            seg_q=tuple(seg_q), seg_spans=tuple(seg_spans),
+        )
+        with torch.enable_grad():
+            qd = q.detach().requires_grad_(query.requires_grad)
+            kd = [t.detach().requires_grad_(True) for t in srcs_k]
+            vd = [t.detach().requires_grad_(True) for t in srcs_v]
+            out, _ = attention(qd, att_layout, kd, vd, scale)
+        ctx.graph = (qd, kd, vd, out, src_index, layout, a_keys, a_vals)
+        return out.detach().transpose(0, 1).unsqueeze(0)
+
+    @staticmethod
+    @torch.autograd.function.once_differentiable
+    def backward(ctx, grad_out):
+        qd, kd, vd, out, src_index, layout, a_keys, a_vals = ctx.graph
+        g = grad_out[0].transpose(0, 1)
+        inputs = ([qd] if qd.requires_grad else []) + kd + vd
+        grads = torch.autograd.grad(out, inputs, g)
+        it = iter(grads)
+        dq = next(it).transpose(0, 1).unsqueeze(0) if qd.requires_grad else None
+        dks = [next(it) for _ in kd]
+        dvs = [next(it) for _ in vd]
+        # ancestor grads in input order; a chunk object appearing several
+        # times receives its summed gradient once (autograd adds per input)
+        seen = set()
+        anc_k, anc_v = [], []
+        for ks, vs in zip(reversed(a_keys), reversed(a_vals)):
+            for kc, vc in zip(ks, vs):
+                ident = (id(kc), id(vc))
+                if kc.shape[0] == 0:
+                    anc_k.append(torch.zeros_like(kc))
+                    anc_v.append(torch.zeros_like(vc))
+                elif ident in seen:
+                    anc_k.append(None)
+                    anc_v.append(None)
+                else:
+                    seen.add(ident)
+                    anc_k.append(dks[src_index[ident]])
+                    anc_v.append(dvs[src_index[ident]])
+        return (dq, dks[0], dvs[0], None, None, *anc_k, *anc_v)
+
+
+def ragged_causal_attention(queries, keys, values, scale):
+    """``_ragged_causal_sdpa``: per segment ``[1,Hq,T_i,D]`` over ``[S_i,Hkv,D]``."""
+    if not queries:
+        return []
+    outs = []
+    # one launch for the cohort: each segment is its own key run
+    q_rows = [_as_rows(_query_rows(q)) for q in queries]
+    lengths = [q.shape[0] for q in q_rows]
+    packed = torch.cat(q_rows, 0)
+    srcs_k = [_as_rows(k) for k in keys]
+    srcs_v = [_as_rows(v) for v in values]
+    runs = tuple(Run(i, 0, k.shape[0]) for i, k in enumerate(srcs_k))
+    seg_q, row0 = [], 0
+    for n in lengths:
+        seg_q.append((row0, n))
+        row0 += n
+    layout = AttnLayout(
+        q_rows=packed.shape[0], hq=packed.shape[1], hkv=srcs_k[0].shape[1],
+        source_rows=tuple(k.shape[0] for k in srcs_k), runs=runs,
+        seg_q=tuple(seg_q), seg_spans=tuple(((i, 0),) for i in range(len(srcs_k))),
+    )
+    out, _ = attention(packed, layout, srcs_k, srcs_v, scale)
+    for piece in out.split(lengths, 0):
+        outs.append(piece.transpose(0, 1).unsqueeze(0))
+    return outs
+
+
+# ---------------------------------------------------------------------------
+# forest
+# ---------------------------------------------------------------------------
+def forest_layout(plan, hq: int, hkv: int) -> AttnLayout:
+    """Segments = non-empty nodes, runs = node ranges of the one K/V tensor.
+
+    ``plan`` is an ExecutionPlan (engine/plan.py:41-73) or anything with
+    ``node_start``, ``node_end`` (per node) and ``key_ranges`` (per node:
+    ancestor spans then the node's own span, engine/plan.py:248-256).
+    """
+    cached = getattr(plan, "_thundersync_hip_layouts", None)
+    if cached is not None and (hq, hkv) in cached:
+        return cached[(hq, hkv)]
+    starts = [int(x) for x in plan.node_start.tolist()]
+    ends = [int(x) for x in plan.node_end.tolist()]
+    p = int(plan.n_physical) if hasattr(plan, "n_physical") else max(ends, default=0)
+    run_of_start = {}
+    runs = []
+    for n, (s, e) in enumerate(zip(starts, ends)):
+        if e > s:
+            run_of_start[(s, e)] = len(runs)
+            runs.append(Run(0, s, e - s))
+    order = sorted((n for n in range(len(starts)) if ends[n] > starts[n]), key=lambda n: starts[n])
+    seg_q, seg_spans = [], []
+    for n in order:
+        spans, pos = [], 0
+        for s, e in plan.key_ranges[n]:
+            if e <= s:
+                continue
+            if (s, e) not in run_of_start:
+                raise ValueError(f"key range ({s}, {e}) of node {n} is not a node range")
+            spans.append((run_of_start[(s, e)], pos))
+            pos += e - s
+        seg_q.append((starts[n], ends[n] - starts[n]))
+        seg_spans.append(tuple(spans))
+    layout = AttnLayout(
+        q_rows=p, hq=hq, hkv=hkv, source_rows=(p,), runs=tuple(runs),
+        seg_q=tuple(seg_q), seg_spans=tuple(seg_spans),
+    )
+    try:
+        if cached is None:
+            cached = {}
+            object.__setattr__(plan, "_thundersync_hip_layouts", cached)
+        cached[(hq, hkv)] = layout
+    except (AttributeError, TypeError):
+        pass
+    return layout
+
+
+def forest_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, plan, *, scale: float | None = None):
+    """Attention over a segment forest on the physical stream (engine/attention.py:186-231).
+
+    ``q`` ``[P, Hq, D]``, ``k``/``v`` ``[P, Hkv, D]``; returns ``[P, Hq, D]``.
+    Every node attends to its ancestors in full and to itself causally, in
+    one launch per direction; no mask and no ancestor concatenation.
+    """
+    scale = scale if scale is not None else 1.0 / math.sqrt(q.shape[-1])
+    if q.shape[1] % k.shape[1]:
+        raise ValueError(f"query heads {q.shape[1]} are not divisible by KV heads {k.shape[1]}")
+    layout = forest_layout(plan, q.shape[1], k.shape[1])
+    out, _ = attention(_as_rows(q), layout, [_as_rows(k)], [_as_rows(v)], scale)
+    return out
+
+
+# ---------------------------------------------------------------------------
+# transformers AttentionInterface adapters
+# ---------------------------------------------------------------------------
+HIP_ATTENTION_NAME = "thundersync_hip"
+HIP_FOREST_ATTENTION_NAME = "thundersync_hip_forest"
+_PLANS: dict[torch.device, object] = {}
+
+
+def hip_attention_forward(module, query, key, value, attention_mask, scaling=None, dropout=0.0, **kwargs):
+    """Causal attention over one sequence, heads last on the way out.
+
+    The signature and contract of ``fa4_attention_forward``
+    (accel/fa4_attention.py:22-53): ``[B, H, T, D]`` in, ``[B, T, H, D]``
+    out, grouped K/V heads carried natively, dropout refused.
+    """
+    if dropout:
+        raise ValueError("attention dropout is not supported on this path")
+    outs = []
+    for b in range(query.shape[0]):
+        k = key[b].transpose(0, 1)
+        v = value[b].transpose(0, 1)
+        o = causal_attention(query[b : b + 1], [k], [v], scaling if scaling is not None else query.shape[-1] ** -0.5)
+        outs.append(o.transpose(1, 2))
+    return torch.cat(outs, 0), None
+
+
+def forest_attention_forward(module, query, key, value, attention_mask, dropout=0.0, scaling=None, **kwargs):
+    """HF adapter of engine/step.py:60-99 over the plan bound by :func:`forest_context`."""
+    plan = _PLANS.get(query.device)
+    if plan is None:
+        raise RuntimeError("forest attention was invoked outside `forest_context`")
+    if query.shape[0] != 1:
+        raise ValueError(f"the forest is already the batch; expected batch dim 1, got {query.shape[0]}")
+    out = forest_attention(query[0].transpose(0, 1), key[0].transpose(0, 1), value[0].transpose(0, 1),
+                           plan, scale=scaling)
+    return out.unsqueeze(0), None
+
+
+class forest_context:
+    """Bind a plan for the duration of a forward (and backward), per device."""
+
+    def __init__(self, plan, device=None):
+        self.plan = plan
+        self.device = torch.device(device) if device is not None else plan.token_ids.device
+
+    def __enter__(self):
+        self.previous = _PLANS.get(self.device)
+        _PLANS[self.device] = self.plan
+        return self.plan
+
+    def __exit__(self, *exc):
+        if self.previous is None:
+            _PLANS.pop(self.device, None)
+        else:
+            _PLANS[self.device] = self.previous
+        return False
+
+
+def register_attention() -> bool:
+    """Register both adapters with transformers' AttentionInterface."""
+    try:
+        from transformers.modeling_utils import AttentionInterface
+    except Exception:
+        return False
+    AttentionInterface.register(HIP_ATTENTION_NAME, hip_attention_forward)
+    AttentionInterface.register(HIP_FOREST_ATTENTION_NAME, forest_attention_forward)
+    return True

@@ -1,0 +1,686 @@
+// Forest / packed bottom-right-causal GQA attention for gfx950 (bf16, D = 128).
+//
+// One description (segments of query rows, runs of keys read in place, see
+// include/thundersync_hip.h) drives three kernels:
+//
+//   fwd      query-stationary: a work-group owns a block of query rows of one
+//            segment for GC query heads of one GQA group, streams the
+//            segment's key runs through LDS 64 keys at a time (K and V tiles
+//            shared by the GC heads), and keeps an online softmax per row.
+//   dq       query-stationary like fwd, recomputing P from the saved LSE.
+//   dkdv     key-stationary: a work-group owns 64 keys of one run and one KV
+//            head, visits every segment that reads the run, and accumulates
+//            dK/dV for all query heads of the group in registers -- no
+//            atomics, fixed order, so the gradients are deterministic.
+//
+// MFMA mapping (v_mfma_f32_16x16x32_bf16, lane layouts pinned by the
+// layout probe test):
+//   fwd/dq  S^T = K Q^T  (A = K rows from LDS, B = Q^T held in registers);
+//           the accumulator layout gives each lane one query column, so the
+//           softmax statistics of a query live in the four lanes that share
+//           (lane & 15) and P^T is already in the B-operand layout of
+//           O^T += V^T P^T.  V^T (and K^T for dQ) are fed from LDS rows
+//           through an 8x8 register transpose.
+//   dkdv    S = Q K^T, dP = dO V^T (A from LDS rows, B = K^T/V^T held in
+//           registers); dV^T += dO^T P and dK^T += Q^T dS with dO^T / Q^T
+//           from LDS rows through the register transpose.
+// Both sides of every contraction use the same slot permutation of the
+// contracted index, which is all the MFMA requires.
+#include "common.h"
+#include "../../include/thundersync_hip.h"
+
+namespace ts {
+namespace attn {
+
+constexpr int D = 128;
+constexpr int BK = 64;          // keys per tile (fwd / dq) and per dkdv block
+constexpr int kThreads = 256;   // 4 waves
+constexpr int PITCH = D + 8;    // LDS row pitch in elements (272 bytes)
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+__device__ __forceinline__ float neg_inf() { return -__builtin_huge_valf(); }
+
+__device__ __forceinline__ u32x4 ld16(const bf16* p) { return *reinterpret_cast<const u32x4*>(p); }
+__device__ __forceinline__ void st16(bf16* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
+
+// A 64 x 128 tile of K or V rows moved global -> registers -> LDS by 256
+// threads; 16 consecutive threads read one 256-byte row.
+struct Tile {
+  u32x4 v[4];
+};
+
+__device__ __forceinline__ void tile_load(Tile& t, const bf16* base, int64_t row_stride, int nvalid,
+                                          int tid) {
+#pragma unroll
+  for (int it = 0; it < 4; ++it) {
+    const int idx = it * kThreads + tid;
+    const int row = idx >> 4, chunk = idx & 15;
+    if (row < nvalid)
+      t.v[it] = ld16(base + (int64_t)row * row_stride + chunk * 8);
+    else
+      t.v[it] = u32x4{0u, 0u, 0u, 0u};
+  }
+}
+
+__device__ __forceinline__ void tile_store(const Tile& t, bf16* lds, int tid) {
+#pragma unroll
+  for (int it = 0; it < 4; ++it) {
+    const int idx = it * kThreads + tid;
+    st16(lds + (idx >> 4) * PITCH + (idx & 15) * 8, t.v[it]);
+  }
+}
+
+// rows [0, 32) x 128 of a per-head query-row tensor -> LDS (256 threads, 2 loads each)
+__device__ __forceinline__ void rows32_to_lds(bf16* lds, const bf16* base, int64_t row_stride,
+                                              int nvalid, int tid) {
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    const int idx = it * kThreads + tid;
+    const int row = idx >> 4, chunk = idx & 15;
+    u32x4 v = u32x4{0u, 0u, 0u, 0u};
+    if (row < nvalid) v = ld16(base + (int64_t)row * row_stride + chunk * 8);
+    st16(lds + row * PITCH + chunk * 8, v);
+  }
+}
+
+// Eight LDS rows (row index given per slot j) at column c0, transposed: out[e]
+// holds column c0 + e of the eight rows, slot j from row rows[j].
+__device__ __forceinline__ void lds_rows_transposed(const bf16* lds, const int rows[8], int c0,
+                                                    bf16x8 out[8]) {
+  u32x4 in[8], tr[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) in[j] = ld16(lds + rows[j] * PITCH + c0);
+  transpose8x8(in, tr);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) out[e] = as_bf16x8(tr[e]);
+}
+
+// the row of slot j for lane group g: 4g + (j & 3) + 16 (j >> 2)
+__device__ __forceinline__ void slot_rows(int g, int base, int rows[8]) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) rows[j] = base + 4 * g + (j & 3) + 16 * (j >> 2);
+}
+
+__device__ __forceinline__ bf16x8 pack8(const float* x) {
+  u32x4 r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) r[i] = pack_bf2(x[2 * i], x[2 * i + 1]);
+  return as_bf16x8(r);
+}
+
+// Load a wave's 32 query rows x 128 as B operands of S^T = K Q^T:
+// reg[qb][ks] = row (16 qb + (lane & 15)), columns 32 ks + 8 (lane >> 4) .. +7.
+__device__ __forceinline__ void load_rows_b(bf16x8 reg[2][4], const bf16* base, int64_t row_stride,
+                                            int nvalid, int lane) {
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) {
+    const int row = 16 * qb + (lane & 15);
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      u32x4 v = u32x4{0u, 0u, 0u, 0u};
+      if (row < nvalid) v = ld16(base + (int64_t)row * row_stride + 32 * ks + 8 * (lane >> 4));
+      reg[qb][ks] = as_bf16x8(v);
+    }
+  }
+}
+
+// S^T tile (64 keys x 32 rows) = K_lds Q^T: s[kb][qb] lane holds keys
+// 16 kb + 4 (lane >> 4) + i, row 16 qb + (lane & 15).
+__device__ __forceinline__ void tile_scores(f32x4 s[4][2], const bf16* sk, const bf16x8 qreg[2][4],
+                                            int lane) {
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb) {
+    s[kb][0] = f32x4{0.f, 0.f, 0.f, 0.f};
+    s[kb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const bf16x8 a = as_bf16x8(ld16(sk + (16 * kb + (lane & 15)) * PITCH + 32 * ks + 8 * (lane >> 4)));
+      s[kb][0] = mfma16(a, qreg[0][ks], s[kb][0]);
+      s[kb][1] = mfma16(a, qreg[1][ks], s[kb][1]);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// forward
+// ---------------------------------------------------------------------------
+template <int GC>
+__global__ __launch_bounds__(kThreads, 2) void fwd_kernel(ts_attn_problem P, ts_attn_rows Q,
+                                                          ts_attn_rows O, float* __restrict__ lse,
+                                                          int64_t lse_ld) {
+  __shared__ __attribute__((aligned(16))) bf16 sk[BK * PITCH];
+  __shared__ __attribute__((aligned(16))) bf16 sv[BK * PITCH];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int seg_id = P.q_work[2 * blockIdx.x];
+  const int q0 = P.q_work[2 * blockIdx.x + 1];
+  const int group = P.hq / P.hkv;
+  const int chunks = group / GC;
+  const int hk = blockIdx.y / chunks;
+  const int h = hk * group + (blockIdx.y % chunks) * GC + (wave % GC);
+  const ts_attn_segment seg = P.segs[seg_id];
+  const int T = seg.q_len;
+  const int off = seg.kv_len - seg.q_len;
+  const int wq0 = q0 + 32 * (wave / GC);
+  const int wg_last = min(q0 + P.q_block, T) - 1;
+  const bool active = wq0 < T;
+  const int w_last = min(wq0 + 32, T) - 1;
+  const float c = P.scale * kLog2e;
+
+  bf16x8 qreg[2][4];
+  const bf16* qbase = (const bf16*)Q.ptr + (seg.q_row0 + wq0) * Q.row_stride + (int64_t)h * Q.head_stride;
+  load_rows_b(qreg, qbase, Q.row_stride, active ? T - wq0 : 0, lane);
+
+  f32x4 o[2][8];
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[qb][e] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m[2] = {neg_inf(), neg_inf()};
+  float lsum[2] = {0.f, 0.f};
+
+  for (int sp = 0; sp < seg.nspan; ++sp) {
+    const ts_attn_ref ref = P.seg_spans[seg.span0 + sp];
+    const ts_attn_run run = P.runs[ref.index];
+    const bf16* kb0 = (const bf16*)run.k + (int64_t)hk * run.k_head_stride;
+    const bf16* vb0 = (const bf16*)run.v + (int64_t)hk * run.v_head_stride;
+    for (int kt0 = 0; kt0 < run.len; kt0 += BK) {
+      if (ref.kpos + kt0 > off + wg_last) break;  // later keys are invisible to every row
+      const int nvalid = min(BK, run.len - kt0);
+      Tile tk, tv;
+      tile_load(tk, kb0 + (int64_t)kt0 * run.k_row_stride, run.k_row_stride, nvalid, tid);
+      tile_load(tv, vb0 + (int64_t)kt0 * run.v_row_stride, run.v_row_stride, nvalid, tid);
+      __syncthreads();
+      tile_store(tk, sk, tid);
+      tile_store(tv, sv, tid);
+      __syncthreads();
+      if (!active || ref.kpos + kt0 > off + w_last) continue;
+
+      f32x4 s[4][2];
+      tile_scores(s, sk, qreg, lane);
+      const bool need_mask = (kt0 + BK > run.len) || (ref.kpos + kt0 + BK - 1 > off + wq0);
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            float val = s[kb][qb][i] * c;
+            if (need_mask) {
+              const int key = kt0 + 16 * kb + 4 * (lane >> 4) + i;
+              const int row = wq0 + 16 * qb + (lane & 15);
+              if (key >= run.len || ref.kpos + key > off + row) val = neg_inf();
+            }
+            s[kb][qb][i] = val;
+          }
+      // online softmax, one query column per lane (shared by lanes l, l^16, l^32, l^48)
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) {
+        float mx = neg_inf();
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[kb][qb][i]);
+        mx = fmaxf(mx, shfl_xor(mx, 16));
+        mx = fmaxf(mx, shfl_xor(mx, 32));
+        const float mnew = fmaxf(m[qb], mx);
+        const float mref = (mnew == neg_inf()) ? 0.f : mnew;
+        const float alpha = fast_exp2(m[qb] - mref);
+        m[qb] = mnew;
+        float ps = 0.f;
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float p = fast_exp2(s[kb][qb][i] - mref);
+            s[kb][qb][i] = p;
+            ps += p;
+          }
+        lsum[qb] = lsum[qb] * alpha + ps;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[qb][e] *= alpha;
+      }
+      // O^T += V^T P^T, 32 keys per k-step
+#pragma unroll
+      for (int ss = 0; ss < 2; ++ss) {
+        bf16x8 pk[2];
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) {
+          float tmp[8];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) tmp[j] = s[2 * ss + (j >> 2)][qb][j & 3];
+          pk[qb] = pack8(tmp);
+        }
+        int rows[8];
+        slot_rows(lane >> 4, 32 * ss, rows);
+        bf16x8 vt[8];
+        lds_rows_transposed(sv, rows, 8 * (lane & 15), vt);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          o[0][e] = mfma16(vt[e], pk[0], o[0][e]);
+          o[1][e] = mfma16(vt[e], pk[1], o[1][e]);
+        }
+      }
+    }
+  }
+  if (!active) return;
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) {
+    float l = lsum[qb];
+    l += shfl_xor(l, 16);
+    l += shfl_xor(l, 32);
+    const int row = wq0 + 16 * qb + (lane & 15);
+    if (row >= T) continue;
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+    bf16* orow = (bf16*)O.ptr + (seg.q_row0 + row) * O.row_stride + (int64_t)h * O.head_stride +
+                 32 * (lane >> 4);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float tmp[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) tmp[e] = o[qb][e][i] * inv;
+      st16(orow + 8 * i, as_u32x4(pack8(tmp)));
+    }
+    if ((lane >> 4) == 0)
+      lse[(int64_t)h * lse_ld + seg.q_row0 + row] = l > 0.f ? (m[qb] + fast_log2(l)) * kLn2 : neg_inf();
+  }
+}
+
+// ---------------------------------------------------------------------------
+// backward preprocess: delta[h][row] = sum_d dO * O (fp32)
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kThreads) void delta_kernel(ts_attn_rows O, ts_attn_rows dO,
+                                                         float* __restrict__ delta, int64_t lse_ld,
+                                                         int64_t rows, int hq) {
+  const int64_t pair = (int64_t)blockIdx.x * (kThreads / 16) + threadIdx.x / 16;
+  const int sub = threadIdx.x & 15;
+  const int64_t row = pair / hq;
+  const int h = (int)(pair % hq);
+  if (row >= rows) return;
+  const u32x4 a = ld16((const bf16*)O.ptr + row * O.row_stride + (int64_t)h * O.head_stride + 8 * sub);
+  const u32x4 b = ld16((const bf16*)dO.ptr + row * dO.row_stride + (int64_t)h * dO.head_stride + 8 * sub);
+  float acc = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    acc = fmaf(bf_bits_to_f(a[i] & 0xffffu), bf_bits_to_f(b[i] & 0xffffu), acc);
+    acc = fmaf(bf_bits_to_f(a[i] >> 16), bf_bits_to_f(b[i] >> 16), acc);
+  }
+#pragma unroll
+  for (int msk = 8; msk >= 1; msk >>= 1) acc += shfl_xor(acc, msk);
+  if (sub == 0) delta[(int64_t)h * lse_ld + row] = acc;
+}
+
+// ---------------------------------------------------------------------------
+// backward dQ (query-stationary)
+// ---------------------------------------------------------------------------
+template <int GC>
+__global__ __launch_bounds__(kThreads, 1) void dq_kernel(ts_attn_problem P, ts_attn_rows Q,
+                                                         ts_attn_rows dO, const float* __restrict__ lse,
+                                                         const float* __restrict__ delta,
+                                                         int64_t lse_ld, ts_attn_rows dQ) {
+  __shared__ __attribute__((aligned(16))) bf16 sk[BK * PITCH];
+  __shared__ __attribute__((aligned(16))) bf16 sv[BK * PITCH];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int seg_id = P.q_work[2 * blockIdx.x];
+  const int q0 = P.q_work[2 * blockIdx.x + 1];
+  const int group = P.hq / P.hkv;
+  const int chunks = group / GC;
+  const int hk = blockIdx.y / chunks;
+  const int h = hk * group + (blockIdx.y % chunks) * GC + (wave % GC);
+  const ts_attn_segment seg = P.segs[seg_id];
+  const int T = seg.q_len;
+  const int off = seg.kv_len - seg.q_len;
+  const int wq0 = q0 + 32 * (wave / GC);
+  const int wg_last = min(q0 + P.q_block, T) - 1;
+  const bool active = wq0 < T;
+  const int w_last = min(wq0 + 32, T) - 1;
+  const float c = P.scale * kLog2e;
+
+  bf16x8 qreg[2][4], dreg[2][4];
+  const int64_t qoff = (seg.q_row0 + wq0);
+  load_rows_b(qreg, (const bf16*)Q.ptr + qoff * Q.row_stride + (int64_t)h * Q.head_stride, Q.row_stride,
+              active ? T - wq0 : 0, lane);
+  load_rows_b(dreg, (const bf16*)dO.ptr + qoff * dO.row_stride + (int64_t)h * dO.head_stride,
+              dO.row_stride, active ? T - wq0 : 0, lane);
+  float lse2[2], dlt[2];
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) {
+    const int row = wq0 + 16 * qb + (lane & 15);
+    lse2[qb] = __builtin_huge_valf();
+    dlt[qb] = 0.f;
+    if (active && row < T) {
+      const float v = lse[(int64_t)h * lse_ld + seg.q_row0 + row];
+      lse2[qb] = v == neg_inf() ? __builtin_huge_valf() : v * kLog2e;
+      dlt[qb] = delta[(int64_t)h * lse_ld + seg.q_row0 + row];
+    }
+  }
+  f32x4 acc[2][8];
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[qb][e] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int sp = 0; sp < seg.nspan; ++sp) {
+    const ts_attn_ref ref = P.seg_spans[seg.span0 + sp];
+    const ts_attn_run run = P.runs[ref.index];
+    const bf16* kb0 = (const bf16*)run.k + (int64_t)hk * run.k_head_stride;
+    const bf16* vb0 = (const bf16*)run.v + (int64_t)hk * run.v_head_stride;
+    for (int kt0 = 0; kt0 < run.len; kt0 += BK) {
+      if (ref.kpos + kt0 > off + wg_last) break;
+      const int nvalid = min(BK, run.len - kt0);
+      Tile tk, tv;
+      tile_load(tk, kb0 + (int64_t)kt0 * run.k_row_stride, run.k_row_stride, nvalid, tid);
+      tile_load(tv, vb0 + (int64_t)kt0 * run.v_row_stride, run.v_row_stride, nvalid, tid);
+      __syncthreads();
+      tile_store(tk, sk, tid);
+      tile_store(tv, sv, tid);
+      __syncthreads();
+      if (!active || ref.kpos + kt0 > off + w_last) continue;
+
+      f32x4 s[4][2], dp[4][2];
+      tile_scores(s, sk, qreg, lane);
+      tile_scores(dp, sv, dreg, lane);  // dP^T = V dO^T, same shape as S^T
+      const bool need_mask = (kt0 + BK > run.len) || (ref.kpos + kt0 + BK - 1 > off + wq0);
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            float p = fast_exp2(s[kb][qb][i] * c - lse2[qb]);
+            if (need_mask) {
+              const int key = kt0 + 16 * kb + 4 * (lane >> 4) + i;
+              const int row = wq0 + 16 * qb + (lane & 15);
+              if (key >= run.len || ref.kpos + key > off + row) p = 0.f;
+            }
+            s[kb][qb][i] = p * (dp[kb][qb][i] - dlt[qb]);  // dS^T
+          }
+      // dQ^T += K^T dS^T, 32 keys per k-step
+#pragma unroll
+      for (int ss = 0; ss < 2; ++ss) {
+        bf16x8 dsk[2];
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) {
+          float tmp[8];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) tmp[j] = s[2 * ss + (j >> 2)][qb][j & 3];
+          dsk[qb] = pack8(tmp);
+        }
+        int rows[8];
+        slot_rows(lane >> 4, 32 * ss, rows);
+        bf16x8 kt[8];
+        lds_rows_transposed(sk, rows, 8 * (lane & 15), kt);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          acc[0][e] = mfma16(kt[e], dsk[0], acc[0][e]);
+          acc[1][e] = mfma16(kt[e], dsk[1], acc[1][e]);
+        }
+      }
+    }
+  }
+  if (!active) return;
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) {
+    const int row = wq0 + 16 * qb + (lane & 15);
+    if (row >= T) continue;
+    bf16* drow = (bf16*)dQ.ptr + (seg.q_row0 + row) * dQ.row_stride + (int64_t)h * dQ.head_stride +
+                 32 * (lane >> 4);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float tmp[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) tmp[e] = acc[qb][e][i] * P.scale;
+      st16(drow + 8 * i, as_u32x4(pack8(tmp)));
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// backward dK / dV (key-stationary)
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kThreads, 2) void dkdv_kernel(ts_attn_problem P, ts_attn_rows Q,
+                                                           ts_attn_rows dO, const float* __restrict__ lse,
+                                                           const float* __restrict__ delta,
+                                                           int64_t lse_ld) {
+  __shared__ __attribute__((aligned(16))) bf16 sq[32 * PITCH];
+  __shared__ __attribute__((aligned(16))) bf16 sd[32 * PITCH];
+  __shared__ float s_lse2[32];
+  __shared__ float s_dlt[32];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int run_id = P.kv_work[2 * blockIdx.x];
+  const int k0 = P.kv_work[2 * blockIdx.x + 1];
+  const int hk = blockIdx.y;
+  const int group = P.hq / P.hkv;
+  const ts_attn_run run = P.runs[run_id];
+  const int wk0 = k0 + 16 * wave;                 // first key (run-local) of this wave
+  const int mykey = wk0 + (lane & 15);            // key column this lane holds
+  const bool wave_has_keys = wk0 < run.len;
+  const float c = P.scale * kLog2e;
+
+  // K^T / V^T B operands: key (lane & 15), d = 32 ks + 8 (lane >> 4) .. +7
+  bf16x8 kreg[4], vreg[4];
+  {
+    const bf16* kp = (const bf16*)run.k + (int64_t)mykey * run.k_row_stride + (int64_t)hk * run.k_head_stride;
+    const bf16* vp = (const bf16*)run.v + (int64_t)mykey * run.v_row_stride + (int64_t)hk * run.v_head_stride;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      u32x4 a = u32x4{0u, 0u, 0u, 0u}, b = u32x4{0u, 0u, 0u, 0u};
+      if (mykey < run.len) {
+        a = ld16(kp + 32 * ks + 8 * (lane >> 4));
+        b = ld16(vp + 32 * ks + 8 * (lane >> 4));
+      }
+      kreg[ks] = as_bf16x8(a);
+      vreg[ks] = as_bf16x8(b);
+    }
+  }
+  f32x4 dk[8], dv[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    dk[e] = f32x4{0.f, 0.f, 0.f, 0.f};
+    dv[e] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  for (int vi = 0; vi < run.nvisit; ++vi) {
+    const ts_attn_ref ref = P.run_visits[run.visit0 + vi];
+    const ts_attn_segment seg = P.segs[ref.index];
+    const int T = seg.q_len;
+    const int off = seg.kv_len - seg.q_len;
+    // row r sees key k iff kpos + k <= off + r
+    int r_start = ref.kpos + k0 - off;
+    if (r_start < 0) r_start = 0;
+    r_start &= ~31;
+    for (int r0 = r_start; r0 < T; r0 += 32) {
+      const int nrows = min(32, T - r0);
+      // the wave's keys are all invisible to this block when its first key
+      // is beyond the block's last row
+      const bool wave_active = wave_has_keys && (ref.kpos + wk0 <= off + r0 + nrows - 1);
+      for (int g = 0; g < group; ++g) {
+        const int h = hk * group + g;
+        __syncthreads();
+        const int64_t row0 = seg.q_row0 + r0;
+        rows32_to_lds(sq, (const bf16*)Q.ptr + row0 * Q.row_stride + (int64_t)h * Q.head_stride,
+                      Q.row_stride, nrows, tid);
+        rows32_to_lds(sd, (const bf16*)dO.ptr + row0 * dO.row_stride + (int64_t)h * dO.head_stride,
+                      dO.row_stride, nrows, tid);
+        if (tid < 32) {
+          float l2 = __builtin_huge_valf(), dl = 0.f;
+          if (tid < nrows) {
+            const float v = lse[(int64_t)h * lse_ld + row0 + tid];
+            l2 = v == neg_inf() ? __builtin_huge_valf() : v * kLog2e;
+            dl = delta[(int64_t)h * lse_ld + row0 + tid];
+          }
+          s_lse2[tid] = l2;
+          s_dlt[tid] = dl;
+        }
+        __syncthreads();
+        if (!wave_active) continue;
+
+        // S = Q K^T and dP = dO V^T: [qb] lane holds rows 16 qb + 4 (lane >> 4) + i, key (lane & 15)
+        f32x4 s[2], dp[2];
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) {
+          s[qb] = f32x4{0.f, 0.f, 0.f, 0.f};
+          dp[qb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int ks = 0; ks < 4; ++ks) {
+            const int r = 16 * qb + (lane & 15);
+            const bf16x8 aq = as_bf16x8(ld16(sq + r * PITCH + 32 * ks + 8 * (lane >> 4)));
+            const bf16x8 ad = as_bf16x8(ld16(sd + r * PITCH + 32 * ks + 8 * (lane >> 4)));
+            s[qb] = mfma16(aq, kreg[ks], s[qb]);
+            dp[qb] = mfma16(ad, vreg[ks], dp[qb]);
+          }
+        }
+        float pv[8], dsv[8];
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int rl = 16 * qb + 4 * (lane >> 4) + i;
+            float p = fast_exp2(s[qb][i] * c - s_lse2[rl]);
+            if (rl >= nrows || mykey >= run.len || ref.kpos + mykey > off + r0 + rl) p = 0.f;
+            pv[4 * qb + i] = p;
+            dsv[4 * qb + i] = p * (dp[qb][i] - s_dlt[rl]);
+          }
+        const bf16x8 pk = pack8(pv);
+        const bf16x8 dsk = pack8(dsv);
+        int rows[8];
+        slot_rows(lane >> 4, 0, rows);
+        bf16x8 at[8];
+        lds_rows_transposed(sd, rows, 8 * (lane & 15), at);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dv[e] = mfma16(at[e], pk, dv[e]);
+        lds_rows_transposed(sq, rows, 8 * (lane & 15), at);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dk[e] = mfma16(at[e], dsk, dk[e]);
+      }
+    }
+  }
+  if (mykey >= run.len) return;
+  if (run.dk) {
+    bf16* p = (bf16*)run.dk + (int64_t)mykey * run.dk_row_stride + (int64_t)hk * run.dk_head_stride +
+              32 * (lane >> 4);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float tmp[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) tmp[e] = dk[e][i] * P.scale;
+      st16(p + 8 * i, as_u32x4(pack8(tmp)));
+    }
+  }
+  if (run.dv) {
+    bf16* p = (bf16*)run.dv + (int64_t)mykey * run.dv_row_stride + (int64_t)hk * run.dv_head_stride +
+              32 * (lane >> 4);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float tmp[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) tmp[e] = dv[e][i];
+      st16(p + 8 * i, as_u32x4(pack8(tmp)));
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+int heads_per_block(int group) {
+  if (group % 4 == 0) return 4;
+  if (group % 2 == 0) return 2;
+  return 1;
+}
+
+bool aligned_rows(const ts_attn_rows& r) {
+  return r.ptr && (r.ptr % 16 == 0) && (r.row_stride % 8 == 0) && (r.head_stride % 8 == 0) &&
+         r.row_stride > 0;
+}
+
+int validate(const ts_attn_problem* p, const char* what) {
+  TS_CHECK_ARG(p != nullptr, "%s: null problem", what);
+  TS_CHECK_ARG(p->head_dim == D, "%s: head_dim %d unsupported (128 only)", what, p->head_dim);
+  TS_CHECK_ARG(p->hq > 0 && p->hkv > 0 && p->hq % p->hkv == 0, "%s: hq %d not a multiple of hkv %d",
+               what, p->hq, p->hkv);
+  const int gc = heads_per_block(p->hq / p->hkv);
+  TS_CHECK_ARG(p->q_block == 32 * 4 / gc, "%s: q_block %d, expected %d for group %d", what,
+               p->q_block, 32 * 4 / gc, p->hq / p->hkv);
+  TS_CHECK_ARG(p->kv_block == BK, "%s: kv_block %d, expected %d", what, p->kv_block, BK);
+  TS_CHECK_ARG(p->n_q_work >= 0 && p->n_kv_work >= 0 && p->n_segs >= 0 && p->n_runs >= 0,
+               "%s: negative table size", what);
+  TS_CHECK_ARG(p->n_q_work == 0 || (p->q_work && p->segs && p->seg_spans && p->runs),
+               "%s: null table", what);
+  TS_CHECK_ARG((int64_t)(p->hq / p->hkv / gc) * p->hkv <= 65535, "%s: too many heads", what);
+  return TS_OK;
+}
+
+}  // namespace attn
+}  // namespace ts
+
+extern "C" {
+
+int ts_attn_heads_per_block(int group) { return group > 0 ? ts::attn::heads_per_block(group) : 0; }
+
+int ts_attn_fwd(const ts_attn_problem* problem, ts_attn_rows q, ts_attn_rows out, float* lse,
+                int64_t lse_ld, void* stream) {
+  using namespace ts::attn;
+  int st = validate(problem, "ts_attn_fwd");
+  if (st != TS_OK) return st;
+  const ts_attn_problem& P = *problem;
+  if (P.n_q_work == 0) return TS_OK;
+  TS_CHECK_ARG(aligned_rows(q) && aligned_rows(out), "ts_attn_fwd: q/out must be 16-byte aligned "
+               "with strides that are multiples of 8 elements");
+  TS_CHECK_ARG(lse && lse_ld >= P.q_rows, "ts_attn_fwd: lse null or lse_ld %lld < rows %lld",
+               (long long)lse_ld, (long long)P.q_rows);
+  const int group = P.hq / P.hkv;
+  const int gc = heads_per_block(group);
+  const dim3 grid((unsigned)P.n_q_work, (unsigned)(P.hkv * (group / gc)));
+  hipStream_t s = (hipStream_t)stream;
+  if (gc == 4)
+    hipLaunchKernelGGL(fwd_kernel<4>, grid, dim3(kThreads), 0, s, P, q, out, lse, lse_ld);
+  else if (gc == 2)
+    hipLaunchKernelGGL(fwd_kernel<2>, grid, dim3(kThreads), 0, s, P, q, out, lse, lse_ld);
+  else
+    hipLaunchKernelGGL(fwd_kernel<1>, grid, dim3(kThreads), 0, s, P, q, out, lse, lse_ld);
+  return ts::check_launch("ts_attn_fwd");
+}
+
+int ts_attn_bwd(const ts_attn_problem* problem, ts_attn_rows q, ts_attn_rows out, ts_attn_rows dout,
+                const float* lse, int64_t lse_ld, float* delta, ts_attn_rows dq, void* stream) {
+  using namespace ts::attn;
+  int st = validate(problem, "ts_attn_bwd");
+  if (st != TS_OK) return st;
+  const ts_attn_problem& P = *problem;
+  if (P.n_q_work == 0 && P.n_kv_work == 0) return TS_OK;
+  TS_CHECK_ARG(aligned_rows(q) && aligned_rows(out) && aligned_rows(dout) && aligned_rows(dq),
+               "ts_attn_bwd: q/out/dout/dq must be 16-byte aligned with strides that are "
+               "multiples of 8 elements");
+  TS_CHECK_ARG(lse && delta && lse_ld >= P.q_rows, "ts_attn_bwd: lse/delta null or lse_ld too small");
+  TS_CHECK_ARG(P.n_kv_work == 0 || (P.kv_work && P.run_visits), "ts_attn_bwd: null kv tables");
+  hipStream_t s = (hipStream_t)stream;
+  const int64_t pairs = P.q_rows * P.hq;
+  if (pairs > 0) {
+    hipLaunchKernelGGL(delta_kernel, dim3((unsigned)((pairs + 15) / 16)), dim3(kThreads), 0, s, out,
+                       dout, delta, lse_ld, P.q_rows, P.hq);
+    st = ts::check_launch("ts_attn_bwd (delta)");
+    if (st != TS_OK) return st;
+  }
+  const int group = P.hq / P.hkv;
+  const int gc = heads_per_block(group);
+  if (P.n_q_work > 0) {
+    const dim3 grid((unsigned)P.n_q_work, (unsigned)(P.hkv * (group / gc)));
+    if (gc == 4)
+      hipLaunchKernelGGL(dq_kernel<4>, grid, dim3(kThreads), 0, s, P, q, dout, lse, delta, lse_ld, dq);
+    else if (gc == 2)
+      hipLaunchKernelGGL(dq_kernel<2>, grid, dim3(kThreads), 0, s, P, q, dout, lse, delta, lse_ld, dq);
+    else
+      hipLaunchKernelGGL(dq_kernel<1>, grid, dim3(kThreads), 0, s, P, q, dout, lse, delta, lse_ld, dq);
+    st = ts::check_launch("ts_attn_bwd (dq)");
+    if (st != TS_OK) return st;
+  }
+  if (P.n_kv_work > 0) {
+    const dim3 grid((unsigned)P.n_kv_work, (unsigned)P.hkv);
+    hipLaunchKernelGGL(dkdv_kernel, grid, dim3(kThreads), 0, s, P, q, dout, lse, delta, lse_ld);
+    st = ts::check_launch("ts_attn_bwd (dkdv)");
+  }
+  return st;
+}
+
+}  // extern "C"
