@@ -1,8 +1,9 @@
 """RMSNorm HIP kernels against the CPU oracle (accel/rms_norm.py restated).
 
-Bars: the primal within one unit in the last place of the output dtype (the
-fp32 sum of squares is reduced in a different order than torch's, which can
-move rstd by an ulp and, rarely, a rounding of the output); rstd within 2e-6
+Bars: the primal within two units in the last place of the output dtype
+(the fp32 sum of squares is reduced in a different order than torch's, which
+can move rstd by an ulp; the primal rounds twice -- xhat to the dtype, then
+w * xhat -- and each rounding can then land one unit apart); rstd within 2e-6
 relative; dx and dw (fp32 VJP, cast once) within the output dtype's rounding
 of the fp64 closed form.  dW is a fixed-order reduction: two runs are
 bit-identical.
@@ -42,9 +43,9 @@ def test_forward_matches_oracle(cuda, rows, width, dtype):
     got, rstd = rms_norm_forward(x.to(cuda), w.to(cuda), 1e-6)
     torch.cuda.synchronize()
     torch.testing.assert_close(rstd.cpu(), want_rstd, rtol=2e-6, atol=0)
-    # one output ulp for 16-bit outputs; fp32 outputs carry rstd's own
+    # two output units for 16-bit outputs; fp32 outputs carry rstd's own
     # reduction-order difference (a few fp32 ulps)
-    units = 1.01 if dtype != torch.float32 else 8.0
+    units = 2.02 if dtype != torch.float32 else 8.0
     tol = want.float().abs() * ulp(dtype) * units + 1e-30
     err = (got.cpu().float() - want.float()).abs()
     assert bool((err <= tol).all()), float((err / tol).max())

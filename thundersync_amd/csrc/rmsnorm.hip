@@ -230,46 +230,47 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_bwd_vec(
   for (int c = threadIdx.x; c < width; c += kThreads) part[(int64_t)blockIdx.x * width + c] = lds_dw[c];
 }
 
-// backward, scalar path: one wave per row, dW partial per block via LDS
+// backward, scalar path (any width): the block's 256 threads work on one
+// row at a time; thread t owns columns t, t + 256, ... of the dW partial, so
+// one LDS row of `width` floats holds it without conflicts between threads.
 template <typename T>
 __global__ __launch_bounds__(kThreads) void rmsnorm_bwd_scalar(
     const T* __restrict__ dy, const T* __restrict__ x, const T* __restrict__ w,
     const float* __restrict__ rstd, T* __restrict__ dx, float* __restrict__ part,
     int64_t rows, int width, int64_t slab, int want_dx, int want_dw) {
-  extern __shared__ float lds_dw[];  // [4][width]
+  extern __shared__ float lds_dw[];  // [width] (+ 4 floats for the row sum)
+  float* red = lds_dw + width;
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
   const int64_t r0 = (int64_t)blockIdx.x * slab;
   const int64_t r1 = min(rows, r0 + slab);
-  float* mine = lds_dw + wave * width;
-  for (int c = lane; c < width; c += kWave) mine[c] = 0.f;
+  for (int c = threadIdx.x; c < width; c += kThreads) lds_dw[c] = 0.f;
   const float inv_w = 1.f / (float)width;
-  for (int64_t row = r0 + wave; row < r1; row += kThreads / kWave) {
+  for (int64_t row = r0; row < r1; ++row) {
     const float r = rstd[row];
     const T* xr = x + row * width;
     const T* dr = dy + row * width;
     float dot = 0.f;
-    for (int c = lane; c < width; c += kWave) {
+    for (int c = threadIdx.x; c < width; c += kThreads) {
       const float d = to_f(dr[c]);
       const float xv = to_f(xr[c]);
-      mine[c] = fmaf(d * xv, r, mine[c]);
+      lds_dw[c] = fmaf(d * xv, r, lds_dw[c]);
       dot = fmaf(d * to_f(w[c]), xv * r, dot);
     }
     if (want_dx) {
-      dot = wave_sum(dot) * inv_w;
-      for (int c = lane; c < width; c += kWave) {
+      dot = wave_sum(dot);
+      if (lane == 0) red[wave] = dot;
+      __syncthreads();
+      dot = (red[0] + red[1] + red[2] + red[3]) * inv_w;
+      __syncthreads();
+      for (int c = threadIdx.x; c < width; c += kThreads) {
         const float xh = to_f(xr[c]) * r;
         dx[row * width + c] = from_f<T>(r * (to_f(dr[c]) * to_f(w[c]) - xh * dot));
       }
     }
   }
   if (!want_dw) return;
-  __syncthreads();
-  for (int c = threadIdx.x; c < width; c += kThreads) {
-    float s = lds_dw[c];
-    for (int g = 1; g < kThreads / kWave; ++g) s += lds_dw[g * width + c];
-    part[(int64_t)blockIdx.x * width + c] = s;
-  }
+  for (int c = threadIdx.x; c < width; c += kThreads) part[(int64_t)blockIdx.x * width + c] = lds_dw[c];
 }
 
 // dW = T(sum over partial rows, in order)
@@ -337,7 +338,7 @@ int launch_fwd(const void* x, const void* w, void* y, float* rstd, int64_t rows,
     return check_launch("ts_rmsnorm_fwd");                                                  \
   }
   TS_FWD(4, 1) TS_FWD(8, 1) TS_FWD(16, 1) TS_FWD(32, 1) TS_FWD(64, 1)
-  TS_FWD(64, 2) TS_FWD(64, 4) TS_FWD(64, 8) TS_FWD(64, 16)
+  TS_FWD(4, 2) TS_FWD(8, 2) TS_FWD(16, 2) TS_FWD(32, 2) TS_FWD(64, 2) TS_FWD(64, 4) TS_FWD(64, 8) TS_FWD(64, 16)
 #undef TS_FWD
   set_error("ts_rmsnorm_fwd: no kernel for width %d", width);
   return TS_ERR_INVALID;
@@ -351,7 +352,7 @@ int launch_bwd(const void* dy, const void* x, const void* w, const float* rstd, 
   const int64_t slab = (rows + parts - 1) / parts;
   const int want_dx = dx != nullptr, want_dw = dw != nullptr;
   if (g.lpr == 0) {
-    const size_t lds = want_dw ? (size_t)4 * width * sizeof(float) : 0;
+    const size_t lds = (size_t)(width + 4) * sizeof(float);
     if (lds > 160 * 1024) {
       set_error("ts_rmsnorm_bwd: width %d too wide for the scalar dW path", width);
       return TS_ERR_INVALID;
@@ -371,7 +372,7 @@ int launch_bwd(const void* dy, const void* x, const void* w, const float* rstd, 
     launched = true;                                                                         \
   }
     TS_BWD(4, 1) TS_BWD(8, 1) TS_BWD(16, 1) TS_BWD(32, 1) TS_BWD(64, 1)
-    TS_BWD(64, 2) TS_BWD(64, 4) TS_BWD(64, 8) TS_BWD(64, 16)
+    TS_BWD(4, 2) TS_BWD(8, 2) TS_BWD(16, 2) TS_BWD(32, 2) TS_BWD(64, 2) TS_BWD(64, 4) TS_BWD(64, 8) TS_BWD(64, 16)
 #undef TS_BWD
     if (!launched) {
       set_error("ts_rmsnorm_bwd: no kernel for width %d", width);
