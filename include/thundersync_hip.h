@@ -180,6 +180,58 @@ int ts_attn_bwd(const ts_attn_problem* problem, ts_attn_rows q, ts_attn_rows out
                 ts_attn_rows dq, void* stream);
 
 /* ------------------------------------------------------------------------
+ * Fused chunked-vocab logprob / entropy (bf16 operands, fp32 results)
+ *
+ * hidden [rows, dim] (row stride ld_hidden), weight [vocab, dim] (ld_weight),
+ * target int64 [rows].  dim and both leading dimensions are multiples of 8
+ * and the bases 16-byte aligned.
+ * ------------------------------------------------------------------------ */
+
+/* Workspace bytes ts_logprob_fwd needs. */
+int64_t ts_logprob_fwd_workspace(int64_t rows, int64_t vocab);
+
+/* logprob[n] = l[n, target[n]] - lse[n] and, when `entropy` is not NULL,
+ * entropy[n] = lse[n] - sum_v softmax(l[n])_v l[n, v], with l = hidden . W^T
+ * accumulated in fp32 on MFMA; lse (natural log) is written for the backward.
+ * A target outside [0, vocab) yields NaN.
+ * Replaces _FusedLinearLogprob.forward and _FusedLinearLogprobEntropy.forward
+ * (accel/fused_logprob.py:69-113, :249-267): its per-chunk fp32 [chunk, V]
+ * logits, amax, logsumexp, gather and softmax passes. */
+int ts_logprob_fwd(const void* hidden, int64_t ld_hidden, const void* weight,
+                   int64_t ld_weight, const int64_t* target, int64_t rows,
+                   int64_t dim, int64_t vocab, float* logprob, float* entropy,
+                   float* lse, void* workspace, int64_t workspace_bytes,
+                   void* stream);
+
+/* weight_t [dim, ld_t] = W^T with columns [vocab, ld_t) zero (ld_t % 8 == 0,
+ * ld_t >= vocab): the K-contiguous operand of ts_logprob_grad_hidden. */
+int ts_logprob_weight_t(const void* weight, int64_t ld_weight, int64_t vocab,
+                        int64_t dim, void* weight_t, int64_t ld_t, void* stream);
+
+/* dlogits [rows, ld_dlogits] (bf16) =
+ *   -p * (g_lp + g_ent * (log p + H)) + g_lp * onehot(target),
+ * p = exp(l - lse), recomputing l on MFMA; columns [vocab, roundup8(vocab))
+ * are written as zero.  grad_ent may be NULL (logprob-only objective).
+ * Replaces the coefficient backward of _FusedLinearLogprob.backward and
+ * _FusedLinearLogprobEntropy.backward (accel/fused_logprob.py:143-165,
+ * :285-295): rematerialised logits, softmax, scatter_add and bf16 cast. */
+int ts_logprob_dlogits(const void* hidden, int64_t ld_hidden, const void* weight,
+                       int64_t ld_weight, const int64_t* target, const float* lse,
+                       const float* entropy, const float* grad_lp,
+                       const float* grad_ent, int64_t rows, int64_t dim,
+                       int64_t vocab, void* dlogits, int64_t ld_dlogits,
+                       void* stream);
+
+/* grad_hidden [rows, dim] (bf16) = dlogits . W, fp32 accumulation on MFMA,
+ * with W given as weight_t [dim, ld_t] (vocab_padded = roundup8(vocab)).
+ * Replaces the hidden VJP GEMM `_matmul_accum(dlogits, weight)`
+ * (accel/fused_logprob.py:175, :297). */
+int ts_logprob_grad_hidden(const void* dlogits, int64_t ld_dlogits,
+                           const void* weight_t, int64_t ld_t, int64_t rows,
+                           int64_t dim, int64_t vocab_padded, void* grad_hidden,
+                           int64_t ld_grad, void* stream);
+
+/* ------------------------------------------------------------------------
  * Diagnostics
  * ------------------------------------------------------------------------ */
 

@@ -1,0 +1,166 @@
+"""HIP fused logprob / entropy against the CPU oracle (the reference's chunk loop).
+
+Bars: per-token logprobs within 1e-3 and entropies
+within 1e-3, on identical bf16 inputs; grad wrt hidden within 1e-2 x
+max|ref| (both sides round dlogits to bf16 before the VJP GEMM, as the
+reference does, and round the result to bf16).  The full-size C3 check
+compares sampled rows: every row's outputs and gradient depend on that row
+alone, so a sample is an exact parity check of those rows.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle import logprob as ref
+from thundersync_amd import fused_logprob as hip
+
+pytestmark = pytest.mark.gpu
+
+
+def _inputs(n, d, v, seed, wscale=0.02):
+    g = torch.Generator().manual_seed(seed)
+    h = torch.randn(n, d, generator=g).to(torch.bfloat16)
+    w = (torch.randn(v, d, generator=g) * wscale).to(torch.bfloat16)
+    t = torch.randint(0, v, (n,), generator=g)
+    g_lp = torch.randn(n, generator=g)
+    g_ent = torch.randn(n, generator=g)
+    return h, w, t, g_lp, g_ent
+
+
+def rel_close(got, want, bar, what):
+    got, want = got.detach().float().cpu(), want.detach().float().cpu()
+    err = (got - want).abs().max().item()
+    scale = max(want.abs().max().item(), 1e-6)
+    assert err <= bar * scale, f"{what}: max-abs {err:.3g} > {bar} x {scale:.3g}"
+
+
+SHAPES = [(129, 64, 501), (64, 32, 203), (1000, 256, 4099), (300, 4096, 32000), (5, 8, 8), (257, 128, 1024)]
+
+
+@pytest.mark.parametrize("n,d,v", SHAPES)
+def test_entropy_values_and_grad(cuda, n, d, v):
+    print(f"logprob entropy n={n} d={d} v={v}", flush=True)
+    h, w, t, g_lp, g_ent = _inputs(n, d, v, seed=n + d + v)
+    want_lp, want_ent = ref.logprob_entropy_forward(h, w, t, 1024)
+    want_gh, _ = ref.logprob_entropy_backward(h, w, t, want_ent, g_lp, g_ent, 1024)
+    hc = h.to(cuda).requires_grad_()
+    lp, ent = hip.fused_logprob_entropy(hc, w.to(cuda), t.to(cuda))
+    assert lp.dtype == torch.float32 and ent.dtype == torch.float32
+    (lp * g_lp.to(cuda) + ent * g_ent.to(cuda)).sum().backward()
+    torch.cuda.synchronize()
+    torch.testing.assert_close(lp.cpu(), want_lp, rtol=0, atol=1e-3)
+    torch.testing.assert_close(ent.cpu(), want_ent, rtol=0, atol=1e-3)
+    rel_close(hc.grad, want_gh, 1e-2, "grad hidden")
+
+
+@pytest.mark.parametrize("n,d,v", SHAPES[:4])
+def test_logprob_only_values_and_grad(cuda, n, d, v):
+    print(f"logprob n={n} d={d} v={v}", flush=True)
+    h, w, t, g_lp, _ = _inputs(n, d, v, seed=2 * n + v)
+    want = ref.logprob_forward(h, w, t, 1024)
+    want_gh, _ = ref.logprob_backward(h, w, t, g_lp, 1024)
+    hc = h.to(cuda).requires_grad_()
+    lp = hip.fused_logprob(hc, w.to(cuda), t.to(cuda), chunk=7)
+    (lp * g_lp.to(cuda)).sum().backward()
+    torch.cuda.synchronize()
+    torch.testing.assert_close(lp.cpu(), want, rtol=0, atol=1e-3)
+    rel_close(hc.grad, want_gh, 1e-2, "grad hidden")
+
+
+def test_weight_gradient_and_frozen_weight(cuda):
+    h, w, t, g_lp, g_ent = _inputs(96, 48, 307, seed=11, wscale=0.05)
+    _, ent = ref.logprob_entropy_forward(h, w, t, 16)
+    want_gh, want_gw = ref.logprob_entropy_backward(h, w, t, ent, g_lp, g_ent, 16, needs_weight_grad=True)
+    hc, wc = h.to(cuda).requires_grad_(), w.to(cuda).requires_grad_()
+    lp, en = hip.fused_logprob_entropy(hc, wc, t.to(cuda), chunk=16)
+    (lp * g_lp.to(cuda) + en * g_ent.to(cuda)).sum().backward()
+    rel_close(hc.grad, want_gh, 1e-2, "grad hidden")
+    rel_close(wc.grad, want_gw, 1e-2, "grad weight")
+    # frozen weight: no weight gradient is formed
+    hc2 = h.to(cuda).requires_grad_()
+    w2 = w.to(cuda)
+    hip.fused_logprob(hc2, w2, t.to(cuda), chunk=8).sum().backward()
+    assert hc2.grad is not None and w2.grad is None
+
+
+def test_known_answer_precision_cases(cuda):
+    # accel precision cases of the reference (tests/test_accel_projection_precision.py:9-41)
+    hidden = torch.tensor([[1, 1]], dtype=torch.bfloat16, device=cuda)
+    weight = torch.tensor([[256, 1], [256, 0]], dtype=torch.bfloat16, device=cuda)
+    target = torch.tensor([0], device=cuda)
+    expected = torch.log_softmax(torch.nn.functional.linear(hidden.float(), weight.float()), -1)
+    lp, ent = hip.fused_logprob_entropy(hidden, weight, target, chunk=1)
+    torch.testing.assert_close(lp, expected[:, 0], rtol=5e-4, atol=5e-4)
+    torch.testing.assert_close(ent, -(expected.exp() * expected).sum(-1), rtol=5e-4, atol=5e-4)
+    hidden = torch.ones(3, 1, dtype=torch.bfloat16, device=cuda)
+    weight = torch.zeros(2, 1, dtype=torch.bfloat16, device=cuda, requires_grad=True)
+    target = torch.zeros(3, dtype=torch.long, device=cuda)
+    coeff = torch.tensor([512.0, 2.0, -512.0], device=cuda)
+    (coeff * hip.fused_logprob(hidden, weight, target, chunk=1)).sum().backward()
+    assert torch.equal(weight.grad, torch.tensor([[1], [-1]], dtype=torch.bfloat16, device=cuda))
+
+
+def test_gathered_logprobs_and_edge_cases(cuda):
+    h, w, t, _, _ = _inputs(64, 32, 203, seed=5)
+    mask = torch.rand(64, generator=torch.Generator().manual_seed(1)) < 0.3
+    got = hip.gathered_logprobs(h.to(cuda), w.to(cuda), t.to(cuda), mask.to(cuda), chunk=16)
+    want = ref.gathered_logprobs(h, w, t, mask, 16)
+    torch.testing.assert_close(got.cpu(), want, rtol=0, atol=1e-3)
+    ones = torch.ones(64, dtype=torch.bool, device=cuda)
+    assert float(hip.gathered_logprobs(h.to(cuda), w.to(cuda), t.to(cuda), ones)[0]) == 0.0
+    zeros = torch.zeros(64, dtype=torch.bool, device=cuda)
+    assert float(hip.gathered_logprobs(h.to(cuda), w.to(cuda), t.to(cuda), zeros).abs().sum()) == 0.0
+    # empty input
+    lp, ent = hip.fused_logprob_entropy(h[:0].to(cuda), w.to(cuda), t[:0].to(cuda))
+    assert lp.shape == (0,) and ent.shape == (0,)
+    # a target outside the vocabulary is reported as NaN, not a wrong number
+    bad = t.clone()
+    bad[3] = 203
+    lp = hip.fused_logprob(h.to(cuda), w.to(cuda), bad.to(cuda))
+    assert torch.isnan(lp[3]).item() and not torch.isnan(lp[:3]).any().item()
+
+
+def test_validation_errors(cuda):
+    h = torch.randn(4, 8, dtype=torch.bfloat16, device=cuda)
+    w = torch.randn(16, 8, dtype=torch.bfloat16, device=cuda)
+    t = torch.zeros(4, dtype=torch.long, device=cuda)
+    with pytest.raises(ValueError, match=r"hidden must be \[N, D\]"):
+        hip.fused_logprob(h[0], w, t)
+    with pytest.raises(ValueError, match="one entry per hidden row"):
+        hip.fused_logprob(h, w, t[:3])
+    with pytest.raises(ValueError, match="does not match hidden dim"):
+        hip.fused_logprob(h, w[:, :4], t)
+    with pytest.raises(TypeError):
+        hip.fused_logprob(h.float(), w.float(), t)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        hip.fused_logprob(h.cpu(), w.cpu(), t.cpu())
+
+
+def test_c3_full_size_sampled_rows(cuda):
+    """C3 shapes: 16384 x 4096 hidden, 151936 x 4096 head, 70% scored rows gated first."""
+    n, d, v = 16384, 4096, 151936
+    g = torch.Generator(device=cuda).manual_seed(0)
+    h = torch.randn(n, d, generator=g, device=cuda, dtype=torch.bfloat16)
+    w = (torch.randn(v, d, generator=g, device=cuda) * 0.02).to(torch.bfloat16)
+    t = torch.randint(0, v, (n,), generator=g, device=cuda)
+    adv = torch.randn(n, generator=g, device=cuda)
+    mask = torch.rand(n, generator=g, device=cuda) < 0.7
+    idx = mask.nonzero(as_tuple=True)[0]
+    hs = h.index_select(0, idx).requires_grad_()
+    print(f"c3 full size: scored rows {idx.numel()}", flush=True)
+    lp, ent = hip.fused_logprob_entropy(hs, w, t[idx])
+    (lp * adv[idx]).sum().backward()
+    torch.cuda.synchronize()
+    sample = torch.arange(0, idx.numel(), max(1, idx.numel() // 24), device=cuda)[:24]
+    sample = torch.cat([sample, torch.tensor([idx.numel() - 1], device=cuda)])
+    hs_cpu = hs.detach()[sample].cpu()
+    w_cpu = w.cpu()
+    t_cpu = t[idx][sample].cpu()
+    want_lp, want_ent = ref.logprob_entropy_forward(hs_cpu, w_cpu, t_cpu, 1024)
+    want_gh, _ = ref.logprob_entropy_backward(hs_cpu, w_cpu, t_cpu, want_ent, adv[idx][sample].cpu(),
+                                              torch.zeros(sample.numel()), 1024)
+    torch.testing.assert_close(lp[sample].cpu(), want_lp, rtol=0, atol=1e-3)
+    torch.testing.assert_close(ent[sample].cpu(), want_ent, rtol=0, atol=1e-3)
+    rel_close(hs.grad[sample], want_gh, 1e-2, "grad hidden (sampled rows)")

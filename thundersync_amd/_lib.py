@@ -42,6 +42,14 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "ts_rmsnorm_bwd_workspace": (_I64, [_I64, _I64]),
     "ts_rmsnorm_bwd": (_INT, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _INT, _P]),
     "ts_probe_layouts": (_INT, [_P, _P, _P, _P, _P, _P, _P]),
+    "ts_logprob_fwd_workspace": (_I64, [_I64, _I64]),
+    "ts_logprob_fwd": (_INT, [_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _P, _P, _P, _P, _I64, _P]),
+    "ts_logprob_weight_t": (_INT, [_P, _I64, _I64, _I64, _P, _I64, _P]),
+    "ts_logprob_dlogits": (
+        _INT,
+        [_P, _I64, _P, _I64, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P, _I64, _P],
+    ),
+    "ts_logprob_grad_hidden": (_INT, [_P, _I64, _P, _I64, _I64, _I64, _I64, _P, _I64, _P]),
     "ts_attn_heads_per_block": (_INT, [_INT]),
     "ts_attn_fwd": (_INT, [ctypes.POINTER(AttnProblem), AttnRows, AttnRows, _P, _I64, _P]),
     "ts_attn_bwd": (

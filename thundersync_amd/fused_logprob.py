@@ -1,0 +1,205 @@
+"""Fused chunked-vocab logprob / entropy on the gfx950 kernels.
+
+Drop-in for the reference's ``accel/fused_logprob.py:197-367``: same
+signatures, same validation errors, same outputs (fp32 ``[N]``), same
+gradient semantics -- gradient with respect to ``hidden`` always, with
+respect to ``weight`` only when ``weight.requires_grad``.
+
+Forward: ``ts_logprob_fwd`` computes logits tile by tile on MFMA and reduces
+them in the GEMM epilogue; no ``[N, V]`` or ``[chunk, V]`` logit block is
+ever stored.  It returns logprob, entropy and the per-row log-sum-exp, which
+the backward reuses instead of recomputing the row statistics.
+
+Backward: ``ts_logprob_dlogits`` recomputes the logits and writes bf16
+dlogits for a block of rows (rounded to bf16 as the reference rounds its
+dlogits to the hidden dtype, fused_logprob.py:165 and :295);
+``ts_logprob_grad_hidden`` multiplies them by the weight (read through a
+transposed copy made once per backward call).  The block is
+``max(chunk, 4096)`` rows, so peak memory stays ``O(block * V)`` as in the
+reference, independent of N.
+
+bf16 only, GPU only: other dtypes and CPU tensors raise.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from .operator_profiling import device_role, operator_range
+
+MIN_BACKWARD_ROWS = 4096
+
+
+def _validate(hidden: torch.Tensor, weight: torch.Tensor, target: torch.Tensor) -> None:
+    # the reference's contract, accel/fused_logprob.py:209-216
+    if hidden.dim() != 2:
+        raise ValueError(f"hidden must be [N, D], got {tuple(hidden.shape)}")
+    if target.shape[0] != hidden.shape[0]:
+        raise ValueError("target must have one entry per hidden row")
+    if weight.shape[1] != hidden.shape[1]:
+        raise ValueError(f"weight {tuple(weight.shape)} does not match hidden dim {hidden.shape[1]}")
+    if not hidden.is_cuda or not weight.is_cuda or not target.is_cuda:
+        raise RuntimeError("thundersync_amd fused logprob runs on the GPU only; got a CPU tensor")
+    if hidden.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
+        raise TypeError(
+            f"thundersync_amd fused logprob takes bf16 hidden and weight, got {hidden.dtype}/{weight.dtype}"
+        )
+
+
+def _pad_dim(t: torch.Tensor) -> torch.Tensor:
+    """Zero-pad the hidden dim to a multiple of 8 (the logits are unchanged)."""
+    pad = (-t.shape[1]) % 8
+    return torch.nn.functional.pad(t, (0, pad)) if pad else t
+
+
+def _rows_ok(t: torch.Tensor) -> torch.Tensor:
+    if t.stride(1) == 1 and t.stride(0) % 8 == 0 and t.data_ptr() % 16 == 0:
+        return t
+    return t.contiguous()
+
+
+def _forward(hidden, weight, target, with_entropy):
+    lib = _lib.require_library()
+    h, w = _rows_ok(_pad_dim(hidden)), _rows_ok(_pad_dim(weight))
+    t = target.to(torch.int64).contiguous()
+    n, d = h.shape
+    v = w.shape[0]
+    lp = torch.empty(n, dtype=torch.float32, device=h.device)
+    lse = torch.empty(n, dtype=torch.float32, device=h.device)
+    ent = torch.empty(n, dtype=torch.float32, device=h.device) if with_entropy else None
+    ws_bytes = int(lib.ts_logprob_fwd_workspace(n, v))
+    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=h.device)
+    _lib.check(
+        lib.ts_logprob_fwd(
+            h.data_ptr(), h.stride(0), w.data_ptr(), w.stride(0), t.data_ptr(), n, d, v,
+            lp.data_ptr(), _lib.ptr(ent), lse.data_ptr(), ws.data_ptr(), ws_bytes,
+            _lib.stream_of(h),
+        ),
+        f"ts_logprob_fwd(rows={n}, dim={d}, vocab={v})",
+    )
+    return lp, ent, lse
+
+
+def _backward(hidden, weight, target, lse, ent, grad_lp, grad_ent, chunk, needs_weight_grad):
+    lib = _lib.require_library()
+    d_in = hidden.shape[1]
+    h, w = _rows_ok(_pad_dim(hidden)), _rows_ok(_pad_dim(weight))
+    t = target.to(torch.int64).contiguous()
+    n, d = h.shape
+    v = w.shape[0]
+    vp = (v + 7) // 8 * 8
+    grad_hidden = torch.empty_like(h)
+    grad_weight = torch.zeros(v, d, dtype=torch.float32, device=h.device) if needs_weight_grad else None
+    if n == 0:
+        return grad_hidden[:, :d_in], (grad_weight[:, :d_in].to(weight.dtype) if grad_weight is not None else None)
+    stream = _lib.stream_of(h)
+    wt = torch.empty(d, vp, dtype=w.dtype, device=w.device)
+    _lib.check(lib.ts_logprob_weight_t(w.data_ptr(), w.stride(0), v, d, wt.data_ptr(), vp, stream),
+               f"ts_logprob_weight_t(vocab={v}, dim={d})")
+    block = max(int(chunk), MIN_BACKWARD_ROWS)
+    block = (block + 127) // 128 * 128
+    block = min(block, (n + 127) // 128 * 128)
+    dl = torch.empty(block, vp, dtype=w.dtype, device=w.device)
+    g_lp = grad_lp.to(torch.float32).contiguous()
+    g_ent = grad_ent.to(torch.float32).contiguous() if grad_ent is not None else None
+    for i in range(0, n, block):
+        rows = min(block, n - i)
+        hi = h[i : i + rows]
+        with operator_range("logprob_head_coefficient_backward", role=device_role(h.device), rows=rows, vocab=v):
+            _lib.check(
+                lib.ts_logprob_dlogits(
+                    hi.data_ptr(), h.stride(0), w.data_ptr(), w.stride(0), t[i:].data_ptr(),
+                    lse[i:].data_ptr(), ent[i:].data_ptr() if ent is not None else None,
+                    g_lp[i:].data_ptr(), g_ent[i:].data_ptr() if g_ent is not None else None,
+                    rows, d, v, dl.data_ptr(), vp, stream,
+                ),
+                f"ts_logprob_dlogits(rows={rows}, dim={d}, vocab={v})",
+            )
+        with operator_range("logprob_head_hidden_vjp", role=device_role(h.device), rows=rows, hidden=d, vocab=v):
+            _lib.check(
+                lib.ts_logprob_grad_hidden(
+                    dl.data_ptr(), vp, wt.data_ptr(), vp, rows, d, vp,
+                    grad_hidden[i:].data_ptr(), grad_hidden.stride(0), stream,
+                ),
+                f"ts_logprob_grad_hidden(rows={rows}, dim={d}, vocab={v})",
+            )
+        if grad_weight is not None:
+            # fp32 accumulation across blocks, cast once (fused_logprob.py:176-193)
+            with operator_range("logprob_head_weight_vjp", role=device_role(h.device), rows=rows, hidden=d, vocab=v):
+                grad_weight.add_(torch.mm(dl[:rows, :v].t(), hi, out_dtype=torch.float32))
+    if d != d_in:
+        grad_hidden = grad_hidden[:, :d_in].contiguous()
+        grad_weight = grad_weight[:, :d_in] if grad_weight is not None else None
+    return grad_hidden, (grad_weight.to(weight.dtype) if grad_weight is not None else None)
+
+
+class _FusedLinearLogprob(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, hidden, weight, target, chunk, needs_weight_grad):
+        with operator_range("fused_logprob_forward", role=device_role(hidden.device), tokens=hidden.shape[0],
+                            hidden=hidden.shape[1], vocab=weight.shape[0], dtype=hidden.dtype):
+            lp, _ent, lse = _forward(hidden, weight, target, False)
+        ctx.save_for_backward(hidden, weight, target, lse)
+        ctx.chunk, ctx.needs_weight_grad = chunk, needs_weight_grad
+        return lp
+
+    @staticmethod
+    @torch.autograd.function.once_differentiable
+    def backward(ctx, grad_out):
+        hidden, weight, target, lse = ctx.saved_tensors
+        with operator_range("fused_logprob_backward", role=device_role(hidden.device), tokens=hidden.shape[0],
+                            hidden=hidden.shape[1], vocab=weight.shape[0], weight_grad=ctx.needs_weight_grad):
+            gh, gw = _backward(hidden, weight, target, lse, None, grad_out, None, ctx.chunk, ctx.needs_weight_grad)
+        return gh, gw, None, None, None
+
+
+class _FusedLinearLogprobEntropy(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, hidden, weight, target, chunk, needs_weight_grad):
+        with operator_range("fused_logprob_entropy_forward", role=device_role(hidden.device),
+                            tokens=hidden.shape[0], hidden=hidden.shape[1], vocab=weight.shape[0]):
+            lp, ent, lse = _forward(hidden, weight, target, True)
+        ctx.save_for_backward(hidden, weight, target, lse, ent)
+        ctx.chunk, ctx.needs_weight_grad = chunk, needs_weight_grad
+        return lp, ent
+
+    @staticmethod
+    @torch.autograd.function.once_differentiable
+    def backward(ctx, grad_lp, grad_ent):
+        hidden, weight, target, lse, ent = ctx.saved_tensors
+        with operator_range("fused_logprob_entropy_backward", role=device_role(hidden.device),
+                            tokens=hidden.shape[0], hidden=hidden.shape[1], vocab=weight.shape[0]):
+            gh, gw = _backward(hidden, weight, target, lse, ent, grad_lp, grad_ent, ctx.chunk,
+                               ctx.needs_weight_grad)
+        return gh, gw, None, None, None
+
+
+def fused_logprob(hidden: torch.Tensor, weight: torch.Tensor, target: torch.Tensor, *, chunk: int = 1024):
+    """Per-position log pi(target | context) without materialising ``[N, V]``."""
+    _validate(hidden, weight, target)
+    return _FusedLinearLogprob.apply(hidden, weight, target, chunk, weight.requires_grad)
+
+
+def fused_logprob_entropy(hidden: torch.Tensor, weight: torch.Tensor, target: torch.Tensor, *,
+                          chunk: int = 1024):
+    """Per-position (logprob, entropy of the full-vocabulary distribution)."""
+    _validate(hidden, weight, target)
+    return _FusedLinearLogprobEntropy.apply(hidden, weight, target, chunk, weight.requires_grad)
+
+
+def gathered_logprobs(hidden: torch.Tensor, weight: torch.Tensor, token_ids: torch.Tensor,
+                      loss_mask: torch.Tensor, *, chunk: int = 1024) -> torch.Tensor:
+    """Logprobs laid back out over the sequence, zero where not needed (FL:341-367).
+
+    Position k is predicted from position k-1's hidden state; position 0 is
+    never scored.  Projection happens only for masked positions.
+    """
+    n = token_ids.shape[0]
+    idx = loss_mask.nonzero(as_tuple=True)[0]
+    idx = idx[idx > 0]
+    if idx.numel() == 0:
+        return torch.zeros(n, dtype=torch.float32, device=hidden.device)
+    lp = fused_logprob(hidden[idx - 1], weight, token_ids[idx], chunk=chunk)
+    out = torch.zeros(n, dtype=lp.dtype, device=lp.device)
+    return out.index_put((idx,), lp)
