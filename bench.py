@@ -1,0 +1,378 @@
+#!/usr/bin/env python3
+"""Benchmark of the hot path on one MI355X; prints ONE JSON line.
+
+Workloads (synthetic data drawn from fixed seeds):
+
+* ``value``: C2 forest attention, forward + backward -- one shared
+  2048-token prompt and 8 sibling completions of lengths U[256, 4096],
+  32 query / 8 KV heads, head dim 128, bf16; TFLOP/s counted as
+  14 * D * Hq * (exactly visible query/key pairs).
+* ``secondary[0]``: C3 fused logprob + entropy, forward + gradient wrt
+  hidden -- hidden [16384, 4096], head [151936, 4096], 70% of rows scored
+  and gated before the projection (the reference's production schedule),
+  frozen head; scored tokens/s, 6 * N * V * D FLOP.
+* ``secondary[1]``: RMSNorm forward + backward on [16384, 4096] bf16; GB/s.
+
+A step is one pass of the operator over its whole input, with inputs
+already resident in HBM.  Per-kernel device time comes from the library's
+own HIP-event brackets (ts_timing_*), recorded on the stream each kernel is
+launched on, over the timed steps; ``roofline`` names the kernel with the
+largest share.  ``cpu_baseline`` times the CPU oracle (the build's op-for-op
+restatement of the reference's eager path) on a bounded sample of the same
+workload, on the host cores.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "forest-attn fwd+bwd TFLOP/s; fused-logprob fwd+bwd tokens/s (1 MI355X)"
+PEAK_BF16_TFLOPS = 2500.0  # dense bf16 MFMA, MI355X
+PEAK_HBM_GBS = 8000.0
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--only", choices=("all", "attention", "logprob", "rmsnorm"), default="all")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    return ap.parse_args()
+
+
+def cpu_threads() -> int:
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:  # pragma: no cover
+        n = os.cpu_count() or 1
+    return max(1, min(n, 16))
+
+
+def timed(step, steps, warmup, kernels):
+    """(ms per step, {kernel: (avg ms per launch, launches per step)})."""
+    import torch
+
+    from thundersync_amd._lib import KernelTimer
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    with KernelTimer():
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            step()
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        per = {}
+        for k in kernels:
+            total, n = KernelTimer.read(k)
+            if n:
+                per[k] = (total / n, n / steps)
+    return (t1 - t0) * 1e3 / steps, per
+
+
+def roofline_of(per, work_per_launch, unit, peak):
+    """Roofline object for the kernel with the largest device time per step."""
+    name = max(per, key=lambda k: per[k][0] * per[k][1])
+    avg_ms, _ = per[name]
+    achieved = work_per_launch[name] / (avg_ms * 1e-3) / (1e12 if unit == "TFLOP/s" else 1e9)
+    return {
+        "kernel": name,
+        "bound": "mfma" if unit == "TFLOP/s" else "hbm",
+        "achieved": round(achieved, 2),
+        "peak": peak,
+        "unit": unit,
+        "frac": round(achieved / peak, 4),
+        "traffic": None,
+        "avg_launch_ms": round(avg_ms, 4),
+    }
+
+
+# ---------------------------------------------------------------------------
+# C2 forest attention
+# ---------------------------------------------------------------------------
+def c2_inputs(seed, device):
+    import torch
+
+    from thundersync_amd import forest
+
+    g = torch.Generator().manual_seed(seed)
+    lengths = torch.randint(256, 4097, (8,), generator=g).tolist()
+    prompt = torch.randint(0, 100000, (2048,), generator=g).tolist()
+    trajs = []
+    for i, n in enumerate(lengths):
+        body = [100000 + i] + torch.randint(0, 100000, (n - 1,), generator=g).tolist()
+        trajs.append(forest.Trajectory([forest.Segment.prompt(prompt), forest.Segment.action(body)],
+                                       group_id=0, traj_id=i))
+    plan = forest.compile_plan(forest.build_forest(trajs))
+    p = plan.n_physical
+    gd = torch.Generator(device=device).manual_seed(seed)
+    q = torch.randn(p, 32, 128, generator=gd, device=device, dtype=torch.bfloat16).requires_grad_()
+    k = torch.randn(p, 8, 128, generator=gd, device=device, dtype=torch.bfloat16).requires_grad_()
+    v = torch.randn(p, 8, 128, generator=gd, device=device, dtype=torch.bfloat16).requires_grad_()
+    dout = torch.randn(p, 32, 128, generator=gd, device=device, dtype=torch.bfloat16)
+    return plan, lengths, q, k, v, dout
+
+
+def bench_attention(args, device):
+    import torch
+
+    from thundersync_amd import attention
+
+    plan, lengths, q, k, v, dout = c2_inputs(args.seed, device)
+    layout = attention.forest_layout(plan, 32, 8)
+    pairs = layout.visible_pairs()
+    d, hq = 128, 32
+
+    def step():
+        q.grad = k.grad = v.grad = None
+        out = attention.forest_attention(q, k, v, plan)
+        out.backward(dout)
+
+    kernels = ["attention.fwd_kernel", "attention.delta_kernel", "attention.dq_kernel", "attention.dkdv_kernel"]
+    ms, per = timed(step, args.steps, args.warmup, kernels)
+    flop = 14 * d * hq * pairs
+    work = {
+        "attention.fwd_kernel": 4 * d * hq * pairs,
+        "attention.dq_kernel": 2 * d * hq * pairs,
+        "attention.dkdv_kernel": 8 * d * hq * pairs,
+        "attention.delta_kernel": 2 * d * hq * plan.n_physical,
+    }
+    result = {
+        "value": round(flop / (ms * 1e-3) / 1e12, 2),
+        "unit": "TFLOP/s",
+        "ms_per_step": round(ms, 4),
+        "roofline": roofline_of(per, work, "TFLOP/s", PEAK_BF16_TFLOPS),
+        "kernels": {k: {"avg_ms": round(a, 4), "launches_per_step": n} for k, (a, n) in per.items()},
+        "config": {
+            "workload": "C2 forest attention fwd+bwd: 2048-token shared prompt + 8 completions "
+                        "U[256,4096], 32/8 heads, head_dim 128, bf16",
+            "completion_lengths": lengths,
+            "tokens": plan.n_physical,
+            "visible_pairs": pairs,
+            "flop_per_step": flop,
+            "seed": args.seed,
+        },
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = attention_cpu_baseline(plan, q, k, v, dout, lengths)
+    return result
+
+
+def attention_cpu_baseline(plan, q, k, v, dout, lengths):
+    """The reference's CPU dispatch (masked SDPA, causal_lower_right, GQA by
+    repeat_interleave; engine/streaming.py:1146-1162) on the prompt node and
+    the first completion node, fp32, forward + backward."""
+    import torch
+
+    from oracle import attention as ref
+
+    torch.set_num_threads(cpu_threads())
+    qc, kc, vc, dc = (t.detach().float().cpu() for t in (q, k, v, dout))
+    starts, ends = plan.node_start.tolist(), plan.node_end.tolist()
+    work = []
+    for n in (0, 1):
+        s, e = starts[n], ends[n]
+        keys = [(a, b) for a, b in plan.key_ranges[n] if b > a]
+        work.append((s, e, keys))
+    pairs = sum((e - s) * (sum(b - a for a, b in keys) - (e - s)) + (e - s) * (e - s + 1) // 2
+                for s, e, keys in work)
+    t0 = time.perf_counter()
+    for s, e, keys in work:
+        qq = qc[s:e].clone().requires_grad_()
+        kk = torch.cat([kc[a:b] for a, b in keys]).requires_grad_()
+        vv = torch.cat([vc[a:b] for a, b in keys]).requires_grad_()
+        out = ref.sdpa_lower_right(qq, kk, vv, 128 ** -0.5)
+        torch.autograd.grad(out, (qq, kk, vv), dc[s:e])
+    dt = time.perf_counter() - t0
+    return {
+        "value": round(14 * 128 * 32 * pairs / dt / 1e12, 4),
+        "unit": "TFLOP/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"prompt node (2048 rows) + first completion node ({lengths[0]} rows) of the same C2 "
+                  f"forest, {pairs} visible pairs, fp32 masked SDPA fwd+bwd on the host",
+        "seconds": round(dt, 3),
+    }
+
+
+# ---------------------------------------------------------------------------
+# C3 fused logprob
+# ---------------------------------------------------------------------------
+def bench_logprob(args, device):
+    import torch
+
+    from thundersync_amd import fused_logprob
+
+    n, d, v = 16384, 4096, 151936
+    g = torch.Generator(device=device).manual_seed(args.seed)
+    hidden = torch.randn(n, d, generator=g, device=device, dtype=torch.bfloat16)
+    weight = (torch.randn(v, d, generator=g, device=device) * 0.02).to(torch.bfloat16)
+    target = torch.randint(0, v, (n,), generator=g, device=device)
+    adv = torch.randn(n, generator=g, device=device)
+    mask = torch.rand(n, generator=g, device=device) < 0.7
+    idx = mask.nonzero(as_tuple=True)[0]
+    h = hidden.index_select(0, idx).requires_grad_()
+    t = target.index_select(0, idx)
+    a = adv.index_select(0, idx)
+    rows = int(idx.numel())
+
+    def step():
+        h.grad = None
+        lp, ent = fused_logprob.fused_logprob_entropy(h, weight, t)
+        lp.backward(a)
+
+    kernels = ["logprob.fwd_stats_kernel", "logprob.combine_kernel", "logprob.transpose_kernel",
+               "logprob.dlogits_kernel", "logprob.grad_hidden_kernel"]
+    ms, per = timed(step, args.steps, args.warmup, kernels)
+    gemm = 2 * rows * v * d
+    work = {
+        "logprob.fwd_stats_kernel": gemm,
+        "logprob.dlogits_kernel": gemm,
+        "logprob.grad_hidden_kernel": gemm,
+        "logprob.combine_kernel": 0,
+        "logprob.transpose_kernel": 0,
+    }
+    flop = 3 * gemm
+    result = {
+        "metric": "fused-logprob fwd+bwd tokens/s",
+        "value": round(rows / (ms * 1e-3), 1),
+        "unit": "tokens/s",
+        "tflops": round(flop / (ms * 1e-3) / 1e12, 2),
+        "mfma_frac": round(flop / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+        "ms_per_step": round(ms, 4),
+        "roofline": roofline_of({k: x for k, x in per.items() if work[k]}, work, "TFLOP/s", PEAK_BF16_TFLOPS),
+        "kernels": {k: {"avg_ms": round(x, 4), "launches_per_step": m} for k, (x, m) in per.items()},
+        "config": {
+            "workload": "C3 fused logprob+entropy fwd + grad wrt hidden: hidden [16384,4096] bf16, "
+                        "head [151936,4096] bf16 N(0,0.02), 70% scored rows gated first, frozen head",
+            "scored_rows": rows,
+            "flop_per_step": flop,
+            "seed": args.seed,
+        },
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = logprob_cpu_baseline(h, weight, t, a)
+    return result
+
+
+def logprob_cpu_baseline(h, weight, t, a, rows=96):
+    """The reference's chunk loop (accel/fused_logprob.py:250-308, CPU branch)
+    on the first `rows` scored rows, fwd + backward wrt hidden."""
+    import torch
+
+    from oracle import logprob as ref
+
+    torch.set_num_threads(cpu_threads())
+    hs = h.detach()[:rows].cpu()
+    w = weight.cpu()
+    ts = t[:rows].cpu()
+    g = a[:rows].cpu()
+    t0 = time.perf_counter()
+    lp, ent = ref.logprob_entropy_forward(hs, w, ts, 1024)
+    ref.logprob_entropy_backward(hs, w, ts, ent, g, torch.zeros(rows), 1024)
+    dt = time.perf_counter() - t0
+    return {
+        "value": round(rows / dt, 2),
+        "unit": "tokens/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"{rows} scored rows of C3 (dim 4096, vocab 151936), chunk 1024, fwd + grad wrt hidden",
+        "seconds": round(dt, 3),
+    }
+
+
+# ---------------------------------------------------------------------------
+# RMSNorm
+# ---------------------------------------------------------------------------
+def bench_rmsnorm(args, device):
+    import torch
+
+    from thundersync_amd import rms_norm
+
+    r, w_ = 16384, 4096
+    g = torch.Generator(device=device).manual_seed(args.seed)
+    x = torch.randn(r, w_, generator=g, device=device, dtype=torch.bfloat16).requires_grad_()
+    w = torch.linspace(0.4, 3.0, w_, device=device).to(torch.bfloat16).requires_grad_()
+    dy = torch.randn(r, w_, generator=g, device=device, dtype=torch.bfloat16)
+
+    def step():
+        x.grad = w.grad = None
+        y = rms_norm.FP32RMSNormVJP.apply(x, w, 1e-6)
+        y.backward(dy)
+
+    kernels = ["rmsnorm.rmsnorm_fwd_vec", "rmsnorm.rmsnorm_bwd_vec", "rmsnorm.rmsnorm_dw_reduce"]
+    ms, per = timed(step, args.steps, args.warmup, kernels)
+    fwd_bytes = 4 * r * w_ + 4 * r + 2 * w_
+    bwd_bytes = 6 * r * w_ + 4 * r + 2 * w_ + 4 * w_
+    work = {"rmsnorm.rmsnorm_fwd_vec": fwd_bytes, "rmsnorm.rmsnorm_bwd_vec": bwd_bytes,
+            "rmsnorm.rmsnorm_dw_reduce": 0}
+    return {
+        "metric": "RMSNorm fwd+bwd GB/s",
+        "value": round((fwd_bytes + bwd_bytes) / (ms * 1e-3) / 1e9, 1),
+        "unit": "GB/s",
+        "ms_per_step": round(ms, 4),
+        "roofline": roofline_of({k: x for k, x in per.items() if work[k]}, work, "GB/s", PEAK_HBM_GBS),
+        "kernels": {k: {"avg_ms": round(x, 4), "launches_per_step": m} for k, (x, m) in per.items()},
+        "config": {"workload": "RMSNorm fwd+bwd [16384, 4096] bf16, FP32 VJP with dW", "seed": args.seed},
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (every box here has one GPU)",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    device = torch.device("cuda:0")
+    torch.cuda.set_device(device)
+    out = {
+        "metric": METRIC,
+        "value": None,
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": None,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {},
+        "secondary": [],
+    }
+    if args.only in ("all", "attention"):
+        att = bench_attention(args, device)
+        out["value"] = att.pop("value")
+        out["ms_per_step"] = att.pop("ms_per_step")
+        out["config"] = att.pop("config")
+        out["roofline"] = att.pop("roofline")
+        out["kernels"] = att.pop("kernels")
+        if "cpu_baseline" in att:
+            out["cpu_baseline"] = att.pop("cpu_baseline")
+    if args.only in ("all", "logprob"):
+        out["secondary"].append(bench_logprob(args, device))
+    if args.only in ("all", "rmsnorm"):
+        out["secondary"].append(bench_rmsnorm(args, device))
+    props = torch.cuda.get_device_properties(device)
+    out["device"] = {"name": props.name, "arch": getattr(props, "gcnArchName", ""),
+                     "cus": props.multi_processor_count}
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

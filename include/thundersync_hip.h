@@ -235,6 +235,18 @@ int ts_logprob_grad_hidden(const void* dlogits, int64_t ld_dlogits,
  * Diagnostics
  * ------------------------------------------------------------------------ */
 
+/* Per-kernel device timing.  While enabled, every kernel launch of the
+ * library is bracketed by two HIP events recorded on its own stream;
+ * ts_timing_read sums the elapsed milliseconds of the bracketed launches of
+ * one kernel ("attention.fwd_kernel", "logprob.dlogits_kernel", ...) and
+ * ts_timing_reset forgets them.  No counterpart in the reference (its
+ * timing goes through torch.profiler / CUDA events around whole
+ * operators, grpo/reward_linear.py:95-105); used by bench.py to report
+ * each kernel's achieved rate against its roofline. */
+int ts_timing_enable(int enable);
+int ts_timing_reset(void);
+int ts_timing_read(const char* kernel, double* total_ms, int64_t* launches);
+
 /* Runs one v_mfma_f32_16x16x32_bf16 and one v_mfma_f32_32x32x16_bf16 on
  * operands the caller lays out per lane (a, b: 64 lanes x 8 bf16 each), and
  * the 8x8 16-bit register transpose on `t_in` (64 lanes x 8 x 8 bf16).

@@ -42,6 +42,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "ts_rmsnorm_bwd_workspace": (_I64, [_I64, _I64]),
     "ts_rmsnorm_bwd": (_INT, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _INT, _P]),
     "ts_probe_layouts": (_INT, [_P, _P, _P, _P, _P, _P, _P]),
+    "ts_timing_enable": (_INT, [_INT]),
+    "ts_timing_reset": (_INT, []),
+    "ts_timing_read": (_INT, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_I64)]),
     "ts_logprob_fwd_workspace": (_I64, [_I64, _I64]),
     "ts_logprob_fwd": (_INT, [_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _P, _P, _P, _P, _I64, _P]),
     "ts_logprob_weight_t": (_INT, [_P, _I64, _I64, _I64, _P, _I64, _P]),
@@ -164,3 +167,30 @@ def stream_of(tensor) -> int:
 
 def ptr(tensor) -> int | None:
     return None if tensor is None else tensor.data_ptr()
+
+
+class KernelTimer:
+    """Per-kernel device time of the library's launches inside a ``with`` block.
+
+    Uses the library's HIP-event brackets (ts_timing_*), which are recorded
+    on the stream each kernel is launched on.
+    """
+
+    def __enter__(self):
+        lib = require_library()
+        lib.ts_timing_reset()
+        lib.ts_timing_enable(1)
+        return self
+
+    def __exit__(self, *exc):
+        require_library().ts_timing_enable(0)
+        return False
+
+    @staticmethod
+    def read(kernel: str) -> tuple[float, int]:
+        """(total milliseconds, launches) of ``kernel`` since the last reset."""
+        lib = require_library()
+        total = ctypes.c_double()
+        n = ctypes.c_int64()
+        check(lib.ts_timing_read(kernel.encode(), ctypes.byref(total), ctypes.byref(n)), "ts_timing_read")
+        return total.value, n.value

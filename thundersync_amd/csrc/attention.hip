@@ -27,6 +27,7 @@
 // Both sides of every contraction use the same slot permutation of the
 // contracted index, which is all the MFMA requires.
 #include "common.h"
+#include "timing.h"
 #include "../../include/thundersync_hip.h"
 
 namespace ts {
@@ -634,11 +635,11 @@ int ts_attn_fwd(const ts_attn_problem* problem, ts_attn_rows q, ts_attn_rows out
   const dim3 grid((unsigned)P.n_q_work, (unsigned)(P.hkv * (group / gc)));
   hipStream_t s = (hipStream_t)stream;
   if (gc == 4)
-    hipLaunchKernelGGL(fwd_kernel<4>, grid, dim3(kThreads), 0, s, P, q, out, lse, lse_ld);
+    { ts::TimedLaunch timed_("attention.fwd_kernel", s); hipLaunchKernelGGL(fwd_kernel<4>, grid, dim3(kThreads), 0, s, P, q, out, lse, lse_ld); }
   else if (gc == 2)
-    hipLaunchKernelGGL(fwd_kernel<2>, grid, dim3(kThreads), 0, s, P, q, out, lse, lse_ld);
+    { ts::TimedLaunch timed_("attention.fwd_kernel", s); hipLaunchKernelGGL(fwd_kernel<2>, grid, dim3(kThreads), 0, s, P, q, out, lse, lse_ld); }
   else
-    hipLaunchKernelGGL(fwd_kernel<1>, grid, dim3(kThreads), 0, s, P, q, out, lse, lse_ld);
+    { ts::TimedLaunch timed_("attention.fwd_kernel", s); hipLaunchKernelGGL(fwd_kernel<1>, grid, dim3(kThreads), 0, s, P, q, out, lse, lse_ld); }
   return ts::check_launch("ts_attn_fwd");
 }
 
@@ -657,8 +658,8 @@ int ts_attn_bwd(const ts_attn_problem* problem, ts_attn_rows q, ts_attn_rows out
   hipStream_t s = (hipStream_t)stream;
   const int64_t pairs = P.q_rows * P.hq;
   if (pairs > 0) {
-    hipLaunchKernelGGL(delta_kernel, dim3((unsigned)((pairs + 15) / 16)), dim3(kThreads), 0, s, out,
-                       dout, delta, lse_ld, P.q_rows, P.hq);
+    { ts::TimedLaunch timed_("attention.delta_kernel", s); hipLaunchKernelGGL(delta_kernel, dim3((unsigned)((pairs + 15) / 16)), dim3(kThreads), 0, s, out,
+                       dout, delta, lse_ld, P.q_rows, P.hq); }
     st = ts::check_launch("ts_attn_bwd (delta)");
     if (st != TS_OK) return st;
   }
@@ -667,17 +668,17 @@ int ts_attn_bwd(const ts_attn_problem* problem, ts_attn_rows q, ts_attn_rows out
   if (P.n_q_work > 0) {
     const dim3 grid((unsigned)P.n_q_work, (unsigned)(P.hkv * (group / gc)));
     if (gc == 4)
-      hipLaunchKernelGGL(dq_kernel<4>, grid, dim3(kThreads), 0, s, P, q, dout, lse, delta, lse_ld, dq);
+      { ts::TimedLaunch timed_("attention.dq_kernel", s); hipLaunchKernelGGL(dq_kernel<4>, grid, dim3(kThreads), 0, s, P, q, dout, lse, delta, lse_ld, dq); }
     else if (gc == 2)
-      hipLaunchKernelGGL(dq_kernel<2>, grid, dim3(kThreads), 0, s, P, q, dout, lse, delta, lse_ld, dq);
+      { ts::TimedLaunch timed_("attention.dq_kernel", s); hipLaunchKernelGGL(dq_kernel<2>, grid, dim3(kThreads), 0, s, P, q, dout, lse, delta, lse_ld, dq); }
     else
-      hipLaunchKernelGGL(dq_kernel<1>, grid, dim3(kThreads), 0, s, P, q, dout, lse, delta, lse_ld, dq);
+      { ts::TimedLaunch timed_("attention.dq_kernel", s); hipLaunchKernelGGL(dq_kernel<1>, grid, dim3(kThreads), 0, s, P, q, dout, lse, delta, lse_ld, dq); }
     st = ts::check_launch("ts_attn_bwd (dq)");
     if (st != TS_OK) return st;
   }
   if (P.n_kv_work > 0) {
     const dim3 grid((unsigned)P.n_kv_work, (unsigned)P.hkv);
-    hipLaunchKernelGGL(dkdv_kernel, grid, dim3(kThreads), 0, s, P, q, dout, lse, delta, lse_ld);
+    { ts::TimedLaunch timed_("attention.dkdv_kernel", s); hipLaunchKernelGGL(dkdv_kernel, grid, dim3(kThreads), 0, s, P, q, dout, lse, delta, lse_ld); }
     st = ts::check_launch("ts_attn_bwd (dkdv)");
   }
   return st;

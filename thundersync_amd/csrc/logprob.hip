@@ -22,6 +22,7 @@
 // time through double-buffered LDS (pitch 72 bf16: conflict-free 16-byte
 // fragment reads), v_mfma_f32_32x32x16_bf16.
 #include "common.h"
+#include "timing.h"
 #include "../../include/thundersync_hip.h"
 
 namespace ts {
@@ -127,6 +128,24 @@ __device__ __forceinline__ void gemm_tile(f32x16 acc[4][2], const bf16* A, int64
   }
 }
 
+// (max, sum exp(l - max), sum exp(l - max) (l - max)) of two disjoint sets of
+// logits, either of which may be empty (max = -inf)
+__device__ __forceinline__ void merge_stats(float& m, float& s, float& e, float mo, float so, float eo) {
+  if (mo == neg_inf()) return;
+  if (m == neg_inf()) {
+    m = mo;
+    s = so;
+    e = eo;
+    return;
+  }
+  const float mn = fmaxf(m, mo);
+  const float a = fast_exp2((m - mn) * kLog2e);
+  const float b = fast_exp2((mo - mn) * kLog2e);
+  e = a * (e + s * (m - mn)) + b * (eo + so * (mo - mn));
+  s = a * s + b * so;
+  m = mn;
+}
+
 __device__ __forceinline__ int a_row(int mi, int i, int lane, int wm) {
   return 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3) + 32 * mi + 128 * wm;
 }
@@ -195,13 +214,7 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_stats_kernel(FwdArgs p) {
     // merge with the other half-wave (lane ^ 32 holds the other vocab rows)
     {
       const float mo = shfl_xor(m, 32), so = shfl_xor(s, 32), eo = shfl_xor(e, 32);
-      const float mn = fmaxf(m, mo);
-      const float a = (m == neg_inf()) ? 0.f : fast_exp2((m - mn) * kLog2e);
-      const float b = (mo == neg_inf()) ? 0.f : fast_exp2((mo - mn) * kLog2e);
-      e = a * (e + s * (m - mn)) + b * (eo + so * (mo - mn));
-      s = a * s + b * so;
-      m = mn;
-      if (m == neg_inf()) { s = 0.f; e = 0.f; }
+      merge_stats(m, s, e, mo, so, eo);
     }
     if (wm == 1 && lane < 32) {
       xm[col] = m;
@@ -210,16 +223,11 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_stats_kernel(FwdArgs p) {
     }
     __syncthreads();
     if (wm == 0 && lane < 32 && n < p.rows) {
-      const float mo = xm[col], so = xs[col], eo = xe[col];
-      const float mn = fmaxf(m, mo);
-      const float a = (m == neg_inf()) ? 0.f : fast_exp2((m - mn) * kLog2e);
-      const float b = (mo == neg_inf()) ? 0.f : fast_exp2((mo - mn) * kLog2e);
-      const float en = a * (e + s * (m - mn)) + b * (eo + so * (mo - mn));
-      const float sn = a * s + b * so;
+      merge_stats(m, s, e, xm[col], xs[col], xe[col]);
       const int64_t o = (int64_t)vt * p.rows + n;
-      p.part_m[o] = mn;
-      p.part_s[o] = sn;
-      p.part_e[o] = en;
+      p.part_m[o] = m;
+      p.part_s[o] = s;
+      p.part_e[o] = e;
     }
     __syncthreads();
   }
@@ -475,13 +483,13 @@ int ts_logprob_fwd(const void* hidden, int64_t ld_hidden, const void* weight, in
   hipStream_t s = (hipStream_t)stream;
   int st = allow_lds((const void*)fwd_stats_kernel, "ts_logprob_fwd");
   if (st != TS_OK) return st;
-  hipLaunchKernelGGL(fwd_stats_kernel, dim3((unsigned)(a.n_ttiles * a.n_vtiles)), dim3(kThreads),
-                     kGemmLds, s, a);
+  { ts::TimedLaunch timed_("logprob.fwd_stats_kernel", s); hipLaunchKernelGGL(fwd_stats_kernel, dim3((unsigned)(a.n_ttiles * a.n_vtiles)), dim3(kThreads),
+                     kGemmLds, s, a); }
   st = ts::check_launch("ts_logprob_fwd (tiles)");
   if (st != TS_OK) return st;
-  hipLaunchKernelGGL(combine_kernel, dim3((unsigned)((rows + kThreads - 1) / kThreads)), dim3(kThreads),
+  { ts::TimedLaunch timed_("logprob.combine_kernel", s); hipLaunchKernelGGL(combine_kernel, dim3((unsigned)((rows + kThreads - 1) / kThreads)), dim3(kThreads),
                      0, s, a.part_m, a.part_s, a.part_e, a.tgt, target, (int)rows, a.n_vtiles,
-                     (int)vocab, logprob, entropy, lse);
+                     (int)vocab, logprob, entropy, lse); }
   return ts::check_launch("ts_logprob_fwd (combine)");
 }
 
@@ -493,9 +501,9 @@ int ts_logprob_weight_t(const void* weight, int64_t ld_weight, int64_t vocab, in
                "ts_logprob_weight_t: bad arguments vocab=%lld dim=%lld ld_t=%lld", (long long)vocab,
                (long long)dim, (long long)ld_t);
   const dim3 grid((unsigned)((ld_t + 63) / 64), (unsigned)((dim + 63) / 64));
-  hipLaunchKernelGGL(transpose_kernel, grid, dim3(kThreads), 0, (hipStream_t)stream,
+  { ts::TimedLaunch timed_("logprob.transpose_kernel", (hipStream_t)stream); hipLaunchKernelGGL(transpose_kernel, grid, dim3(kThreads), 0, (hipStream_t)stream,
                      (const ts::bf16*)weight, ld_weight, (int)vocab, (int)dim, (ts::bf16*)weight_t,
-                     ld_t);
+                     ld_t); }
   return ts::check_launch("ts_logprob_weight_t");
 }
 
@@ -535,8 +543,8 @@ int ts_logprob_dlogits(const void* hidden, int64_t ld_hidden, const void* weight
   TS_CHECK_ARG(a.vocab_pad <= ld_dlogits, "ts_logprob_dlogits: ld_dlogits below padded vocab");
   int st = allow_lds((const void*)dlogits_kernel, "ts_logprob_dlogits");
   if (st != TS_OK) return st;
-  hipLaunchKernelGGL(dlogits_kernel, dim3((unsigned)(a.n_ttiles * a.n_vtiles)), dim3(kThreads),
-                     kGemmLds, (hipStream_t)stream, a);
+  { ts::TimedLaunch timed_("logprob.dlogits_kernel", (hipStream_t)stream); hipLaunchKernelGGL(dlogits_kernel, dim3((unsigned)(a.n_ttiles * a.n_vtiles)), dim3(kThreads),
+                     kGemmLds, (hipStream_t)stream, a); }
   return ts::check_launch("ts_logprob_dlogits");
 }
 
@@ -567,8 +575,8 @@ int ts_logprob_grad_hidden(const void* dlogits, int64_t ld_dlogits, const void* 
   a.ldd = ld_grad;
   int st = allow_lds((const void*)grad_hidden_kernel, "ts_logprob_grad_hidden");
   if (st != TS_OK) return st;
-  hipLaunchKernelGGL(grad_hidden_kernel, dim3((unsigned)(a.n_ttiles * a.n_dtiles)), dim3(kThreads),
-                     kGemmLds, (hipStream_t)stream, a);
+  { ts::TimedLaunch timed_("logprob.grad_hidden_kernel", (hipStream_t)stream); hipLaunchKernelGGL(grad_hidden_kernel, dim3((unsigned)(a.n_ttiles * a.n_dtiles)), dim3(kThreads),
+                     kGemmLds, (hipStream_t)stream, a); }
   return ts::check_launch("ts_logprob_grad_hidden");
 }
 

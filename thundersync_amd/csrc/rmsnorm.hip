@@ -10,6 +10,7 @@
 // Reference semantics: accel/rms_norm.py:9-43 (forward casts, FP32 VJP) and
 // grpo/rms_norm_native.py:8-74 (dW = sum over rows of dy * x * rstd in fp32).
 #include "common.h"
+#include "timing.h"
 #include "../../include/thundersync_hip.h"
 
 namespace ts {
@@ -325,16 +326,16 @@ int launch_fwd(const void* x, const void* w, void* y, float* rstd, int64_t rows,
   const Geometry g = pick(width, 0);
   if (g.lpr == 0) {
     const int64_t blocks = (rows + 3) / 4;
-    hipLaunchKernelGGL(rmsnorm_fwd_scalar<T>, dim3((unsigned)blocks), dim3(kThreads), 0, s,
-                       (const T*)x, (const T*)w, (T*)y, rstd, rows, width, eps);
+    { ts::TimedLaunch timed_("rmsnorm.rmsnorm_fwd_scalar", s); hipLaunchKernelGGL(rmsnorm_fwd_scalar<T>, dim3((unsigned)blocks), dim3(kThreads), 0, s,
+                       (const T*)x, (const T*)w, (T*)y, rstd, rows, width, eps); }
     return check_launch("ts_rmsnorm_fwd");
   }
   const int64_t rows_per_block = 4 * (64 / g.lpr);
   const dim3 grid((unsigned)((rows + rows_per_block - 1) / rows_per_block));
 #define TS_FWD(LPR, NV)                                                                     \
   if (g.lpr == LPR && g.nv == NV) {                                                         \
-    hipLaunchKernelGGL((rmsnorm_fwd_vec<T, LPR, NV>), grid, dim3(kThreads), 0, s,           \
-                       (const T*)x, (const T*)w, (T*)y, rstd, rows, width, eps);            \
+    { ts::TimedLaunch timed_("rmsnorm.rmsnorm_fwd_vec", s); hipLaunchKernelGGL((rmsnorm_fwd_vec<T, LPR, NV>), grid, dim3(kThreads), 0, s,           \
+                       (const T*)x, (const T*)w, (T*)y, rstd, rows, width, eps); }            \
     return check_launch("ts_rmsnorm_fwd");                                                  \
   }
   TS_FWD(4, 1) TS_FWD(8, 1) TS_FWD(16, 1) TS_FWD(32, 1) TS_FWD(64, 1)
@@ -357,18 +358,18 @@ int launch_bwd(const void* dy, const void* x, const void* w, const float* rstd, 
       set_error("ts_rmsnorm_bwd: width %d too wide for the scalar dW path", width);
       return TS_ERR_INVALID;
     }
-    hipLaunchKernelGGL(rmsnorm_bwd_scalar<T>, dim3((unsigned)parts), dim3(kThreads), lds, s,
+    { ts::TimedLaunch timed_("rmsnorm.rmsnorm_bwd_scalar", s); hipLaunchKernelGGL(rmsnorm_bwd_scalar<T>, dim3((unsigned)parts), dim3(kThreads), lds, s,
                        (const T*)dy, (const T*)x, (const T*)w, rstd, (T*)dx, part, rows, width,
-                       slab, want_dx, want_dw);
+                       slab, want_dx, want_dw); }
   } else {
     const size_t lds = want_dw ? (size_t)width * sizeof(float) : 0;
     const dim3 grid((unsigned)parts);
     bool launched = false;
 #define TS_BWD(LPR, NV)                                                                      \
   if (!launched && g.lpr == LPR && g.nv == NV) {                                             \
-    hipLaunchKernelGGL((rmsnorm_bwd_vec<T, LPR, NV>), grid, dim3(kThreads), lds, s,          \
+    { ts::TimedLaunch timed_("rmsnorm.rmsnorm_bwd_vec", s); hipLaunchKernelGGL((rmsnorm_bwd_vec<T, LPR, NV>), grid, dim3(kThreads), lds, s,          \
                        (const T*)dy, (const T*)x, (const T*)w, rstd, (T*)dx, part, rows,     \
-                       width, slab, want_dx, want_dw);                                        \
+                       width, slab, want_dx, want_dw); }                                        \
     launched = true;                                                                         \
   }
     TS_BWD(4, 1) TS_BWD(8, 1) TS_BWD(16, 1) TS_BWD(32, 1) TS_BWD(64, 1)
@@ -381,8 +382,8 @@ int launch_bwd(const void* dy, const void* x, const void* w, const float* rstd, 
   }
   int st = check_launch("ts_rmsnorm_bwd");
   if (st != TS_OK || !want_dw) return st;
-  hipLaunchKernelGGL(rmsnorm_dw_reduce<T>, dim3((unsigned)((width + kThreads - 1) / kThreads)),
-                     dim3(kThreads), 0, s, (const float*)part, (T*)dw, (int)parts, width);
+  { ts::TimedLaunch timed_("rmsnorm.rmsnorm_dw_reduce", s); hipLaunchKernelGGL(rmsnorm_dw_reduce<T>, dim3((unsigned)((width + kThreads - 1) / kThreads)),
+                     dim3(kThreads), 0, s, (const float*)part, (T*)dw, (int)parts, width); }
   return check_launch("ts_rmsnorm_bwd (dW reduce)");
 }
 
