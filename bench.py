@@ -82,11 +82,17 @@ def timed(step, steps, warmup, kernels):
     return (t1 - t0) * 1e3 / steps, per
 
 
-def roofline_of(per, work_per_launch, unit, peak):
-    """Roofline object for the kernel with the largest device time per step."""
+def roofline_of(per, work_per_step, unit, peak):
+    """Roofline object for the kernel with the largest device time per step.
+
+    ``work_per_step`` is the kernel's algorithmic work over one step; a kernel
+    launched several times per step (the logprob backward runs one launch per
+    row block) does that work split over its launches.
+    """
     name = max(per, key=lambda k: per[k][0] * per[k][1])
-    avg_ms, _ = per[name]
-    achieved = work_per_launch[name] / (avg_ms * 1e-3) / (1e12 if unit == "TFLOP/s" else 1e9)
+    avg_ms, launches = per[name]
+    per_launch = work_per_step[name] / launches
+    achieved = per_launch / (avg_ms * 1e-3) / (1e12 if unit == "TFLOP/s" else 1e9)
     return {
         "kernel": name,
         "bound": "mfma" if unit == "TFLOP/s" else "hbm",
@@ -96,6 +102,8 @@ def roofline_of(per, work_per_launch, unit, peak):
         "frac": round(achieved / peak, 4),
         "traffic": None,
         "avg_launch_ms": round(avg_ms, 4),
+        "launches_per_step": launches,
+        "work_per_launch": per_launch,
     }
 
 
