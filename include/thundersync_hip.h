@@ -133,7 +133,7 @@ typedef struct ts_attn_problem {
   const ts_attn_run* runs;
   const ts_attn_ref* run_visits;
   const int32_t* q_work;  /* pairs (segment, first row): one per 32-row block */
-  const int32_t* kv_work; /* pairs (run, first key): one per 64-key block */
+  const int32_t* kv_work; /* pairs (run, first key): one per kv_block keys */
   int32_t n_q_work;
   int32_t n_kv_work;
   int32_t n_segs;
@@ -143,7 +143,7 @@ typedef struct ts_attn_problem {
   int32_t head_dim;
   float scale;
   int32_t q_block;  /* rows per q_work item: 32 * 4 / ts_attn_heads_per_block */
-  int32_t kv_block; /* keys per kv_work item: 64 */
+  int32_t kv_block; /* keys per kv_work item: ts_attn_kv_block(hq / hkv) */
   int64_t q_rows;   /* rows of Q/O/dO/dQ */
 } ts_attn_problem;
 
@@ -151,6 +151,10 @@ typedef struct ts_attn_problem {
  * (hq / hkv): 4 when it divides the group, else 2, else 1.  The rows per
  * q_work item are 32 * 4 / that value. */
 int ts_attn_heads_per_block(int group);
+
+/* Keys per dK/dV work-group for a GQA group size: 48 when 4 divides the
+ * group (one wave per query head), else 64. */
+int ts_attn_kv_block(int group);
 
 typedef struct ts_attn_rows {
   uint64_t ptr; /* device address of row 0, head 0 */
@@ -254,6 +258,14 @@ int ts_timing_read(const char* kernel, double* total_ms, int64_t* launches);
  * Used by the test suite to pin the lane layouts the kernels assume. */
 int ts_probe_layouts(const void* a, const void* b, float* d16, float* d32,
                      const void* t_in, void* t_out, void* stream);
+
+/* Runs, in one wave, a global_load_lds_dwordx4 in which lane i loads the
+ * 16 bytes src[perm[i]] (src: 64 x 16 bytes, perm: 64 ints in [0, 64)) and
+ * copies the resulting 1 KB LDS block to dma_out, then a ds_read_b64_tr_b16
+ * in which lane i addresses element 4 i of an LDS array holding the 16-bit
+ * values 0..511, writing each lane's four values to tr_out (64 x 8 bytes).
+ * Used by the test suite to pin gfx950's LDS DMA and transpose-read layouts. */
+int ts_probe_lds(const void* src, const int* perm, void* dma_out, void* tr_out, void* stream);
 
 #ifdef __cplusplus
 }

@@ -72,3 +72,28 @@ def test_mfma_and_transpose_layouts(cuda):
     np.testing.assert_array_equal(
         t_out.float().cpu().numpy(), np.transpose(t_in, (0, 2, 1))
     )
+
+
+def test_lds_dma_and_transpose_read_layouts(cuda):
+    """Record where global_load_lds_dwordx4 puts each lane's 16 bytes, and the
+    lane mapping of ds_read_b64_tr_b16 over contiguous 8-byte rows."""
+    lib = _lib.require_library()
+    src = torch.arange(64 * 4, dtype=torch.int32, device=cuda)  # 16 bytes per lane: 4l..4l+3
+    perm = torch.tensor(np.random.default_rng(1).permutation(64), dtype=torch.int32, device=cuda)
+    dma = torch.empty(64 * 4, dtype=torch.int32, device=cuda)
+    tr = torch.empty(64 * 4, dtype=torch.int16, device=cuda)
+    print("probe: ts_probe_lds", flush=True)
+    _lib.check(lib.ts_probe_lds(src.data_ptr(), perm.data_ptr(), dma.data_ptr(), tr.data_ptr(),
+                                _lib.stream_of(src)), "ts_probe_lds")
+    torch.cuda.synchronize()
+    got = dma.view(64, 4).cpu().numpy()
+    p = perm.cpu().numpy()
+    # lane i's 16 bytes land at LDS offset 16 i
+    np.testing.assert_array_equal(got, np.stack([np.arange(4 * j, 4 * j + 4) for j in p]))
+    t = tr.view(64, 4).cpu().numpy().astype(np.int64)
+    print("ds_read_b64_tr_b16 lanes 0..19:", t[:20].tolist(), flush=True)
+    # within each group of 16 lanes the four values come from four different
+    # 8-byte rows of that group (a transpose), never from another group
+    for lane in range(64):
+        rows = set((t[lane] // 4).tolist())
+        assert all(16 * (lane // 16) <= r < 16 * (lane // 16) + 16 for r in rows), (lane, t[lane])

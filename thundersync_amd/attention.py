@@ -49,7 +49,6 @@ from ._abi import REF_DTYPE, RUN_DTYPE, SEG_DTYPE, AttnProblem, AttnRows
 from .operator_profiling import operator_range
 
 HEAD_DIM = 128
-KV_BLOCK = 64
 
 
 def heads_per_block(group: int) -> int:
@@ -63,6 +62,11 @@ def heads_per_block(group: int) -> int:
 
 def q_block_rows(hq: int, hkv: int) -> int:
     return 32 * 4 // heads_per_block(hq // hkv)
+
+
+def kv_block_keys(hq: int, hkv: int) -> int:
+    """Keys per dK/dV work-group (mirror of ts_attn_kv_block)."""
+    return 48 if (hq // hkv) % 4 == 0 else 64
 
 
 # ---------------------------------------------------------------------------
@@ -143,11 +147,12 @@ class AttnLayout:
             visit0.append(len(visit_rows))
             visit_rows.extend(vis)
         kv_items = []
+        kvb = kv_block_keys(self.hq, self.hkv)
         for run, vis in enumerate(visits_of):
             if not vis:
                 continue
             length = self.runs[run].length
-            for k0 in range(0, length, KV_BLOCK):
+            for k0 in range(0, length, kvb):
                 cost = 0
                 for s, kpos in vis:
                     off = self.seg_kv[s] - self.seg_q[s][1]
@@ -206,7 +211,7 @@ class AttnLayout:
         return AttnProblem(
             t["segs"], t["seg_spans"], runs_ptr, t["run_visits"], t["q_work"], t["kv_work"],
             t["n_q_work"], t["n_kv_work"], len(self.seg_q), len(self.runs), self.hq, self.hkv,
-            HEAD_DIM, float(scale), q_block_rows(self.hq, self.hkv), KV_BLOCK, self.q_rows,
+            HEAD_DIM, float(scale), q_block_rows(self.hq, self.hkv), kv_block_keys(self.hq, self.hkv), self.q_rows,
         )
 
     # -- reference diagnostics ---------------------------------------------

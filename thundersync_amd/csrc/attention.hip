@@ -26,6 +26,8 @@
 //           from LDS rows through the register transpose.
 // Both sides of every contraction use the same slot permutation of the
 // contracted index, which is all the MFMA requires.
+#include <type_traits>
+
 #include "common.h"
 #include "timing.h"
 #include "../../include/thundersync_hip.h"
@@ -582,6 +584,304 @@ __global__ __launch_bounds__(kThreads, 2) void dkdv_kernel(ts_attn_problem P, ts
 }
 
 // ---------------------------------------------------------------------------
+// backward dK / dV, one wave per query head (GQA groups that are a multiple of 4)
+//
+// A work-group owns 64 keys of one run and one KV head; wave w handles query
+// heads w, w + 4, ... of the group over all 64 keys, so a wave's LDS reads of
+// its head's Q/dO tile feed 64 keys of MFMA work (4x the reuse of a
+// 16-key-per-wave split).  K^T operands stay in registers; the V tile sits in
+// LDS.  Each wave streams its head's 32-row Q/dO tiles (and their 32 LSE and
+// delta values) into its own double-buffered LDS region with
+// global_load_lds_dwordx4 / _dword: no register staging and no work-group
+// barrier inside the loop.  Rows are 256 bytes, 16-byte chunk c of row r at
+// chunk slot c ^ (r & 15): row reads of 16 rows at one chunk, transpose
+// reads and the DMA's 4-row instructions are all conflict-free, and every
+// address is a per-lane offset (4 for row reads, 8 for transpose reads)
+// plus an immediate.  dO^T and Q^T come from ds_read_b64_tr_b16: within
+// each 16-lane group, lane i receives column (i & 3) of the rows addressed
+// by lanes i/4, i/4 + 4, i/4 + 8, i/4 + 12, so lane j addressing row
+// kbase + j/4, columns m0 + 4 (j & 3) yields X[kbase + t][m0 + i], t = 0..3
+// (pinned by the LDS probe test).  The per-head partials are summed across
+// waves through LDS in wave order.
+// ---------------------------------------------------------------------------
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void;
+
+constexpr int kTile32 = 32 * D;              // elements of one 32-row tile (256-byte rows)
+constexpr int kStage32 = 2 * kTile32 + 128;  // Q tile + dO tile + 64 floats (lse, delta)
+
+__device__ __forceinline__ void dma16(const bf16* src, bf16* lds_wave_block) {
+  __builtin_amdgcn_global_load_lds((const void*)src, (lds_void*)lds_wave_block, 16, 0, 0);
+}
+
+// One wave copies rows [0, 4 * ninst) x 128 of a row-major source (rows past
+// nvalid repeat row nvalid - 1) into a swizzled tile: instruction t covers
+// rows 4t .. 4t + 3; lane (g4, j16) fills row 4t + g4, chunk slot j16 with
+// logical chunk j16 ^ ((4t + g4) & 15).  dchunk[t & 3] holds that logical
+// chunk times 8 (elements).
+__device__ __forceinline__ void dma_tile(bf16* tile, const bf16* base, int64_t row_stride, int nvalid,
+                                         int g4, const int dchunk[4], int t0, int t1, int tstep) {
+  for (int t = t0; t < t1; t += tstep) {
+    int r = 4 * t + g4;
+    r = r < nvalid ? r : nvalid - 1;
+    dma16(base + (int64_t)r * row_stride + dchunk[t & 3], tile + t * 512);
+  }
+}
+
+__device__ __forceinline__ u32x2 tr_read(const bf16* p) {
+  const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)p);
+  u32x2 r;
+  __builtin_memcpy(&r, &v, 8);
+  return r;
+}
+
+struct Cursor {
+  int vi;  // visit index; == nvisit at the end
+  int r0;  // first row of the block
+};
+
+template <int KB>
+__global__ __launch_bounds__(kThreads, 1) void dkdv_wave_kernel(ts_attn_problem P, ts_attn_rows Q,
+                                                                ts_attn_rows dO,
+                                                                const float* __restrict__ lse,
+                                                                const float* __restrict__ delta,
+                                                                int64_t lse_ld) {
+  __shared__ __attribute__((aligned(16))) bf16 s_v[16 * KB * D];
+  // per wave and stage: Q tile, dO tile, then 32 lse + 32 delta floats
+  __shared__ __attribute__((aligned(16))) bf16 s_b0[4][kStage32];
+  __shared__ __attribute__((aligned(16))) bf16 s_b1[4][kStage32];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g4 = lane >> 4, j16 = lane & 15;
+  const int run_id = P.kv_work[2 * blockIdx.x];
+  const int k0 = P.kv_work[2 * blockIdx.x + 1];
+  const int hk = blockIdx.y;
+  const int group = P.hq / P.hkv;
+  const ts_attn_run run = P.runs[run_id];
+  constexpr int NK = 16 * KB;  // keys per work-group
+  const int nkeys = min(NK, run.len - k0);
+  const float c = P.scale * kLog2e;
+
+  // per-lane LDS / DMA offsets (elements)
+  int ro[4], to[8], dchunk[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) ro[ks] = j16 * D + (((4 * ks + g4) ^ j16) << 3);
+#pragma unroll
+  for (int mb = 0; mb < 8; ++mb) {
+    const int r = 4 * g4 + (j16 >> 2);
+    const int col = 16 * mb + 4 * (j16 & 3);
+    to[mb] = r * D + ((((col >> 3) ^ r) & 15) << 3) + (col & 7);
+  }
+#pragma unroll
+  for (int t = 0; t < 4; ++t) dchunk[t] = (j16 ^ (4 * t + g4)) << 3;
+
+  // V tile: 4 KB DMA instructions, wave w issues w, w + 4, ...
+  dma_tile(s_v, (const bf16*)run.v + (int64_t)k0 * run.v_row_stride + (int64_t)hk * run.v_head_stride,
+           run.v_row_stride, nkeys, g4, dchunk, wave, 4 * KB, 4);
+  // K^T operands: kreg[kb][ks] = K[k0 + 16 kb + j16][32 ks + 8 g4 ..]
+  bf16x8 kreg[KB][4];
+#pragma unroll
+  for (int kb = 0; kb < KB; ++kb) {
+    const int key = 16 * kb + j16;
+    const bf16* kp = (const bf16*)run.k + (int64_t)(k0 + key) * run.k_row_stride + (int64_t)hk * run.k_head_stride;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+      kreg[kb][ks] = as_bf16x8(key < nkeys ? ld16(kp + 32 * ks + 8 * g4) : u32x4{0u, 0u, 0u, 0u});
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+
+  f32x4 dk[8][KB], dv[8][KB];
+#pragma unroll
+  for (int mb = 0; mb < 8; ++mb)
+#pragma unroll
+    for (int kb = 0; kb < KB; ++kb) {
+      dk[mb][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      dv[mb][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+
+  // first block at or after (vi, r0); skips visits with no visible rows
+  auto settle = [&](Cursor cur) -> Cursor {
+    while (cur.vi < run.nvisit) {
+      const ts_attn_ref ref = P.run_visits[run.visit0 + cur.vi];
+      const ts_attn_segment seg = P.segs[ref.index];
+      if (cur.r0 < 0) {
+        int rs = ref.kpos + k0 - (seg.kv_len - seg.q_len);
+        rs = rs < 0 ? 0 : rs;
+        cur.r0 = rs & ~31;
+      }
+      if (cur.r0 < seg.q_len) return cur;
+      ++cur.vi;
+      cur.r0 = -1;
+    }
+    return cur;
+  };
+  auto issue = [&](Cursor cur, int h, bf16* buf) {
+    const ts_attn_ref ref = P.run_visits[run.visit0 + cur.vi];
+    const ts_attn_segment seg = P.segs[ref.index];
+    const int nrows = min(32, seg.q_len - cur.r0);
+    const int64_t row0 = seg.q_row0 + cur.r0;
+    dma_tile(buf, (const bf16*)Q.ptr + row0 * Q.row_stride + (int64_t)h * Q.head_stride, Q.row_stride,
+             nrows, g4, dchunk, 0, 8, 1);
+    dma_tile(buf + kTile32, (const bf16*)dO.ptr + row0 * dO.row_stride + (int64_t)h * dO.head_stride,
+             dO.row_stride, nrows, g4, dchunk, 0, 8, 1);
+    // lanes 0..31: lse of rows 0..31, lanes 32..63: delta (rows clamped)
+    const int rr = min(lane & 31, nrows - 1);
+    const float* src = (lane < 32 ? lse : delta) + (int64_t)h * lse_ld + row0 + rr;
+    __builtin_amdgcn_global_load_lds((const void*)src, (lds_void*)(buf + 2 * kTile32), 4, 0, 0);
+  };
+
+  // one 32-row block of the current head; buffer roles fixed per call
+  auto step = [&](auto bsel, Cursor& cur, int h) {
+      const ts_attn_ref ref = P.run_visits[run.visit0 + cur.vi];
+      const ts_attn_segment seg = P.segs[ref.index];
+      const int off = seg.kv_len - seg.q_len;
+      const int nrows = min(32, seg.q_len - cur.r0);
+      const int r0 = cur.r0;
+      Cursor nxt = settle(Cursor{cur.vi, cur.r0 + 32});
+      __builtin_amdgcn_s_waitcnt(0);  // this block's tiles have landed
+      // static buffer roles: the LDS reads below and the prefetch into the other
+      // buffer touch different arrays, so no wait for the prefetch is needed
+      bf16* cur_buf = bsel.value == 0 ? s_b0[wave] : s_b1[wave];
+      bf16* nxt_buf = bsel.value == 0 ? s_b1[wave] : s_b0[wave];
+      if (nxt.vi < run.nvisit) issue(nxt, h, nxt_buf);
+      const bf16* tq = cur_buf;
+      const bf16* td = cur_buf + kTile32;
+      const float* sl = reinterpret_cast<const float*>(cur_buf + 2 * kTile32);  // [32] lse, [32] delta
+
+      // S = Q K^T, dP = dO V^T: [qb][kb] holds rows 16 qb + 4 g4 + i, key 16 kb + j16
+      f32x4 sc[2][KB], dp[2][KB];
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+          sc[qb][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+          dp[qb][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        bf16x8 aq[2], ad[2];
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) {
+          aq[qb] = as_bf16x8(ld16(tq + ro[ks] + 16 * qb * D));
+          ad[qb] = as_bf16x8(ld16(td + ro[ks] + 16 * qb * D));
+        }
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+          const bf16x8 vb = as_bf16x8(ld16(s_v + ro[ks] + 16 * kb * D));
+#pragma unroll
+          for (int qb = 0; qb < 2; ++qb) {
+            sc[qb][kb] = mfma16(aq[qb], kreg[kb][ks], sc[qb][kb]);
+            dp[qb][kb] = mfma16(ad[qb], vb, dp[qb][kb]);
+          }
+        }
+      }
+      // this lane's rows: 16 qb + 4 g4 + i
+      float l2[2][4], dl[2][4];
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int rl = 16 * qb + 4 * g4 + i;
+          const float lv = sl[rl];
+          l2[qb][i] = lv == neg_inf() ? __builtin_huge_valf() : lv * kLog2e;
+          dl[qb][i] = sl[32 + rl];
+        }
+      // P and dS as B operands: slot j = 4 qb + i  <->  row 16 qb + 4 g4 + i
+      const bool full = (r0 + 32 <= seg.q_len) & (k0 + NK <= run.len) & (ref.kpos + k0 + NK - 1 <= off + r0);
+      bf16x8 pk[KB], dsk[KB];
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+        const int key = k0 + 16 * kb + j16;
+        float pv[8], dsv[8];
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int rl = 16 * qb + 4 * g4 + i;
+            const bool vis = full | ((rl < nrows) & (key < run.len) & (ref.kpos + key <= off + r0 + rl));
+            const float p = vis ? fast_exp2(sc[qb][kb][i] * c - l2[qb][i]) : 0.f;
+            pv[4 * qb + i] = p;
+            dsv[4 * qb + i] = p * (dp[qb][kb][i] - dl[qb][i]);
+          }
+        pk[kb] = pack8(pv);
+        dsk[kb] = pack8(dsv);
+      }
+      // dV^T += dO^T P, dK^T += Q^T dS: rows d = 16 mb + 4 g4 + i, column key
+#pragma unroll
+      for (int mb = 0; mb < 8; ++mb) {
+        const u32x2 a0 = tr_read(td + to[mb]), a1 = tr_read(td + to[mb] + 16 * D);
+        const u32x2 b0 = tr_read(tq + to[mb]), b1 = tr_read(tq + to[mb] + 16 * D);
+        const bf16x8 a_do = as_bf16x8(u32x4{a0[0], a0[1], a1[0], a1[1]});
+        const bf16x8 a_q = as_bf16x8(u32x4{b0[0], b0[1], b1[0], b1[1]});
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+          dv[mb][kb] = mfma16(a_do, pk[kb], dv[mb][kb]);
+          dk[mb][kb] = mfma16(a_q, dsk[kb], dk[mb][kb]);
+        }
+      }
+      cur = nxt;
+  };
+
+  for (int g = wave; g < group; g += 4) {
+    const int h = hk * group + g;
+    Cursor cur = settle(Cursor{0, -1});
+    if (cur.vi < run.nvisit) issue(cur, h, s_b0[wave]);
+    while (cur.vi < run.nvisit) {
+      step(std::integral_constant<int, 0>{}, cur, h);
+      if (cur.vi >= run.nvisit) break;
+      step(std::integral_constant<int, 1>{}, cur, h);
+    }
+  }
+
+  // sum the waves' partials in wave order: wave w stages [NK keys][128 d] fp32
+  // (16-byte chunk c of key k at slot c ^ (k & 31)) in s_b0[2w] (w < 2) or
+  // s_b1[2(w - 2)], 2 x kStage32 bf16 >= 32 KB; every thread then adds the
+  // four partials of its outputs
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  auto stage = [&](int w) -> float* {
+    return reinterpret_cast<float*>(w < 2 ? s_b0[2 * w] : s_b1[2 * (w - 2)]);
+  };
+#pragma unroll
+  for (int which = 0; which < 2; ++which) {
+    float* mine = stage(wave);
+#pragma unroll
+    for (int mb = 0; mb < 8; ++mb)
+#pragma unroll
+      for (int kb = 0; kb < KB; ++kb) {
+        const int key = 16 * kb + j16;
+        const int chunk = 4 * mb + g4;  // d = 16 mb + 4 g4 .. +3
+        *reinterpret_cast<f32x4*>(mine + key * D + ((chunk ^ (key & 31)) << 2)) =
+            which == 0 ? dk[mb][kb] : dv[mb][kb];
+      }
+    __syncthreads();
+    const uint64_t base = which == 0 ? run.dk : run.dv;
+    const int64_t rs = which == 0 ? run.dk_row_stride : run.dv_row_stride;
+    const int64_t hs = which == 0 ? run.dk_head_stride : run.dv_head_stride;
+    const float mult = which == 0 ? P.scale : 1.f;
+#pragma unroll
+    for (int t = 0; t < KB; ++t) {
+      const int e = t * kThreads + tid;  // NK x 16 outputs of 8 elements
+      const int key = e >> 4, d8 = (e & 15) * 8;
+      float acc8[8];
+#pragma unroll
+      for (int hc = 0; hc < 2; ++hc) {
+        const int chunk = (d8 >> 2) + hc;
+        const int slot = key * D + ((chunk ^ (key & 31)) << 2);
+        f32x4 sum = *reinterpret_cast<const f32x4*>(stage(0) + slot);
+#pragma unroll
+        for (int w = 1; w < 4; ++w) sum += *reinterpret_cast<const f32x4*>(stage(w) + slot);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) acc8[4 * hc + q] = sum[q] * mult;
+      }
+      if (base && key < nkeys)
+        st16((bf16*)base + (int64_t)(k0 + key) * rs + (int64_t)hk * hs + d8, as_u32x4(pack8(acc8)));
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
 int heads_per_block(int group) {
@@ -589,6 +889,10 @@ int heads_per_block(int group) {
   if (group % 2 == 0) return 2;
   return 1;
 }
+
+// keys per dK/dV work-group: 48 for the one-wave-per-head kernel (its 192
+// dK/dV accumulators and 48 S/dP values fill the 256 AGPRs), else 64
+int kv_block_keys(int group) { return group % 4 == 0 ? 48 : BK; }
 
 bool aligned_rows(const ts_attn_rows& r) {
   return r.ptr && (r.ptr % 16 == 0) && (r.row_stride % 8 == 0) && (r.head_stride % 8 == 0) &&
@@ -603,7 +907,8 @@ int validate(const ts_attn_problem* p, const char* what) {
   const int gc = heads_per_block(p->hq / p->hkv);
   TS_CHECK_ARG(p->q_block == 32 * 4 / gc, "%s: q_block %d, expected %d for group %d", what,
                p->q_block, 32 * 4 / gc, p->hq / p->hkv);
-  TS_CHECK_ARG(p->kv_block == BK, "%s: kv_block %d, expected %d", what, p->kv_block, BK);
+  TS_CHECK_ARG(p->kv_block == kv_block_keys(p->hq / p->hkv), "%s: kv_block %d, expected %d", what,
+               p->kv_block, kv_block_keys(p->hq / p->hkv));
   TS_CHECK_ARG(p->n_q_work >= 0 && p->n_kv_work >= 0 && p->n_segs >= 0 && p->n_runs >= 0,
                "%s: negative table size", what);
   TS_CHECK_ARG(p->n_q_work == 0 || (p->q_work && p->segs && p->seg_spans && p->runs),
@@ -618,6 +923,8 @@ int validate(const ts_attn_problem* p, const char* what) {
 extern "C" {
 
 int ts_attn_heads_per_block(int group) { return group > 0 ? ts::attn::heads_per_block(group) : 0; }
+
+int ts_attn_kv_block(int group) { return group > 0 ? ts::attn::kv_block_keys(group) : 0; }
 
 int ts_attn_fwd(const ts_attn_problem* problem, ts_attn_rows q, ts_attn_rows out, float* lse,
                 int64_t lse_ld, void* stream) {
@@ -678,7 +985,11 @@ int ts_attn_bwd(const ts_attn_problem* problem, ts_attn_rows q, ts_attn_rows out
   }
   if (P.n_kv_work > 0) {
     const dim3 grid((unsigned)P.n_kv_work, (unsigned)P.hkv);
-    { ts::TimedLaunch timed_("attention.dkdv_kernel", s); hipLaunchKernelGGL(dkdv_kernel, grid, dim3(kThreads), 0, s, P, q, dout, lse, delta, lse_ld); }
+    if (group % 4 == 0) {
+      { ts::TimedLaunch timed_("attention.dkdv_kernel", s); hipLaunchKernelGGL(dkdv_wave_kernel<3>, grid, dim3(kThreads), 0, s, P, q, dout, lse, delta, lse_ld); }
+    } else {
+      { ts::TimedLaunch timed_("attention.dkdv_kernel", s); hipLaunchKernelGGL(dkdv_kernel, grid, dim3(kThreads), 0, s, P, q, dout, lse, delta, lse_ld); }
+    }
     st = ts::check_launch("ts_attn_bwd (dkdv)");
   }
   return st;

@@ -28,8 +28,8 @@ constexpr int kWave = 64;
 enum DType : int { kF32 = 0, kF16 = 1, kBF16 = 2 };
 
 // ---------------------------------------------------------------------------
-// scalar conversions.  bf16 rounding is round-to-nearest-even, the rounding
-// torch applies in `.to(torch.bfloat16)`.
+// scalar conversions.  bf16 rounding is round-to-nearest-even (the hardware
+// conversion), the rounding torch applies in `.to(torch.bfloat16)`.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float bf_bits_to_f(uint32_t h) {
   return __uint_as_float(h << 16);
@@ -46,17 +46,18 @@ __device__ __forceinline__ float to_f(f16 x) { return (float)x; }
 
 template <typename T> __device__ __forceinline__ T from_f(float x);
 template <> __device__ __forceinline__ float from_f<float>(float x) { return x; }
-template <> __device__ __forceinline__ bf16 from_f<bf16>(float x) {
-  uint16_t b = (uint16_t)f_to_bf_bits(x);
-  bf16 r;
-  __builtin_memcpy(&r, &b, 2);
-  return r;
-}
+template <> __device__ __forceinline__ bf16 from_f<bf16>(float x) { return (bf16)x; }
 template <> __device__ __forceinline__ f16 from_f<f16>(float x) { return (f16)x; }
 
-// pack two floats into one dword of two bf16 (lo = a, hi = b)
+// pack two floats into one dword of two bf16 (lo = a, hi = b), rounded to
+// nearest even by gfx950's v_cvt_pk_bf16_f32
 __device__ __forceinline__ uint32_t pack_bf2(float a, float b) {
-  return f_to_bf_bits(a) | (f_to_bf_bits(b) << 16);
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  const bf16x2 h = __builtin_convertvector((f32x2{a, b}), bf16x2);
+  uint32_t r;
+  __builtin_memcpy(&r, &h, 4);
+  return r;
 }
 
 // ---------------------------------------------------------------------------

@@ -43,6 +43,32 @@ __global__ __launch_bounds__(64) void probe_layouts_kernel(
   for (int j = 0; j < 8; ++j) t_out[l * 8 + j] = out[j];
 }
 
+// One wave: (1) global_load_lds_dwordx4 with lane i loading src[perm[i]]
+// into a 1 KB LDS block, read back in LDS order; (2) ds_read_b64_tr_b16 with
+// lane i addressing byte 8 * i of an LDS block holding 16-bit values 0..511.
+// All accesses stay inside the 1 KB block.
+__global__ __launch_bounds__(64) void probe_lds_kernel(const u32x4* __restrict__ src,
+                                                       const int* __restrict__ perm,
+                                                       u32x4* __restrict__ dma_out,
+                                                       u32x2* __restrict__ tr_out) {
+  __shared__ __attribute__((aligned(16))) u32x4 block[64];
+  __shared__ __attribute__((aligned(16))) uint16_t vals[512];
+  const int l = threadIdx.x;
+  __builtin_amdgcn_global_load_lds((const void*)(src + perm[l]),
+                                   (__attribute__((address_space(3))) void*)block, 16, 0, 0);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  dma_out[l] = block[l];
+  for (int i = l; i < 512; i += 64) vals[i] = (uint16_t)i;
+  __syncthreads();
+  typedef short i16x4 __attribute__((ext_vector_type(4)));
+  i16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) i16x4*)(vals + 4 * l));
+  u32x2 o;
+  __builtin_memcpy(&o, &r, 8);
+  tr_out[l] = o;
+}
+
 }  // namespace ts
 
 extern "C" {
@@ -58,6 +84,13 @@ int ts_probe_layouts(const void* a, const void* b, float* d16, float* d32,
                      (const ts::u32x4*)a, (const ts::u32x4*)b, d16, d32,
                      (const ts::u32x4*)t_in, (ts::u32x4*)t_out);
   return ts::check_launch("ts_probe_layouts");
+}
+
+int ts_probe_lds(const void* src, const int* perm, void* dma_out, void* tr_out, void* stream) {
+  TS_CHECK_ARG(src && perm && dma_out && tr_out, "ts_probe_lds: null pointer");
+  hipLaunchKernelGGL(ts::probe_lds_kernel, dim3(1), dim3(64), 0, (hipStream_t)stream,
+                     (const ts::u32x4*)src, perm, (ts::u32x4*)dma_out, (ts::u32x2*)tr_out);
+  return ts::check_launch("ts_probe_lds");
 }
 
 }  // extern "C"
