@@ -7,11 +7,15 @@ Workloads (synthetic data drawn from fixed seeds):
   2048-token prompt and 8 sibling completions of lengths U[256, 4096],
   32 query / 8 KV heads, head dim 128, bf16; TFLOP/s counted as
   14 * D * Hq * (exactly visible query/key pairs).
-* ``secondary[0]``: C3 fused logprob + entropy, forward + gradient wrt
+* ``secondary[0]``: C4 chunked retained-KV attention, forward + backward --
+  4 groups of a 1024-token prompt and 4 completions U[1024, 16384], every
+  512-token query chunk over the group's prompt chunks, its trajectory's
+  earlier chunks and itself, K/V held as one tensor per chunk.
+* ``secondary[1]``: C3 fused logprob + entropy, forward + gradient wrt
   hidden -- hidden [16384, 4096], head [151936, 4096], 70% of rows scored
   and gated before the projection (the reference's production schedule),
   frozen head; scored tokens/s, 6 * N * V * D FLOP.
-* ``secondary[1]``: RMSNorm forward + backward on [16384, 4096] bf16; GB/s.
+* ``secondary[2]``: RMSNorm forward + backward on [16384, 4096] bf16; GB/s.
 
 A step is one pass of the operator over its whole input, with inputs
 already resident in HBM.  Per-kernel device time comes from the library's
@@ -46,7 +50,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--seed", type=int, default=0)
-    ap.add_argument("--only", choices=("all", "attention", "logprob", "rmsnorm"), default="all")
+    ap.add_argument("--only", choices=("all", "attention", "chunked", "logprob", "rmsnorm"), default="all")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     return ap.parse_args()
 
@@ -216,6 +220,148 @@ def attention_cpu_baseline(plan, q, k, v, dout, lengths):
 
 
 # ---------------------------------------------------------------------------
+# C4 chunked retained-KV attention
+# ---------------------------------------------------------------------------
+def c4_layout(seed, chunk=512, groups=4, per_group=4, prompt=1024, lo=1024, hi=16384):
+    """(lengths, chunk_rows, query chunks, q_rows) of the C4 pack.
+
+    Each group's prompt and each trajectory is cut into `chunk`-token query
+    chunks; a chunk reads the group's prompt chunks, the earlier chunks of
+    its trajectory and itself (bottom-right causal).  Rows are laid out group
+    by group: prompt, then its trajectories in order.
+    """
+    import torch
+
+    g = torch.Generator().manual_seed(seed)
+    lengths = torch.randint(lo, hi + 1, (groups * per_group,), generator=g).tolist()
+    chunk_rows, chunks, row = [], [], 0
+
+    def cut(n, path):
+        nonlocal row
+        for c0 in range(0, n, chunk):
+            m = min(chunk, n - c0)
+            chunk_rows.append(m)
+            path.append(len(chunk_rows) - 1)
+            chunks.append((row, m, tuple(path)))
+            row += m
+
+    for grp in range(groups):
+        prompt_path = []
+        cut(prompt, prompt_path)
+        for t in range(per_group):
+            cut(lengths[grp * per_group + t], list(prompt_path))
+    return lengths, chunk_rows, chunks, row
+
+
+def c4_inputs(seed, device):
+    import torch
+
+    from thundersync_amd import attention
+
+    lengths, chunk_rows, chunks, rows = c4_layout(seed)
+    layout = attention.retained_chunk_layout(rows, chunk_rows, chunks, 32, 8)
+    gd = torch.Generator(device=device).manual_seed(seed)
+    q = torch.randn(rows, 32, 128, generator=gd, device=device, dtype=torch.bfloat16).requires_grad_()
+    ks = [torch.randn(n, 8, 128, generator=gd, device=device, dtype=torch.bfloat16).requires_grad_()
+          for n in chunk_rows]
+    vs = [torch.randn(n, 8, 128, generator=gd, device=device, dtype=torch.bfloat16).requires_grad_()
+          for n in chunk_rows]
+    dout = torch.randn(rows, 32, 128, generator=gd, device=device, dtype=torch.bfloat16)
+    return lengths, chunks, layout, q, ks, vs, dout
+
+
+def bench_chunked(args, device):
+    import torch
+
+    from thundersync_amd import attention
+
+    lengths, chunks, layout, q, ks, vs, dout = c4_inputs(args.seed, device)
+    pairs = layout.visible_pairs()
+    d, hq = 128, 32
+    leaves = [q, *ks, *vs]
+
+    def step():
+        for t in leaves:
+            t.grad = None
+        out = attention.retained_chunk_attention(q, ks, vs, layout, 128 ** -0.5)
+        out.backward(dout)
+
+    kernels = ["attention.fwd_kernel", "attention.delta_kernel", "attention.dq_kernel", "attention.dkdv_kernel"]
+    ms, per = timed(step, args.steps, args.warmup, kernels)
+    flop = 14 * d * hq * pairs
+    work = {
+        "attention.fwd_kernel": 4 * d * hq * pairs,
+        "attention.dq_kernel": 2 * d * hq * pairs,
+        "attention.dkdv_kernel": 8 * d * hq * pairs,
+        "attention.delta_kernel": 2 * d * hq * layout.q_rows,
+    }
+    result = {
+        "metric": "chunked retained-KV attn fwd+bwd TFLOP/s",
+        "value": round(flop / (ms * 1e-3) / 1e12, 2),
+        "unit": "TFLOP/s",
+        "ms_per_step": round(ms, 4),
+        "roofline": roofline_of(per, work, "TFLOP/s", PEAK_BF16_TFLOPS),
+        "kernels": {k: {"avg_ms": round(a, 4), "launches_per_step": n} for k, (a, n) in per.items()},
+        "config": {
+            "workload": "C4 chunked retained-KV attention fwd+bwd: 4 groups x (1024-token prompt + 4 "
+                        "completions U[1024,16384]), 512-token query chunks over per-chunk K/V tensors, "
+                        "32/8 heads, head_dim 128, bf16, all chunks in one launch per direction",
+            "completion_lengths": lengths,
+            "tokens": layout.q_rows,
+            "query_chunks": len(chunks),
+            "visible_pairs": pairs,
+            "flop_per_step": flop,
+            "seed": args.seed,
+        },
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = chunked_cpu_baseline(chunks, lengths, q, ks, vs, dout)
+    return result
+
+
+def chunked_cpu_baseline(chunks, lengths, q, ks, vs, dout, chunk=512, prompt=1024):
+    """The reference's CPU dispatch (masked SDPA, causal_lower_right;
+    engine/streaming.py:1146-1162) on every query chunk of the first
+    trajectory, each over the concatenation of its retained K/V, fp32
+    forward + backward."""
+    import torch
+
+    from oracle import attention as ref
+
+    torch.set_num_threads(cpu_threads())
+    # group 0 lays out its prompt chunks first, then the first trajectory's chunks
+    first = prompt // chunk
+    last = first + -(-lengths[0] // chunk)
+    sample = list(range(first, last))
+    host, pairs = [], 0
+    for i in sample:
+        row0, m, path = chunks[i]
+        qq = q.detach()[row0 : row0 + m].float().cpu()
+        kk = [ks[c].detach().float().cpu() for c in path]
+        vv = [vs[c].detach().float().cpu() for c in path]
+        s = sum(k.shape[0] for k in kk)
+        pairs += m * (s - m) + m * (m + 1) // 2
+        host.append((qq, kk, vv, dout[row0 : row0 + m].float().cpu()))
+    t0 = time.perf_counter()
+    for qq, kk, vv, dd in host:
+        qq = qq.requires_grad_()
+        kc = torch.cat(kk).requires_grad_()  # the reference's ancestor cat
+        vc = torch.cat(vv).requires_grad_()
+        out = ref.sdpa_lower_right(qq, kc, vc, 128 ** -0.5)
+        torch.autograd.grad(out, (qq, kc, vc), dd)
+    dt = time.perf_counter() - t0
+    return {
+        "value": round(14 * 128 * 32 * pairs / dt / 1e12, 4),
+        "unit": "TFLOP/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"the {len(sample)} query chunks of the first C4 trajectory ({pairs} visible pairs), "
+                  "fp32 masked SDPA fwd+bwd over the concatenated retained K/V on the host",
+        "seconds": round(dt, 3),
+    }
+
+
+# ---------------------------------------------------------------------------
 # C3 fused logprob
 # ---------------------------------------------------------------------------
 def bench_logprob(args, device):
@@ -372,6 +518,8 @@ def main():
         out["kernels"] = att.pop("kernels")
         if "cpu_baseline" in att:
             out["cpu_baseline"] = att.pop("cpu_baseline")
+    if args.only in ("all", "chunked"):
+        out["secondary"].append(bench_chunked(args, device))
     if args.only in ("all", "logprob"):
         out["secondary"].append(bench_logprob(args, device))
     if args.only in ("all", "rmsnorm"):

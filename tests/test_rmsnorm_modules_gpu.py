@@ -1,0 +1,114 @@
+"""RMSNorm module swaps on the HIP kernels.
+
+* ``use_stable_qwen3_rms_norm`` (accel/rms_norm.py:55-70 of the reference):
+  every Qwen3RMSNorm of a model is replaced, Parameters keep their identity,
+  and the forward matches the stock module within the bf16 bar of the
+  kernel tests (two roundings).
+* ``use_compiled_source_rms_norm`` (grpo/rms_norm.py:44-84,
+  grpo/rms_norm_native.py:98-115): bf16 StableQwen3RMSNorm modules become
+  NativeSourceRMSNorm once both trials pass; fp32 modules are left alone; the
+  native VJP equals FP32RMSNormVJP's bit for bit (same kernels) and agrees
+  with the oracle.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle import rms_norm as ref
+
+pytestmark = pytest.mark.gpu
+
+transformers = pytest.importorskip("transformers")
+
+
+def tiny_model(device, dtype):
+    from transformers import Qwen3Config
+    from transformers.models.qwen3.modeling_qwen3 import Qwen3Model
+
+    cfg = Qwen3Config(vocab_size=64, hidden_size=128, intermediate_size=256, num_hidden_layers=2,
+                      num_attention_heads=4, num_key_value_heads=2, head_dim=32)
+    torch.manual_seed(0)
+    model = Qwen3Model(cfg).to(device=device, dtype=dtype)
+    for m in model.modules():
+        if hasattr(m, "variance_epsilon"):
+            with torch.no_grad():
+                m.weight.copy_(torch.linspace(0.4, 3.0, m.weight.numel()))
+    return model
+
+
+def norms(model):
+    from transformers.models.qwen3.modeling_qwen3 import Qwen3RMSNorm
+
+    return {n: m for n, m in model.named_modules() if isinstance(m, Qwen3RMSNorm)}
+
+
+def test_stable_swap_keeps_parameters_and_primal(cuda):
+    from thundersync_amd.rms_norm import StableQwen3RMSNorm, use_stable_qwen3_rms_norm
+
+    print("stable qwen3 rms norm swap", flush=True)
+    model = tiny_model(cuda, torch.bfloat16)
+    before = norms(model)
+    weights = {n: m.weight for n, m in before.items()}
+    x = torch.randn(3, 7, 128, device=cuda, dtype=torch.bfloat16)
+    stock = {n: m(x if m.weight.numel() == 128 else x[..., :32]).detach() for n, m in before.items()}
+    assert use_stable_qwen3_rms_norm(model) == len(before)
+    after = norms(model)
+    assert all(isinstance(m, StableQwen3RMSNorm) for m in after.values())
+    assert all(after[n].weight is weights[n] for n in after)
+    assert use_stable_qwen3_rms_norm(model) == 0
+    for n, m in after.items():
+        xi = (x if m.weight.numel() == 128 else x[..., :32]).clone().requires_grad_()
+        y = m(xi)
+        assert y.grad_fn is not None
+        assert (y.float() - stock[n].float()).abs().max().item() <= 2 * 2 ** -7 * 3
+
+
+def test_source_swap_and_native_vjp(cuda):
+    from thundersync_amd import capability
+    from thundersync_amd.rms_norm import FP32RMSNormVJP, use_stable_qwen3_rms_norm
+    from thundersync_amd.source_rms_norm import (NativeSourceRMSNorm, native_source_rms_trial,
+                                                 use_compiled_source_rms_norm)
+
+    print("source rms norm swap", flush=True)
+    capability.reset_kernel_probes()
+    native_source_rms_trial(cuda, torch.bfloat16, 128)
+    model = tiny_model(cuda, torch.bfloat16)
+    use_stable_qwen3_rms_norm(model)
+    weights = {n: m.weight for n, m in norms(model).items()}
+    assert use_compiled_source_rms_norm(model) == len(weights)
+    swapped = norms(model)
+    assert all(isinstance(m, NativeSourceRMSNorm) for m in swapped.values())
+    assert all(swapped[n].weight is weights[n] for n in swapped)
+    records = capability.kernel_probe_records()
+    assert {r["kernel"] for r in records} >= {"grpo_source_rms_norm_forward", "grpo_source_rms_norm_native_vjp"}
+    assert all(r["runs"] for r in records), records
+
+    norm = next(iter(swapped.values()))
+    width = norm.weight.numel()
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(129, width, generator=g).to(torch.bfloat16)
+    dy = torch.randn(129, width, generator=g).to(torch.bfloat16)
+    xa = x.to(cuda).requires_grad_()
+    norm.weight.grad = None
+    ya = norm(xa)
+    ya.backward(dy.to(cuda))
+    dw_native = norm.weight.grad.clone()
+    xb = x.to(cuda).requires_grad_()
+    wb = norm.weight.detach().clone().requires_grad_()
+    yb = FP32RMSNormVJP.apply(xb, wb, norm.variance_epsilon)
+    yb.backward(dy.to(cuda))
+    assert torch.equal(ya, yb) and torch.equal(xa.grad, xb.grad) and torch.equal(dw_native, wb.grad)
+    want_dx, want_dw = ref.rms_norm_backward(dy, x, norm.weight.detach().cpu(), norm.variance_epsilon)
+    torch.testing.assert_close(xa.grad.cpu().float(), want_dx.float(), rtol=2e-2, atol=2e-2)
+    torch.testing.assert_close(dw_native.cpu().float(), want_dw.float(), rtol=2e-2, atol=1e-1)
+
+
+def test_source_swap_skips_fp32(cuda):
+    from thundersync_amd.rms_norm import use_stable_qwen3_rms_norm
+    from thundersync_amd.source_rms_norm import use_compiled_source_rms_norm
+
+    model = tiny_model(cuda, torch.float32)
+    use_stable_qwen3_rms_norm(model)
+    assert use_compiled_source_rms_norm(model) == 0

@@ -28,7 +28,11 @@ Reference entry points mirrored here (same argument meaning):
   1613-1836), with ancestors in the reference's "last segment first" order;
 * :func:`ragged_causal_attention` -- ``_ragged_causal_sdpa`` (:1165-1226);
 * :func:`forest_attention` -- ``forest_attention(q, k, v, plan, *, scale)``
-  (engine/attention.py:186-231).
+  (engine/attention.py:186-231);
+* :func:`retained_chunk_layout` / :func:`retained_chunk_attention` -- every
+  query chunk of a streamed pack over its retained per-chunk K/V in one
+  launch, each chunk being the call ``_ChunkedCausalSDPA`` makes
+  (engine/streaming.py:1314-1423).
 
 There is no host path: CPU tensors, unsupported dtypes or head dims raise.
 """
@@ -605,6 +609,45 @@ def ragged_causal_attention(queries, keys, values, scale):
     for piece in out.split(lengths, 0):
         outs.append(piece.transpose(0, 1).unsqueeze(0))
     return outs
+
+
+# ---------------------------------------------------------------------------
+# retained chunks
+# ---------------------------------------------------------------------------
+def retained_chunk_layout(q_rows: int, chunk_rows: Sequence[int], chunks: Sequence[tuple[int, int, Sequence[int]]],
+                          hq: int, hkv: int) -> AttnLayout:
+    """Query chunks over graph-retained per-chunk K/V, all in one launch.
+
+    ``chunk_rows[i]`` is the row count of retained chunk ``i`` (one K and one
+    V tensor each); ``chunks`` lists every query chunk as ``(q_row0, q_len,
+    path)`` where ``path`` names, in key order, the retained chunks the query
+    chunk reads -- the prompt's chunks, the earlier chunks of its trajectory
+    and its own chunk last.  Each query chunk is the bottom-right-causal call
+    ``_ChunkedCausalSDPA`` makes per chunk (engine/streaming.py:1314-1354);
+    the retained tensors are read in place, never concatenated.
+    """
+    runs = tuple(Run(i, 0, n) for i, n in enumerate(chunk_rows))
+    seg_q, seg_spans = [], []
+    for row0, length, path in chunks:
+        spans, pos = [], 0
+        for c in path:
+            if not 0 <= c < len(runs):
+                raise ValueError(f"query chunk at row {row0} names retained chunk {c} of {len(runs)}")
+            spans.append((c, pos))
+            pos += runs[c].length
+        seg_q.append((row0, length))
+        seg_spans.append(tuple(spans))
+    return AttnLayout(q_rows=q_rows, hq=hq, hkv=hkv, source_rows=tuple(chunk_rows), runs=runs,
+                      seg_q=tuple(seg_q), seg_spans=tuple(seg_spans))
+
+
+def retained_chunk_attention(query: torch.Tensor, ks: Sequence[torch.Tensor], vs: Sequence[torch.Tensor],
+                             layout: AttnLayout, scale: float) -> torch.Tensor:
+    """``query`` ``[R, Hq, 128]`` over retained chunks ``ks``/``vs`` (each
+    ``[S_c, Hkv, 128]``) as described by :func:`retained_chunk_layout`;
+    differentiable wrt the query and every retained chunk."""
+    out, _ = attention(_as_rows(query), layout, [_as_rows(k) for k in ks], [_as_rows(v) for v in vs], scale)
+    return out
 
 
 # ---------------------------------------------------------------------------
