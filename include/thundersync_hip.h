@@ -173,14 +173,17 @@ int ts_attn_fwd(const ts_attn_problem* problem, ts_attn_rows q, ts_attn_rows out
 
 /* Backward: dq (bf16, same row layout contract as q) and each run's dK/dV
  * (bf16, written through the run's dk/dv, summed over the run's visits in a
- * fixed order -- no atomics).  `delta` is a caller-provided fp32 workspace of
- * hq * lse_ld floats (rowsum(dO * O)).
+ * fixed order -- no atomics).  `rowstats` is a caller-provided fp32
+ * workspace of 2 * hq * lse_ld floats: the backward writes, per (head, row),
+ * the pair (lse * log2(e), rowsum(dO * O)) and reads it back.  q and dout
+ * row strides must be below 2^25 elements and every run's K/V row stride
+ * below 2^24 (byte offsets of a tile fit 32 bits).
  * Replaces _flash_split_grouped_backward (engine/streaming.py:734-768),
  * _ChunkedCausalSDPA.backward (:1378-1423), _PackedFlashSplit.backward and
  * its two varlen flash backward calls (:1777-1836), the per-segment
  * recompute of _RaggedAttentionIndependentVJP.backward (:1273-1297). */
 int ts_attn_bwd(const ts_attn_problem* problem, ts_attn_rows q, ts_attn_rows out,
-                ts_attn_rows dout, const float* lse, int64_t lse_ld, float* delta,
+                ts_attn_rows dout, const float* lse, int64_t lse_ld, float* rowstats,
                 ts_attn_rows dq, void* stream);
 
 /* ------------------------------------------------------------------------
@@ -263,9 +266,15 @@ int ts_probe_layouts(const void* a, const void* b, float* d16, float* d32,
  * 16 bytes src[perm[i]] (src: 64 x 16 bytes, perm: 64 ints in [0, 64)) and
  * copies the resulting 1 KB LDS block to dma_out, then a ds_read_b64_tr_b16
  * in which lane i addresses element 4 i of an LDS array holding the 16-bit
- * values 0..511, writing each lane's four values to tr_out (64 x 8 bytes).
- * Used by the test suite to pin gfx950's LDS DMA and transpose-read layouts. */
-int ts_probe_lds(const void* src, const int* perm, void* dma_out, void* tr_out, void* stream);
+ * values 0..511, writing each lane's four values to tr_out (64 x 8 bytes),
+ * then a buffer_load_dwordx4 ... lds through a raw buffer resource over the
+ * first valid_bytes (0..1024) of src, lane i at byte offset 16 perm[i], into
+ * an LDS block prefilled with 0xdeadbeef, copied to buf_out (1 KB): lanes
+ * whose offset is at or past valid_bytes are out of range and must leave
+ * zeros.  Used by the test suite to pin gfx950's LDS DMA, transpose-read and
+ * buffer range-check behaviour. */
+int ts_probe_lds(const void* src, const int* perm, void* dma_out, void* tr_out, void* buf_out,
+                 int valid_bytes, void* stream);
 
 #ifdef __cplusplus
 }

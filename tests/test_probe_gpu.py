@@ -82,14 +82,25 @@ def test_lds_dma_and_transpose_read_layouts(cuda):
     perm = torch.tensor(np.random.default_rng(1).permutation(64), dtype=torch.int32, device=cuda)
     dma = torch.empty(64 * 4, dtype=torch.int32, device=cuda)
     tr = torch.empty(64 * 4, dtype=torch.int16, device=cuda)
+    buf = torch.empty(64 * 4, dtype=torch.int32, device=cuda)
+    valid = 16 * 37 + 8  # rows 0..36 in range; row 37 straddles the end; 38.. out of range
     print("probe: ts_probe_lds", flush=True)
     _lib.check(lib.ts_probe_lds(src.data_ptr(), perm.data_ptr(), dma.data_ptr(), tr.data_ptr(),
-                                _lib.stream_of(src)), "ts_probe_lds")
+                                buf.data_ptr(), valid, _lib.stream_of(src)), "ts_probe_lds")
     torch.cuda.synchronize()
     got = dma.view(64, 4).cpu().numpy()
     p = perm.cpu().numpy()
     # lane i's 16 bytes land at LDS offset 16 i
     np.testing.assert_array_equal(got, np.stack([np.arange(4 * j, 4 * j + 4) for j in p]))
+    # buffer DMA: lane i's 16 bytes at LDS offset 16 i; a lane wholly past the
+    # resource's range writes zeros (the kernels rely on this for ragged tiles)
+    gotb = buf.view(64, 4).cpu().numpy()
+    print("buffer DMA straddling lane:", gotb[int(np.where(p == 37)[0][0])].tolist(), flush=True)
+    for lane, j in enumerate(p):
+        if 16 * j + 16 <= valid:
+            np.testing.assert_array_equal(gotb[lane], np.arange(4 * j, 4 * j + 4), err_msg=f"lane {lane}")
+        elif 16 * j >= valid:
+            np.testing.assert_array_equal(gotb[lane], np.zeros(4), err_msg=f"lane {lane}")
     t = tr.view(64, 4).cpu().numpy().astype(np.int64)
     print("ds_read_b64_tr_b16 lanes 0..19:", t[:20].tolist(), flush=True)
     # within each group of 16 lanes the four values come from four different

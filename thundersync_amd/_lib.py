@@ -42,7 +42,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "ts_rmsnorm_bwd_workspace": (_I64, [_I64, _I64]),
     "ts_rmsnorm_bwd": (_INT, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _INT, _P]),
     "ts_probe_layouts": (_INT, [_P, _P, _P, _P, _P, _P, _P]),
-    "ts_probe_lds": (_INT, [_P, _P, _P, _P, _P]),
+    "ts_probe_lds": (_INT, [_P, _P, _P, _P, _P, _INT, _P]),
     "ts_timing_enable": (_INT, [_INT]),
     "ts_timing_reset": (_INT, []),
     "ts_timing_read": (_INT, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_I64)]),

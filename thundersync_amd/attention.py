@@ -227,11 +227,14 @@ class AttnLayout:
         return total
 
 
-def _check_rows_tensor(t: torch.Tensor, name: str, heads: int) -> None:
+def _check_rows_tensor(t: torch.Tensor, name: str, heads: int, max_row_stride: int = 1 << 24) -> None:
     if t.dim() != 3 or t.shape[1] != heads or t.shape[2] != HEAD_DIM:
         raise ValueError(f"{name} must be [rows, {heads}, {HEAD_DIM}], got {tuple(t.shape)}")
     if t.stride(2) != 1 or t.stride(0) % 8 or t.stride(1) % 8 or t.data_ptr() % 16:
         raise ValueError(f"{name} needs a contiguous head dim, 16-byte alignment and 8-element strides")
+    if t.stride(0) >= max_row_stride:
+        # the kernels address a tile's rows with 32-bit byte offsets
+        raise ValueError(f"{name} row stride {t.stride(0)} must be below {max_row_stride} elements")
 
 
 def _rows(t: torch.Tensor) -> AttnRows:
@@ -330,12 +333,12 @@ class _Attention(torch.autograd.Function):
                 dkeys[i].zero_()
                 dvalues[i].zero_()
         runs, host = _run_table(layout, keys, values, dkeys, dvalues)
-        delta = torch.empty(layout.hq, max(layout.q_rows, 1), dtype=torch.float32, device=query.device)
+        rowstats = torch.empty(layout.hq, max(layout.q_rows, 1), 2, dtype=torch.float32, device=query.device)
         problem = layout.problem(query.device, runs.data_ptr(), ctx.scale)
         with operator_range("hip_attention_backward", rows=layout.q_rows, segments=len(layout.seg_q)):
             _lib.check(
                 lib.ts_attn_bwd(ctypes.byref(problem), _rows(query), _rows(out), _rows(dout),
-                                lse.data_ptr(), lse.shape[1], delta.data_ptr(), _rows(dq),
+                                lse.data_ptr(), lse.shape[1], rowstats.data_ptr(), _rows(dq),
                                 _lib.stream_of(query)),
                 f"ts_attn_bwd(rows={layout.q_rows}, hq={layout.hq}, hkv={layout.hkv})",
             )

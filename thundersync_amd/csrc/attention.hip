@@ -145,6 +145,26 @@ __device__ __forceinline__ void tile_scores(f32x4 s[4][2], const bf16* sk, const
   }
 }
 
+// Work-groups are dispatched round-robin over the 8 XCDs (linear id b runs on
+// XCD b % 8), each with its own L2.  The grid is one-dimensional over
+// (head chunk, work item) with the work items of one head chunk contiguous;
+// within every full window of 64 ids, XCD c receives the 8 consecutive tasks
+// 8c .. 8c + 7, so neighbours in the cost-sorted work list -- which read the
+// same key or query rows -- share an L2.  A final partial window keeps the
+// identity map.  Returns the work item; `y` receives the head chunk.
+__device__ __forceinline__ int task_of(int n_items, int& y) {
+  const int b = (int)blockIdx.x;
+  const int total = (int)gridDim.x;
+  const int base = b & ~63;
+  int t = b;
+  if (base + 64 <= total) {
+    const int r = b & 63;
+    t = base + ((r & 7) << 3) + (r >> 3);
+  }
+  y = t / n_items;
+  return t - y * n_items;
+}
+
 // ---------------------------------------------------------------------------
 // forward
 // ---------------------------------------------------------------------------
@@ -155,13 +175,15 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_kernel(ts_attn_problem P, ts_
   __shared__ __attribute__((aligned(16))) bf16 sk[BK * PITCH];
   __shared__ __attribute__((aligned(16))) bf16 sv[BK * PITCH];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int seg_id = P.q_work[2 * blockIdx.x];
-  const int q0 = P.q_work[2 * blockIdx.x + 1];
+  int yb;
+  const int item = task_of(P.n_q_work, yb);
+  const int seg_id = uniform_table(P.q_work)[2 * item];
+  const int q0 = uniform_table(P.q_work)[2 * item + 1];
   const int group = P.hq / P.hkv;
   const int chunks = group / GC;
-  const int hk = blockIdx.y / chunks;
-  const int h = hk * group + (blockIdx.y % chunks) * GC + (wave % GC);
-  const ts_attn_segment seg = P.segs[seg_id];
+  const int hk = yb / chunks;
+  const int h = hk * group + (yb % chunks) * GC + (wave % GC);
+  const ts_attn_segment seg = load_uniform(P.segs, seg_id);
   const int T = seg.q_len;
   const int off = seg.kv_len - seg.q_len;
   const int wq0 = q0 + 32 * (wave / GC);
@@ -183,8 +205,8 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_kernel(ts_attn_problem P, ts_
   float lsum[2] = {0.f, 0.f};
 
   for (int sp = 0; sp < seg.nspan; ++sp) {
-    const ts_attn_ref ref = P.seg_spans[seg.span0 + sp];
-    const ts_attn_run run = P.runs[ref.index];
+    const ts_attn_ref ref = load_uniform(P.seg_spans, seg.span0 + sp);
+    const ts_attn_run run = load_uniform(P.runs, ref.index);
     const bf16* kb0 = (const bf16*)run.k + (int64_t)hk * run.k_head_stride;
     const bf16* vb0 = (const bf16*)run.v + (int64_t)hk * run.v_head_stride;
     for (int kt0 = 0; kt0 < run.len; kt0 += BK) {
@@ -290,10 +312,14 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_kernel(ts_attn_problem P, ts_
 }
 
 // ---------------------------------------------------------------------------
-// backward preprocess: delta[h][row] = sum_d dO * O (fp32)
+// backward preprocess: per (head, row) the pair (lse * log2(e), delta) with
+// delta = sum_d dO * O (fp32); a row that saw no key (lse = -inf) gets +inf
+// so that exp2(s * scale * log2(e) - lse2) is 0.  The two values of a row are
+// adjacent so the backward kernels fetch a tile's statistics in one load.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(kThreads) void delta_kernel(ts_attn_rows O, ts_attn_rows dO,
-                                                         float* __restrict__ delta, int64_t lse_ld,
+                                                         const float* __restrict__ lse,
+                                                         float* __restrict__ rowstats, int64_t lse_ld,
                                                          int64_t rows, int hq) {
   const int64_t pair = (int64_t)blockIdx.x * (kThreads / 16) + threadIdx.x / 16;
   const int sub = threadIdx.x & 15;
@@ -310,7 +336,12 @@ __global__ __launch_bounds__(kThreads) void delta_kernel(ts_attn_rows O, ts_attn
   }
 #pragma unroll
   for (int msk = 8; msk >= 1; msk >>= 1) acc += shfl_xor(acc, msk);
-  if (sub == 0) delta[(int64_t)h * lse_ld + row] = acc;
+  if (sub == 0) {
+    const int64_t at = (int64_t)h * lse_ld + row;
+    const float l = lse[at];
+    rowstats[2 * at] = l == neg_inf() ? __builtin_huge_valf() : l * kLog2e;
+    rowstats[2 * at + 1] = acc;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -318,19 +349,20 @@ __global__ __launch_bounds__(kThreads) void delta_kernel(ts_attn_rows O, ts_attn
 // ---------------------------------------------------------------------------
 template <int GC>
 __global__ __launch_bounds__(kThreads, 1) void dq_kernel(ts_attn_problem P, ts_attn_rows Q,
-                                                         ts_attn_rows dO, const float* __restrict__ lse,
-                                                         const float* __restrict__ delta,
+                                                         ts_attn_rows dO, const float* __restrict__ rowstats,
                                                          int64_t lse_ld, ts_attn_rows dQ) {
   __shared__ __attribute__((aligned(16))) bf16 sk[BK * PITCH];
   __shared__ __attribute__((aligned(16))) bf16 sv[BK * PITCH];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int seg_id = P.q_work[2 * blockIdx.x];
-  const int q0 = P.q_work[2 * blockIdx.x + 1];
+  int yb;
+  const int item = task_of(P.n_q_work, yb);
+  const int seg_id = uniform_table(P.q_work)[2 * item];
+  const int q0 = uniform_table(P.q_work)[2 * item + 1];
   const int group = P.hq / P.hkv;
   const int chunks = group / GC;
-  const int hk = blockIdx.y / chunks;
-  const int h = hk * group + (blockIdx.y % chunks) * GC + (wave % GC);
-  const ts_attn_segment seg = P.segs[seg_id];
+  const int hk = yb / chunks;
+  const int h = hk * group + (yb % chunks) * GC + (wave % GC);
+  const ts_attn_segment seg = load_uniform(P.segs, seg_id);
   const int T = seg.q_len;
   const int off = seg.kv_len - seg.q_len;
   const int wq0 = q0 + 32 * (wave / GC);
@@ -352,9 +384,9 @@ __global__ __launch_bounds__(kThreads, 1) void dq_kernel(ts_attn_problem P, ts_a
     lse2[qb] = __builtin_huge_valf();
     dlt[qb] = 0.f;
     if (active && row < T) {
-      const float v = lse[(int64_t)h * lse_ld + seg.q_row0 + row];
-      lse2[qb] = v == neg_inf() ? __builtin_huge_valf() : v * kLog2e;
-      dlt[qb] = delta[(int64_t)h * lse_ld + seg.q_row0 + row];
+      const int64_t at = 2 * ((int64_t)h * lse_ld + seg.q_row0 + row);
+      lse2[qb] = rowstats[at];
+      dlt[qb] = rowstats[at + 1];
     }
   }
   f32x4 acc[2][8];
@@ -364,8 +396,8 @@ __global__ __launch_bounds__(kThreads, 1) void dq_kernel(ts_attn_problem P, ts_a
     for (int e = 0; e < 8; ++e) acc[qb][e] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   for (int sp = 0; sp < seg.nspan; ++sp) {
-    const ts_attn_ref ref = P.seg_spans[seg.span0 + sp];
-    const ts_attn_run run = P.runs[ref.index];
+    const ts_attn_ref ref = load_uniform(P.seg_spans, seg.span0 + sp);
+    const ts_attn_run run = load_uniform(P.runs, ref.index);
     const bf16* kb0 = (const bf16*)run.k + (int64_t)hk * run.k_head_stride;
     const bf16* vb0 = (const bf16*)run.v + (int64_t)hk * run.v_head_stride;
     for (int kt0 = 0; kt0 < run.len; kt0 += BK) {
@@ -442,19 +474,19 @@ __global__ __launch_bounds__(kThreads, 1) void dq_kernel(ts_attn_problem P, ts_a
 // backward dK / dV (key-stationary)
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(kThreads, 2) void dkdv_kernel(ts_attn_problem P, ts_attn_rows Q,
-                                                           ts_attn_rows dO, const float* __restrict__ lse,
-                                                           const float* __restrict__ delta,
+                                                           ts_attn_rows dO, const float* __restrict__ rowstats,
                                                            int64_t lse_ld) {
   __shared__ __attribute__((aligned(16))) bf16 sq[32 * PITCH];
   __shared__ __attribute__((aligned(16))) bf16 sd[32 * PITCH];
   __shared__ float s_lse2[32];
   __shared__ float s_dlt[32];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int run_id = P.kv_work[2 * blockIdx.x];
-  const int k0 = P.kv_work[2 * blockIdx.x + 1];
-  const int hk = blockIdx.y;
+  int hk;
+  const int item = task_of(P.n_kv_work, hk);
+  const int run_id = uniform_table(P.kv_work)[2 * item];
+  const int k0 = uniform_table(P.kv_work)[2 * item + 1];
   const int group = P.hq / P.hkv;
-  const ts_attn_run run = P.runs[run_id];
+  const ts_attn_run run = load_uniform(P.runs, run_id);
   const int wk0 = k0 + 16 * wave;                 // first key (run-local) of this wave
   const int mykey = wk0 + (lane & 15);            // key column this lane holds
   const bool wave_has_keys = wk0 < run.len;
@@ -484,8 +516,8 @@ __global__ __launch_bounds__(kThreads, 2) void dkdv_kernel(ts_attn_problem P, ts
   }
 
   for (int vi = 0; vi < run.nvisit; ++vi) {
-    const ts_attn_ref ref = P.run_visits[run.visit0 + vi];
-    const ts_attn_segment seg = P.segs[ref.index];
+    const ts_attn_ref ref = load_uniform(P.run_visits, run.visit0 + vi);
+    const ts_attn_segment seg = load_uniform(P.segs, ref.index);
     const int T = seg.q_len;
     const int off = seg.kv_len - seg.q_len;
     // row r sees key k iff kpos + k <= off + r
@@ -508,9 +540,9 @@ __global__ __launch_bounds__(kThreads, 2) void dkdv_kernel(ts_attn_problem P, ts
         if (tid < 32) {
           float l2 = __builtin_huge_valf(), dl = 0.f;
           if (tid < nrows) {
-            const float v = lse[(int64_t)h * lse_ld + row0 + tid];
-            l2 = v == neg_inf() ? __builtin_huge_valf() : v * kLog2e;
-            dl = delta[(int64_t)h * lse_ld + row0 + tid];
+            const int64_t at = 2 * ((int64_t)h * lse_ld + row0 + tid);
+            l2 = rowstats[at];
+            dl = rowstats[at + 1];
           }
           s_lse2[tid] = l2;
           s_dlt[tid] = dl;
@@ -586,47 +618,30 @@ __global__ __launch_bounds__(kThreads, 2) void dkdv_kernel(ts_attn_problem P, ts
 // ---------------------------------------------------------------------------
 // backward dK / dV, one wave per query head (GQA groups that are a multiple of 4)
 //
-// A work-group owns 64 keys of one run and one KV head; wave w handles query
-// heads w, w + 4, ... of the group over all 64 keys, so a wave's LDS reads of
-// its head's Q/dO tile feed 64 keys of MFMA work (4x the reuse of a
-// 16-key-per-wave split).  K^T operands stay in registers; the V tile sits in
-// LDS.  Each wave streams its head's 32-row Q/dO tiles (and their 32 LSE and
-// delta values) into its own double-buffered LDS region with
-// global_load_lds_dwordx4 / _dword: no register staging and no work-group
-// barrier inside the loop.  Rows are 256 bytes, 16-byte chunk c of row r at
-// chunk slot c ^ (r & 15): row reads of 16 rows at one chunk, transpose
-// reads and the DMA's 4-row instructions are all conflict-free, and every
-// address is a per-lane offset (4 for row reads, 8 for transpose reads)
-// plus an immediate.  dO^T and Q^T come from ds_read_b64_tr_b16: within
-// each 16-lane group, lane i receives column (i & 3) of the rows addressed
-// by lanes i/4, i/4 + 4, i/4 + 8, i/4 + 12, so lane j addressing row
-// kbase + j/4, columns m0 + 4 (j & 3) yields X[kbase + t][m0 + i], t = 0..3
-// (pinned by the LDS probe test).  The per-head partials are summed across
-// waves through LDS in wave order.
+// A work-group owns 16 KB keys of one run and one KV head; wave w handles query
+// heads w, w + 4, ... of the group over all of them, so a wave's LDS reads of
+// its head's Q/dO tile feed 16 KB keys of MFMA work.  K^T operands stay in
+// registers; the V tile sits in LDS.  Each wave streams its head's 32-row
+// Q/dO tiles and their 32 (lse * log2 e, delta) pairs into its own
+// double-buffered LDS region with buffer_load ... lds: the buffer resource of
+// a tile covers exactly its valid rows, so rows past a segment's end arrive
+// as zeros (no clamping, no masking: a zero row has S = dP = 0, statistics
+// (0, 0), hence dS = 0 and a zero dO row, and adds nothing), and every
+// lane's address is a constant byte offset fixed at kernel start.  Rows are
+// 256 bytes, 16-byte chunk c of row r at chunk slot c ^ (r & 15): row reads of
+// 16 rows at one chunk, transpose reads and the DMA's 4-row instructions are
+// all conflict-free.  dO^T and Q^T come from ds_read_b64_tr_b16: within each
+// 16-lane group, lane i receives column (i & 3) of the rows addressed by
+// lanes i/4, i/4 + 4, i/4 + 8, i/4 + 12, so lane j addressing row kbase +
+// j/4, columns m0 + 4 (j & 3) yields X[kbase + t][m0 + i], t = 0..3 (pinned
+// by the LDS probe test).  The causal mask is applied only to tiles that
+// cross the diagonal.  The per-head partials are summed across waves through
+// LDS in wave order.
 // ---------------------------------------------------------------------------
 typedef short s16x4 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) void lds_void;
 
 constexpr int kTile32 = 32 * D;              // elements of one 32-row tile (256-byte rows)
-constexpr int kStage32 = 2 * kTile32 + 128;  // Q tile + dO tile + 64 floats (lse, delta)
-
-__device__ __forceinline__ void dma16(const bf16* src, bf16* lds_wave_block) {
-  __builtin_amdgcn_global_load_lds((const void*)src, (lds_void*)lds_wave_block, 16, 0, 0);
-}
-
-// One wave copies rows [0, 4 * ninst) x 128 of a row-major source (rows past
-// nvalid repeat row nvalid - 1) into a swizzled tile: instruction t covers
-// rows 4t .. 4t + 3; lane (g4, j16) fills row 4t + g4, chunk slot j16 with
-// logical chunk j16 ^ ((4t + g4) & 15).  dchunk[t & 3] holds that logical
-// chunk times 8 (elements).
-__device__ __forceinline__ void dma_tile(bf16* tile, const bf16* base, int64_t row_stride, int nvalid,
-                                         int g4, const int dchunk[4], int t0, int t1, int tstep) {
-  for (int t = t0; t < t1; t += tstep) {
-    int r = 4 * t + g4;
-    r = r < nvalid ? r : nvalid - 1;
-    dma16(base + (int64_t)r * row_stride + dchunk[t & 3], tile + t * 512);
-  }
-}
+constexpr int kStage32 = 2 * kTile32 + 128;  // Q tile + dO tile + 32 (lse2, delta) pairs
 
 __device__ __forceinline__ u32x2 tr_read(const bf16* p) {
   const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)p);
@@ -643,25 +658,26 @@ struct Cursor {
 template <int KB>
 __global__ __launch_bounds__(kThreads, 1) void dkdv_wave_kernel(ts_attn_problem P, ts_attn_rows Q,
                                                                 ts_attn_rows dO,
-                                                                const float* __restrict__ lse,
-                                                                const float* __restrict__ delta,
+                                                                const float* __restrict__ rowstats,
                                                                 int64_t lse_ld) {
   __shared__ __attribute__((aligned(16))) bf16 s_v[16 * KB * D];
-  // per wave and stage: Q tile, dO tile, then 32 lse + 32 delta floats
+  // per wave and stage: Q tile, dO tile, then 32 (lse2, delta) pairs
   __shared__ __attribute__((aligned(16))) bf16 s_b0[4][kStage32];
   __shared__ __attribute__((aligned(16))) bf16 s_b1[4][kStage32];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g4 = lane >> 4, j16 = lane & 15;
-  const int run_id = P.kv_work[2 * blockIdx.x];
-  const int k0 = P.kv_work[2 * blockIdx.x + 1];
-  const int hk = blockIdx.y;
+  int hk;
+  const int item = task_of(P.n_kv_work, hk);
+  const int run_id = uniform_table(P.kv_work)[2 * item];
+  const int k0 = uniform_table(P.kv_work)[2 * item + 1];
   const int group = P.hq / P.hkv;
-  const ts_attn_run run = P.runs[run_id];
+  const ts_attn_run run = load_uniform(P.runs, run_id);
   constexpr int NK = 16 * KB;  // keys per work-group
   const int nkeys = min(NK, run.len - k0);
   const float c = P.scale * kLog2e;
 
-  // per-lane LDS / DMA offsets (elements)
+  // per-lane LDS offsets (elements)
   int ro[4], to[8], dchunk[4];
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) ro[ks] = j16 * D + (((4 * ks + g4) ^ j16) << 3);
@@ -671,12 +687,25 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_wave_kernel(ts_attn_problem 
     const int col = 16 * mb + 4 * (j16 & 3);
     to[mb] = r * D + ((((col >> 3) ^ r) & 15) << 3) + (col & 7);
   }
+  // DMA instruction t fills rows 4t .. 4t + 3; lane (g4, j16) the row 4t + g4,
+  // chunk slot j16 with logical chunk j16 ^ (4 (t & 3) + g4)
 #pragma unroll
   for (int t = 0; t < 4; ++t) dchunk[t] = (j16 ^ (4 * t + g4)) << 3;
+  // byte offsets of this lane's row and chunk within a 16-row half tile
+  int qoff[4], doff[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    qoff[t] = (int)(((4 * t + g4) * Q.row_stride + dchunk[t]) * 2);
+    doff[t] = (int)(((4 * t + g4) * dO.row_stride + dchunk[t]) * 2);
+  }
 
-  // V tile: 4 KB DMA instructions, wave w issues w, w + 4, ...
-  dma_tile(s_v, (const bf16*)run.v + (int64_t)k0 * run.v_row_stride + (int64_t)hk * run.v_head_stride,
-           run.v_row_stride, nkeys, g4, dchunk, wave, 4 * KB, 4);
+  // V tile (rows past the run arrive as zeros); wave w issues instructions w, w + 4, ...
+  {
+    const bf16* vb = (const bf16*)run.v + (int64_t)k0 * run.v_row_stride + (int64_t)hk * run.v_head_stride;
+    const rsrc_t rv = make_rsrc(vb, (uint32_t)(nkeys * run.v_row_stride * 2));
+    for (int t = wave; t < 4 * KB; t += 4)
+      buffer_dma16(rv, s_v + t * 512, (int)(((4 * t + g4) * run.v_row_stride + dchunk[t & 3]) * 2));
+  }
   // K^T operands: kreg[kb][ks] = K[k0 + 16 kb + j16][32 ks + 8 g4 ..]
   bf16x8 kreg[KB][4];
 #pragma unroll
@@ -702,8 +731,8 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_wave_kernel(ts_attn_problem 
   // first block at or after (vi, r0); skips visits with no visible rows
   auto settle = [&](Cursor cur) -> Cursor {
     while (cur.vi < run.nvisit) {
-      const ts_attn_ref ref = P.run_visits[run.visit0 + cur.vi];
-      const ts_attn_segment seg = P.segs[ref.index];
+      const ts_attn_ref ref = load_uniform(P.run_visits, run.visit0 + cur.vi);
+      const ts_attn_segment seg = load_uniform(P.segs, ref.index);
       if (cur.r0 < 0) {
         int rs = ref.kpos + k0 - (seg.kv_len - seg.q_len);
         rs = rs < 0 ? 0 : rs;
@@ -716,26 +745,34 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_wave_kernel(ts_attn_problem 
     return cur;
   };
   auto issue = [&](Cursor cur, int h, bf16* buf) {
-    const ts_attn_ref ref = P.run_visits[run.visit0 + cur.vi];
-    const ts_attn_segment seg = P.segs[ref.index];
+    const ts_attn_ref ref = load_uniform(P.run_visits, run.visit0 + cur.vi);
+    const ts_attn_segment seg = load_uniform(P.segs, ref.index);
     const int nrows = min(32, seg.q_len - cur.r0);
+    const int n_lo = min(16, nrows), n_hi = nrows - n_lo;
     const int64_t row0 = seg.q_row0 + cur.r0;
-    dma_tile(buf, (const bf16*)Q.ptr + row0 * Q.row_stride + (int64_t)h * Q.head_stride, Q.row_stride,
-             nrows, g4, dchunk, 0, 8, 1);
-    dma_tile(buf + kTile32, (const bf16*)dO.ptr + row0 * dO.row_stride + (int64_t)h * dO.head_stride,
-             dO.row_stride, nrows, g4, dchunk, 0, 8, 1);
-    // lanes 0..31: lse of rows 0..31, lanes 32..63: delta (rows clamped)
-    const int rr = min(lane & 31, nrows - 1);
-    const float* src = (lane < 32 ? lse : delta) + (int64_t)h * lse_ld + row0 + rr;
-    __builtin_amdgcn_global_load_lds((const void*)src, (lds_void*)(buf + 2 * kTile32), 4, 0, 0);
+    const bf16* qb = (const bf16*)Q.ptr + row0 * Q.row_stride + (int64_t)h * Q.head_stride;
+    const bf16* db = (const bf16*)dO.ptr + row0 * dO.row_stride + (int64_t)h * dO.head_stride;
+    const rsrc_t q_lo = make_rsrc(qb, (uint32_t)(n_lo * Q.row_stride * 2));
+    const rsrc_t q_hi = make_rsrc(qb + 16 * Q.row_stride, (uint32_t)(n_hi * Q.row_stride * 2));
+    const rsrc_t d_lo = make_rsrc(db, (uint32_t)(n_lo * dO.row_stride * 2));
+    const rsrc_t d_hi = make_rsrc(db + 16 * dO.row_stride, (uint32_t)(n_hi * dO.row_stride * 2));
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      buffer_dma16(q_lo, buf + t * 512, qoff[t]);
+      buffer_dma16(q_hi, buf + (4 + t) * 512, qoff[t]);
+      buffer_dma16(d_lo, buf + kTile32 + t * 512, doff[t]);
+      buffer_dma16(d_hi, buf + kTile32 + (4 + t) * 512, doff[t]);
+    }
+    // 32 rows x 8 bytes of statistics: lanes 0..15, 16 bytes each
+    const rsrc_t rs = make_rsrc(rowstats + 2 * ((int64_t)h * lse_ld + row0), (uint32_t)(nrows * 8));
+    if (lane < 16) buffer_dma16(rs, buf + 2 * kTile32, lane * 16);
   };
 
   // one 32-row block of the current head; buffer roles fixed per call
   auto step = [&](auto bsel, Cursor& cur, int h) {
-      const ts_attn_ref ref = P.run_visits[run.visit0 + cur.vi];
-      const ts_attn_segment seg = P.segs[ref.index];
+      const ts_attn_ref ref = load_uniform(P.run_visits, run.visit0 + cur.vi);
+      const ts_attn_segment seg = load_uniform(P.segs, ref.index);
       const int off = seg.kv_len - seg.q_len;
-      const int nrows = min(32, seg.q_len - cur.r0);
       const int r0 = cur.r0;
       Cursor nxt = settle(Cursor{cur.vi, cur.r0 + 32});
       __builtin_amdgcn_s_waitcnt(0);  // this block's tiles have landed
@@ -746,7 +783,7 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_wave_kernel(ts_attn_problem 
       if (nxt.vi < run.nvisit) issue(nxt, h, nxt_buf);
       const bf16* tq = cur_buf;
       const bf16* td = cur_buf + kTile32;
-      const float* sl = reinterpret_cast<const float*>(cur_buf + 2 * kTile32);  // [32] lse, [32] delta
+      const float* sl = reinterpret_cast<const float*>(cur_buf + 2 * kTile32);  // [32] (lse2, delta)
 
       // S = Q K^T, dP = dO V^T: [qb][kb] holds rows 16 qb + 4 g4 + i, key 16 kb + j16
       f32x4 sc[2][KB], dp[2][KB];
@@ -782,29 +819,43 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_wave_kernel(ts_attn_problem 
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int rl = 16 * qb + 4 * g4 + i;
-          const float lv = sl[rl];
-          l2[qb][i] = lv == neg_inf() ? __builtin_huge_valf() : lv * kLog2e;
-          dl[qb][i] = sl[32 + rl];
+          l2[qb][i] = sl[2 * rl];
+          dl[qb][i] = sl[2 * rl + 1];
         }
       // P and dS as B operands: slot j = 4 qb + i  <->  row 16 qb + 4 g4 + i
-      const bool full = (r0 + 32 <= seg.q_len) & (k0 + NK <= run.len) & (ref.kpos + k0 + NK - 1 <= off + r0);
       bf16x8 pk[KB], dsk[KB];
+      if (ref.kpos + k0 + NK - 1 > off + r0) {  // the block crosses the diagonal
 #pragma unroll
-      for (int kb = 0; kb < KB; ++kb) {
-        const int key = k0 + 16 * kb + j16;
-        float pv[8], dsv[8];
+        for (int kb = 0; kb < KB; ++kb) {
+          const int lim = off + r0 - ref.kpos - (k0 + 16 * kb + j16);  // row rl sees the key iff rl >= -lim
+          float pv[8], dsv[8];
 #pragma unroll
-        for (int qb = 0; qb < 2; ++qb)
+          for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int rl = 16 * qb + 4 * g4 + i;
-            const bool vis = full | ((rl < nrows) & (key < run.len) & (ref.kpos + key <= off + r0 + rl));
-            const float p = vis ? fast_exp2(sc[qb][kb][i] * c - l2[qb][i]) : 0.f;
-            pv[4 * qb + i] = p;
-            dsv[4 * qb + i] = p * (dp[qb][kb][i] - dl[qb][i]);
-          }
-        pk[kb] = pack8(pv);
-        dsk[kb] = pack8(dsv);
+            for (int i = 0; i < 4; ++i) {
+              const int rl = 16 * qb + 4 * g4 + i;
+              const float p = rl + lim >= 0 ? fast_exp2(sc[qb][kb][i] * c - l2[qb][i]) : 0.f;
+              pv[4 * qb + i] = p;
+              dsv[4 * qb + i] = p * (dp[qb][kb][i] - dl[qb][i]);
+            }
+          pk[kb] = pack8(pv);
+          dsk[kb] = pack8(dsv);
+        }
+      } else {
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb) {
+          float pv[8], dsv[8];
+#pragma unroll
+          for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const float p = fast_exp2(sc[qb][kb][i] * c - l2[qb][i]);
+              pv[4 * qb + i] = p;
+              dsv[4 * qb + i] = p * (dp[qb][kb][i] - dl[qb][i]);
+            }
+          pk[kb] = pack8(pv);
+          dsk[kb] = pack8(dsv);
+        }
       }
       // dV^T += dO^T P, dK^T += Q^T dS: rows d = 16 mb + 4 g4 + i, column key
 #pragma unroll
@@ -913,7 +964,8 @@ int validate(const ts_attn_problem* p, const char* what) {
                "%s: negative table size", what);
   TS_CHECK_ARG(p->n_q_work == 0 || (p->q_work && p->segs && p->seg_spans && p->runs),
                "%s: null table", what);
-  TS_CHECK_ARG((int64_t)(p->hq / p->hkv / gc) * p->hkv <= 65535, "%s: too many heads", what);
+  TS_CHECK_ARG((int64_t)p->n_q_work * (p->hq / gc) < (1ll << 31) && (int64_t)p->n_kv_work * p->hkv < (1ll << 31),
+               "%s: work list too long", what);
   return TS_OK;
 }
 
@@ -939,7 +991,7 @@ int ts_attn_fwd(const ts_attn_problem* problem, ts_attn_rows q, ts_attn_rows out
                (long long)lse_ld, (long long)P.q_rows);
   const int group = P.hq / P.hkv;
   const int gc = heads_per_block(group);
-  const dim3 grid((unsigned)P.n_q_work, (unsigned)(P.hkv * (group / gc)));
+  const dim3 grid((unsigned)(P.n_q_work * P.hkv * (group / gc)));
   hipStream_t s = (hipStream_t)stream;
   if (gc == 4)
     { ts::TimedLaunch timed_("attention.fwd_kernel", s); hipLaunchKernelGGL(fwd_kernel<4>, grid, dim3(kThreads), 0, s, P, q, out, lse, lse_ld); }
@@ -951,7 +1003,7 @@ int ts_attn_fwd(const ts_attn_problem* problem, ts_attn_rows q, ts_attn_rows out
 }
 
 int ts_attn_bwd(const ts_attn_problem* problem, ts_attn_rows q, ts_attn_rows out, ts_attn_rows dout,
-                const float* lse, int64_t lse_ld, float* delta, ts_attn_rows dq, void* stream) {
+                const float* lse, int64_t lse_ld, float* rowstats, ts_attn_rows dq, void* stream) {
   using namespace ts::attn;
   int st = validate(problem, "ts_attn_bwd");
   if (st != TS_OK) return st;
@@ -960,35 +1012,37 @@ int ts_attn_bwd(const ts_attn_problem* problem, ts_attn_rows q, ts_attn_rows out
   TS_CHECK_ARG(aligned_rows(q) && aligned_rows(out) && aligned_rows(dout) && aligned_rows(dq),
                "ts_attn_bwd: q/out/dout/dq must be 16-byte aligned with strides that are "
                "multiples of 8 elements");
-  TS_CHECK_ARG(lse && delta && lse_ld >= P.q_rows, "ts_attn_bwd: lse/delta null or lse_ld too small");
+  TS_CHECK_ARG(q.row_stride < (1ll << 25) && dout.row_stride < (1ll << 25),
+               "ts_attn_bwd: q/dout row strides must be below 2^25 elements");
+  TS_CHECK_ARG(lse && rowstats && lse_ld >= P.q_rows, "ts_attn_bwd: lse/rowstats null or lse_ld too small");
   TS_CHECK_ARG(P.n_kv_work == 0 || (P.kv_work && P.run_visits), "ts_attn_bwd: null kv tables");
   hipStream_t s = (hipStream_t)stream;
   const int64_t pairs = P.q_rows * P.hq;
   if (pairs > 0) {
     { ts::TimedLaunch timed_("attention.delta_kernel", s); hipLaunchKernelGGL(delta_kernel, dim3((unsigned)((pairs + 15) / 16)), dim3(kThreads), 0, s, out,
-                       dout, delta, lse_ld, P.q_rows, P.hq); }
+                       dout, lse, rowstats, lse_ld, P.q_rows, P.hq); }
     st = ts::check_launch("ts_attn_bwd (delta)");
     if (st != TS_OK) return st;
   }
   const int group = P.hq / P.hkv;
   const int gc = heads_per_block(group);
   if (P.n_q_work > 0) {
-    const dim3 grid((unsigned)P.n_q_work, (unsigned)(P.hkv * (group / gc)));
+    const dim3 grid((unsigned)(P.n_q_work * P.hkv * (group / gc)));
     if (gc == 4)
-      { ts::TimedLaunch timed_("attention.dq_kernel", s); hipLaunchKernelGGL(dq_kernel<4>, grid, dim3(kThreads), 0, s, P, q, dout, lse, delta, lse_ld, dq); }
+      { ts::TimedLaunch timed_("attention.dq_kernel", s); hipLaunchKernelGGL(dq_kernel<4>, grid, dim3(kThreads), 0, s, P, q, dout, rowstats, lse_ld, dq); }
     else if (gc == 2)
-      { ts::TimedLaunch timed_("attention.dq_kernel", s); hipLaunchKernelGGL(dq_kernel<2>, grid, dim3(kThreads), 0, s, P, q, dout, lse, delta, lse_ld, dq); }
+      { ts::TimedLaunch timed_("attention.dq_kernel", s); hipLaunchKernelGGL(dq_kernel<2>, grid, dim3(kThreads), 0, s, P, q, dout, rowstats, lse_ld, dq); }
     else
-      { ts::TimedLaunch timed_("attention.dq_kernel", s); hipLaunchKernelGGL(dq_kernel<1>, grid, dim3(kThreads), 0, s, P, q, dout, lse, delta, lse_ld, dq); }
+      { ts::TimedLaunch timed_("attention.dq_kernel", s); hipLaunchKernelGGL(dq_kernel<1>, grid, dim3(kThreads), 0, s, P, q, dout, rowstats, lse_ld, dq); }
     st = ts::check_launch("ts_attn_bwd (dq)");
     if (st != TS_OK) return st;
   }
   if (P.n_kv_work > 0) {
-    const dim3 grid((unsigned)P.n_kv_work, (unsigned)P.hkv);
+    const dim3 grid((unsigned)(P.n_kv_work * P.hkv));
     if (group % 4 == 0) {
-      { ts::TimedLaunch timed_("attention.dkdv_kernel", s); hipLaunchKernelGGL(dkdv_wave_kernel<3>, grid, dim3(kThreads), 0, s, P, q, dout, lse, delta, lse_ld); }
+      { ts::TimedLaunch timed_("attention.dkdv_kernel", s); hipLaunchKernelGGL(dkdv_wave_kernel<3>, grid, dim3(kThreads), 0, s, P, q, dout, rowstats, lse_ld); }
     } else {
-      { ts::TimedLaunch timed_("attention.dkdv_kernel", s); hipLaunchKernelGGL(dkdv_kernel, grid, dim3(kThreads), 0, s, P, q, dout, lse, delta, lse_ld); }
+      { ts::TimedLaunch timed_("attention.dkdv_kernel", s); hipLaunchKernelGGL(dkdv_kernel, grid, dim3(kThreads), 0, s, P, q, dout, rowstats, lse_ld); }
     }
     st = ts::check_launch("ts_attn_bwd (dkdv)");
   }

@@ -110,6 +110,57 @@ __device__ __forceinline__ void transpose8x8(const u32x4 in[8], u32x4 out[8]) {
 }
 
 // ---------------------------------------------------------------------------
+// buffer resources and direct-to-LDS loads
+//
+// A raw buffer resource (stride 0) covers `bytes` bytes from `base`; a load
+// whose per-lane byte offset is at or past `bytes` is out of range, touches no
+// memory and returns zeros (for the LDS form: writes zeros to LDS).  Word 3 is
+// gfx9's raw-buffer descriptor: data format 32, no swizzle, no index add.
+// ---------------------------------------------------------------------------
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
+// A read-only table viewed through the constant address space: loads at
+// wave-uniform indices become scalar loads (SGPR results), which buffer
+// resources and LDS DMA bases require.  Only for memory no kernel writes.
+template <typename T>
+__device__ __forceinline__ const __attribute__((address_space(4))) T* uniform_table(const T* p) {
+  return (const __attribute__((address_space(4))) T*)p;
+}
+// Element i of a read-only table of dword-sized-multiple structs, loaded as
+// above (use at wave-uniform indices).
+template <typename T>
+__device__ __forceinline__ T load_uniform(const T* p, int64_t i) {
+  static_assert(sizeof(T) % 4 == 0, "dword-multiple structs only");
+  const __attribute__((address_space(4))) uint32_t* q =
+      (const __attribute__((address_space(4))) uint32_t*)(p + i);
+  uint32_t w[sizeof(T) / 4];
+#pragma unroll
+  for (int k = 0; k < (int)(sizeof(T) / 4); ++k) w[k] = q[k];
+  T v;
+  __builtin_memcpy(&v, w, sizeof(T));
+  return v;
+}
+typedef __attribute__((address_space(3))) void lds_void;
+constexpr int kRawBufferWord3 = 0x00020000;
+
+// `base` and `bytes` must be wave-uniform; they are read from lane 0 so that
+// the descriptor lives in SGPRs even where the compiler cannot prove
+// uniformity (no per-lane waterfall loop around the loads).
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t a = (uint64_t)base;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+  const uint32_t n = __builtin_amdgcn_readfirstlane(bytes);
+  return __builtin_amdgcn_make_buffer_rsrc((void*)(((uint64_t)hi << 32) | lo), (short)0, (int)n,
+                                           kRawBufferWord3);
+}
+// 16 bytes per lane from base + voffset into LDS: lane i writes lds + 16 i.
+// `lds` must be wave-uniform.
+__device__ __forceinline__ void buffer_dma16(rsrc_t r, void* lds, int voffset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)lds, 16, voffset, 0, 0, 0);
+}
+
+// ---------------------------------------------------------------------------
 // wave reductions over lanes that differ in the given xor masks
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float shfl_xor(float v, int mask) {

@@ -45,20 +45,31 @@ __global__ __launch_bounds__(64) void probe_layouts_kernel(
 
 // One wave: (1) global_load_lds_dwordx4 with lane i loading src[perm[i]]
 // into a 1 KB LDS block, read back in LDS order; (2) ds_read_b64_tr_b16 with
-// lane i addressing byte 8 * i of an LDS block holding 16-bit values 0..511.
-// All accesses stay inside the 1 KB block.
+// lane i addressing byte 8 * i of an LDS block holding 16-bit values 0..511;
+// (3) buffer_load_dwordx4 ... lds through a buffer resource over the first
+// `valid_bytes` of src, lane i at byte offset 16 * perm[i]: lanes whose offset
+// is at or past valid_bytes are out of range, read nothing and must leave
+// zeros in LDS.  All LDS accesses stay inside their 1 KB blocks and every
+// in-range global read lies inside src (64 x 16 bytes).
 __global__ __launch_bounds__(64) void probe_lds_kernel(const u32x4* __restrict__ src,
                                                        const int* __restrict__ perm,
                                                        u32x4* __restrict__ dma_out,
-                                                       u32x2* __restrict__ tr_out) {
+                                                       u32x2* __restrict__ tr_out,
+                                                       u32x4* __restrict__ buf_out, int valid_bytes) {
   __shared__ __attribute__((aligned(16))) u32x4 block[64];
+  __shared__ __attribute__((aligned(16))) u32x4 block2[64];
   __shared__ __attribute__((aligned(16))) uint16_t vals[512];
   const int l = threadIdx.x;
   __builtin_amdgcn_global_load_lds((const void*)(src + perm[l]),
                                    (__attribute__((address_space(3))) void*)block, 16, 0, 0);
+  block2[l] = u32x4{0xdeadbeefu, 0xdeadbeefu, 0xdeadbeefu, 0xdeadbeefu};
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  buffer_dma16(make_rsrc(src, (uint32_t)valid_bytes), block2, 16 * perm[l]);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   dma_out[l] = block[l];
+  buf_out[l] = block2[l];
   for (int i = l; i < 512; i += 64) vals[i] = (uint16_t)i;
   __syncthreads();
   typedef short i16x4 __attribute__((ext_vector_type(4)));
@@ -86,10 +97,13 @@ int ts_probe_layouts(const void* a, const void* b, float* d16, float* d32,
   return ts::check_launch("ts_probe_layouts");
 }
 
-int ts_probe_lds(const void* src, const int* perm, void* dma_out, void* tr_out, void* stream) {
-  TS_CHECK_ARG(src && perm && dma_out && tr_out, "ts_probe_lds: null pointer");
+int ts_probe_lds(const void* src, const int* perm, void* dma_out, void* tr_out, void* buf_out,
+                 int valid_bytes, void* stream) {
+  TS_CHECK_ARG(src && perm && dma_out && tr_out && buf_out, "ts_probe_lds: null pointer");
+  TS_CHECK_ARG(valid_bytes >= 0 && valid_bytes <= 64 * 16, "ts_probe_lds: valid_bytes outside [0, 1024]");
   hipLaunchKernelGGL(ts::probe_lds_kernel, dim3(1), dim3(64), 0, (hipStream_t)stream,
-                     (const ts::u32x4*)src, perm, (ts::u32x4*)dma_out, (ts::u32x2*)tr_out);
+                     (const ts::u32x4*)src, perm, (ts::u32x4*)dma_out, (ts::u32x2*)tr_out,
+                     (ts::u32x4*)buf_out, valid_bytes);
   return ts::check_launch("ts_probe_lds");
 }
 
