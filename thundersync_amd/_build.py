@@ -43,8 +43,18 @@ def device_flags() -> list[str]:
     ]
 
 
+# Extra code-generation flags per translation unit.  attention_dq.hip: the dQ
+# kernel's S/dP tiles and dQ accumulators fit the VGPRs, and MFMA results
+# written to VGPRs spare it per-tile copies out of the accumulation registers
+# (the dK/dV kernel, which needs the accumulation registers for its 48-key
+# accumulators, keeps the default).
+FILE_FLAGS = {
+    "attention_dq.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+}
+
+
 def _compile(src: Path, obj: Path) -> tuple[Path, str]:
-    cmd = [hipcc(), *device_flags(), "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *device_flags(), *FILE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     noise = "is not a recognized feature for this target"
     log = "\n".join(

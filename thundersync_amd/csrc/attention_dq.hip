@@ -1,0 +1,411 @@
+// Attention backward: row statistics and dQ (query-stationary).
+#include "attention_impl.h"
+
+namespace ts {
+namespace attn {
+
+// ---------------------------------------------------------------------------
+// backward preprocess: per (head, row) the pair (lse * log2(e), delta) with
+// delta = sum_d dO * O (fp32); a row that saw no key (lse = -inf) gets +inf
+// so that exp2(s * scale * log2(e) - lse2) is 0.  The two values of a row are
+// adjacent so the backward kernels fetch a tile's statistics in one load.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kThreads) void delta_kernel(ts_attn_rows O, ts_attn_rows dO,
+                                                         const float* __restrict__ lse,
+                                                         float* __restrict__ rowstats, int64_t lse_ld,
+                                                         int64_t rows, int hq) {
+  const int64_t pair = (int64_t)blockIdx.x * (kThreads / 16) + threadIdx.x / 16;
+  const int sub = threadIdx.x & 15;
+  const int64_t row = pair / hq;
+  const int h = (int)(pair % hq);
+  if (row >= rows) return;
+  const u32x4 a = ld16((const bf16*)O.ptr + row * O.row_stride + (int64_t)h * O.head_stride + 8 * sub);
+  const u32x4 b = ld16((const bf16*)dO.ptr + row * dO.row_stride + (int64_t)h * dO.head_stride + 8 * sub);
+  float acc = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    acc = fmaf(bf_bits_to_f(a[i] & 0xffffu), bf_bits_to_f(b[i] & 0xffffu), acc);
+    acc = fmaf(bf_bits_to_f(a[i] >> 16), bf_bits_to_f(b[i] >> 16), acc);
+  }
+#pragma unroll
+  for (int msk = 8; msk >= 1; msk >>= 1) acc += shfl_xor(acc, msk);
+  if (sub == 0) {
+    const int64_t at = (int64_t)h * lse_ld + row;
+    const float l = lse[at];
+    rowstats[2 * at] = l == neg_inf() ? __builtin_huge_valf() : l * kLog2e;
+    rowstats[2 * at + 1] = acc;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// backward dQ (query-stationary)
+// ---------------------------------------------------------------------------
+template <int GC>
+__global__ __launch_bounds__(kThreads, 1) void dq_kernel(ts_attn_problem P, ts_attn_rows Q,
+                                                         ts_attn_rows dO, const float* __restrict__ rowstats,
+                                                         int64_t lse_ld, ts_attn_rows dQ) {
+  __shared__ __attribute__((aligned(16))) bf16 sk[BK * PITCH];
+  __shared__ __attribute__((aligned(16))) bf16 sv[BK * PITCH];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  int yb;
+  const int item = task_of(P.n_q_work, yb);
+  const int seg_id = uniform_table(P.q_work)[2 * item];
+  const int q0 = uniform_table(P.q_work)[2 * item + 1];
+  const int group = P.hq / P.hkv;
+  const int chunks = group / GC;
+  const int hk = yb / chunks;
+  const int h = hk * group + (yb % chunks) * GC + (wave % GC);
+  const ts_attn_segment seg = load_uniform(P.segs, seg_id);
+  const int T = seg.q_len;
+  const int off = seg.kv_len - seg.q_len;
+  const int wq0 = q0 + 32 * (wave / GC);
+  const int wg_last = min(q0 + P.q_block, T) - 1;
+  const bool active = wq0 < T;
+  const int w_last = min(wq0 + 32, T) - 1;
+  const float c = P.scale * kLog2e;
+
+  bf16x8 qreg[2][4], dreg[2][4];
+  const int64_t qoff = (seg.q_row0 + wq0);
+  load_rows_b(qreg, (const bf16*)Q.ptr + qoff * Q.row_stride + (int64_t)h * Q.head_stride, Q.row_stride,
+              active ? T - wq0 : 0, lane);
+  load_rows_b(dreg, (const bf16*)dO.ptr + qoff * dO.row_stride + (int64_t)h * dO.head_stride,
+              dO.row_stride, active ? T - wq0 : 0, lane);
+  float lse2[2], dlt[2];
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) {
+    const int row = wq0 + 16 * qb + (lane & 15);
+    lse2[qb] = __builtin_huge_valf();
+    dlt[qb] = 0.f;
+    if (active && row < T) {
+      const int64_t at = 2 * ((int64_t)h * lse_ld + seg.q_row0 + row);
+      lse2[qb] = rowstats[at];
+      dlt[qb] = rowstats[at + 1];
+    }
+  }
+  f32x4 acc[2][8];
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[qb][e] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  for (int sp = 0; sp < seg.nspan; ++sp) {
+    const ts_attn_ref ref = load_uniform(P.seg_spans, seg.span0 + sp);
+    const ts_attn_run run = load_uniform(P.runs, ref.index);
+    const bf16* kb0 = (const bf16*)run.k + (int64_t)hk * run.k_head_stride;
+    const bf16* vb0 = (const bf16*)run.v + (int64_t)hk * run.v_head_stride;
+    for (int kt0 = 0; kt0 < run.len; kt0 += BK) {
+      if (ref.kpos + kt0 > off + wg_last) break;
+      const int nvalid = min(BK, run.len - kt0);
+      Tile tk, tv;
+      tile_load(tk, kb0 + (int64_t)kt0 * run.k_row_stride, run.k_row_stride, nvalid, tid);
+      tile_load(tv, vb0 + (int64_t)kt0 * run.v_row_stride, run.v_row_stride, nvalid, tid);
+      __syncthreads();
+      tile_store(tk, sk, tid);
+      tile_store(tv, sv, tid);
+      __syncthreads();
+      if (!active || ref.kpos + kt0 > off + w_last) continue;
+
+      f32x4 s[4][2], dp[4][2];
+      tile_scores(s, sk, qreg, lane);
+      tile_scores(dp, sv, dreg, lane);  // dP^T = V dO^T, same shape as S^T
+      const bool need_mask = (kt0 + BK > run.len) || (ref.kpos + kt0 + BK - 1 > off + wq0);
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            float p = fast_exp2(s[kb][qb][i] * c - lse2[qb]);
+            if (need_mask) {
+              const int key = kt0 + 16 * kb + 4 * (lane >> 4) + i;
+              const int row = wq0 + 16 * qb + (lane & 15);
+              if (key >= run.len || ref.kpos + key > off + row) p = 0.f;
+            }
+            s[kb][qb][i] = p * (dp[kb][qb][i] - dlt[qb]);  // dS^T
+          }
+      // dQ^T += K^T dS^T, 32 keys per k-step
+#pragma unroll
+      for (int ss = 0; ss < 2; ++ss) {
+        bf16x8 dsk[2];
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) {
+          float tmp[8];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) tmp[j] = s[2 * ss + (j >> 2)][qb][j & 3];
+          dsk[qb] = pack8(tmp);
+        }
+        int rows[8];
+        slot_rows(lane >> 4, 32 * ss, rows);
+        bf16x8 kt[8];
+        lds_rows_transposed(sk, rows, 8 * (lane & 15), kt);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          acc[0][e] = mfma16(kt[e], dsk[0], acc[0][e]);
+          acc[1][e] = mfma16(kt[e], dsk[1], acc[1][e]);
+        }
+      }
+    }
+  }
+  if (!active) return;
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) {
+    const int row = wq0 + 16 * qb + (lane & 15);
+    if (row >= T) continue;
+    bf16* drow = (bf16*)dQ.ptr + (seg.q_row0 + row) * dQ.row_stride + (int64_t)h * dQ.head_stride +
+                 32 * (lane >> 4);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float tmp[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) tmp[e] = acc[qb][e][i] * P.scale;
+      st16(drow + 8 * i, as_u32x4(pack8(tmp)));
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// backward dQ for GQA groups that are a multiple of 4 (query-stationary)
+//
+// A work-group owns 32 query rows of one segment for the 4 query heads of one
+// quarter of a GQA group (one wave per head).  Q and dO rows stay in
+// registers as B operands, with the rows' (lse * log2 e, delta) pairs.  The
+// segment's key runs stream through 64-key K/V tiles that all four waves
+// share: double-buffered LDS stages filled by buffer_load ... lds (each wave
+// issues a quarter of a tile's instructions; rows past a run's end arrive as
+// zeros and add nothing, because a zero K row contributes zero to dQ), one
+// work-group barrier per tile.  Tiles use the dK/dV kernel's 256-byte rows
+// with chunk c of row r at slot c ^ (r & 15): K and V rows feed S^T = K Q^T
+// and dP^T = V dO^T as A operands, K^T for dQ^T += K^T dS^T comes from
+// ds_read_b64_tr_b16.  Only tiles that cross the diagonal are masked.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kThreads, 1) void dq_wave_kernel(ts_attn_problem P, ts_attn_rows Q,
+                                                              ts_attn_rows dO,
+                                                              const float* __restrict__ rowstats,
+                                                              int64_t lse_ld, ts_attn_rows dQ) {
+  __shared__ __attribute__((aligned(16))) bf16 s_k0[kKV64];
+  __shared__ __attribute__((aligned(16))) bf16 s_v0[kKV64];
+  __shared__ __attribute__((aligned(16))) bf16 s_k1[kKV64];
+  __shared__ __attribute__((aligned(16))) bf16 s_v1[kKV64];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g4 = lane >> 4, j16 = lane & 15;
+  int yb;
+  const int item = task_of(P.n_q_work, yb);
+  const int seg_id = uniform_table(P.q_work)[2 * item];
+  const int q0 = uniform_table(P.q_work)[2 * item + 1];
+  const int group = P.hq / P.hkv;
+  const int chunks = group / 4;
+  const int hk = yb / chunks;
+  const int h = hk * group + (yb % chunks) * 4 + wave;
+  const ts_attn_segment seg = load_uniform(P.segs, seg_id);
+  const int T = seg.q_len;
+  const int off = seg.kv_len - seg.q_len;
+  const int last = min(q0 + 32, T) - 1;
+  const float c = P.scale * kLog2e;
+
+  // Q / dO rows as B operands: reg[qb][ks] = row q0 + 16 qb + j16, columns 32 ks + 8 g4 ..
+  bf16x8 qreg[2][4], dreg[2][4];
+  const int64_t row0 = seg.q_row0 + q0;
+  load_rows_b(qreg, (const bf16*)Q.ptr + row0 * Q.row_stride + (int64_t)h * Q.head_stride, Q.row_stride,
+              T - q0, lane);
+  load_rows_b(dreg, (const bf16*)dO.ptr + row0 * dO.row_stride + (int64_t)h * dO.head_stride,
+              dO.row_stride, T - q0, lane);
+  // rows past the segment: zero Q and dO with statistics (0, 0) give dS = 0
+  float lse2[2], dlt[2];
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) {
+    const int row = q0 + 16 * qb + j16;
+    lse2[qb] = 0.f;
+    dlt[qb] = 0.f;
+    if (row < T) {
+      const int64_t at = 2 * ((int64_t)h * lse_ld + seg.q_row0 + row);
+      lse2[qb] = rowstats[at];
+      dlt[qb] = rowstats[at + 1];
+    }
+  }
+  f32x4 acc[8][2];
+#pragma unroll
+  for (int mb = 0; mb < 8; ++mb) {
+    acc[mb][0] = f32x4{0.f, 0.f, 0.f, 0.f};
+    acc[mb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  // per-lane LDS offsets (elements): row reads and transpose reads as in dK/dV
+  int ro[4], to[8];
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) ro[ks] = j16 * D + (((4 * ks + g4) ^ j16) << 3);
+#pragma unroll
+  for (int mb = 0; mb < 8; ++mb) {
+    const int r = 4 * g4 + (j16 >> 2);
+    const int col = 16 * mb + 4 * (j16 & 3);
+    to[mb] = r * D + ((((col >> 3) ^ r) & 15) << 3) + (col & 7);
+  }
+  // DMA: this wave issues instructions t = wave + 4 u (rows 4 t .. 4 t + 3) of
+  // each tile; lane (g4, j16) fills row 4 t + g4, slot j16 with logical chunk
+  // j16 ^ (4 wave + g4)
+  const int dma_row = 4 * wave + g4;
+  const int dma_chunk = (j16 ^ (4 * wave + g4)) << 3;
+
+  // next visible tile after `tc` in key order (sp == nspan: none left; once a
+  // tile starts past the block's last visible key, so do all later ones)
+  auto advance = [&](TileCursor tc) -> TileCursor {
+    tc.kt0 += BK;
+    while (tc.sp < seg.nspan) {
+      const ts_attn_ref ref = load_uniform(P.seg_spans, seg.span0 + tc.sp);
+      const ts_attn_run run = load_uniform(P.runs, ref.index);
+      if (tc.kt0 >= run.len) {
+        ++tc.sp;
+        tc.kt0 = 0;
+        continue;
+      }
+      if (ref.kpos + tc.kt0 > off + last) tc.sp = seg.nspan;
+      break;
+    }
+    return tc;
+  };
+  auto issue = [&](TileCursor tc, bf16* sk, bf16* sv) {
+    const ts_attn_ref ref = load_uniform(P.seg_spans, seg.span0 + tc.sp);
+    const ts_attn_run run = load_uniform(P.runs, ref.index);
+    const int nvalid = min(BK, run.len - tc.kt0);
+    const bf16* kb = (const bf16*)run.k + (int64_t)tc.kt0 * run.k_row_stride + (int64_t)hk * run.k_head_stride;
+    const bf16* vb = (const bf16*)run.v + (int64_t)tc.kt0 * run.v_row_stride + (int64_t)hk * run.v_head_stride;
+    const rsrc_t rk = make_rsrc(kb, (uint32_t)(nvalid * run.k_row_stride * 2));
+    const rsrc_t rv = make_rsrc(vb, (uint32_t)(nvalid * run.v_row_stride * 2));
+    const int ko = (int)((dma_row * run.k_row_stride + dma_chunk) * 2);
+    const int vo = (int)((dma_row * run.v_row_stride + dma_chunk) * 2);
+    const int kstep = (int)(16 * run.k_row_stride * 2), vstep = (int)(16 * run.v_row_stride * 2);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      buffer_dma16(rk, sk + (wave + 4 * u) * 512, ko + u * kstep);
+      buffer_dma16(rv, sv + (wave + 4 * u) * 512, vo + u * vstep);
+    }
+  };
+
+  auto step = [&](auto bsel, TileCursor& cur) {
+    const int kpos = load_uniform(P.seg_spans, seg.span0 + cur.sp).kpos;
+    const int kt0 = cur.kt0;
+    const TileCursor nxt = advance(cur);
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's part of the tile has landed
+    __syncthreads();                // every part has, and the other stage is free
+    const bf16* tk = bsel.value == 0 ? s_k0 : s_k1;
+    const bf16* tv = bsel.value == 0 ? s_v0 : s_v1;
+    if (nxt.sp < seg.nspan) issue(nxt, bsel.value == 0 ? s_k1 : s_k0, bsel.value == 0 ? s_v1 : s_v0);
+
+    const bool diag = kpos + kt0 + BK - 1 > off + q0;
+    // two halves of 32 keys: S^T = K Q^T, dP^T = V dO^T for keys 32 ss .. 32 ss + 31
+    // ([kb][qb] lane holds keys 32 ss + 16 kb + 4 g4 + i, row 16 qb + j16), then
+    // dQ^T += K^T dS^T with slot j <-> key 32 ss + 16 (j >> 2) + 4 g4 + (j & 3)
+#pragma unroll
+    for (int ss = 0; ss < 2; ++ss) {
+      f32x4 sc[2][2], dp[2][2];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) {
+          sc[kb][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
+          dp[kb][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+          const bf16x8 ak = as_bf16x8(ld16(tk + ro[ks] + (32 * ss + 16 * kb) * D));
+          const bf16x8 av = as_bf16x8(ld16(tv + ro[ks] + (32 * ss + 16 * kb) * D));
+#pragma unroll
+          for (int qb = 0; qb < 2; ++qb) {
+            sc[kb][qb] = mfma16(ak, qreg[qb][ks], sc[kb][qb]);
+            dp[kb][qb] = mfma16(av, dreg[qb][ks], dp[kb][qb]);
+          }
+        }
+      // dS^T = P^T (dP^T - delta), P^T = exp2(S^T c - lse2); masked only across the diagonal
+      if (diag) {
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int qb = 0; qb < 2; ++qb) {
+            // row q0 + 16 qb + j16 sees key kt0 + 32 ss + 16 kb + 4 g4 + i iff i <= lim
+            const int lim = off + q0 + 16 * qb + j16 - kpos - kt0 - 32 * ss - 16 * kb - 4 * g4;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const float p = i <= lim ? fast_exp2(sc[kb][qb][i] * c - lse2[qb]) : 0.f;
+              sc[kb][qb][i] = p * (dp[kb][qb][i] - dlt[qb]);
+            }
+          }
+      } else {
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const float p = fast_exp2(sc[kb][qb][i] * c - lse2[qb]);
+              sc[kb][qb][i] = p * (dp[kb][qb][i] - dlt[qb]);
+            }
+      }
+      bf16x8 dsk[2];
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) {
+        float tmp[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) tmp[j] = sc[j >> 2][qb][j & 3];
+        dsk[qb] = pack8(tmp);
+      }
+#pragma unroll
+      for (int mb = 0; mb < 8; ++mb) {
+        const u32x2 a0 = tr_read(tk + to[mb] + 32 * ss * D);
+        const u32x2 a1 = tr_read(tk + to[mb] + (32 * ss + 16) * D);
+        const bf16x8 a = as_bf16x8(u32x4{a0[0], a0[1], a1[0], a1[1]});
+        acc[mb][0] = mfma16(a, dsk[0], acc[mb][0]);
+        acc[mb][1] = mfma16(a, dsk[1], acc[mb][1]);
+      }
+    }
+    cur = nxt;
+  };
+
+  TileCursor cur = advance(TileCursor{0, -BK});
+  if (cur.sp < seg.nspan) issue(cur, s_k0, s_v0);
+  while (cur.sp < seg.nspan) {
+    step(std::integral_constant<int, 0>{}, cur);
+    if (cur.sp >= seg.nspan) break;
+    step(std::integral_constant<int, 1>{}, cur);
+  }
+
+  // dQ^T: acc[mb][qb] lane holds d = 16 mb + 4 g4 + i of row q0 + 16 qb + j16
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) {
+    const int row = q0 + 16 * qb + j16;
+    if (row >= T) continue;
+    bf16* drow = (bf16*)dQ.ptr + (seg.q_row0 + row) * dQ.row_stride + (int64_t)h * dQ.head_stride + 4 * g4;
+#pragma unroll
+    for (int mb = 0; mb < 8; ++mb) {
+      const f32x4 v = acc[mb][qb] * P.scale;
+      *reinterpret_cast<u32x2*>(drow + 16 * mb) = u32x2{pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3])};
+    }
+  }
+}
+
+int launch_delta(const ts_attn_problem& P, ts_attn_rows out, ts_attn_rows dout, const float* lse,
+                 float* rowstats, int64_t lse_ld, hipStream_t s) {
+  const int64_t pairs = P.q_rows * P.hq;
+  if (pairs == 0) return TS_OK;
+  { ts::TimedLaunch timed_("attention.delta_kernel", s); hipLaunchKernelGGL(delta_kernel, dim3((unsigned)((pairs + 15) / 16)), dim3(kThreads), 0, s, out,
+                     dout, lse, rowstats, lse_ld, P.q_rows, P.hq); }
+  return ts::check_launch("ts_attn_bwd (delta)");
+}
+
+int launch_dq(const ts_attn_problem& P, ts_attn_rows q, ts_attn_rows dout, const float* rowstats,
+              int64_t lse_ld, ts_attn_rows dq, hipStream_t s) {
+  const int group = P.hq / P.hkv;
+  const int gc = heads_per_block(group);
+  const dim3 grid((unsigned)(P.n_q_work * P.hkv * (group / gc)));
+  if (gc == 4)
+    { ts::TimedLaunch timed_("attention.dq_kernel", s); hipLaunchKernelGGL(dq_wave_kernel, grid, dim3(kThreads), 0, s, P, q, dout, rowstats, lse_ld, dq); }
+  else if (gc == 2)
+    { ts::TimedLaunch timed_("attention.dq_kernel", s); hipLaunchKernelGGL(dq_kernel<2>, grid, dim3(kThreads), 0, s, P, q, dout, rowstats, lse_ld, dq); }
+  else
+    { ts::TimedLaunch timed_("attention.dq_kernel", s); hipLaunchKernelGGL(dq_kernel<1>, grid, dim3(kThreads), 0, s, P, q, dout, rowstats, lse_ld, dq); }
+  return ts::check_launch("ts_attn_bwd (dq)");
+}
+
+}  // namespace attn
+}  // namespace ts

@@ -1,0 +1,200 @@
+// Device helpers and host launchers shared by the attention translation units
+// (attention.hip: entry points; attention_fwd.hip, attention_dq.hip,
+// attention_dkdv.hip: kernels).  The kernels are compiled in separate units
+// so each can take its own code-generation flags.
+#pragma once
+#include <type_traits>
+
+#include "common.h"
+#include "timing.h"
+#include "../../include/thundersync_hip.h"
+
+namespace ts {
+namespace attn {
+
+
+constexpr int D = 128;
+constexpr int BK = 64;          // keys per tile (fwd / dq) and per dkdv block
+constexpr int kThreads = 256;   // 4 waves
+constexpr int PITCH = D + 8;    // LDS row pitch in elements (272 bytes)
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+__device__ __forceinline__ float neg_inf() { return -__builtin_huge_valf(); }
+
+__device__ __forceinline__ u32x4 ld16(const bf16* p) { return *reinterpret_cast<const u32x4*>(p); }
+__device__ __forceinline__ void st16(bf16* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
+
+// A 64 x 128 tile of K or V rows moved global -> registers -> LDS by 256
+// threads; 16 consecutive threads read one 256-byte row.
+struct Tile {
+  u32x4 v[4];
+};
+
+__device__ __forceinline__ void tile_load(Tile& t, const bf16* base, int64_t row_stride, int nvalid,
+                                          int tid) {
+#pragma unroll
+  for (int it = 0; it < 4; ++it) {
+    const int idx = it * kThreads + tid;
+    const int row = idx >> 4, chunk = idx & 15;
+    if (row < nvalid)
+      t.v[it] = ld16(base + (int64_t)row * row_stride + chunk * 8);
+    else
+      t.v[it] = u32x4{0u, 0u, 0u, 0u};
+  }
+}
+
+__device__ __forceinline__ void tile_store(const Tile& t, bf16* lds, int tid) {
+#pragma unroll
+  for (int it = 0; it < 4; ++it) {
+    const int idx = it * kThreads + tid;
+    st16(lds + (idx >> 4) * PITCH + (idx & 15) * 8, t.v[it]);
+  }
+}
+
+// rows [0, 32) x 128 of a per-head query-row tensor -> LDS (256 threads, 2 loads each)
+__device__ __forceinline__ void rows32_to_lds(bf16* lds, const bf16* base, int64_t row_stride,
+                                              int nvalid, int tid) {
+#pragma unroll
+  for (int it = 0; it < 2; ++it) {
+    const int idx = it * kThreads + tid;
+    const int row = idx >> 4, chunk = idx & 15;
+    u32x4 v = u32x4{0u, 0u, 0u, 0u};
+    if (row < nvalid) v = ld16(base + (int64_t)row * row_stride + chunk * 8);
+    st16(lds + row * PITCH + chunk * 8, v);
+  }
+}
+
+// Eight LDS rows (row index given per slot j) at column c0, transposed: out[e]
+// holds column c0 + e of the eight rows, slot j from row rows[j].
+__device__ __forceinline__ void lds_rows_transposed(const bf16* lds, const int rows[8], int c0,
+                                                    bf16x8 out[8]) {
+  u32x4 in[8], tr[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) in[j] = ld16(lds + rows[j] * PITCH + c0);
+  transpose8x8(in, tr);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) out[e] = as_bf16x8(tr[e]);
+}
+
+// the row of slot j for lane group g: 4g + (j & 3) + 16 (j >> 2)
+__device__ __forceinline__ void slot_rows(int g, int base, int rows[8]) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) rows[j] = base + 4 * g + (j & 3) + 16 * (j >> 2);
+}
+
+__device__ __forceinline__ bf16x8 pack8(const float* x) {
+  u32x4 r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) r[i] = pack_bf2(x[2 * i], x[2 * i + 1]);
+  return as_bf16x8(r);
+}
+
+// Load a wave's 32 query rows x 128 as B operands of S^T = K Q^T:
+// reg[qb][ks] = row (16 qb + (lane & 15)), columns 32 ks + 8 (lane >> 4) .. +7.
+__device__ __forceinline__ void load_rows_b(bf16x8 reg[2][4], const bf16* base, int64_t row_stride,
+                                            int nvalid, int lane) {
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) {
+    const int row = 16 * qb + (lane & 15);
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      u32x4 v = u32x4{0u, 0u, 0u, 0u};
+      if (row < nvalid) v = ld16(base + (int64_t)row * row_stride + 32 * ks + 8 * (lane >> 4));
+      reg[qb][ks] = as_bf16x8(v);
+    }
+  }
+}
+
+// S^T tile (64 keys x 32 rows) = K_lds Q^T: s[kb][qb] lane holds keys
+// 16 kb + 4 (lane >> 4) + i, row 16 qb + (lane & 15).
+__device__ __forceinline__ void tile_scores(f32x4 s[4][2], const bf16* sk, const bf16x8 qreg[2][4],
+                                            int lane) {
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb) {
+    s[kb][0] = f32x4{0.f, 0.f, 0.f, 0.f};
+    s[kb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const bf16x8 a = as_bf16x8(ld16(sk + (16 * kb + (lane & 15)) * PITCH + 32 * ks + 8 * (lane >> 4)));
+      s[kb][0] = mfma16(a, qreg[0][ks], s[kb][0]);
+      s[kb][1] = mfma16(a, qreg[1][ks], s[kb][1]);
+    }
+  }
+}
+
+// Work-groups are dispatched round-robin over the 8 XCDs (linear id b runs on
+// XCD b % 8), each with its own L2.  The grid is one-dimensional over
+// (head chunk, work item) with the work items of one head chunk contiguous;
+// within every full window of 64 ids, XCD c receives the 8 consecutive tasks
+// 8c .. 8c + 7, so neighbours in the cost-sorted work list -- which read the
+// same key or query rows -- share an L2.  A final partial window keeps the
+// identity map.  Returns the work item; `y` receives the head chunk.
+__device__ __forceinline__ int task_of(int n_items, int& y) {
+  const int b = (int)blockIdx.x;
+  const int total = (int)gridDim.x;
+  const int base = b & ~63;
+  int t = b;
+  if (base + 64 <= total) {
+    const int r = b & 63;
+    t = base + ((r & 7) << 3) + (r >> 3);
+  }
+  y = t / n_items;
+  return t - y * n_items;
+}
+
+
+// ---------------------------------------------------------------------------
+// 256-byte-row LDS tiles (buffer DMA + transposed reads)
+// ---------------------------------------------------------------------------
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kTile32 = 32 * D;              // elements of one 32-row tile (256-byte rows)
+constexpr int kStage32 = 2 * kTile32 + 128;  // Q tile + dO tile + 32 (lse2, delta) pairs
+
+__device__ __forceinline__ u32x2 tr_read(const bf16* p) {
+  const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)p);
+  u32x2 r;
+  __builtin_memcpy(&r, &v, 8);
+  return r;
+}
+
+struct Cursor {
+  int vi;  // visit index; == nvisit at the end
+  int r0;  // first row of the block
+};
+
+
+constexpr int kKV64 = BK * D;  // elements of one 64-key tile
+
+struct TileCursor {
+  int sp;   // span index; == nspan at the end
+  int kt0;  // first run-local key of the tile
+};
+
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+inline int heads_per_block(int group) {
+  if (group % 4 == 0) return 4;
+  if (group % 2 == 0) return 2;
+  return 1;
+}
+
+// keys per dK/dV work-group: 48 for the one-wave-per-head kernel (its 192
+// dK/dV accumulators and 48 S/dP values fill the 256 AGPRs), else 64
+inline int kv_block_keys(int group) { return group % 4 == 0 ? 48 : BK; }
+
+// launchers (one per kernel family); each returns a TS_* status
+int launch_fwd(const ts_attn_problem& P, ts_attn_rows q, ts_attn_rows out, float* lse, int64_t lse_ld,
+               hipStream_t s);
+int launch_delta(const ts_attn_problem& P, ts_attn_rows out, ts_attn_rows dout, const float* lse,
+                 float* rowstats, int64_t lse_ld, hipStream_t s);
+int launch_dq(const ts_attn_problem& P, ts_attn_rows q, ts_attn_rows dout, const float* rowstats,
+              int64_t lse_ld, ts_attn_rows dq, hipStream_t s);
+int launch_dkdv(const ts_attn_problem& P, ts_attn_rows q, ts_attn_rows dout, const float* rowstats,
+                int64_t lse_ld, hipStream_t s);
+
+}  // namespace attn
+}  // namespace ts
