@@ -230,66 +230,19 @@ __global__ __launch_bounds__(kThreads, 1) void dq_wave_kernel(ts_attn_problem P,
     acc[mb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
-  // per-lane LDS offsets (elements): row reads and transpose reads as in dK/dV
   int ro[4], to[8];
-#pragma unroll
-  for (int ks = 0; ks < 4; ++ks) ro[ks] = j16 * D + (((4 * ks + g4) ^ j16) << 3);
-#pragma unroll
-  for (int mb = 0; mb < 8; ++mb) {
-    const int r = 4 * g4 + (j16 >> 2);
-    const int col = 16 * mb + 4 * (j16 & 3);
-    to[mb] = r * D + ((((col >> 3) ^ r) & 15) << 3) + (col & 7);
-  }
-  // DMA: this wave issues instructions t = wave + 4 u (rows 4 t .. 4 t + 3) of
-  // each tile; lane (g4, j16) fills row 4 t + g4, slot j16 with logical chunk
-  // j16 ^ (4 wave + g4)
-  const int dma_row = 4 * wave + g4;
-  const int dma_chunk = (j16 ^ (4 * wave + g4)) << 3;
-
-  // next visible tile after `tc` in key order (sp == nspan: none left; once a
-  // tile starts past the block's last visible key, so do all later ones)
-  auto advance = [&](TileCursor tc) -> TileCursor {
-    tc.kt0 += BK;
-    while (tc.sp < seg.nspan) {
-      const ts_attn_ref ref = load_uniform(P.seg_spans, seg.span0 + tc.sp);
-      const ts_attn_run run = load_uniform(P.runs, ref.index);
-      if (tc.kt0 >= run.len) {
-        ++tc.sp;
-        tc.kt0 = 0;
-        continue;
-      }
-      if (ref.kpos + tc.kt0 > off + last) tc.sp = seg.nspan;
-      break;
-    }
-    return tc;
-  };
-  auto issue = [&](TileCursor tc, bf16* sk, bf16* sv) {
-    const ts_attn_ref ref = load_uniform(P.seg_spans, seg.span0 + tc.sp);
-    const ts_attn_run run = load_uniform(P.runs, ref.index);
-    const int nvalid = min(BK, run.len - tc.kt0);
-    const bf16* kb = (const bf16*)run.k + (int64_t)tc.kt0 * run.k_row_stride + (int64_t)hk * run.k_head_stride;
-    const bf16* vb = (const bf16*)run.v + (int64_t)tc.kt0 * run.v_row_stride + (int64_t)hk * run.v_head_stride;
-    const rsrc_t rk = make_rsrc(kb, (uint32_t)(nvalid * run.k_row_stride * 2));
-    const rsrc_t rv = make_rsrc(vb, (uint32_t)(nvalid * run.v_row_stride * 2));
-    const int ko = (int)((dma_row * run.k_row_stride + dma_chunk) * 2);
-    const int vo = (int)((dma_row * run.v_row_stride + dma_chunk) * 2);
-    const int kstep = (int)(16 * run.k_row_stride * 2), vstep = (int)(16 * run.v_row_stride * 2);
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      buffer_dma16(rk, sk + (wave + 4 * u) * 512, ko + u * kstep);
-      buffer_dma16(rv, sv + (wave + 4 * u) * 512, vo + u * vstep);
-    }
-  };
+  swizzled_offsets(lane, ro, to);
 
   auto step = [&](auto bsel, TileCursor& cur) {
     const int kpos = load_uniform(P.seg_spans, seg.span0 + cur.sp).kpos;
     const int kt0 = cur.kt0;
-    const TileCursor nxt = advance(cur);
+    const TileCursor nxt = next_kv_tile(P, seg, last, cur);
     __builtin_amdgcn_s_waitcnt(0);  // this wave's part of the tile has landed
     __syncthreads();                // every part has, and the other stage is free
     const bf16* tk = bsel.value == 0 ? s_k0 : s_k1;
     const bf16* tv = bsel.value == 0 ? s_v0 : s_v1;
-    if (nxt.sp < seg.nspan) issue(nxt, bsel.value == 0 ? s_k1 : s_k0, bsel.value == 0 ? s_v1 : s_v0);
+    if (nxt.sp < seg.nspan)
+      issue_kv_tile(P, seg, hk, wave, lane, nxt, bsel.value == 0 ? s_k1 : s_k0, bsel.value == 0 ? s_v1 : s_v0);
 
     const bool diag = kpos + kt0 + BK - 1 > off + q0;
     // two halves of 32 keys: S^T = K Q^T, dP^T = V dO^T for keys 32 ss .. 32 ss + 31
@@ -362,8 +315,8 @@ __global__ __launch_bounds__(kThreads, 1) void dq_wave_kernel(ts_attn_problem P,
     cur = nxt;
   };
 
-  TileCursor cur = advance(TileCursor{0, -BK});
-  if (cur.sp < seg.nspan) issue(cur, s_k0, s_v0);
+  TileCursor cur = next_kv_tile(P, seg, last, TileCursor{0, -BK});
+  if (cur.sp < seg.nspan) issue_kv_tile(P, seg, hk, wave, lane, cur, s_k0, s_v0);
   while (cur.sp < seg.nspan) {
     step(std::integral_constant<int, 0>{}, cur);
     if (cur.sp >= seg.nspan) break;

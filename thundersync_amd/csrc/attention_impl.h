@@ -172,6 +172,71 @@ struct TileCursor {
   int kt0;  // first run-local key of the tile
 };
 
+// Next 64-key tile after `tc` in a segment's key order that some row up to
+// `last` (segment-local) can see; sp == nspan when none is left.  Spans are in
+// key order, so once a tile starts past the last visible key so do all later
+// ones.  Start from TileCursor{0, -BK}.
+__device__ __forceinline__ TileCursor next_kv_tile(const ts_attn_problem& P, const ts_attn_segment& seg,
+                                                   int last, TileCursor tc) {
+  const int off = seg.kv_len - seg.q_len;
+  tc.kt0 += BK;
+  while (tc.sp < seg.nspan) {
+    const ts_attn_ref ref = load_uniform(P.seg_spans, seg.span0 + tc.sp);
+    const ts_attn_run run = load_uniform(P.runs, ref.index);
+    if (tc.kt0 >= run.len) {
+      ++tc.sp;
+      tc.kt0 = 0;
+      continue;
+    }
+    if (ref.kpos + tc.kt0 > off + last) tc.sp = seg.nspan;
+    break;
+  }
+  return tc;
+}
+
+// DMA of one 64-key K/V tile of KV head hk into swizzled LDS tiles (256-byte
+// rows, chunk c of row r at slot c ^ (r & 15)).  The four waves of a
+// work-group each issue instructions t = wave + 4 u (rows 4 t .. 4 t + 3);
+// lane (g4, j16) fills row 4 t + g4, slot j16 with logical chunk
+// j16 ^ (4 wave + g4).  Rows past the run arrive as zeros.
+__device__ __forceinline__ void issue_kv_tile(const ts_attn_problem& P, const ts_attn_segment& seg, int hk,
+                                              int wave, int lane, TileCursor tc, bf16* sk, bf16* sv) {
+  const int g4 = lane >> 4, j16 = lane & 15;
+  const int dma_row = 4 * wave + g4;
+  const int dma_chunk = (j16 ^ (4 * wave + g4)) << 3;
+  const ts_attn_ref ref = load_uniform(P.seg_spans, seg.span0 + tc.sp);
+  const ts_attn_run run = load_uniform(P.runs, ref.index);
+  const int nvalid = min(BK, run.len - tc.kt0);
+  const bf16* kb = (const bf16*)run.k + (int64_t)tc.kt0 * run.k_row_stride + (int64_t)hk * run.k_head_stride;
+  const bf16* vb = (const bf16*)run.v + (int64_t)tc.kt0 * run.v_row_stride + (int64_t)hk * run.v_head_stride;
+  const rsrc_t rk = make_rsrc(kb, (uint32_t)(nvalid * run.k_row_stride * 2));
+  const rsrc_t rv = make_rsrc(vb, (uint32_t)(nvalid * run.v_row_stride * 2));
+  const int ko = (int)((dma_row * run.k_row_stride + dma_chunk) * 2);
+  const int vo = (int)((dma_row * run.v_row_stride + dma_chunk) * 2);
+  const int kstep = (int)(16 * run.k_row_stride * 2), vstep = (int)(16 * run.v_row_stride * 2);
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    buffer_dma16(rk, sk + (wave + 4 * u) * 512, ko + u * kstep);
+    buffer_dma16(rv, sv + (wave + 4 * u) * 512, vo + u * vstep);
+  }
+}
+
+// per-lane LDS offsets (elements) into a 256-byte-row swizzled tile:
+// ro[ks]: row j16, logical chunk 4 ks + g4 (A-operand row reads of 16 rows);
+// to[mb]: row 4 g4 + j16 / 4, columns 16 mb + 4 (j16 & 3) .. + 3 (the
+// addresses of a ds_read_b64_tr_b16 that yields X[4 g4 + t][16 mb + j16])
+__device__ __forceinline__ void swizzled_offsets(int lane, int ro[4], int to[8]) {
+  const int g4 = lane >> 4, j16 = lane & 15;
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) ro[ks] = j16 * D + (((4 * ks + g4) ^ j16) << 3);
+#pragma unroll
+  for (int mb = 0; mb < 8; ++mb) {
+    const int r = 4 * g4 + (j16 >> 2);
+    const int col = 16 * mb + 4 * (j16 & 3);
+    to[mb] = r * D + ((((col >> 3) ^ r) & 15) << 3) + (col & 7);
+  }
+}
+
 
 // ---------------------------------------------------------------------------
 // host side
