@@ -145,6 +145,13 @@ typedef struct ts_attn_problem {
   int32_t q_block;  /* rows per q_work item: 32 * 4 / ts_attn_heads_per_block */
   int32_t kv_block; /* keys per kv_work item: ts_attn_kv_block(hq / hkv) */
   int64_t q_rows;   /* rows of Q/O/dO/dQ */
+  /* Launch order.  The work lists are sorted longest first; their first
+   * n_q_long / n_kv_long items run first, item by item across all heads (so
+   * no head's long item is left for the end of the launch), the rest head by
+   * head (all XCDs then stream the same head's rows through the shared
+   * last-level cache).  0 <= n_*_long <= n_*_work. */
+  int32_t n_q_long;
+  int32_t n_kv_long;
 } ts_attn_problem;
 
 /* Query heads one forward/dQ work-group processes for a GQA group size

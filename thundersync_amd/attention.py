@@ -168,9 +168,17 @@ class AttnLayout:
         kv_items.sort()
         q_work = np.array([(s, q0) for _, s, q0 in q_items], np.int32).reshape(-1, 2)
         kv_work = np.array([(r, k0) for _, r, k0 in kv_items], np.int32).reshape(-1, 2)
+        group = self.hq // self.hkv
+        # rows the forward / dQ work-groups re-read: K and V of every run; the
+        # dK/dV work-groups: Q and dO of every row (bf16, all heads)
+        kv_bytes = sum(run.length for run in self.runs) * self.hkv * HEAD_DIM * 2 * 2
+        q_bytes = self.q_rows * self.hq * HEAD_DIM * 2 * 2
+        q_long = _long_items([-c for c, _, _ in q_items], self.hkv * (group // heads_per_block(group)), kv_bytes)
+        kv_long = _long_items([-c for c, _, _ in kv_items], self.hkv, q_bytes)
         seg_spans = np.array(spans, REF_DTYPE) if spans else np.zeros(0, REF_DTYPE)
         run_visits = np.array(visit_rows, REF_DTYPE) if visit_rows else np.zeros(0, REF_DTYPE)
-        return segs, seg_spans, run_visits, q_work, kv_work, visit0, [len(v) for v in visits_of]
+        return (segs, seg_spans, run_visits, q_work, kv_work, visit0, [len(v) for v in visits_of],
+                q_long, kv_long)
 
     def device_tables(self, device: torch.device):
         """Upload the layout's integer tables once per device (pinned, non-blocking)."""
@@ -181,7 +189,7 @@ class AttnLayout:
         with self._lock:
             hit = self._tables.get(key)
             if hit is None:
-                segs, spans, visits, q_work, kv_work, visit0, nvisit = self._host_tables()
+                segs, spans, visits, q_work, kv_work, visit0, nvisit, q_long, kv_long = self._host_tables()
                 parts = [segs.view(np.uint8), spans.view(np.uint8), visits.view(np.uint8),
                          q_work.view(np.uint8).reshape(-1), kv_work.view(np.uint8).reshape(-1)]
                 offsets, total = [], 0
@@ -206,6 +214,8 @@ class AttnLayout:
                     "n_kv_work": int(kv_work.shape[0]),
                     "visit0": visit0,
                     "nvisit": nvisit,
+                    "n_q_long": q_long,
+                    "n_kv_long": kv_long,
                 }
                 self._tables[key] = hit
         return hit
@@ -216,6 +226,7 @@ class AttnLayout:
             t["segs"], t["seg_spans"], runs_ptr, t["run_visits"], t["q_work"], t["kv_work"],
             t["n_q_work"], t["n_kv_work"], len(self.seg_q), len(self.runs), self.hq, self.hkv,
             HEAD_DIM, float(scale), q_block_rows(self.hq, self.hkv), kv_block_keys(self.hq, self.hkv), self.q_rows,
+            t["n_q_long"], t["n_kv_long"],
         )
 
     # -- reference diagnostics ---------------------------------------------
@@ -225,6 +236,36 @@ class AttnLayout:
         for (_, t), s in zip(self.seg_q, self.seg_kv):
             total += t * (s - t) + t * (t + 1) // 2
         return total
+
+
+# MI355X: work-group slots of one launch (256 CUs, one attention work-group
+# each) and the last-level cache shared by the 8 XCDs
+LAUNCH_SLOTS = 256
+SHARED_CACHE_BYTES = 256 << 20
+
+
+def _long_items(costs: Sequence[int], heads: int, reread_bytes: int, slots: int = LAUNCH_SLOTS) -> int:
+    """How many of the (descending) ``costs`` run item-major at the head of the
+    launch (ts_attn_problem.n_*_long).
+
+    When the rows the work-groups re-read (``reread_bytes``, all heads) fit in
+    half the shared last-level cache, every item does: each XCD then serves
+    fixed heads and keeps their rows in its L2 while the shared cache holds
+    the rest.  Otherwise only the items long enough to stretch the end of the
+    launch when started late -- a quarter or more of a slot's average share
+    of the whole launch (``heads`` copies of every item) -- and the rest run
+    head by head, all XCDs streaming one head's rows through the shared cache.
+    """
+    if reread_bytes <= SHARED_CACHE_BYTES // 2:
+        return len(costs)
+    total = sum(costs) * heads
+    if not costs or total == 0:
+        return 0
+    threshold = 0.25 * total / slots
+    n = 0
+    while n < len(costs) and costs[n] >= threshold:
+        n += 1
+    return n
 
 
 def _check_rows_tensor(t: torch.Tensor, name: str, heads: int, max_row_stride: int = 1 << 24) -> None:

@@ -50,6 +50,8 @@ int validate(const ts_attn_problem* p, const char* what) {
                p->kv_block, kv_block_keys(p->hq / p->hkv));
   TS_CHECK_ARG(p->n_q_work >= 0 && p->n_kv_work >= 0 && p->n_segs >= 0 && p->n_runs >= 0,
                "%s: negative table size", what);
+  TS_CHECK_ARG(p->n_q_long >= 0 && p->n_q_long <= p->n_q_work && p->n_kv_long >= 0 &&
+               p->n_kv_long <= p->n_kv_work, "%s: long-item counts outside the work lists", what);
   TS_CHECK_ARG(p->n_q_work == 0 || (p->q_work && p->segs && p->seg_spans && p->runs),
                "%s: null table", what);
   TS_CHECK_ARG((int64_t)p->n_q_work * (p->hq / gc) < (1ll << 31) && (int64_t)p->n_kv_work * p->hkv < (1ll << 31),

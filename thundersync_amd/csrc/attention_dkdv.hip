@@ -16,7 +16,7 @@ __global__ __launch_bounds__(kThreads, 2) void dkdv_kernel(ts_attn_problem P, ts
   __shared__ float s_dlt[32];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   int hk;
-  const int item = task_of(P.n_kv_work, hk);
+  const int item = task_of(P.n_kv_work, P.n_kv_long, hk);
   const int run_id = uniform_table(P.kv_work)[2 * item];
   const int k0 = uniform_table(P.kv_work)[2 * item + 1];
   const int group = P.hq / P.hkv;
@@ -185,7 +185,7 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_wave_kernel(ts_attn_problem 
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g4 = lane >> 4, j16 = lane & 15;
   int hk;
-  const int item = task_of(P.n_kv_work, hk);
+  const int item = task_of(P.n_kv_work, P.n_kv_long, hk);
   const int run_id = uniform_table(P.kv_work)[2 * item];
   const int k0 = uniform_table(P.kv_work)[2 * item + 1];
   const int group = P.hq / P.hkv;

@@ -48,7 +48,7 @@ __global__ __launch_bounds__(kThreads, 1) void dq_kernel(ts_attn_problem P, ts_a
   __shared__ __attribute__((aligned(16))) bf16 sv[BK * PITCH];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   int yb;
-  const int item = task_of(P.n_q_work, yb);
+  const int item = task_of(P.n_q_work, P.n_q_long, yb);
   const int seg_id = uniform_table(P.q_work)[2 * item];
   const int q0 = uniform_table(P.q_work)[2 * item + 1];
   const int group = P.hq / P.hkv;
@@ -190,7 +190,7 @@ __global__ __launch_bounds__(kThreads, 1) void dq_wave_kernel(ts_attn_problem P,
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g4 = lane >> 4, j16 = lane & 15;
   int yb;
-  const int item = task_of(P.n_q_work, yb);
+  const int item = task_of(P.n_q_work, P.n_q_long, yb);
   const int seg_id = uniform_table(P.q_work)[2 * item];
   const int q0 = uniform_table(P.q_work)[2 * item + 1];
   const int group = P.hq / P.hkv;

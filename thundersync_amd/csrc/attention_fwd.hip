@@ -15,7 +15,7 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_kernel(ts_attn_problem P, ts_
   __shared__ __attribute__((aligned(16))) bf16 sv[BK * PITCH];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   int yb;
-  const int item = task_of(P.n_q_work, yb);
+  const int item = task_of(P.n_q_work, P.n_q_long, yb);
   const int seg_id = uniform_table(P.q_work)[2 * item];
   const int q0 = uniform_table(P.q_work)[2 * item + 1];
   const int group = P.hq / P.hkv;
@@ -180,7 +180,7 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_wave_kernel(ts_attn_problem P
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g4 = lane >> 4, j16 = lane & 15;
   int yb;
-  const int item = task_of(P.n_q_work, yb);
+  const int item = task_of(P.n_q_work, P.n_q_long, yb);
   const int seg_id = uniform_table(P.q_work)[2 * item];
   const int q0 = uniform_table(P.q_work)[2 * item + 1];
   const int group = P.hq / P.hkv;

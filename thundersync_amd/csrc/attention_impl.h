@@ -123,24 +123,33 @@ __device__ __forceinline__ void tile_scores(f32x4 s[4][2], const bf16* sk, const
   }
 }
 
-// Work-groups are dispatched round-robin over the 8 XCDs (linear id b runs on
-// XCD b % 8), each with its own L2.  The grid is one-dimensional over
-// (head chunk, work item) with the work items of one head chunk contiguous;
-// within every full window of 64 ids, XCD c receives the 8 consecutive tasks
-// 8c .. 8c + 7, so neighbours in the cost-sorted work list -- which read the
-// same key or query rows -- share an L2.  A final partial window keeps the
-// identity map.  Returns the work item; `y` receives the head chunk.
-__device__ __forceinline__ int task_of(int n_items, int& y) {
-  const int b = (int)blockIdx.x;
-  const int total = (int)gridDim.x;
-  const int base = b & ~63;
-  int t = b;
-  if (base + 64 <= total) {
-    const int r = b & 63;
-    t = base + ((r & 7) << 3) + (r >> 3);
+// The grid is one-dimensional over (work item, head chunk) pairs.  Work lists
+// are sorted longest first.  The first n_long items run item-major (every
+// head's longest items start before any short ones, so none is left for the
+// tail of the launch); the remaining items run head-major, all XCDs streaming
+// the same head's rows through the shared last-level cache.  Work-groups are
+// dispatched round-robin over the 8 XCDs (linear id b runs on XCD b % 8);
+// within every full window of 64 head-major ids XCD c receives 8 consecutive
+// items of one head, neighbours in the cost-sorted list that read the same
+// rows and share its L2.  Returns the work item; `y` receives the head chunk.
+__device__ __forceinline__ int task_of(int n_items, int n_long, int& y) {
+  const int t = (int)blockIdx.x;
+  const int gy = (int)gridDim.x / n_items;
+  if (t < n_long * gy) {
+    const int item = t / gy;
+    y = t - item * gy;
+    return item;
   }
-  y = t / n_items;
-  return t - y * n_items;
+  const int n_rest = n_items - n_long;
+  const int b = t - n_long * gy;
+  const int base = b & ~63;
+  int u = b;
+  if (base + 64 <= n_rest * gy) {
+    const int r = b & 63;
+    u = base + ((r & 7) << 3) + (r >> 3);
+  }
+  y = u / n_rest;
+  return n_long + (u - y * n_rest);
 }
 
 
