@@ -86,7 +86,22 @@ def timed(step, steps, warmup, kernels):
     return (t1 - t0) * 1e3 / steps, per
 
 
-def roofline_of(per, work_per_step, unit, peak):
+def measured_traffic(workload, kernel):
+    """HBM bytes per launch of `kernel` in `workload` from profiles/traffic.json:
+    rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs of this script with
+    ``--only <workload>``, each scaled by what the counter reads for a plain
+    device copy of known size.  None when the table has no entry."""
+    path = ROOT / "profiles" / "traffic.json"
+    if not path.exists():
+        return None, None
+    table = json.loads(path.read_text())
+    entry = table.get("workloads", {}).get(workload, {}).get(kernel)
+    if entry is None:
+        return None, None
+    return entry["traffic_bytes"], table.get("measured_at_commit")
+
+
+def roofline_of(per, work_per_step, unit, peak, workload):
     """Roofline object for the kernel with the largest device time per step.
 
     ``work_per_step`` is the kernel's algorithmic work over one step; a kernel
@@ -97,6 +112,7 @@ def roofline_of(per, work_per_step, unit, peak):
     avg_ms, launches = per[name]
     per_launch = work_per_step[name] / launches
     achieved = per_launch / (avg_ms * 1e-3) / (1e12 if unit == "TFLOP/s" else 1e9)
+    traffic, commit = measured_traffic(workload, name)
     return {
         "kernel": name,
         "bound": "mfma" if unit == "TFLOP/s" else "hbm",
@@ -104,7 +120,8 @@ def roofline_of(per, work_per_step, unit, peak):
         "peak": peak,
         "unit": unit,
         "frac": round(achieved / peak, 4),
-        "traffic": None,
+        "traffic": traffic,
+        "traffic_source": f"profiles/traffic.json, measured at commit {commit}" if traffic is not None else None,
         "avg_launch_ms": round(avg_ms, 4),
         "launches_per_step": launches,
         "work_per_launch": per_launch,
@@ -165,7 +182,7 @@ def bench_attention(args, device):
         "value": round(flop / (ms * 1e-3) / 1e12, 2),
         "unit": "TFLOP/s",
         "ms_per_step": round(ms, 4),
-        "roofline": roofline_of(per, work, "TFLOP/s", PEAK_BF16_TFLOPS),
+        "roofline": roofline_of(per, work, "TFLOP/s", PEAK_BF16_TFLOPS, "attention"),
         "kernels": {k: {"avg_ms": round(a, 4), "launches_per_step": n} for k, (a, n) in per.items()},
         "config": {
             "workload": "C2 forest attention fwd+bwd: 2048-token shared prompt + 8 completions "
@@ -300,7 +317,7 @@ def bench_chunked(args, device):
         "value": round(flop / (ms * 1e-3) / 1e12, 2),
         "unit": "TFLOP/s",
         "ms_per_step": round(ms, 4),
-        "roofline": roofline_of(per, work, "TFLOP/s", PEAK_BF16_TFLOPS),
+        "roofline": roofline_of(per, work, "TFLOP/s", PEAK_BF16_TFLOPS, "chunked"),
         "kernels": {k: {"avg_ms": round(a, 4), "launches_per_step": n} for k, (a, n) in per.items()},
         "config": {
             "workload": "C4 chunked retained-KV attention fwd+bwd: 4 groups x (1024-token prompt + 4 "
@@ -406,7 +423,7 @@ def bench_logprob(args, device):
         "tflops": round(flop / (ms * 1e-3) / 1e12, 2),
         "mfma_frac": round(flop / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
         "ms_per_step": round(ms, 4),
-        "roofline": roofline_of({k: x for k, x in per.items() if work[k]}, work, "TFLOP/s", PEAK_BF16_TFLOPS),
+        "roofline": roofline_of({k: x for k, x in per.items() if work[k]}, work, "TFLOP/s", PEAK_BF16_TFLOPS, "logprob"),
         "kernels": {k: {"avg_ms": round(x, 4), "launches_per_step": m} for k, (x, m) in per.items()},
         "config": {
             "workload": "C3 fused logprob+entropy fwd + grad wrt hidden: hidden [16384,4096] bf16, "
@@ -477,7 +494,7 @@ def bench_rmsnorm(args, device):
         "value": round((fwd_bytes + bwd_bytes) / (ms * 1e-3) / 1e9, 1),
         "unit": "GB/s",
         "ms_per_step": round(ms, 4),
-        "roofline": roofline_of({k: x for k, x in per.items() if work[k]}, work, "GB/s", PEAK_HBM_GBS),
+        "roofline": roofline_of({k: x for k, x in per.items() if work[k]}, work, "GB/s", PEAK_HBM_GBS, "rmsnorm"),
         "kernels": {k: {"avg_ms": round(x, 4), "launches_per_step": m} for k, (x, m) in per.items()},
         "config": {"workload": "RMSNorm fwd+bwd [16384, 4096] bf16, FP32 VJP with dW", "seed": args.seed},
     }
