@@ -160,6 +160,31 @@ __device__ __forceinline__ void buffer_dma16(rsrc_t r, void* lds, int voffset) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)lds, 16, voffset, 0, 0, 0);
 }
 
+// A raw buffer descriptor as four SGPR words (base[31:0]; base[47:32] with
+// stride 0; num_records; word 3 as above).  `base` and `bytes` must be
+// wave-uniform.
+__device__ __forceinline__ u32x4 raw_descriptor(const void* base, uint32_t bytes) {
+  const uint64_t a = (uint64_t)base;
+  const uint32_t w0 = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)a);
+  const uint32_t w1 = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(a >> 32)) & 0xffffu;
+  const uint32_t w2 = (uint32_t)__builtin_amdgcn_readfirstlane(bytes);
+  return u32x4{w0, w1, w2, (uint32_t)kRawBufferWord3};
+}
+
+// 16 bytes per lane from the descriptor's base + voffset into LDS (lane i
+// writes lds + 16 i), issued so that the compiler does not track it: no wait
+// is inserted for it anywhere, and the caller accounts for it with explicit
+// vmcnt waits (it counts as one vector-memory instruction of the issuing
+// wave) and a barrier before other waves read the data.  `lds` must be
+// wave-uniform; M0 carries it.
+__device__ __forceinline__ void buffer_dma16_untracked(u32x4 desc, void* lds, int voffset) {
+  const uint32_t m0 = (uint32_t)(uintptr_t)(lds_void*)lds;
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+               :
+               : "s"(m0), "v"(voffset), "s"(desc)
+               : "memory", "m0");
+}
+
 // ---------------------------------------------------------------------------
 // wave reductions over lanes that differ in the given xor masks
 // ---------------------------------------------------------------------------

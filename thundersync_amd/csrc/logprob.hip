@@ -18,9 +18,12 @@
 //             stores a [rows, V] bf16 block; a second GEMM multiplies it by
 //             W (given as W^T so both operands are K-contiguous) into dh.
 //
-// GEMM core: 256 x 128 work-group tile, 4 waves of 128 x 64, K staged 64 at a
-// time through double-buffered LDS (pitch 72 bf16: conflict-free 16-byte
-// fragment reads), v_mfma_f32_32x32x16_bf16.
+// GEMM core: 256 x 256 work-group tile, 4 waves of 128 x 128 (accumulators in
+// the accumulation registers), v_mfma_f32_32x32x16_bf16.  K streams 32 at a
+// time through a 4-stage LDS ring filled by buffer_load ... lds (no register
+// staging), three stages ahead of the MFMAs, one work-group barrier per stage.
+// Rows past an operand's valid rows and 8-element K chunks past K arrive as
+// zeros (buffer range checking), so ragged edges need no masking in the loop.
 #include "common.h"
 #include "timing.h"
 #include "../../include/thundersync_hip.h"
@@ -29,104 +32,176 @@ namespace ts {
 namespace lp {
 
 constexpr int kThreads = 256;
-constexpr int BM = 256;       // A rows per work-group
-constexpr int BN = 128;       // B rows per work-group
-constexpr int BK = 64;        // K per LDS stage
-constexpr int PITCH = BK + 8; // LDS row pitch (elements)
-constexpr int kStage = (BM + BN) * PITCH;  // elements per stage
+constexpr int TM = 256;  // A rows (vocab rows, or hidden dims) per work-group
+constexpr int TN = 256;  // B rows (tokens) per work-group
+constexpr int TK = 32;   // K per LDS stage
+constexpr int kStageElems = (TM + TN) * TK;  // 32 KB: A [TM][TK], then B [TN][TK]
+constexpr int BM = TM;   // vocab rows per forward partial
 constexpr float kLog2e = 1.4426950408889634f;
 
 __device__ __forceinline__ float neg_inf() { return -__builtin_huge_valf(); }
 __device__ __forceinline__ u32x4 ld16(const bf16* p) { return *reinterpret_cast<const u32x4*>(p); }
 
 // Work-groups are dispatched round-robin over the 8 XCDs; renumber them so each
-// XCD runs a contiguous range of logical tiles (which share operand panels in
-// that XCD's L2).
+// XCD runs a contiguous range of logical tiles.
 __device__ __forceinline__ int xcd_logical(int bid, int total) {
   const int per = total / 8, rem = total % 8;
   const int xcd = bid % 8, local = bid / 8;
   return xcd < rem ? xcd * (per + 1) + local : rem * (per + 1) + (xcd - rem) * per + local;
 }
 
-struct Frag {
-  u32x4 a[8];  // A tile: 256 rows x 64 k -> 2048 16-byte chunks, 8 per thread
-  u32x4 b[4];  // B tile: 128 rows x 64 k -> 1024 chunks, 4 per thread
+// Logical tile -> (A tile, B tile) in groups of 4 A tiles: consecutive ids walk
+// the B tiles of a group with its 4 A tiles innermost, so the ~32 work-groups
+// an XCD runs at once cover 4 A panels x ~8 B panels and share both in L2.
+__device__ __forceinline__ void grouped_tile(int id, int n_a, int n_b, int& ta, int& tb) {
+  constexpr int G = 4;
+  const int g = id / (G * n_b);
+  const int r = id - g * G * n_b;
+  const int ga = min(G, n_a - g * G);
+  tb = r / ga;
+  ta = g * G + (r - tb * ga);
+}
+
+// One operand's share of a stage: 256 rows x 64 bytes = 16 instructions of 16
+// rows each, issued by the 4 waves as t = wave + 4 u.  Lane i of an
+// instruction fills row 16 t + i / 4, slot i & 3 with the logical 16-byte
+// chunk c = (i & 3) ^ (i >> 4): row r's chunk c sits at slot c ^ ((r >> 2) & 3),
+// so the 16 rows of a fragment read at one chunk hit 16 distinct bank groups.
+struct Streamer {
+  const bf16* base;  // row 0, k 0
+  int64_t ld;
+  int rows;          // valid rows from base (>= 1)
+  int K;
+  int voff[4];       // byte offset of this lane's row and chunk within a stage, per u
+  int kchunk;        // this lane's chunk start within a stage (elements)
+  __device__ __forceinline__ void init(const bf16* b, int64_t ld_, int rows_, int K_, int wave, int lane) {
+    base = b;
+    ld = ld_;
+    rows = rows_;
+    K = K_;
+    kchunk = 8 * ((lane & 3) ^ (lane >> 4));
+#pragma unroll
+    for (int u = 0; u < 4; ++u) voff[u] = (int)(((16 * (wave + 4 * u) + (lane >> 2)) * ld + kchunk) * 2);
+  }
+  // K columns [k0, k0 + TK) into dst (wave-uniform)
+  __device__ __forceinline__ void issue(bf16* dst, int k0, int wave) const {
+    const u32x4 r = raw_descriptor(base + k0, (uint32_t)(((int64_t)(rows - 1) * ld + TK) * 2));
+    const bool in_k = k0 + kchunk < K;  // a chunk past K reads nothing: zeros
+#pragma unroll
+    for (int u = 0; u < 4; ++u) buffer_dma16_untracked(r, dst + (wave + 4 * u) * 512, in_k ? voff[u] : 0x7ffffff0);
+  }
 };
 
-__device__ __forceinline__ void load_stage(Frag& f, const bf16* A, int64_t lda, int a_rows,
-                                           const bf16* B, int64_t ldb, int b_rows, int k0, int K,
-                                           int tid) {
-#pragma unroll
-  for (int it = 0; it < 8; ++it) {
-    const int c = it * kThreads + tid;
-    const int row = c >> 3, kc = k0 + (c & 7) * 8;
-    f.a[it] = (row < a_rows && kc < K) ? ld16(A + (int64_t)row * lda + kc) : u32x4{0u, 0u, 0u, 0u};
-  }
-#pragma unroll
-  for (int it = 0; it < 4; ++it) {
-    const int c = it * kThreads + tid;
-    const int row = c >> 3, kc = k0 + (c & 7) * 8;
-    f.b[it] = (row < b_rows && kc < K) ? ld16(B + (int64_t)row * ldb + kc) : u32x4{0u, 0u, 0u, 0u};
-  }
-}
-
-__device__ __forceinline__ void store_stage(const Frag& f, bf16* lds, int tid) {
-  bf16* sa = lds;
-  bf16* sb = lds + BM * PITCH;
-#pragma unroll
-  for (int it = 0; it < 8; ++it) {
-    const int c = it * kThreads + tid;
-    *reinterpret_cast<u32x4*>(sa + (c >> 3) * PITCH + (c & 7) * 8) = f.a[it];
-  }
-#pragma unroll
-  for (int it = 0; it < 4; ++it) {
-    const int c = it * kThreads + tid;
-    *reinterpret_cast<u32x4*>(sb + (c >> 3) * PITCH + (c & 7) * 8) = f.b[it];
-  }
-}
-
-// acc[mi][ni]: 32x32 block (A rows 128 wm + 32 mi, B rows 64 wn + 32 ni).
-// Lane l holds B row (l & 31) + 32 ni + 64 wn and A rows
+// acc[mi][ni]: 32x32 block (A rows 128 wm + 32 mi, B rows 128 wn + 32 ni).
+// Lane l holds B row (l & 31) + 32 ni + 128 wn and A rows
 // 8 (i >> 2) + 4 (l >> 5) + (i & 3) + 32 mi + 128 wm, i = 0..15.
-__device__ __forceinline__ void gemm_tile(f32x16 acc[4][2], const bf16* A, int64_t lda, int a_rows,
-                                          const bf16* B, int64_t ldb, int b_rows, int K, bf16* lds) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+__device__ __forceinline__ int a_row(int mi, int i, int lane, int wm) {
+  return 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3) + 32 * mi + 128 * wm;
+}
+
+// the MFMAs of one stage: two k-steps of 16 (all fragment reads issued first)
+__device__ __forceinline__ void mma_stage(f32x16 acc[4][4], const bf16* st, const int fa[2], const int fb[2]) {
+  bf16x8 af[2][4], bfr[2][4];
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk) {
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) af[kk][mi] = as_bf16x8(ld16(st + fa[kk] + 32 * mi * TK));
+#pragma unroll
+    for (int ni = 0; ni < 4; ++ni) bfr[kk][ni] = as_bf16x8(ld16(st + fb[kk] + 32 * ni * TK));
+  }
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+      for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = mfma32(af[kk][mi], bfr[kk][ni], acc[mi][ni]);
+  // schedule: the 8 reads of k-step 0, then its 16 MFMAs with the 8 reads of
+  // k-step 1 interleaved (one read per two MFMAs), then k-step 1's MFMAs
+  __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);  // DS reads
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // MFMA
+    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+  }
+  __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
+}
+
+// wait until at most 8 * ahead of this wave's DMA instructions are in flight
+__device__ __forceinline__ void wait_dma(int ahead) {
+  if (ahead >= 2) __builtin_amdgcn_s_waitcnt(0x4F70);       // vmcnt(16)
+  else if (ahead == 1) __builtin_amdgcn_s_waitcnt(0x0F78);  // vmcnt(8)
+  else __builtin_amdgcn_s_waitcnt(0x0F70);                  // vmcnt(0)
+}
+
+// C tile = A[256 rows] . B[256 rows]^T over K (both K-contiguous), through the
+// LDS ring s0..s3 (distinct arrays, so the compiler sees that a refill and
+// the reads of another stage never alias).  The ring is free on return.
+__device__ __forceinline__ void gemm_tile(f32x16 acc[4][4], const bf16* A, int64_t lda, int a_rows,
+                                          const bf16* B, int64_t ldb, int b_rows, int K, bf16* s0,
+                                          bf16* s1, bf16* s2, bf16* s3) {
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave & 1, wn = wave >> 1;
 #pragma unroll
   for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
-    for (int ni = 0; ni < 2; ++ni)
+    for (int ni = 0; ni < 4; ++ni)
 #pragma unroll
       for (int i = 0; i < 16; ++i) acc[mi][ni][i] = 0.f;
-  const int nk = (K + BK - 1) / BK;
-  Frag f;
-  load_stage(f, A, lda, a_rows, B, ldb, b_rows, 0, K, tid);
-  store_stage(f, lds, tid);
-  __syncthreads();
-  for (int kt = 0; kt < nk; ++kt) {
-    const bool more = kt + 1 < nk;
-    if (more) load_stage(f, A, lda, a_rows, B, ldb, b_rows, (kt + 1) * BK, K, tid);
-    const bf16* sa = lds + (kt & 1) * kStage;
-    const bf16* sb = sa + BM * PITCH;
+  Streamer sa, sb;
+  sa.init(A, lda, a_rows, K, wave, lane);
+  sb.init(B, ldb, b_rows, K, wave, lane);
+  // fragment offsets (elements) within a stage: row 128 w + (l & 31) of the A
+  // (B) half, logical chunk 2 kk + (l >> 5) at slot chunk ^ ((row >> 2) & 3)
+  int fa[2], fb[2];
 #pragma unroll
-    for (int kk = 0; kk < BK / 16; ++kk) {
-      const int kof = kk * 16 + 8 * (lane >> 5);
-      bf16x8 af[4], bfr[2];
-#pragma unroll
-      for (int mi = 0; mi < 4; ++mi)
-        af[mi] = as_bf16x8(ld16(sa + (128 * wm + 32 * mi + (lane & 31)) * PITCH + kof));
-#pragma unroll
-      for (int ni = 0; ni < 2; ++ni)
-        bfr[ni] = as_bf16x8(ld16(sb + (64 * wn + 32 * ni + (lane & 31)) * PITCH + kof));
-#pragma unroll
-      for (int mi = 0; mi < 4; ++mi)
-#pragma unroll
-        for (int ni = 0; ni < 2; ++ni) acc[mi][ni] = mfma32(af[mi], bfr[ni], acc[mi][ni]);
-    }
-    if (more) store_stage(f, lds + ((kt + 1) & 1) * kStage, tid);
-    __syncthreads();
+  for (int kk = 0; kk < 2; ++kk) {
+    const int slot = ((2 * kk + (lane >> 5)) ^ ((lane >> 2) & 3)) << 3;
+    fa[kk] = (128 * wm + (lane & 31)) * TK + slot;
+    fb[kk] = TM * TK + (128 * wn + (lane & 31)) * TK + slot;
   }
+  const int nk = (K + TK - 1) / TK;
+  auto issue = [&](bf16* st, int kt) {
+    sa.issue(st, kt * TK, wave);
+    sb.issue(st + TM * TK, kt * TK, wave);
+  };
+  issue(s0, 0);
+  if (nk > 1) issue(s1, 1);
+  if (nk > 2) issue(s2, 2);
+  // step kt: this wave's DMA of stage kt has landed (later stages may still be
+  // in flight); the barrier makes every wave's share visible and certifies that
+  // all waves are done with the stage refilled next
+  auto step = [&](const bf16* cur, bf16* refill, int kt) {
+    __builtin_amdgcn_sched_barrier(0);  // keep each stage's loads inside its stage
+    wait_dma(min(nk - 1 - kt, 2));
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+    if (kt + 3 < nk) issue(refill, kt + 3);
+    mma_stage(acc, cur, fa, fb);
+  };
+  int kt = 0;
+  for (; kt + 4 <= nk; kt += 4) {
+    step(s0, s3, kt);
+    step(s1, s0, kt + 1);
+    step(s2, s1, kt + 2);
+    step(s3, s2, kt + 3);
+  }
+  if (kt < nk) step(s0, s3, kt);
+  if (kt + 1 < nk) step(s1, s0, kt + 1);
+  if (kt + 2 < nk) step(s2, s1, kt + 2);
+  __builtin_amdgcn_sched_barrier(0);
+  __syncthreads();
 }
+
+// the work-group's LDS: the GEMM ring (4 stages, each with 2 KB of slack so
+// that a quarter of a staged output tile fits one stage), reused by the
+// epilogues
+constexpr int kRingElems = kStageElems + 1024;
+#define LP_RING                                                    \
+  __shared__ __attribute__((aligned(16))) bf16 s0[kRingElems];     \
+  __shared__ __attribute__((aligned(16))) bf16 s1[kRingElems];     \
+  __shared__ __attribute__((aligned(16))) bf16 s2[kRingElems];     \
+  __shared__ __attribute__((aligned(16))) bf16 s3[kRingElems];
 
 // (max, sum exp(l - max), sum exp(l - max) (l - max)) of two disjoint sets of
 // logits, either of which may be empty (max = -inf)
@@ -144,10 +219,6 @@ __device__ __forceinline__ void merge_stats(float& m, float& s, float& e, float 
   e = a * (e + s * (m - mn)) + b * (eo + so * (mo - mn));
   s = a * s + b * so;
   m = mn;
-}
-
-__device__ __forceinline__ int a_row(int mi, int i, int lane, int wm) {
-  return 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3) + 32 * mi + 128 * wm;
 }
 
 // ---------------------------------------------------------------------------
@@ -168,23 +239,22 @@ struct FwdArgs {
 };
 
 __global__ __launch_bounds__(kThreads, 1) void fwd_stats_kernel(FwdArgs p) {
-  extern __shared__ __attribute__((aligned(16))) bf16 lds[];
+  LP_RING
   const int total = p.n_ttiles * p.n_vtiles;
-  const int id = xcd_logical(blockIdx.x, total);
-  const int tt = id % p.n_ttiles, vt = id / p.n_ttiles;
-  const int v0 = vt * BM, n0 = tt * BN;
-  f32x16 acc[4][2];
-  gemm_tile(acc, p.w + (int64_t)v0 * p.ldw, p.ldw, min(BM, p.vocab - v0), p.h + (int64_t)n0 * p.ldh,
-            p.ldh, min(BN, p.rows - n0), p.dim, lds);
+  int vt, tt;
+  grouped_tile(xcd_logical(blockIdx.x, total), p.n_vtiles, p.n_ttiles, vt, tt);
+  const int v0 = vt * TM, n0 = tt * TN;
+  f32x16 acc[4][4];
+  gemm_tile(acc, p.w + (int64_t)v0 * p.ldw, p.ldw, min(TM, p.vocab - v0), p.h + (int64_t)n0 * p.ldh,
+            p.ldh, min(TN, p.rows - n0), p.dim, s0, s1, s2, s3);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave & 1, wn = wave >> 1;
-  // LDS is free after the final barrier of gemm_tile
-  float* xm = reinterpret_cast<float*>(lds);  // [BN] per token, from the wm = 1 waves
-  float* xs = xm + BN;
-  float* xe = xs + BN;
+  float* xm = reinterpret_cast<float*>(s0);  // [TN] per token, from the wm = 1 waves
+  float* xs = xm + TN;
+  float* xe = xs + TN;
 #pragma unroll
-  for (int ni = 0; ni < 2; ++ni) {
-    const int col = 64 * wn + 32 * ni + (lane & 31);
+  for (int ni = 0; ni < 4; ++ni) {
+    const int col = 128 * wn + 32 * ni + (lane & 31);
     const int n = n0 + col;
     const int64_t t = n < p.rows ? p.target[n] : -1;
     float m = neg_inf();
@@ -198,7 +268,7 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_stats_kernel(FwdArgs p) {
           if (v == t) p.tgt[n] = acc[mi][ni][i];
         }
       }
-    float s = 0.f, e = 0.f;
+    float sum = 0.f, e = 0.f;
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
@@ -207,26 +277,26 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_stats_kernel(FwdArgs p) {
         if (v < p.vocab) {
           const float d = acc[mi][ni][i] - m;
           const float q = fast_exp2(d * kLog2e);
-          s += q;
+          sum += q;
           e = fmaf(q, d, e);
         }
       }
     // merge with the other half-wave (lane ^ 32 holds the other vocab rows)
     {
-      const float mo = shfl_xor(m, 32), so = shfl_xor(s, 32), eo = shfl_xor(e, 32);
-      merge_stats(m, s, e, mo, so, eo);
+      const float mo = shfl_xor(m, 32), so = shfl_xor(sum, 32), eo = shfl_xor(e, 32);
+      merge_stats(m, sum, e, mo, so, eo);
     }
     if (wm == 1 && lane < 32) {
       xm[col] = m;
-      xs[col] = s;
+      xs[col] = sum;
       xe[col] = e;
     }
     __syncthreads();
     if (wm == 0 && lane < 32 && n < p.rows) {
-      merge_stats(m, s, e, xm[col], xs[col], xe[col]);
+      merge_stats(m, sum, e, xm[col], xs[col], xe[col]);
       const int64_t o = (int64_t)vt * p.rows + n;
       p.part_m[o] = m;
-      p.part_s[o] = s;
+      p.part_s[o] = sum;
       p.part_e[o] = e;
     }
     __syncthreads();
@@ -283,22 +353,26 @@ struct DlArgs {
   int64_t ldl;
 };
 
-constexpr int OPITCH = BM + 8;  // staging pitch (bf16) for the [BN][BM] dlogits tile
+constexpr int OPITCH = TM + 8;  // staging pitch (bf16) of [64 tokens][TM vocab] quarter tiles
+static_assert(64 * OPITCH <= kRingElems, "a quarter of the dlogits tile fits one ring stage");
 
 __global__ __launch_bounds__(kThreads, 1) void dlogits_kernel(DlArgs p) {
-  extern __shared__ __attribute__((aligned(16))) bf16 lds[];
+  LP_RING
   const int total = p.n_ttiles * p.n_vtiles;
-  const int id = xcd_logical(blockIdx.x, total);
-  const int tt = id % p.n_ttiles, vt = id / p.n_ttiles;
-  const int v0 = vt * BM, n0 = tt * BN;
-  f32x16 acc[4][2];
-  gemm_tile(acc, p.w + (int64_t)v0 * p.ldw, p.ldw, min(BM, p.vocab - v0), p.h + (int64_t)n0 * p.ldh,
-            p.ldh, min(BN, p.rows - n0), p.dim, lds);
+  int vt, tt;
+  grouped_tile(xcd_logical(blockIdx.x, total), p.n_vtiles, p.n_ttiles, vt, tt);
+  const int v0 = vt * TM, n0 = tt * TN;
+  f32x16 acc[4][4];
+  gemm_tile(acc, p.w + (int64_t)v0 * p.ldw, p.ldw, min(TM, p.vocab - v0), p.h + (int64_t)n0 * p.ldh,
+            p.ldh, min(TN, p.rows - n0), p.dim, s0, s1, s2, s3);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave & 1, wn = wave >> 1;
+  // tokens 64 q .. 64 q + 63 of the tile are staged in ring stage q as [64][OPITCH]
+  auto quarter = [&](int q) -> bf16* { return q == 0 ? s0 : q == 1 ? s1 : q == 2 ? s2 : s3; };
 #pragma unroll
-  for (int ni = 0; ni < 2; ++ni) {
-    const int col = 64 * wn + 32 * ni + (lane & 31);
+  for (int ni = 0; ni < 4; ++ni) {
+    const int col = 128 * wn + 32 * ni + (lane & 31);  // token within the tile
+    bf16* out = quarter(col >> 6) + (col & 63) * OPITCH;
     const int n = n0 + col;
     float lse_n = 0.f, h_n = 0.f, glp = 0.f, gent = 0.f;
     int64_t t = -1;
@@ -335,21 +409,20 @@ __global__ __launch_bounds__(kThreads, 1) void dlogits_kernel(DlArgs p) {
           packed[j >> 1] = pack_bf2(d2[0], d2[1]);
         }
         // vocab rows a_row(mi, 4 i4 .. 4 i4 + 3) are consecutive: one 8-byte write
-        const int r = a_row(mi, 4 * i4, lane, wm);
-        *reinterpret_cast<u32x2*>(lds + col * OPITCH + r) = u32x2{packed[0], packed[1]};
+        *reinterpret_cast<u32x2*>(out + a_row(mi, 4 * i4, lane, wm)) = u32x2{packed[0], packed[1]};
       }
   }
   __syncthreads();
-  // coalesced store of the [BN tokens][BM vocab] tile
-  const int vmax = min(BM, p.vocab_pad - v0);
+  // coalesced store of the [TN tokens][TM vocab] tile
+  const int vmax = min(TM, p.vocab_pad - v0);
 #pragma unroll 4
-  for (int it = 0; it < (BN * BM / 8) / kThreads; ++it) {
+  for (int it = 0; it < (TN * TM / 8) / kThreads; ++it) {
     const int c = it * kThreads + tid;
-    const int row = c / (BM / 8), chunk = (c % (BM / 8)) * 8;
+    const int row = c / (TM / 8), chunk = (c % (TM / 8)) * 8;
     const int n = n0 + row;
     if (n < p.rows && chunk < vmax)
       *reinterpret_cast<u32x4*>(p.dl + (int64_t)n * p.ldl + v0 + chunk) =
-          *reinterpret_cast<const u32x4*>(lds + row * OPITCH + chunk);
+          *reinterpret_cast<const u32x4*>(quarter(row >> 6) + (row & 63) * OPITCH + chunk);
   }
 }
 
@@ -368,19 +441,19 @@ struct DhArgs {
 };
 
 __global__ __launch_bounds__(kThreads, 1) void grad_hidden_kernel(DhArgs p) {
-  extern __shared__ __attribute__((aligned(16))) bf16 lds[];
+  LP_RING
   const int total = p.n_ttiles * p.n_dtiles;
-  const int id = xcd_logical(blockIdx.x, total);
-  const int dt = id % p.n_dtiles, tt = id / p.n_dtiles;
-  const int d0 = dt * BM, n0 = tt * BN;
-  f32x16 acc[4][2];
-  gemm_tile(acc, p.wt + (int64_t)d0 * p.ldt, p.ldt, min(BM, p.dim - d0), p.dl + (int64_t)n0 * p.ldl,
-            p.ldl, min(BN, p.rows - n0), p.kdim, lds);
+  int dt, tt;
+  grouped_tile(xcd_logical(blockIdx.x, total), p.n_dtiles, p.n_ttiles, dt, tt);
+  const int d0 = dt * TM, n0 = tt * TN;
+  f32x16 acc[4][4];
+  gemm_tile(acc, p.wt + (int64_t)d0 * p.ldt, p.ldt, min(TM, p.dim - d0), p.dl + (int64_t)n0 * p.ldl,
+            p.ldl, min(TN, p.rows - n0), p.kdim, s0, s1, s2, s3);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave & 1, wn = wave >> 1;
 #pragma unroll
-  for (int ni = 0; ni < 2; ++ni) {
-    const int n = n0 + 64 * wn + 32 * ni + (lane & 31);
+  for (int ni = 0; ni < 4; ++ni) {
+    const int n = n0 + 128 * wn + 32 * ni + (lane & 31);
     if (n >= p.rows) continue;
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi)
@@ -419,21 +492,7 @@ __global__ __launch_bounds__(kThreads) void transpose_kernel(const bf16* __restr
   }
 }
 
-constexpr size_t kGemmLds = 2 * kStage * sizeof(bf16);
-static_assert((size_t)BN * OPITCH * sizeof(bf16) <= kGemmLds, "staging tile fits the GEMM LDS");
-
 bool ok16(const void* p) { return ((uintptr_t)p & 15) == 0; }
-
-// kernels with more than 64 KB of dynamic LDS must say so before launch
-int allow_lds(const void* fn, const char* what) {
-  if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGemmLds) !=
-      hipSuccess) {
-    (void)hipGetLastError();
-    set_error("%s: cannot reserve %zu bytes of LDS", what, kGemmLds);
-    return TS_ERR_LAUNCH;
-  }
-  return TS_OK;
-}
 
 }  // namespace lp
 }  // namespace ts
@@ -472,7 +531,7 @@ int ts_logprob_fwd(const void* hidden, int64_t ld_hidden, const void* weight, in
   a.rows = (int)rows;
   a.dim = (int)dim;
   a.vocab = (int)vocab;
-  a.n_ttiles = (int)((rows + BN - 1) / BN);
+  a.n_ttiles = (int)((rows + TN - 1) / TN);
   a.n_vtiles = (int)((vocab + BM - 1) / BM);
   float* ws = (float*)workspace;
   a.part_m = ws;
@@ -481,11 +540,9 @@ int ts_logprob_fwd(const void* hidden, int64_t ld_hidden, const void* weight, in
   a.tgt = ws + 3 * (int64_t)a.n_vtiles * rows;
   TS_CHECK_ARG((int64_t)a.n_ttiles * a.n_vtiles < (1ll << 31), "ts_logprob_fwd: grid too large");
   hipStream_t s = (hipStream_t)stream;
-  int st = allow_lds((const void*)fwd_stats_kernel, "ts_logprob_fwd");
-  if (st != TS_OK) return st;
   { ts::TimedLaunch timed_("logprob.fwd_stats_kernel", s); hipLaunchKernelGGL(fwd_stats_kernel, dim3((unsigned)(a.n_ttiles * a.n_vtiles)), dim3(kThreads),
-                     kGemmLds, s, a); }
-  st = ts::check_launch("ts_logprob_fwd (tiles)");
+                     0, s, a); }
+  int st = ts::check_launch("ts_logprob_fwd (tiles)");
   if (st != TS_OK) return st;
   { ts::TimedLaunch timed_("logprob.combine_kernel", s); hipLaunchKernelGGL(combine_kernel, dim3((unsigned)((rows + kThreads - 1) / kThreads)), dim3(kThreads),
                      0, s, a.part_m, a.part_s, a.part_e, a.tgt, target, (int)rows, a.n_vtiles,
@@ -536,15 +593,13 @@ int ts_logprob_dlogits(const void* hidden, int64_t ld_hidden, const void* weight
   a.dim = (int)dim;
   a.vocab = (int)vocab;
   a.vocab_pad = (int)((vocab + 7) / 8 * 8);
-  a.n_ttiles = (int)((rows + BN - 1) / BN);
+  a.n_ttiles = (int)((rows + TN - 1) / TN);
   a.n_vtiles = (int)((a.vocab_pad + BM - 1) / BM);
   a.dl = (ts::bf16*)dlogits;
   a.ldl = ld_dlogits;
   TS_CHECK_ARG(a.vocab_pad <= ld_dlogits, "ts_logprob_dlogits: ld_dlogits below padded vocab");
-  int st = allow_lds((const void*)dlogits_kernel, "ts_logprob_dlogits");
-  if (st != TS_OK) return st;
   { ts::TimedLaunch timed_("logprob.dlogits_kernel", (hipStream_t)stream); hipLaunchKernelGGL(dlogits_kernel, dim3((unsigned)(a.n_ttiles * a.n_vtiles)), dim3(kThreads),
-                     kGemmLds, (hipStream_t)stream, a); }
+                     0, (hipStream_t)stream, a); }
   return ts::check_launch("ts_logprob_dlogits");
 }
 
@@ -569,14 +624,12 @@ int ts_logprob_grad_hidden(const void* dlogits, int64_t ld_dlogits, const void* 
   a.rows = (int)rows;
   a.dim = (int)dim;
   a.kdim = (int)vocab_padded;
-  a.n_ttiles = (int)((rows + BN - 1) / BN);
-  a.n_dtiles = (int)((dim + BM - 1) / BM);
+  a.n_ttiles = (int)((rows + TN - 1) / TN);
+  a.n_dtiles = (int)((dim + TM - 1) / TM);
   a.dh = (ts::bf16*)grad_hidden;
   a.ldd = ld_grad;
-  int st = allow_lds((const void*)grad_hidden_kernel, "ts_logprob_grad_hidden");
-  if (st != TS_OK) return st;
   { ts::TimedLaunch timed_("logprob.grad_hidden_kernel", (hipStream_t)stream); hipLaunchKernelGGL(grad_hidden_kernel, dim3((unsigned)(a.n_ttiles * a.n_dtiles)), dim3(kThreads),
-                     kGemmLds, (hipStream_t)stream, a); }
+                     0, (hipStream_t)stream, a); }
   return ts::check_launch("ts_logprob_grad_hidden");
 }
 
