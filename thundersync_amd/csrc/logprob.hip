@@ -83,12 +83,14 @@ struct Streamer {
 #pragma unroll
     for (int u = 0; u < 4; ++u) voff[u] = (int)(((16 * (wave + 4 * u) + (lane >> 2)) * ld + kchunk) * 2);
   }
-  // K columns [k0, k0 + TK) into dst (wave-uniform)
-  __device__ __forceinline__ void issue(bf16* dst, int k0, int wave) const {
-    const u32x4 r = raw_descriptor(base + k0, (uint32_t)(((int64_t)(rows - 1) * ld + TK) * 2));
-    const bool in_k = k0 + kchunk < K;  // a chunk past K reads nothing: zeros
-#pragma unroll
-    for (int u = 0; u < 4; ++u) buffer_dma16_untracked(r, dst + (wave + 4 * u) * 512, in_k ? voff[u] : 0x7ffffff0);
+  // descriptor and this lane's chunk validity for K columns [k0, k0 + TK)
+  __device__ __forceinline__ u32x4 descriptor(int k0) const {
+    return raw_descriptor(base + k0, (uint32_t)(((int64_t)(rows - 1) * ld + TK) * 2));
+  }
+  // instruction u of this wave's share of the stage into dst (wave-uniform);
+  // a chunk past K reads nothing: zeros
+  __device__ __forceinline__ void issue(u32x4 r, bool in_k, bf16* dst, int u, int wave) const {
+    buffer_dma16_untracked(r, dst + (wave + 4 * u) * 512, in_k ? voff[u] : 0x7ffffff0);
   }
 };
 
@@ -99,31 +101,33 @@ __device__ __forceinline__ int a_row(int mi, int i, int lane, int wm) {
   return 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3) + 32 * mi + 128 * wm;
 }
 
-// the MFMAs of one stage: two k-steps of 16 (all fragment reads issued first)
-__device__ __forceinline__ void mma_stage(f32x16 acc[4][4], const bf16* st, const int fa[2], const int fb[2]) {
-  bf16x8 af[2][4], bfr[2][4];
+// The MFMAs of one stage (two k-steps of 16) in a fixed order: the 8
+// fragment reads of k-step 0, then eight groups of {two k-step-0 MFMAs, one
+// k-step-1 fragment read, one refill DMA instruction}, then the 16 k-step-1
+// MFMAs.  Spreading the refill over the MFMAs keeps the wave issuing MFMAs
+// while the DMA is in flight.
+template <class Dma>
+__device__ __forceinline__ void mma_stage(f32x16 acc[4][4], const bf16* st, const int fa[2], const int fb[2],
+                                          Dma&& dma) {
+  bf16x8 a0[4], b0[4], f1[8];  // f1: k-step 1 A (0..3) and B (4..7)
 #pragma unroll
-  for (int kk = 0; kk < 2; ++kk) {
+  for (int mi = 0; mi < 4; ++mi) a0[mi] = as_bf16x8(ld16(st + fa[0] + 32 * mi * TK));
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi) af[kk][mi] = as_bf16x8(ld16(st + fa[kk] + 32 * mi * TK));
+  for (int ni = 0; ni < 4; ++ni) b0[ni] = as_bf16x8(ld16(st + fb[0] + 32 * ni * TK));
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int ni = 0; ni < 4; ++ni) bfr[kk][ni] = as_bf16x8(ld16(st + fb[kk] + 32 * ni * TK));
+  for (int g = 0; g < 8; ++g) {
+    const int mi = g >> 1, n0 = 2 * (g & 1);
+    acc[mi][n0] = mfma32(a0[mi], b0[n0], acc[mi][n0]);
+    acc[mi][n0 + 1] = mfma32(a0[mi], b0[n0 + 1], acc[mi][n0 + 1]);
+    f1[g] = as_bf16x8(ld16(st + (g < 4 ? fa[1] : fb[1]) + 32 * (g & 3) * TK));
+    dma(g);
+    __builtin_amdgcn_sched_barrier(0);
   }
 #pragma unroll
-  for (int kk = 0; kk < 2; ++kk)
+  for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi)
-#pragma unroll
-      for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = mfma32(af[kk][mi], bfr[kk][ni], acc[mi][ni]);
-  // schedule: the 8 reads of k-step 0, then its 16 MFMAs with the 8 reads of
-  // k-step 1 interleaved (one read per two MFMAs), then k-step 1's MFMAs
-  __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);  // DS reads
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);  // MFMA
-    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
-  }
-  __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
+    for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = mfma32(f1[mi], f1[4 + ni], acc[mi][ni]);
 }
 
 // wait until at most 8 * ahead of this wave's DMA instructions are in flight
@@ -162,8 +166,13 @@ __device__ __forceinline__ void gemm_tile(f32x16 acc[4][4], const bf16* A, int64
   }
   const int nk = (K + TK - 1) / TK;
   auto issue = [&](bf16* st, int kt) {
-    sa.issue(st, kt * TK, wave);
-    sb.issue(st + TM * TK, kt * TK, wave);
+    const u32x4 ra = sa.descriptor(kt * TK), rb = sb.descriptor(kt * TK);
+    const bool ka = kt * TK + sa.kchunk < K, kb = kt * TK + sb.kchunk < K;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      sa.issue(ra, ka, st, u, wave);
+      sb.issue(rb, kb, st + TM * TK, u, wave);
+    }
   };
   issue(s0, 0);
   if (nk > 1) issue(s1, 1);
@@ -176,8 +185,16 @@ __device__ __forceinline__ void gemm_tile(f32x16 acc[4][4], const bf16* A, int64
     wait_dma(min(nk - 1 - kt, 2));
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
     __builtin_amdgcn_s_barrier();
-    if (kt + 3 < nk) issue(refill, kt + 3);
-    mma_stage(acc, cur, fa, fb);
+    const bool refill_now = kt + 3 < nk;
+    const int k0 = (kt + 3) * TK;
+    const u32x4 ra = sa.descriptor(k0), rb = sb.descriptor(k0);
+    const bool ka = k0 + sa.kchunk < K, kb = k0 + sb.kchunk < K;
+    mma_stage(acc, cur, fa, fb, [&](int g) {
+      if (refill_now) {
+        if (g < 4) sa.issue(ra, ka, refill, g, wave);
+        else sb.issue(rb, kb, refill + TM * TK, g - 4, wave);
+      }
+    });
   };
   int kt = 0;
   for (; kt + 4 <= nk; kt += 4) {
