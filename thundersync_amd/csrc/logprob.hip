@@ -18,7 +18,8 @@
 //             stores a [rows, V] bf16 block; a second GEMM multiplies it by
 //             W (given as W^T so both operands are K-contiguous) into dh.
 //
-// GEMM core: 256 x 256 work-group tile, 4 waves of 128 x 128 (accumulators in
+// GEMM core: 256 x 256 work-group tile, 8 waves of 128 x 64 (two per SIMD, so
+// one wave's memory instructions overlap the other's MFMAs; accumulators in
 // the accumulation registers), v_mfma_f32_32x32x16_bf16.  K streams 32 at a
 // time through a 4-stage LDS ring filled by buffer_load ... lds (no register
 // staging), three stages ahead of the MFMAs, one work-group barrier per stage.
@@ -31,7 +32,9 @@
 namespace ts {
 namespace lp {
 
-constexpr int kThreads = 256;
+constexpr int kThreads = 256;      // combine / transpose kernels
+constexpr int kGemmThreads = 512;  // GEMM work-groups: 8 waves, 2 per SIMD
+constexpr int NI = 2;              // 32-column B blocks per wave (wave tile 128 x 64)
 constexpr int TM = 256;  // A rows (vocab rows, or hidden dims) per work-group
 constexpr int TN = 256;  // B rows (tokens) per work-group
 constexpr int TK = 32;   // K per LDS stage
@@ -63,7 +66,7 @@ __device__ __forceinline__ void grouped_tile(int id, int n_a, int n_b, int& ta, 
 }
 
 // One operand's share of a stage: 256 rows x 64 bytes = 16 instructions of 16
-// rows each, issued by the 4 waves as t = wave + 4 u.  Lane i of an
+// rows each, issued by the 8 waves as t = wave + 8 u.  Lane i of an
 // instruction fills row 16 t + i / 4, slot i & 3 with the logical 16-byte
 // chunk c = (i & 3) ^ (i >> 4): row r's chunk c sits at slot c ^ ((r >> 2) & 3),
 // so the 16 rows of a fragment read at one chunk hit 16 distinct bank groups.
@@ -72,7 +75,7 @@ struct Streamer {
   int64_t ld;
   int rows;          // valid rows from base (>= 1)
   int K;
-  int voff[4];       // byte offset of this lane's row and chunk within a stage, per u
+  int voff[2];       // byte offset of this lane's row and chunk within a stage, per u
   int kchunk;        // this lane's chunk start within a stage (elements)
   __device__ __forceinline__ void init(const bf16* b, int64_t ld_, int rows_, int K_, int wave, int lane) {
     base = b;
@@ -81,7 +84,7 @@ struct Streamer {
     K = K_;
     kchunk = 8 * ((lane & 3) ^ (lane >> 4));
 #pragma unroll
-    for (int u = 0; u < 4; ++u) voff[u] = (int)(((16 * (wave + 4 * u) + (lane >> 2)) * ld + kchunk) * 2);
+    for (int u = 0; u < 2; ++u) voff[u] = (int)(((16 * (wave + 8 * u) + (lane >> 2)) * ld + kchunk) * 2);
   }
   // descriptor and this lane's chunk validity for K columns [k0, k0 + TK)
   __device__ __forceinline__ u32x4 descriptor(int k0) const {
@@ -90,57 +93,61 @@ struct Streamer {
   // instruction u of this wave's share of the stage into dst (wave-uniform);
   // a chunk past K reads nothing: zeros
   __device__ __forceinline__ void issue(u32x4 r, bool in_k, bf16* dst, int u, int wave) const {
-    buffer_dma16_untracked(r, dst + (wave + 4 * u) * 512, in_k ? voff[u] : 0x7ffffff0);
+    buffer_dma16_untracked(r, dst + (wave + 8 * u) * 512, in_k ? voff[u] : 0x7ffffff0);
   }
 };
 
-// acc[mi][ni]: 32x32 block (A rows 128 wm + 32 mi, B rows 128 wn + 32 ni).
-// Lane l holds B row (l & 31) + 32 ni + 128 wn and A rows
+// acc[mi][ni]: 32x32 block (A rows 128 wm + 32 mi, B rows 64 wn + 32 ni),
+// wm = wave & 1, wn = wave >> 1.  Lane l holds B row (l & 31) + 32 ni + 64 wn and A rows
 // 8 (i >> 2) + 4 (l >> 5) + (i & 3) + 32 mi + 128 wm, i = 0..15.
 __device__ __forceinline__ int a_row(int mi, int i, int lane, int wm) {
   return 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3) + 32 * mi + 128 * wm;
 }
 
-// The MFMAs of one stage (two k-steps of 16) in a fixed order: the 8
-// fragment reads of k-step 0, then eight groups of {two k-step-0 MFMAs, one
-// k-step-1 fragment read, one refill DMA instruction}, then the 16 k-step-1
-// MFMAs.  Spreading the refill over the MFMAs keeps the wave issuing MFMAs
-// while the DMA is in flight.
+// The MFMAs of one stage (two k-steps of 16) in a fixed order: the 6
+// fragment reads of k-step 0, then four groups of {two k-step-0 MFMAs, one or
+// two k-step-1 fragment reads, one refill DMA instruction}, then the 8
+// k-step-1 MFMAs.  Spreading the refill over the MFMAs keeps the wave issuing
+// MFMAs while the DMA is in flight.
 template <class Dma>
-__device__ __forceinline__ void mma_stage(f32x16 acc[4][4], const bf16* st, const int fa[2], const int fb[2],
+__device__ __forceinline__ void mma_stage(f32x16 acc[4][NI], const bf16* st, const int fa[2], const int fb[2],
                                           Dma&& dma) {
-  bf16x8 a0[4], b0[4], f1[8];  // f1: k-step 1 A (0..3) and B (4..7)
+  bf16x8 a0[4], b0[NI], a1[4], b1[NI];
 #pragma unroll
   for (int mi = 0; mi < 4; ++mi) a0[mi] = as_bf16x8(ld16(st + fa[0] + 32 * mi * TK));
 #pragma unroll
-  for (int ni = 0; ni < 4; ++ni) b0[ni] = as_bf16x8(ld16(st + fb[0] + 32 * ni * TK));
+  for (int ni = 0; ni < NI; ++ni) b0[ni] = as_bf16x8(ld16(st + fb[0] + 32 * ni * TK));
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-  for (int g = 0; g < 8; ++g) {
-    const int mi = g >> 1, n0 = 2 * (g & 1);
-    acc[mi][n0] = mfma32(a0[mi], b0[n0], acc[mi][n0]);
-    acc[mi][n0 + 1] = mfma32(a0[mi], b0[n0 + 1], acc[mi][n0 + 1]);
-    f1[g] = as_bf16x8(ld16(st + (g < 4 ? fa[1] : fb[1]) + 32 * (g & 3) * TK));
+  for (int g = 0; g < 4; ++g) {
+    acc[g][0] = mfma32(a0[g], b0[0], acc[g][0]);
+    acc[g][1] = mfma32(a0[g], b0[1], acc[g][1]);
+    if (g < 2) {
+      a1[2 * g] = as_bf16x8(ld16(st + fa[1] + 32 * (2 * g) * TK));
+      a1[2 * g + 1] = as_bf16x8(ld16(st + fa[1] + 32 * (2 * g + 1) * TK));
+    } else {
+      b1[g - 2] = as_bf16x8(ld16(st + fb[1] + 32 * (g - 2) * TK));
+    }
     dma(g);
     __builtin_amdgcn_sched_barrier(0);
   }
 #pragma unroll
   for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
-    for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = mfma32(f1[mi], f1[4 + ni], acc[mi][ni]);
+    for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = mfma32(a1[mi], b1[ni], acc[mi][ni]);
 }
 
-// wait until at most 8 * ahead of this wave's DMA instructions are in flight
+// wait until at most 4 * ahead of this wave's DMA instructions are in flight
 __device__ __forceinline__ void wait_dma(int ahead) {
-  if (ahead >= 2) __builtin_amdgcn_s_waitcnt(0x4F70);       // vmcnt(16)
-  else if (ahead == 1) __builtin_amdgcn_s_waitcnt(0x0F78);  // vmcnt(8)
+  if (ahead >= 2) __builtin_amdgcn_s_waitcnt(0x0F78);       // vmcnt(8)
+  else if (ahead == 1) __builtin_amdgcn_s_waitcnt(0x0F74);  // vmcnt(4)
   else __builtin_amdgcn_s_waitcnt(0x0F70);                  // vmcnt(0)
 }
 
 // C tile = A[256 rows] . B[256 rows]^T over K (both K-contiguous), through the
 // LDS ring s0..s3 (distinct arrays, so the compiler sees that a refill and
 // the reads of another stage never alias).  The ring is free on return.
-__device__ __forceinline__ void gemm_tile(f32x16 acc[4][4], const bf16* A, int64_t lda, int a_rows,
+__device__ __forceinline__ void gemm_tile(f32x16 acc[4][NI], const bf16* A, int64_t lda, int a_rows,
                                           const bf16* B, int64_t ldb, int b_rows, int K, bf16* s0,
                                           bf16* s1, bf16* s2, bf16* s3) {
   const int tid = threadIdx.x, lane = tid & 63;
@@ -149,7 +156,7 @@ __device__ __forceinline__ void gemm_tile(f32x16 acc[4][4], const bf16* A, int64
 #pragma unroll
   for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
-    for (int ni = 0; ni < 4; ++ni)
+    for (int ni = 0; ni < NI; ++ni)
 #pragma unroll
       for (int i = 0; i < 16; ++i) acc[mi][ni][i] = 0.f;
   Streamer sa, sb;
@@ -162,14 +169,14 @@ __device__ __forceinline__ void gemm_tile(f32x16 acc[4][4], const bf16* A, int64
   for (int kk = 0; kk < 2; ++kk) {
     const int slot = ((2 * kk + (lane >> 5)) ^ ((lane >> 2) & 3)) << 3;
     fa[kk] = (128 * wm + (lane & 31)) * TK + slot;
-    fb[kk] = TM * TK + (128 * wn + (lane & 31)) * TK + slot;
+    fb[kk] = TM * TK + (64 * wn + (lane & 31)) * TK + slot;
   }
   const int nk = (K + TK - 1) / TK;
   auto issue = [&](bf16* st, int kt) {
     const u32x4 ra = sa.descriptor(kt * TK), rb = sb.descriptor(kt * TK);
     const bool ka = kt * TK + sa.kchunk < K, kb = kt * TK + sb.kchunk < K;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < 2; ++u) {
       sa.issue(ra, ka, st, u, wave);
       sb.issue(rb, kb, st + TM * TK, u, wave);
     }
@@ -191,8 +198,8 @@ __device__ __forceinline__ void gemm_tile(f32x16 acc[4][4], const bf16* A, int64
     const bool ka = k0 + sa.kchunk < K, kb = k0 + sb.kchunk < K;
     mma_stage(acc, cur, fa, fb, [&](int g) {
       if (refill_now) {
-        if (g < 4) sa.issue(ra, ka, refill, g, wave);
-        else sb.issue(rb, kb, refill + TM * TK, g - 4, wave);
+        if (g < 2) sa.issue(ra, ka, refill, g, wave);
+        else sb.issue(rb, kb, refill + TM * TK, g - 2, wave);
       }
     });
   };
@@ -255,13 +262,13 @@ struct FwdArgs {
   float* tgt;      // [rows] target logit
 };
 
-__global__ __launch_bounds__(kThreads, 1) void fwd_stats_kernel(FwdArgs p) {
+__global__ __launch_bounds__(kGemmThreads, 1) void fwd_stats_kernel(FwdArgs p) {
   LP_RING
   const int total = p.n_ttiles * p.n_vtiles;
   int vt, tt;
   grouped_tile(xcd_logical(blockIdx.x, total), p.n_vtiles, p.n_ttiles, vt, tt);
   const int v0 = vt * TM, n0 = tt * TN;
-  f32x16 acc[4][4];
+  f32x16 acc[4][NI];
   gemm_tile(acc, p.w + (int64_t)v0 * p.ldw, p.ldw, min(TM, p.vocab - v0), p.h + (int64_t)n0 * p.ldh,
             p.ldh, min(TN, p.rows - n0), p.dim, s0, s1, s2, s3);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -270,8 +277,8 @@ __global__ __launch_bounds__(kThreads, 1) void fwd_stats_kernel(FwdArgs p) {
   float* xs = xm + TN;
   float* xe = xs + TN;
 #pragma unroll
-  for (int ni = 0; ni < 4; ++ni) {
-    const int col = 128 * wn + 32 * ni + (lane & 31);
+  for (int ni = 0; ni < NI; ++ni) {
+    const int col = 64 * wn + 32 * ni + (lane & 31);
     const int n = n0 + col;
     const int64_t t = n < p.rows ? p.target[n] : -1;
     float m = neg_inf();
@@ -373,13 +380,13 @@ struct DlArgs {
 constexpr int OPITCH = TM + 8;  // staging pitch (bf16) of [64 tokens][TM vocab] quarter tiles
 static_assert(64 * OPITCH <= kRingElems, "a quarter of the dlogits tile fits one ring stage");
 
-__global__ __launch_bounds__(kThreads, 1) void dlogits_kernel(DlArgs p) {
+__global__ __launch_bounds__(kGemmThreads, 1) void dlogits_kernel(DlArgs p) {
   LP_RING
   const int total = p.n_ttiles * p.n_vtiles;
   int vt, tt;
   grouped_tile(xcd_logical(blockIdx.x, total), p.n_vtiles, p.n_ttiles, vt, tt);
   const int v0 = vt * TM, n0 = tt * TN;
-  f32x16 acc[4][4];
+  f32x16 acc[4][NI];
   gemm_tile(acc, p.w + (int64_t)v0 * p.ldw, p.ldw, min(TM, p.vocab - v0), p.h + (int64_t)n0 * p.ldh,
             p.ldh, min(TN, p.rows - n0), p.dim, s0, s1, s2, s3);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -387,8 +394,8 @@ __global__ __launch_bounds__(kThreads, 1) void dlogits_kernel(DlArgs p) {
   // tokens 64 q .. 64 q + 63 of the tile are staged in ring stage q as [64][OPITCH]
   auto quarter = [&](int q) -> bf16* { return q == 0 ? s0 : q == 1 ? s1 : q == 2 ? s2 : s3; };
 #pragma unroll
-  for (int ni = 0; ni < 4; ++ni) {
-    const int col = 128 * wn + 32 * ni + (lane & 31);  // token within the tile
+  for (int ni = 0; ni < NI; ++ni) {
+    const int col = 64 * wn + 32 * ni + (lane & 31);  // token within the tile
     bf16* out = quarter(col >> 6) + (col & 63) * OPITCH;
     const int n = n0 + col;
     float lse_n = 0.f, h_n = 0.f, glp = 0.f, gent = 0.f;
@@ -433,8 +440,8 @@ __global__ __launch_bounds__(kThreads, 1) void dlogits_kernel(DlArgs p) {
   // coalesced store of the [TN tokens][TM vocab] tile
   const int vmax = min(TM, p.vocab_pad - v0);
 #pragma unroll 4
-  for (int it = 0; it < (TN * TM / 8) / kThreads; ++it) {
-    const int c = it * kThreads + tid;
+  for (int it = 0; it < (TN * TM / 8) / kGemmThreads; ++it) {
+    const int c = it * kGemmThreads + tid;
     const int row = c / (TM / 8), chunk = (c % (TM / 8)) * 8;
     const int n = n0 + row;
     if (n < p.rows && chunk < vmax)
@@ -457,20 +464,20 @@ struct DhArgs {
   int64_t ldd;
 };
 
-__global__ __launch_bounds__(kThreads, 1) void grad_hidden_kernel(DhArgs p) {
+__global__ __launch_bounds__(kGemmThreads, 1) void grad_hidden_kernel(DhArgs p) {
   LP_RING
   const int total = p.n_ttiles * p.n_dtiles;
   int dt, tt;
   grouped_tile(xcd_logical(blockIdx.x, total), p.n_dtiles, p.n_ttiles, dt, tt);
   const int d0 = dt * TM, n0 = tt * TN;
-  f32x16 acc[4][4];
+  f32x16 acc[4][NI];
   gemm_tile(acc, p.wt + (int64_t)d0 * p.ldt, p.ldt, min(TM, p.dim - d0), p.dl + (int64_t)n0 * p.ldl,
             p.ldl, min(TN, p.rows - n0), p.kdim, s0, s1, s2, s3);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave & 1, wn = wave >> 1;
 #pragma unroll
-  for (int ni = 0; ni < 4; ++ni) {
-    const int n = n0 + 128 * wn + 32 * ni + (lane & 31);
+  for (int ni = 0; ni < NI; ++ni) {
+    const int n = n0 + 64 * wn + 32 * ni + (lane & 31);
     if (n >= p.rows) continue;
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi)
@@ -557,7 +564,7 @@ int ts_logprob_fwd(const void* hidden, int64_t ld_hidden, const void* weight, in
   a.tgt = ws + 3 * (int64_t)a.n_vtiles * rows;
   TS_CHECK_ARG((int64_t)a.n_ttiles * a.n_vtiles < (1ll << 31), "ts_logprob_fwd: grid too large");
   hipStream_t s = (hipStream_t)stream;
-  { ts::TimedLaunch timed_("logprob.fwd_stats_kernel", s); hipLaunchKernelGGL(fwd_stats_kernel, dim3((unsigned)(a.n_ttiles * a.n_vtiles)), dim3(kThreads),
+  { ts::TimedLaunch timed_("logprob.fwd_stats_kernel", s); hipLaunchKernelGGL(fwd_stats_kernel, dim3((unsigned)(a.n_ttiles * a.n_vtiles)), dim3(kGemmThreads),
                      0, s, a); }
   int st = ts::check_launch("ts_logprob_fwd (tiles)");
   if (st != TS_OK) return st;
@@ -615,7 +622,7 @@ int ts_logprob_dlogits(const void* hidden, int64_t ld_hidden, const void* weight
   a.dl = (ts::bf16*)dlogits;
   a.ldl = ld_dlogits;
   TS_CHECK_ARG(a.vocab_pad <= ld_dlogits, "ts_logprob_dlogits: ld_dlogits below padded vocab");
-  { ts::TimedLaunch timed_("logprob.dlogits_kernel", (hipStream_t)stream); hipLaunchKernelGGL(dlogits_kernel, dim3((unsigned)(a.n_ttiles * a.n_vtiles)), dim3(kThreads),
+  { ts::TimedLaunch timed_("logprob.dlogits_kernel", (hipStream_t)stream); hipLaunchKernelGGL(dlogits_kernel, dim3((unsigned)(a.n_ttiles * a.n_vtiles)), dim3(kGemmThreads),
                      0, (hipStream_t)stream, a); }
   return ts::check_launch("ts_logprob_dlogits");
 }
@@ -645,7 +652,7 @@ int ts_logprob_grad_hidden(const void* dlogits, int64_t ld_dlogits, const void* 
   a.n_dtiles = (int)((dim + TM - 1) / TM);
   a.dh = (ts::bf16*)grad_hidden;
   a.ldd = ld_grad;
-  { ts::TimedLaunch timed_("logprob.grad_hidden_kernel", (hipStream_t)stream); hipLaunchKernelGGL(grad_hidden_kernel, dim3((unsigned)(a.n_ttiles * a.n_dtiles)), dim3(kThreads),
+  { ts::TimedLaunch timed_("logprob.grad_hidden_kernel", (hipStream_t)stream); hipLaunchKernelGGL(grad_hidden_kernel, dim3((unsigned)(a.n_ttiles * a.n_dtiles)), dim3(kGemmThreads),
                      0, (hipStream_t)stream, a); }
   return ts::check_launch("ts_logprob_grad_hidden");
 }
