@@ -404,7 +404,7 @@ def bench_logprob(args, device):
         lp, ent = fused_logprob.fused_logprob_entropy(h, weight, t)
         lp.backward(a)
 
-    kernels = ["logprob.fwd_stats_kernel", "logprob.combine_kernel", "logprob.transpose_kernel",
+    kernels = ["logprob.fwd_stats_kernel", "logprob.target_logit_kernel", "logprob.combine_kernel", "logprob.transpose_kernel",
                "logprob.dlogits_kernel", "logprob.grad_hidden_kernel"]
     ms, per = timed(step, args.steps, args.warmup, kernels)
     gemm = 2 * rows * v * d
@@ -413,6 +413,7 @@ def bench_logprob(args, device):
         "logprob.dlogits_kernel": gemm,
         "logprob.grad_hidden_kernel": gemm,
         "logprob.combine_kernel": 0,
+        "logprob.target_logit_kernel": 0,
         "logprob.transpose_kernel": 0,
     }
     flop = 3 * gemm

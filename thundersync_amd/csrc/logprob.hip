@@ -276,35 +276,47 @@ __global__ __launch_bounds__(kGemmThreads, 1) void fwd_stats_kernel(FwdArgs p) {
   float* xm = reinterpret_cast<float*>(s0);  // [TN] per token, from the wm = 1 waves
   float* xs = xm + TN;
   float* xe = xs + TN;
+  // rows past the vocabulary (last vocab tile only) take no part
+  if (v0 + TM > p.vocab) {
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+      for (int ni = 0; ni < NI; ++ni)
+#pragma unroll
+        for (int i = 0; i < 16; ++i)
+          if (v0 + a_row(mi, i, lane, wm) >= p.vocab) acc[mi][ni][i] = neg_inf();
+  }
 #pragma unroll
   for (int ni = 0; ni < NI; ++ni) {
     const int col = 64 * wn + 32 * ni + (lane & 31);
     const int n = n0 + col;
-    const int64_t t = n < p.rows ? p.target[n] : -1;
     float m = neg_inf();
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int v = v0 + a_row(mi, i, lane, wm);
-        if (v < p.vocab) {
-          m = fmaxf(m, acc[mi][ni][i]);
-          if (v == t) p.tgt[n] = acc[mi][ni][i];
-        }
-      }
+      for (int i = 0; i < 16; i += 2) m = fmaxf(m, fmaxf(acc[mi][ni][i], acc[mi][ni][i + 1]));
     float sum = 0.f, e = 0.f;
+    if (v0 + TM <= p.vocab) {
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi)
+      for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int v = v0 + a_row(mi, i, lane, wm);
-        if (v < p.vocab) {
+        for (int i = 0; i < 16; ++i) {
           const float d = acc[mi][ni][i] - m;
           const float q = fast_exp2(d * kLog2e);
           sum += q;
           e = fmaf(q, d, e);
         }
-      }
+    } else if (m != neg_inf()) {
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const float d = acc[mi][ni][i] - m;  // -inf for rows past the vocabulary: q = 0
+          const float q = fast_exp2(d * kLog2e);
+          sum += q;
+          e = q > 0.f ? fmaf(q, d, e) : e;
+        }
+    }
     // merge with the other half-wave (lane ^ 32 holds the other vocab rows)
     {
       const float mo = shfl_xor(m, 32), so = shfl_xor(sum, 32), eo = shfl_xor(e, 32);
@@ -327,7 +339,37 @@ __global__ __launch_bounds__(kGemmThreads, 1) void fwd_stats_kernel(FwdArgs p) {
   }
 }
 
-// merge the per-vocab-tile partials of each token
+// target logit l[n, t] = sum_d h[n, d] W[t, d] (fp32 sum of exact bf16
+// products), one wave per row; rows with t outside [0, vocab) are skipped
+// (the combine kernel writes NaN for them)
+__global__ __launch_bounds__(kThreads) void target_logit_kernel(const bf16* __restrict__ h, int64_t ldh,
+                                                                const bf16* __restrict__ w, int64_t ldw,
+                                                                const int64_t* __restrict__ target, int rows,
+                                                                int dim, int vocab, float* __restrict__ tgt) {
+  const int lane = threadIdx.x & 63;
+  const int n = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+  if (n >= rows) return;
+  const int64_t t = target[n];
+  if (t < 0 || t >= vocab) return;
+  const bf16* hr = h + (int64_t)n * ldh;
+  const bf16* wr = w + t * ldw;
+  float acc = 0.f;
+  for (int d = 8 * lane; d < dim; d += 512) {
+    const u32x4 a = ld16(hr + d), b = ld16(wr + d);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      acc = fmaf(bf_bits_to_f(a[i] & 0xffffu), bf_bits_to_f(b[i] & 0xffffu), acc);
+      acc = fmaf(bf_bits_to_f(a[i] >> 16), bf_bits_to_f(b[i] >> 16), acc);
+    }
+  }
+  acc = wave_sum(acc);
+  if (lane == 0) tgt[n] = acc;
+}
+
+// merge the per-vocab-tile partials of each token: a work-group owns 64 tokens;
+// its 4 waves merge the tiles t = wave, wave + 4, ... (lanes read 64
+// consecutive tokens of one tile: coalesced), then wave 0 merges the four
+// partial states in wave order
 __global__ __launch_bounds__(kThreads) void combine_kernel(const float* __restrict__ pm,
                                                            const float* __restrict__ ps,
                                                            const float* __restrict__ pe,
@@ -337,19 +379,23 @@ __global__ __launch_bounds__(kThreads) void combine_kernel(const float* __restri
                                                            float* __restrict__ logprob,
                                                            float* __restrict__ entropy,
                                                            float* __restrict__ lse) {
-  const int n = blockIdx.x * kThreads + threadIdx.x;
-  if (n >= rows) return;
-  float M = neg_inf();
-  for (int t = 0; t < n_vtiles; ++t) M = fmaxf(M, pm[(int64_t)t * rows + n]);
-  float S = 0.f, E = 0.f;
-  for (int t = 0; t < n_vtiles; ++t) {
-    const int64_t o = (int64_t)t * rows + n;
-    const float m = pm[o];
-    if (m == neg_inf()) continue;
-    const float a = expf(m - M);
-    S = fmaf(a, ps[o], S);
-    E = fmaf(a, pe[o] + ps[o] * (m - M), E);
+  __shared__ float sm[4][64], ss[4][64], se[4][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int n = blockIdx.x * 64 + lane;
+  float M = neg_inf(), S = 0.f, E = 0.f;  // E: sum exp(l - M) (l - M)
+  if (n < rows) {
+    for (int t = wave; t < n_vtiles; t += 4) {
+      const int64_t o = (int64_t)t * rows + n;
+      merge_stats(M, S, E, pm[o], ps[o], pe[o]);
+    }
   }
+  sm[wave][lane] = M;
+  ss[wave][lane] = S;
+  se[wave][lane] = E;
+  __syncthreads();
+  if (wave != 0 || n >= rows) return;
+#pragma unroll
+  for (int w = 1; w < 4; ++w) merge_stats(M, S, E, sm[w][lane], ss[w][lane], se[w][lane]);
   const float logs = logf(S);
   const int64_t tg = target[n];
   const bool ok = tg >= 0 && tg < vocab;
@@ -568,7 +614,11 @@ int ts_logprob_fwd(const void* hidden, int64_t ld_hidden, const void* weight, in
                      0, s, a); }
   int st = ts::check_launch("ts_logprob_fwd (tiles)");
   if (st != TS_OK) return st;
-  { ts::TimedLaunch timed_("logprob.combine_kernel", s); hipLaunchKernelGGL(combine_kernel, dim3((unsigned)((rows + kThreads - 1) / kThreads)), dim3(kThreads),
+  { ts::TimedLaunch timed_("logprob.target_logit_kernel", s); hipLaunchKernelGGL(target_logit_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(kThreads),
+                     0, s, a.h, a.ldh, a.w, a.ldw, target, (int)rows, (int)dim, (int)vocab, a.tgt); }
+  st = ts::check_launch("ts_logprob_fwd (target logits)");
+  if (st != TS_OK) return st;
+  { ts::TimedLaunch timed_("logprob.combine_kernel", s); hipLaunchKernelGGL(combine_kernel, dim3((unsigned)((rows + 63) / 64)), dim3(kThreads),
                      0, s, a.part_m, a.part_s, a.part_e, a.tgt, target, (int)rows, a.n_vtiles,
                      (int)vocab, logprob, entropy, lse); }
   return ts::check_launch("ts_logprob_fwd (combine)");
