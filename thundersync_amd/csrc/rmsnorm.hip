@@ -68,6 +68,56 @@ template <> __device__ __forceinline__ void store8<float>(float* p, const float 
   *reinterpret_cast<f32x4*>(p + 4) = b;
 }
 
+// eight consecutive elements kept as loaded (16-bit types: four dwords), so a
+// row held across a loop iteration costs half the registers of its floats
+template <typename T> struct Packed8 { u32x4 v; };
+template <> struct Packed8<float> { f32x4 a, b; };
+
+template <typename T> __device__ __forceinline__ Packed8<T> load_packed(const T* p) {
+  return Packed8<T>{*reinterpret_cast<const u32x4*>(p)};
+}
+template <> __device__ __forceinline__ Packed8<float> load_packed<float>(const float* p) {
+  return Packed8<float>{*reinterpret_cast<const f32x4*>(p), *reinterpret_cast<const f32x4*>(p + 4)};
+}
+template <typename T> __device__ __forceinline__ void store_packed(T* p, const Packed8<T>& r) {
+  *reinterpret_cast<u32x4*>(p) = r.v;
+}
+template <> __device__ __forceinline__ void store_packed<float>(float* p, const Packed8<float>& r) {
+  *reinterpret_cast<f32x4*>(p) = r.a;
+  *reinterpret_cast<f32x4*>(p + 4) = r.b;
+}
+// hide a value's origin from the optimiser (an empty asm that "changes" it), so
+// products formed from it once are formed again rather than kept live
+template <typename T> __device__ __forceinline__ Packed8<T> opaque(Packed8<T> r) {
+  asm volatile("" : "+v"(r.v));
+  return r;
+}
+template <> __device__ __forceinline__ Packed8<float> opaque<float>(Packed8<float> r) {
+  asm volatile("" : "+v"(r.a), "+v"(r.b));
+  return r;
+}
+template <typename T> __device__ __forceinline__ void unpack(const Packed8<T>& r, float (&o)[8]);
+template <> __device__ __forceinline__ void unpack<bf16>(const Packed8<bf16>& r, float (&o)[8]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    o[2 * i] = __uint_as_float(r.v[i] << 16);
+    o[2 * i + 1] = __uint_as_float(r.v[i] & 0xffff0000u);
+  }
+}
+template <> __device__ __forceinline__ void unpack<f16>(const Packed8<f16>& r, float (&o)[8]) {
+  typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+  const h8 h = __builtin_bit_cast(h8, r.v);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) o[i] = (float)h[i];
+}
+template <> __device__ __forceinline__ void unpack<float>(const Packed8<float>& r, float (&o)[8]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    o[i] = r.a[i];
+    o[4 + i] = r.b[i];
+  }
+}
+
 // round a float through T and back
 template <typename T> __device__ __forceinline__ float round_t(float x) {
   return to_f(from_f<T>(x));
@@ -82,10 +132,14 @@ template <int LPR> __device__ __forceinline__ float row_sum(float v) {
 // ---------------------------------------------------------------------------
 // forward, vector path (width % 8 == 0)
 // ---------------------------------------------------------------------------
-template <typename T, int LPR, int NV>
+template <typename T, int LPR, int NV, bool FULL>
 __global__ __launch_bounds__(kThreads) void rmsnorm_fwd_vec(
     const T* __restrict__ x, const T* __restrict__ w, T* __restrict__ y,
     float* __restrict__ rstd, int64_t rows, int width, float eps) {
+  // FULL: every lane's NV vectors lie inside the row (width == 8 * LPR * NV).
+  // Otherwise a vector past the row end is loaded from the row's last vector
+  // (in bounds) and ignored, so no load sits behind a branch: loads behind
+  // per-vector branches are each waited for before the next is issued.
   constexpr int kRowsPerWave = kWave / LPR;
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
@@ -94,15 +148,20 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_fwd_vec(
   if (row >= rows) return;
   const int nvec = width / 8;
   const T* xr = x + row * width;
-  float v[NV][8];
-  float ss = 0.f;
+  Packed8<T> v[NV];
 #pragma unroll
   for (int k = 0; k < NV; ++k) {
     const int vi = sub + k * LPR;
-    if (vi < nvec) {
-      load8<T>(xr + vi * 8, v[k]);
+    v[k] = load_packed<T>(xr + (FULL ? vi : min(vi, nvec - 1)) * 8);
+  }
+  float ss = 0.f;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) ss = fmaf(v[k][i], v[k][i], ss);
+  for (int k = 0; k < NV; ++k) {
+    if (FULL || sub + k * LPR < nvec) {
+      float f[8];
+      unpack<T>(v[k], f);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ss = fmaf(f[i], f[i], ss);
     }
   }
   ss = row_sum<LPR>(ss);
@@ -112,13 +171,12 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_fwd_vec(
 #pragma unroll
   for (int k = 0; k < NV; ++k) {
     const int vi = sub + k * LPR;
-    if (vi < nvec) {
-      float wv[8], o[8];
-      load8<T>(w + vi * 8, wv);
+    float wv[8], f[8], o[8];
+    unpack<T>(load_packed<T>(w + (FULL ? vi : min(vi, nvec - 1)) * 8), wv);
+    unpack<T>(v[k], f);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) o[i] = wv[i] * round_t<T>(v[k][i] * r);
-      store8<T>(yr + vi * 8, o);
-    }
+    for (int i = 0; i < 8; ++i) o[i] = wv[i] * round_t<T>(f[i] * r);
+    if (FULL || vi < nvec) store8<T>(yr + vi * 8, o);
   }
 }
 
@@ -147,16 +205,34 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_fwd_scalar(
 // ---------------------------------------------------------------------------
 // backward, vector path.  Block b owns rows [b*slab, (b+1)*slab) and writes
 // one fp32 partial dW row into part[b]; rmsnorm_dw_reduce sums the partials
-// in block order.
+// in a fixed order.
+//
+// The kernel streams x and dy once, so its speed is the number of row bytes
+// in flight per CU.  Each wave owns one row (LPR = 64) or 64/LPR rows at a
+// time and, when registers allow (BwdShape::kPrefetch), issues the loads of
+// its next row before working on the current one.  Rows are held as loaded
+// (Packed8) and unpacked twice -- once for dW and the row dot product, once
+// for dx -- and w sits in LDS, so that two 8-wave blocks' worth of registers
+// (<= 256 per lane) hold the prefetched row, the current row and the fp32 dW
+// accumulators.
 // ---------------------------------------------------------------------------
-template <typename T, int LPR, int NV>
-__global__ __launch_bounds__(kThreads) void rmsnorm_bwd_vec(
+template <typename T, int NV, bool FULL> struct BwdShape {
+  // prefetch where the compiled kernel then still fits 256 VGPRs unspilled
+  static constexpr bool kPrefetch = NV <= 4 || (sizeof(T) == 2 && NV == 8 && FULL);
+  static constexpr int kWaves = NV <= 8 ? 8 : 4;
+  static constexpr int kThreads = kWaves * kWave;
+};
+
+template <typename T, int LPR, int NV, bool FULL>
+__global__ __launch_bounds__((BwdShape<T, NV, FULL>::kThreads)) void rmsnorm_bwd_vec(
     const T* __restrict__ dy, const T* __restrict__ x, const T* __restrict__ w,
     const float* __restrict__ rstd, T* __restrict__ dx, float* __restrict__ part,
     int64_t rows, int width, int64_t slab, int want_dx, int want_dw) {
+  using Shape = BwdShape<T, NV, FULL>;
   constexpr int kRowsPerWave = kWave / LPR;
-  constexpr int kRowsPerPass = (kThreads / kWave) * kRowsPerWave;
-  extern __shared__ float lds_dw[];  // [width] when want_dw
+  constexpr int kRowsPerPass = Shape::kWaves * kRowsPerWave;
+  extern __shared__ float lds_dw[];  // [width] fp32 dW, then w as T [width]
+  T* lds_w = reinterpret_cast<T*>(lds_dw + width);
   const int lane = threadIdx.x & (kWave - 1);
   const int wave = threadIdx.x / kWave;
   const int sub = lane % LPR;
@@ -165,48 +241,87 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_bwd_vec(
   const int64_t r0 = (int64_t)blockIdx.x * slab;
   const int64_t r1 = min(rows, r0 + slab);
 
-  float wv[NV][8];
+  for (int v = threadIdx.x; v < nvec; v += Shape::kThreads)
+    store_packed<T>(lds_w + v * 8, load_packed<T>(w + v * 8));
+
+  // vector k of this lane: vi = sub + k*LPR; past the row end it reads the
+  // row's last vector (in bounds) and is masked out
+  auto col = [&](int k) { return FULL ? sub + k * LPR : min(sub + k * LPR, nvec - 1); };
+  auto valid = [&](int k) { return FULL || sub + k * LPR < nvec; };
+  auto load_row = [&](int64_t row, Packed8<T> (&xo)[NV], Packed8<T> (&go)[NV], float& ro) {
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      xo[k] = load_packed<T>(x + row * width + col(k) * 8);
+      go[k] = load_packed<T>(dy + row * width + col(k) * 8);
+    }
+    ro = rstd[row];
+  };
+
   float acc[NV][8];
 #pragma unroll
-  for (int k = 0; k < NV; ++k) {
-    const int vi = sub + k * LPR;
+  for (int k = 0; k < NV; ++k)
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc[k][i] = 0.f;
-    if (vi < nvec) load8<T>(w + vi * 8, wv[k]);
-  }
   const float inv_w = 1.f / (float)width;
-  for (int64_t row = r0 + rsub; row < r1; row += kRowsPerPass) {
-    const float r = rstd[row];
-    float xv[NV][8], gv[NV][8];
+  int64_t row = r0 + rsub;
+  Packed8<T> xa[NV], ga[NV];
+  float ra = 0.f;
+  if (row < r1) load_row(row, xa, ga, ra);
+  __syncthreads();  // lds_w
+  for (; row < r1; row += kRowsPerPass) {
+    const int64_t next = row + kRowsPerPass;
+    Packed8<T> xb[NV], gb[NV];
+    float rb = 0.f;
+    if (Shape::kPrefetch && next < r1) load_row(next, xb, gb, rb);
     float dot = 0.f;
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
-      const int vi = sub + k * LPR;
-      if (vi < nvec) {
-        float dv[8];
-        load8<T>(x + row * width + vi * 8, xv[k]);
-        load8<T>(dy + row * width + vi * 8, dv);
+      if (valid(k)) {
+        float xv[8], dv[8], wv[8];
+        unpack<T>(xa[k], xv);
+        unpack<T>(ga[k], dv);
+        unpack<T>(load_packed<T>(lds_w + col(k) * 8), wv);
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-          acc[k][i] = fmaf(dv[i] * xv[k][i], r, acc[k][i]);
-          gv[k][i] = dv[i] * wv[k][i];
-          xv[k][i] *= r;  // xhat
-          dot = fmaf(gv[k][i], xv[k][i], dot);
+          acc[k][i] = fmaf(dv[i] * xv[i], ra, acc[k][i]);
+          dot = fmaf(dv[i] * wv[i], xv[i] * ra, dot);
         }
       }
     }
+    // finish the first pass here: otherwise the optimiser sinks the dot
+    // product into the dx branch and the dW update past it, keeping the
+    // unpacked row live across the second pass
+    asm volatile("" : "+v"(dot));
+#pragma unroll
+    for (int k = 0; k < NV; ++k)
+      asm volatile("" : "+v"(acc[k][0]), "+v"(acc[k][1]), "+v"(acc[k][2]), "+v"(acc[k][3]),
+                   "+v"(acc[k][4]), "+v"(acc[k][5]), "+v"(acc[k][6]), "+v"(acc[k][7]));
     if (want_dx) {
       dot = row_sum<LPR>(dot) * inv_w;
 #pragma unroll
       for (int k = 0; k < NV; ++k) {
-        const int vi = sub + k * LPR;
-        if (vi < nvec) {
-          float o[8];
+        if (valid(k)) {
+          // recompute dy*w and xhat instead of keeping the first pass's
+          // 16*NV products live across the row sum
+          float xv[8], dv[8], wv[8], o[8];
+          unpack<T>(opaque<T>(xa[k]), xv);
+          unpack<T>(opaque<T>(ga[k]), dv);
+          unpack<T>(opaque<T>(load_packed<T>(lds_w + col(k) * 8)), wv);
 #pragma unroll
-          for (int i = 0; i < 8; ++i) o[i] = r * (gv[k][i] - xv[k][i] * dot);
-          store8<T>(dx + row * width + vi * 8, o);
+          for (int i = 0; i < 8; ++i) o[i] = ra * (dv[i] * wv[i] - (xv[i] * ra) * dot);
+          store8<T>(dx + row * width + col(k) * 8, o);
         }
       }
+    }
+    if (Shape::kPrefetch) {
+#pragma unroll
+      for (int k = 0; k < NV; ++k) {
+        xa[k] = xb[k];
+        ga[k] = gb[k];
+      }
+      ra = rb;
+    } else if (next < r1) {
+      load_row(next, xa, ga, ra);
     }
   }
   if (!want_dw) return;
@@ -216,11 +331,10 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_bwd_vec(
     if (rsub == g) {
 #pragma unroll
       for (int k = 0; k < NV; ++k) {
-        const int vi = sub + k * LPR;
-        if (vi < nvec) {
+        if (valid(k)) {
 #pragma unroll
           for (int i = 0; i < 8; ++i) {
-            float* p = &lds_dw[vi * 8 + i];
+            float* p = &lds_dw[col(k) * 8 + i];
             *p = (g == 0) ? acc[k][i] : (*p + acc[k][i]);
           }
         }
@@ -228,7 +342,8 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_bwd_vec(
     }
     __syncthreads();
   }
-  for (int c = threadIdx.x; c < width; c += kThreads) part[(int64_t)blockIdx.x * width + c] = lds_dw[c];
+  for (int c = threadIdx.x; c < width; c += Shape::kThreads)
+    part[(int64_t)blockIdx.x * width + c] = lds_dw[c];
 }
 
 // backward, scalar path (any width): the block's 256 threads work on one
@@ -274,15 +389,47 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_bwd_scalar(
   for (int c = threadIdx.x; c < width; c += kThreads) part[(int64_t)blockIdx.x * width + c] = lds_dw[c];
 }
 
-// dW = T(sum over partial rows, in order)
+// dW = T(sum over partial rows in a fixed order).  A block owns 64 columns
+// (one per lane, so each load is a 256-byte row piece); its 16 waves each sum
+// a contiguous run of partial rows, sixteen independent loads at a time, and
+// wave 0 adds the 16 wave sums in wave order.
+constexpr int kReduceWaves = 16;
+
 template <typename T>
-__global__ __launch_bounds__(kThreads) void rmsnorm_dw_reduce(
+__global__ __launch_bounds__(kReduceWaves * kWave) void rmsnorm_dw_reduce(
     const float* __restrict__ part, T* __restrict__ dw, int nparts, int width) {
-  const int c = blockIdx.x * kThreads + threadIdx.x;
-  if (c >= width) return;
+  __shared__ float red[kReduceWaves][kWave];
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wave = threadIdx.x / kWave;
+  const int c = blockIdx.x * kWave + lane;
+  const int cc = min(c, width - 1);
+  const int per = (nparts + kReduceWaves - 1) / kReduceWaves;
+  const int p0 = min(nparts, wave * per);
+  const int p1 = min(nparts, p0 + per);
   float s = 0.f;
-  for (int p = 0; p < nparts; ++p) s += part[(int64_t)p * width + c];
-  dw[c] = from_f<T>(s);
+  int p = p0;
+  for (; p + 16 <= p1; p += 16) {
+    float v[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) v[j] = part[(int64_t)(p + j) * width + cc];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) s += v[j];
+  }
+  for (; p < p1; ++p) s += part[(int64_t)p * width + cc];
+  red[wave][lane] = s;
+  __syncthreads();
+  if (wave != 0 || c >= width) return;
+  float t = red[0][lane];
+#pragma unroll
+  for (int q = 1; q < kReduceWaves; ++q) t += red[q][lane];
+  dw[c] = from_f<T>(t);
+}
+
+// dW of zero rows
+template <typename T>
+__global__ __launch_bounds__(kThreads) void zero_fill(T* __restrict__ out, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  if (i < n) out[i] = from_f<T>(0.f);
 }
 
 // --------------------------------------------------------------------------
@@ -309,13 +456,14 @@ Geometry pick(int64_t width, int dtype) {
   return g;
 }
 
-constexpr int64_t kMaxParts = 256;
-
-int64_t bwd_parts(int64_t rows) {
-  // at least 32 rows per block so the partial rows stay a small fraction of
-  // the traffic; at most kMaxParts blocks
+int64_t bwd_parts(int64_t rows, int64_t width) {
+  // at least 32 rows per block, so the partial rows (written and read once)
+  // stay within 8/(6*32) of the kernel's traffic; at most 256 blocks for rows
+  // of 2048 and more elements -- one 8-wave block per CU is enough bytes in
+  // flight there -- and up to 1024 for narrower rows, whose blocks carry less
   int64_t parts = (rows + 31) / 32;
-  if (parts > kMaxParts) parts = kMaxParts;
+  const int64_t max_parts = width >= 2048 ? 256 : 1024;
+  if (parts > max_parts) parts = max_parts;
   if (parts < 1) parts = 1;
   return parts;
 }
@@ -332,10 +480,16 @@ int launch_fwd(const void* x, const void* w, void* y, float* rstd, int64_t rows,
   }
   const int64_t rows_per_block = 4 * (64 / g.lpr);
   const dim3 grid((unsigned)((rows + rows_per_block - 1) / rows_per_block));
+  const bool full = width == 8 * g.lpr * g.nv;
 #define TS_FWD(LPR, NV)                                                                     \
   if (g.lpr == LPR && g.nv == NV) {                                                         \
-    { ts::TimedLaunch timed_("rmsnorm.rmsnorm_fwd_vec", s); hipLaunchKernelGGL((rmsnorm_fwd_vec<T, LPR, NV>), grid, dim3(kThreads), 0, s,           \
-                       (const T*)x, (const T*)w, (T*)y, rstd, rows, width, eps); }            \
+    ts::TimedLaunch timed_("rmsnorm.rmsnorm_fwd_vec", s);                                   \
+    if (full)                                                                               \
+      hipLaunchKernelGGL((rmsnorm_fwd_vec<T, LPR, NV, true>), grid, dim3(kThreads), 0, s,   \
+                         (const T*)x, (const T*)w, (T*)y, rstd, rows, width, eps);          \
+    else                                                                                    \
+      hipLaunchKernelGGL((rmsnorm_fwd_vec<T, LPR, NV, false>), grid, dim3(kThreads), 0, s,  \
+                         (const T*)x, (const T*)w, (T*)y, rstd, rows, width, eps);          \
     return check_launch("ts_rmsnorm_fwd");                                                  \
   }
   TS_FWD(4, 1) TS_FWD(8, 1) TS_FWD(16, 1) TS_FWD(32, 1) TS_FWD(64, 1)
@@ -349,7 +503,7 @@ template <typename T>
 int launch_bwd(const void* dy, const void* x, const void* w, const float* rstd, void* dx,
                void* dw, float* part, int64_t rows, int width, hipStream_t s) {
   const Geometry g = pick(width, 0);
-  const int64_t parts = bwd_parts(rows);
+  const int64_t parts = bwd_parts(rows, width);
   const int64_t slab = (rows + parts - 1) / parts;
   const int want_dx = dx != nullptr, want_dw = dw != nullptr;
   if (g.lpr == 0) {
@@ -362,14 +516,24 @@ int launch_bwd(const void* dy, const void* x, const void* w, const float* rstd, 
                        (const T*)dy, (const T*)x, (const T*)w, rstd, (T*)dx, part, rows, width,
                        slab, want_dx, want_dw); }
   } else {
-    const size_t lds = want_dw ? (size_t)width * sizeof(float) : 0;
+    // LDS: the fp32 dW row, then w as T
+    const size_t lds = (size_t)width * (sizeof(float) + sizeof(T));
     const dim3 grid((unsigned)parts);
+    const bool full = width == 8 * g.lpr * g.nv;
     bool launched = false;
 #define TS_BWD(LPR, NV)                                                                      \
   if (!launched && g.lpr == LPR && g.nv == NV) {                                             \
-    { ts::TimedLaunch timed_("rmsnorm.rmsnorm_bwd_vec", s); hipLaunchKernelGGL((rmsnorm_bwd_vec<T, LPR, NV>), grid, dim3(kThreads), lds, s,          \
-                       (const T*)dy, (const T*)x, (const T*)w, rstd, (T*)dx, part, rows,     \
-                       width, slab, want_dx, want_dw); }                                        \
+    ts::TimedLaunch timed_("rmsnorm.rmsnorm_bwd_vec", s);                                    \
+    if (full)                                                                                \
+      hipLaunchKernelGGL((rmsnorm_bwd_vec<T, LPR, NV, true>), grid,                          \
+                         dim3(BwdShape<T, NV, true>::kThreads), lds, s,                      \
+                         (const T*)dy, (const T*)x, (const T*)w, rstd, (T*)dx, part, rows,   \
+                         width, slab, want_dx, want_dw);                                     \
+    else                                                                                     \
+      hipLaunchKernelGGL((rmsnorm_bwd_vec<T, LPR, NV, false>), grid,                         \
+                         dim3(BwdShape<T, NV, false>::kThreads), lds, s,                     \
+                         (const T*)dy, (const T*)x, (const T*)w, rstd, (T*)dx, part, rows,   \
+                         width, slab, want_dx, want_dw);                                     \
     launched = true;                                                                         \
   }
     TS_BWD(4, 1) TS_BWD(8, 1) TS_BWD(16, 1) TS_BWD(32, 1) TS_BWD(64, 1)
@@ -382,9 +546,16 @@ int launch_bwd(const void* dy, const void* x, const void* w, const float* rstd, 
   }
   int st = check_launch("ts_rmsnorm_bwd");
   if (st != TS_OK || !want_dw) return st;
-  { ts::TimedLaunch timed_("rmsnorm.rmsnorm_dw_reduce", s); hipLaunchKernelGGL(rmsnorm_dw_reduce<T>, dim3((unsigned)((width + kThreads - 1) / kThreads)),
-                     dim3(kThreads), 0, s, (const float*)part, (T*)dw, (int)parts, width); }
+  { ts::TimedLaunch timed_("rmsnorm.rmsnorm_dw_reduce", s); hipLaunchKernelGGL(rmsnorm_dw_reduce<T>, dim3((unsigned)((width + kWave - 1) / kWave)),
+                     dim3(kReduceWaves * kWave), 0, s, (const float*)part, (T*)dw, (int)parts, width); }
   return check_launch("ts_rmsnorm_bwd (dW reduce)");
+}
+
+template <typename T>
+int launch_zero(void* out, int64_t n, hipStream_t s) {
+  hipLaunchKernelGGL(zero_fill<T>, dim3((unsigned)((n + kThreads - 1) / kThreads)), dim3(kThreads), 0, s,
+                     (T*)out, n);
+  return check_launch("ts_rmsnorm_bwd (zero dW)");
 }
 
 }  // namespace
@@ -411,7 +582,7 @@ int ts_rmsnorm_fwd(const void* x, const void* w, void* y, float* rstd, int64_t r
 
 int64_t ts_rmsnorm_bwd_workspace(int64_t rows, int64_t width) {
   if (rows <= 0 || width <= 0) return 0;
-  return ts::bwd_parts(rows) * width * (int64_t)sizeof(float);
+  return ts::bwd_parts(rows, width) * width * (int64_t)sizeof(float);
 }
 
 int ts_rmsnorm_bwd(const void* dy, const void* x, const void* w, const float* rstd, void* dx,
@@ -423,12 +594,15 @@ int ts_rmsnorm_bwd(const void* dy, const void* x, const void* w, const float* rs
                (long long)width);
   hipStream_t s = (hipStream_t)stream;
   if (rows == 0) {
-    if (dw) {
-      const int64_t esz = dtype == TS_F32 ? 4 : 2;
-      if (hipMemsetAsync(dw, 0, (size_t)(width * esz), s) != hipSuccess)
-        return ts::check_launch("ts_rmsnorm_bwd (zero dW)");
+    // a fill kernel rather than a memset node, so the call can be captured
+    if (!dw) return TS_OK;
+    switch (dtype) {
+      case TS_BF16: return ts::launch_zero<ts::bf16>(dw, width, s);
+      case TS_F16: return ts::launch_zero<ts::f16>(dw, width, s);
+      case TS_F32: return ts::launch_zero<float>(dw, width, s);
     }
-    return TS_OK;
+    ts::set_error("ts_rmsnorm_bwd: unsupported dtype code %d", dtype);
+    return TS_ERR_INVALID;
   }
   if (dw) {
     const int64_t need = ts_rmsnorm_bwd_workspace(rows, width);
