@@ -142,7 +142,7 @@ typedef struct ts_attn_problem {
   int32_t hkv;
   int32_t head_dim;
   float scale;
-  int32_t q_block;  /* rows per q_work item: 32 * 4 / ts_attn_heads_per_block */
+  int32_t q_block;  /* rows per q_work item: ts_attn_q_block(hq / hkv) */
   int32_t kv_block; /* keys per kv_work item: ts_attn_kv_block(hq / hkv) */
   int64_t q_rows;   /* rows of Q/O/dO/dQ */
   /* Launch order.  The work lists are sorted longest first; their first
@@ -155,9 +155,12 @@ typedef struct ts_attn_problem {
 } ts_attn_problem;
 
 /* Query heads one forward/dQ work-group processes for a GQA group size
- * (hq / hkv): 4 when it divides the group, else 2, else 1.  The rows per
- * q_work item are 32 * 4 / that value. */
+ * (hq / hkv): 4 when it divides the group, else 2, else 1. */
 int ts_attn_heads_per_block(int group);
+
+/* Query rows per forward/dQ work item for a GQA group size:
+ * 32 * 4 / ts_attn_heads_per_block(group). */
+int ts_attn_q_block(int group);
 
 /* Keys per dK/dV work-group for a GQA group size: 48 when 4 divides the
  * group (one wave per query head), else 64. */
@@ -282,6 +285,14 @@ int ts_probe_layouts(const void* a, const void* b, float* d16, float* d32,
  * buffer range-check behaviour. */
 int ts_probe_lds(const void* src, const int* perm, void* dma_out, void* tr_out, void* buf_out,
                  int valid_bytes, void* stream);
+
+/* Runs, in one wave over in[0..63], the cross-row reductions the kernels use
+ * (maximum and sum over lanes l, l ^ 16, l ^ 32, l ^ 48 by v_permlane16_swap
+ * and v_permlane32_swap) and the raw swaps.  Writes out[0..383]: the maximum,
+ * the sum, the two results of v_permlane16_swap(in, in) and the two of
+ * v_permlane32_swap(in, in), 64 floats each.  Used by the test suite to pin
+ * the lane semantics (no counterpart in the reference). */
+int ts_probe_lanes(const float* in, float* out, void* stream);
 
 #ifdef __cplusplus
 }

@@ -108,3 +108,26 @@ def test_lds_dma_and_transpose_read_layouts(cuda):
     for lane in range(64):
         rows = set((t[lane] // 4).tolist())
         assert all(16 * (lane // 16) <= r < 16 * (lane // 16) + 16 for r in rows), (lane, t[lane])
+
+
+def test_cross_row_lane_reductions(cuda):
+    """rows_max4 / rows_sum4 combine lanes l, l^16, l^32, l^48 (the attention
+    softmax's column reductions), pinned against numpy on distinct values."""
+    lib = _lib.require_library()
+    x = np.random.default_rng(5).permutation(64).astype(np.float32) - 20.0
+    src = torch.tensor(x, device=cuda)
+    out = torch.empty(6 * 64, dtype=torch.float32, device=cuda)
+    print("probe: ts_probe_lanes", flush=True)
+    _lib.check(lib.ts_probe_lanes(src.data_ptr(), out.data_ptr(), _lib.stream_of(src)), "ts_probe_lanes")
+    torch.cuda.synchronize()
+    got = out.view(6, 64).cpu().numpy()
+    rows = x.reshape(4, 16)
+    np.testing.assert_array_equal(got[0], np.tile(rows.max(axis=0), 4))
+    np.testing.assert_array_equal(got[1], np.tile(rows.sum(axis=0), 4))
+    # each swap pairs rows 0/1 and 2/3 (16) or the two halves (32); together
+    # the two results of one swap hold both members of every pair
+    for k, partner in ((2, 16), (4, 32)):
+        pair = np.sort(np.stack([got[k], got[k + 1]]), axis=0)
+        want = np.sort(np.stack([x, x[np.arange(64) ^ partner]]), axis=0)
+        np.testing.assert_array_equal(pair, want)
+    print("permlane16_swap:", got[2][:20].tolist(), got[3][:20].tolist(), flush=True)

@@ -43,6 +43,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "ts_rmsnorm_bwd": (_INT, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _INT, _P]),
     "ts_probe_layouts": (_INT, [_P, _P, _P, _P, _P, _P, _P]),
     "ts_probe_lds": (_INT, [_P, _P, _P, _P, _P, _INT, _P]),
+    "ts_probe_lanes": (_INT, [_P, _P, _P]),
     "ts_timing_enable": (_INT, [_INT]),
     "ts_timing_reset": (_INT, []),
     "ts_timing_read": (_INT, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_I64)]),
@@ -56,6 +57,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "ts_logprob_grad_hidden": (_INT, [_P, _I64, _P, _I64, _I64, _I64, _I64, _P, _I64, _P]),
     "ts_attn_heads_per_block": (_INT, [_INT]),
     "ts_attn_kv_block": (_INT, [_INT]),
+    "ts_attn_q_block": (_INT, [_INT]),
     "ts_attn_fwd": (_INT, [ctypes.POINTER(AttnProblem), AttnRows, AttnRows, _P, _I64, _P]),
     "ts_attn_bwd": (
         _INT,

@@ -65,6 +65,7 @@ def heads_per_block(group: int) -> int:
 
 
 def q_block_rows(hq: int, hkv: int) -> int:
+    """Query rows per forward/dQ work item (mirror of ts_attn_q_block)."""
     return 32 * 4 // heads_per_block(hq // hkv)
 
 

@@ -44,8 +44,8 @@ int validate(const ts_attn_problem* p, const char* what) {
   TS_CHECK_ARG(p->hq > 0 && p->hkv > 0 && p->hq % p->hkv == 0, "%s: hq %d not a multiple of hkv %d",
                what, p->hq, p->hkv);
   const int gc = heads_per_block(p->hq / p->hkv);
-  TS_CHECK_ARG(p->q_block == 32 * 4 / gc, "%s: q_block %d, expected %d for group %d", what,
-               p->q_block, 32 * 4 / gc, p->hq / p->hkv);
+  TS_CHECK_ARG(p->q_block == q_block_rows(p->hq / p->hkv), "%s: q_block %d, expected %d for group %d",
+               what, p->q_block, q_block_rows(p->hq / p->hkv), p->hq / p->hkv);
   TS_CHECK_ARG(p->kv_block == kv_block_keys(p->hq / p->hkv), "%s: kv_block %d, expected %d", what,
                p->kv_block, kv_block_keys(p->hq / p->hkv));
   TS_CHECK_ARG(p->n_q_work >= 0 && p->n_kv_work >= 0 && p->n_segs >= 0 && p->n_runs >= 0,
@@ -67,6 +67,7 @@ extern "C" {
 int ts_attn_heads_per_block(int group) { return group > 0 ? ts::attn::heads_per_block(group) : 0; }
 
 int ts_attn_kv_block(int group) { return group > 0 ? ts::attn::kv_block_keys(group) : 0; }
+int ts_attn_q_block(int group) { return group > 0 ? ts::attn::q_block_rows(group) : 0; }
 
 int ts_attn_fwd(const ts_attn_problem* problem, ts_attn_rows q, ts_attn_rows out, float* lse,
                 int64_t lse_ld, void* stream) {

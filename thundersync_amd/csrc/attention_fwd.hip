@@ -254,8 +254,7 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_wave_kernel(ts_attn_problem P
       for (int qb = 0; qb < 2; ++qb) {
         float mx = fmaxf(fmaxf(fmaxf(sc[0][qb][0], sc[0][qb][1]), fmaxf(sc[0][qb][2], sc[0][qb][3])),
                          fmaxf(fmaxf(sc[1][qb][0], sc[1][qb][1]), fmaxf(sc[1][qb][2], sc[1][qb][3])));
-        mx = fmaxf(mx, shfl_xor(mx, 16));
-        mx = fmaxf(mx, shfl_xor(mx, 32));
+        mx = rows_max4(mx);
         const float mt = mx * c;  // maximum in log2 units (-inf if the column sees none of these keys)
         const bool move = mt > m[qb] + kRescaleSlack;
         if (__builtin_amdgcn_ballot_w64(move) != 0) {
@@ -309,9 +308,7 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_wave_kernel(ts_attn_problem P
   // O = acc / l; acc[mb][qb] lane holds d = 16 mb + 4 g4 + i of row q0 + 16 qb + j16
 #pragma unroll
   for (int qb = 0; qb < 2; ++qb) {
-    float ls = l[qb];
-    ls += shfl_xor(ls, 16);
-    ls += shfl_xor(ls, 32);
+    const float ls = rows_sum4(l[qb]);
     const int row = q0 + 16 * qb + j16;
     if (row >= T) continue;
     const float inv = ls > 0.f ? 1.f / ls : 0.f;

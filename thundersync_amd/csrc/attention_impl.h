@@ -90,12 +90,13 @@ __device__ __forceinline__ bf16x8 pack8(const float* x) {
   return as_bf16x8(r);
 }
 
-// Load a wave's 32 query rows x 128 as B operands of S^T = K Q^T:
+// Load a wave's 16 NQB query rows x 128 as B operands of S^T = K Q^T:
 // reg[qb][ks] = row (16 qb + (lane & 15)), columns 32 ks + 8 (lane >> 4) .. +7.
-__device__ __forceinline__ void load_rows_b(bf16x8 reg[2][4], const bf16* base, int64_t row_stride,
+template <int NQB>
+__device__ __forceinline__ void load_rows_b(bf16x8 (&reg)[NQB][4], const bf16* base, int64_t row_stride,
                                             int nvalid, int lane) {
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb) {
+  for (int qb = 0; qb < NQB; ++qb) {
     const int row = 16 * qb + (lane & 15);
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
@@ -255,6 +256,9 @@ inline int heads_per_block(int group) {
   if (group % 2 == 0) return 2;
   return 1;
 }
+
+// query rows per forward / dQ work item: 32 per query head of the work-group
+inline int q_block_rows(int group) { return 32 * 4 / heads_per_block(group); }
 
 // keys per dK/dV work-group: 48 for the one-wave-per-head kernel (its 192
 // dK/dV accumulators and 48 S/dP values fill the 256 AGPRs), else 64

@@ -191,6 +191,24 @@ __device__ __forceinline__ void buffer_dma16_untracked(u32x4 desc, void* lds, in
 __device__ __forceinline__ float shfl_xor(float v, int mask) {
   return __shfl_xor(v, mask, kWave);
 }
+// Reductions over the four 16-lane rows of a wave at one position in the row
+// (lanes l, l ^ 16, l ^ 32, l ^ 48) with gfx950's lane-swap instructions,
+// which are VALU operations (no LDS round trip as with ds_bpermute).
+// v_permlane16_swap of a value with itself returns the rows as (0, 0, 2, 2)
+// and (1, 1, 3, 3), v_permlane32_swap the halves as (lo, lo) and (hi, hi);
+// every lane therefore combines the same operands in the same order.
+__device__ __forceinline__ float rows_max4(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float rows_sum4(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) v += shfl_xor(v, m);

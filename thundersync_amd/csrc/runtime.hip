@@ -80,6 +80,22 @@ __global__ __launch_bounds__(64) void probe_lds_kernel(const u32x4* __restrict__
   tr_out[l] = o;
 }
 
+// out[0:64] rows_max4, out[64:128] rows_sum4 of in[lane]; out[128:192] and
+// out[192:256] the two results of v_permlane16_swap(in, in), out[256:320]
+// and out[320:384] those of v_permlane32_swap(in, in)
+__global__ void probe_lanes_kernel(const float* __restrict__ in, float* __restrict__ out) {
+  const int l = threadIdx.x;
+  const float x = in[l];
+  out[l] = rows_max4(x);
+  out[64 + l] = rows_sum4(x);
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  out[128 + l] = __uint_as_float(a[0]);
+  out[192 + l] = __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  out[256 + l] = __uint_as_float(b[0]);
+  out[320 + l] = __uint_as_float(b[1]);
+}
+
 }  // namespace ts
 
 extern "C" {
@@ -95,6 +111,12 @@ int ts_probe_layouts(const void* a, const void* b, float* d16, float* d32,
                      (const ts::u32x4*)a, (const ts::u32x4*)b, d16, d32,
                      (const ts::u32x4*)t_in, (ts::u32x4*)t_out);
   return ts::check_launch("ts_probe_layouts");
+}
+
+int ts_probe_lanes(const float* in, float* out, void* stream) {
+  TS_CHECK_ARG(in && out, "ts_probe_lanes: null pointer");
+  hipLaunchKernelGGL(ts::probe_lanes_kernel, dim3(1), dim3(64), 0, (hipStream_t)stream, in, out);
+  return ts::check_launch("ts_probe_lanes");
 }
 
 int ts_probe_lds(const void* src, const int* perm, void* dma_out, void* tr_out, void* buf_out,
