@@ -154,8 +154,8 @@ __global__ __launch_bounds__(kThreads, 2) void dkdv_kernel(ts_attn_problem P, ts
 //
 // A work-group owns 16 KB keys of one run and one KV head; wave w handles query
 // heads w, w + 4, ... of the group over all of them, so a wave's LDS reads of
-// its head's Q/dO tile feed 16 KB keys of MFMA work.  K^T operands stay in
-// registers; the V tile sits in LDS.  Each wave streams its head's 32-row
+// its head's Q/dO tile feed 16 KB keys of MFMA work.  The K^T and V^T
+// operands stay in registers.  Each wave streams its head's 32-row
 // Q/dO tiles and their 32 (lse * log2 e, delta) pairs into its own
 // double-buffered LDS region with buffer_load ... lds: the buffer resource of
 // a tile covers exactly its valid rows, so rows past a segment's end arrive
@@ -177,7 +177,6 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_wave_kernel(ts_attn_problem 
                                                                 ts_attn_rows dO,
                                                                 const float* __restrict__ rowstats,
                                                                 int64_t lse_ld) {
-  __shared__ __attribute__((aligned(16))) bf16 s_v[16 * KB * D];
   // per wave and stage: Q tile, dO tile, then 32 (lse2, delta) pairs
   __shared__ __attribute__((aligned(16))) bf16 s_b0[4][kStage32];
   __shared__ __attribute__((aligned(16))) bf16 s_b1[4][kStage32];
@@ -216,22 +215,18 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_wave_kernel(ts_attn_problem 
     doff[t] = (int)(((4 * t + g4) * dO.row_stride + dchunk[t]) * 2);
   }
 
-  // V tile (rows past the run arrive as zeros); wave w issues instructions w, w + 4, ...
-  {
-    const bf16* vb = (const bf16*)run.v + (int64_t)k0 * run.v_row_stride + (int64_t)hk * run.v_head_stride;
-    const rsrc_t rv = make_rsrc(vb, (uint32_t)(nkeys * run.v_row_stride * 2));
-    for (int t = wave; t < 4 * KB; t += 4)
-      buffer_dma16(rv, s_v + t * 512, (int)(((4 * t + g4) * run.v_row_stride + dchunk[t & 3]) * 2));
-  }
-  // K^T operands: kreg[kb][ks] = K[k0 + 16 kb + j16][32 ks + 8 g4 ..]
-  bf16x8 kreg[KB][4];
+  // K^T and V^T operands: kreg[kb][ks] = K[k0 + 16 kb + j16][32 ks + 8 g4 ..], vreg likewise
+  bf16x8 kreg[KB][4], vreg[KB][4];
 #pragma unroll
   for (int kb = 0; kb < KB; ++kb) {
     const int key = 16 * kb + j16;
     const bf16* kp = (const bf16*)run.k + (int64_t)(k0 + key) * run.k_row_stride + (int64_t)hk * run.k_head_stride;
+    const bf16* vp = (const bf16*)run.v + (int64_t)(k0 + key) * run.v_row_stride + (int64_t)hk * run.v_head_stride;
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
+    for (int ks = 0; ks < 4; ++ks) {
       kreg[kb][ks] = as_bf16x8(key < nkeys ? ld16(kp + 32 * ks + 8 * g4) : u32x4{0u, 0u, 0u, 0u});
+      vreg[kb][ks] = as_bf16x8(key < nkeys ? ld16(vp + 32 * ks + 8 * g4) : u32x4{0u, 0u, 0u, 0u});
+    }
   }
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
@@ -321,11 +316,10 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_wave_kernel(ts_attn_problem 
         }
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) {
-          const bf16x8 vb = as_bf16x8(ld16(s_v + ro[ks] + 16 * kb * D));
-#pragma unroll
+  #pragma unroll
           for (int qb = 0; qb < 2; ++qb) {
             sc[qb][kb] = mfma16(aq[qb], kreg[kb][ks], sc[qb][kb]);
-            dp[qb][kb] = mfma16(ad[qb], vb, dp[qb][kb]);
+            dp[qb][kb] = mfma16(ad[qb], vreg[kb][ks], dp[qb][kb]);
           }
         }
       }

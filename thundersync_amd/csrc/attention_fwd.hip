@@ -85,8 +85,7 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_kernel(ts_attn_problem P, ts_
         for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
           for (int i = 0; i < 4; ++i) mx = fmaxf(mx, s[kb][qb][i]);
-        mx = fmaxf(mx, shfl_xor(mx, 16));
-        mx = fmaxf(mx, shfl_xor(mx, 32));
+        mx = rows_max4(mx);
         const float mnew = fmaxf(m[qb], mx);
         const float mref = (mnew == neg_inf()) ? 0.f : mnew;
         const float alpha = fast_exp2(m[qb] - mref);
@@ -130,9 +129,7 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_kernel(ts_attn_problem P, ts_
   if (!active) return;
 #pragma unroll
   for (int qb = 0; qb < 2; ++qb) {
-    float l = lsum[qb];
-    l += shfl_xor(l, 16);
-    l += shfl_xor(l, 32);
+    const float l = rows_sum4(lsum[qb]);
     const int row = wq0 + 16 * qb + (lane & 15);
     if (row >= T) continue;
     const float inv = l > 0.f ? 1.f / l : 0.f;

@@ -178,7 +178,8 @@ __device__ __forceinline__ u32x4 raw_descriptor(const void* base, uint32_t bytes
 // wave) and a barrier before other waves read the data.  `lds` must be
 // wave-uniform; M0 carries it.
 __device__ __forceinline__ void buffer_dma16_untracked(u32x4 desc, void* lds, int voffset) {
-  const uint32_t m0 = (uint32_t)(uintptr_t)(lds_void*)lds;
+  // the LDS address is wave-uniform; readfirstlane keeps it in an SGPR
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void*)lds);
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
                :
                : "s"(m0), "v"(voffset), "s"(desc)
