@@ -19,7 +19,10 @@ from thundersync_amd.rms_norm import FP32RMSNormVJP, rms_norm_backward, rms_norm
 
 pytestmark = pytest.mark.gpu
 
-SHAPES = [(3, 128), (129, 128), (64, 4096), (257, 4096), (16, 32), (7, 40), (5, 200), (2, 5), (33, 8192), (4, 12288)]
+SHAPES = [(3, 128), (129, 128), (64, 4096), (257, 4096), (16, 32), (7, 40), (5, 200), (2, 5), (33, 8192), (4, 12288),
+          # backward variants: 8 vectors per lane, part empty (3584); 16 vectors, part empty, four
+          # waves (5120); 282 partial rows of 32 (9000 x 1024); 1024 partial rows of 69 rows (70000 x 128)
+          (37, 3584), (19, 5120), (9000, 1024), (70000, 128)]
 
 
 def ulp(dtype):
