@@ -221,7 +221,8 @@ int ts_logprob_fwd(const void* hidden, int64_t ld_hidden, const void* weight,
                    void* stream);
 
 /* weight_t [dim, ld_t] = W^T with columns [vocab, ld_t) zero (ld_t % 8 == 0,
- * ld_t >= vocab): the K-contiguous operand of ts_logprob_grad_hidden. */
+ * ld_t >= vocab; dim and ld_weight multiples of 8, both pointers 16-byte
+ * aligned): the K-contiguous operand of ts_logprob_grad_hidden. */
 int ts_logprob_weight_t(const void* weight, int64_t ld_weight, int64_t vocab,
                         int64_t dim, void* weight_t, int64_t ld_t, void* stream);
 

@@ -164,3 +164,22 @@ def test_c3_full_size_sampled_rows(cuda):
     torch.testing.assert_close(lp[sample].cpu(), want_lp, rtol=0, atol=1e-3)
     torch.testing.assert_close(ent[sample].cpu(), want_ent, rtol=0, atol=1e-3)
     rel_close(hs.grad[sample], want_gh, 1e-2, "grad hidden (sampled rows)")
+
+
+@pytest.mark.parametrize("v,d", [(1001, 136), (513, 4096), (8, 8)])
+def test_weight_transpose_exact(cuda, v, d):
+    """ts_logprob_weight_t: W^T bit for bit, columns [vocab, ld_t) zero."""
+    from thundersync_amd import _lib
+
+    print(f"weight transpose vocab={v} dim={d}", flush=True)
+    lib = _lib.require_library()
+    g = torch.Generator().manual_seed(v + d)
+    w = torch.randn(v, d, generator=g).to(torch.bfloat16).to(cuda)
+    vp = (v + 7) // 8 * 8
+    wt = torch.full((d, vp), 7.0, dtype=torch.bfloat16, device=cuda)  # padding must be overwritten
+    _lib.check(lib.ts_logprob_weight_t(w.data_ptr(), w.stride(0), v, d, wt.data_ptr(), vp, _lib.stream_of(w)),
+               "ts_logprob_weight_t")
+    torch.cuda.synchronize()
+    want = torch.zeros(d, vp, dtype=torch.bfloat16)
+    want[:, :v] = w.cpu().t()
+    assert torch.equal(wt.cpu(), want)

@@ -542,24 +542,27 @@ __global__ __launch_bounds__(kGemmThreads, 1) void grad_hidden_kernel(DhArgs p) 
   }
 }
 
-// W [vocab][dim] -> W^T [dim][ld] with columns [vocab, ld) zero
+// W [vocab][dim] -> W^T [dim][ld] with columns [vocab, ld) zero.  A thread
+// moves an 8 x 8 block through registers: eight 16-byte row loads, an
+// in-register transpose, eight 16-byte column stores.  A work-group covers 64
+// vocabulary rows x 256 dims; lane (td = t >> 3, tv = t & 7) takes rows
+// 8 tv .. 8 tv + 7 and dims 8 td .. 8 td + 7, so every load and every store
+// instruction of a wave covers 128 contiguous bytes in each of 8 rows.
+// Needs dim % 8 == 0, ld % 8 == 0 and 16-byte aligned rows.
 __global__ __launch_bounds__(kThreads) void transpose_kernel(const bf16* __restrict__ w, int64_t ldw,
                                                              int vocab, int dim, bf16* __restrict__ wt,
                                                              int64_t ldt) {
-  __shared__ uint16_t tile[64][65];
-  const int v0 = blockIdx.x * 64, d0 = blockIdx.y * 64;
-  const uint16_t* src = reinterpret_cast<const uint16_t*>(w);
-  uint16_t* dst = reinterpret_cast<uint16_t*>(wt);
-  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
-  for (int r = ty; r < 64; r += 4) {
-    const int v = v0 + r, d = d0 + tx;
-    tile[r][tx] = (v < vocab && d < dim) ? src[(int64_t)v * ldw + d] : (uint16_t)0;
-  }
-  __syncthreads();
-  for (int r = ty; r < 64; r += 4) {
-    const int d = d0 + r, v = v0 + tx;
-    if (d < dim && v < ldt) dst[(int64_t)d * ldt + v] = tile[tx][r];
-  }
+  const int t = threadIdx.x, tv = t & 7, td = t >> 3;
+  const int64_t v0 = (int64_t)blockIdx.x * 64 + 8 * tv;
+  const int d0 = blockIdx.y * 256 + 8 * td;
+  if (d0 >= dim || v0 >= ldt) return;
+  u32x4 in[8], out[8];
+#pragma unroll
+  for (int r = 0; r < 8; ++r)
+    in[r] = v0 + r < vocab ? *reinterpret_cast<const u32x4*>(w + (v0 + r) * ldw + d0) : u32x4{0u, 0u, 0u, 0u};
+  transpose8x8(in, out);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) *reinterpret_cast<u32x4*>(wt + (int64_t)(d0 + e) * ldt + v0) = out[e];
 }
 
 bool ok16(const void* p) { return ((uintptr_t)p & 15) == 0; }
@@ -631,7 +634,9 @@ int ts_logprob_weight_t(const void* weight, int64_t ld_weight, int64_t vocab, in
                    ld_t % 8 == 0 && vocab < (1 << 30) && dim < (1 << 20),
                "ts_logprob_weight_t: bad arguments vocab=%lld dim=%lld ld_t=%lld", (long long)vocab,
                (long long)dim, (long long)ld_t);
-  const dim3 grid((unsigned)((ld_t + 63) / 64), (unsigned)((dim + 63) / 64));
+  TS_CHECK_ARG(dim % 8 == 0 && ld_weight % 8 == 0 && ok16(weight) && ok16(weight_t),
+               "ts_logprob_weight_t: alignment (16 bytes, dim and ld_weight %% 8)");
+  const dim3 grid((unsigned)((ld_t + 63) / 64), (unsigned)((dim + 255) / 256));
   { ts::TimedLaunch timed_("logprob.transpose_kernel", (hipStream_t)stream); hipLaunchKernelGGL(transpose_kernel, grid, dim3(kThreads), 0, (hipStream_t)stream,
                      (const ts::bf16*)weight, ld_weight, (int)vocab, (int)dim, (ts::bf16*)weight_t,
                      ld_t); }
