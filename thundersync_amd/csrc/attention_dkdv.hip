@@ -162,9 +162,9 @@ __global__ __launch_bounds__(kThreads, 2) void dkdv_kernel(ts_attn_problem P, ts
 // as zeros (no clamping, no masking: a zero row has S = dP = 0, statistics
 // (0, 0), hence dS = 0 and a zero dO row, and adds nothing), and every
 // lane's address is a constant byte offset fixed at kernel start.  Rows are
-// 256 bytes, 16-byte chunk c of row r at chunk slot c ^ (r & 15): row reads of
-// 16 rows at one chunk, transpose reads and the DMA's 4-row instructions are
-// all conflict-free.  dO^T and Q^T come from ds_read_b64_tr_b16: within each
+// 256 bytes, 16-byte chunk c of row r at chunk slot c ^ tile_swizzle(r & 15):
+// row reads of 16 rows at one chunk, transpose reads and the DMA's 4-row
+// instructions are all conflict-free.  dO^T and Q^T come from ds_read_b64_tr_b16: within each
 // 16-lane group, lane i receives column (i & 3) of the rows addressed by
 // lanes i/4, i/4 + 4, i/4 + 8, i/4 + 12, so lane j addressing row kbase +
 // j/4, columns m0 + 4 (j & 3) yields X[kbase + t][m0 + i], t = 0..3 (pinned
@@ -196,17 +196,17 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_wave_kernel(ts_attn_problem 
   // per-lane LDS offsets (elements)
   int ro[4], to[8], dchunk[4];
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks) ro[ks] = j16 * D + (((4 * ks + g4) ^ j16) << 3);
+  for (int ks = 0; ks < 4; ++ks) ro[ks] = j16 * D + (((4 * ks + g4) ^ tile_swizzle(j16)) << 3);
 #pragma unroll
   for (int mb = 0; mb < 8; ++mb) {
     const int r = 4 * g4 + (j16 >> 2);
     const int col = 16 * mb + 4 * (j16 & 3);
-    to[mb] = r * D + ((((col >> 3) ^ r) & 15) << 3) + (col & 7);
+    to[mb] = r * D + ((((col >> 3) ^ tile_swizzle(r)) & 15) << 3) + (col & 7);
   }
   // DMA instruction t fills rows 4t .. 4t + 3; lane (g4, j16) the row 4t + g4,
-  // chunk slot j16 with logical chunk j16 ^ (4 (t & 3) + g4)
+  // chunk slot j16 with logical chunk j16 ^ tile_swizzle(4 (t & 3) + g4)
 #pragma unroll
-  for (int t = 0; t < 4; ++t) dchunk[t] = (j16 ^ (4 * t + g4)) << 3;
+  for (int t = 0; t < 4; ++t) dchunk[t] = (j16 ^ tile_swizzle(4 * t + g4)) << 3;
   // byte offsets of this lane's row and chunk within a 16-row half tile
   int qoff[4], doff[4];
 #pragma unroll

@@ -174,7 +174,7 @@ __global__ __launch_bounds__(kThreads, 1) void dq_kernel(ts_attn_problem P, ts_a
 // issues a quarter of a tile's instructions; rows past a run's end arrive as
 // zeros and add nothing, because a zero K row contributes zero to dQ), one
 // work-group barrier per tile.  Tiles use the dK/dV kernel's 256-byte rows
-// with chunk c of row r at slot c ^ (r & 15): K and V rows feed S^T = K Q^T
+// with chunk c of row r at slot c ^ tile_swizzle(r & 15): K and V rows feed S^T = K Q^T
 // and dP^T = V dO^T as A operands, K^T for dQ^T += K^T dS^T comes from
 // ds_read_b64_tr_b16.  Only tiles that cross the diagonal are masked.
 // ---------------------------------------------------------------------------
