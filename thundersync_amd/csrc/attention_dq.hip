@@ -233,6 +233,104 @@ __global__ __launch_bounds__(kThreads, 1) void dq_wave_kernel(ts_attn_problem P,
   int ro[4], to[8];
   swizzled_offsets(lane, ro, to);
 
+  // one 32-key half ss of a tile: S^T = K Q^T, dP^T = V dO^T for keys
+  // 32 ss .. 32 ss + 31 ([kb][qb] lane holds keys 32 ss + 16 kb + 4 g4 + i,
+  // row 16 qb + j16)
+  auto scores = [&](const bf16* tk, const bf16* tv, int ss, f32x4 (&sc)[2][2], f32x4 (&dp)[2][2])
+      __attribute__((always_inline)) {
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) {
+        sc[kb][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        dp[kb][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const bf16x8 ak = as_bf16x8(ld16(tk + ro[ks] + (32 * ss + 16 * kb) * D));
+        const bf16x8 av = as_bf16x8(ld16(tv + ro[ks] + (32 * ss + 16 * kb) * D));
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) {
+          sc[kb][qb] = mfma16(ak, qreg[qb][ks], sc[kb][qb]);
+          dp[kb][qb] = mfma16(av, dreg[qb][ks], dp[kb][qb]);
+        }
+      }
+  };
+  // dS^T = P^T (dP^T - delta), P^T = exp2(S^T c - lse2), packed as the B
+  // operand of dQ^T += K^T dS^T (slot j <-> key 32 ss + 16 (j >> 2) + 4 g4 +
+  // (j & 3)); DIAG masks keys past each row's diagonal
+  auto dscores = [&](auto diag, int kpos, int kt0, int ss, f32x4 (&sc)[2][2], const f32x4 (&dp)[2][2],
+                     bf16x8 (&dsk)[2]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) {
+        // row q0 + 16 qb + j16 sees key kt0 + 32 ss + 16 kb + 4 g4 + i iff i <= lim
+        const int lim = off + q0 + 16 * qb + j16 - kpos - kt0 - 32 * ss - 16 * kb - 4 * g4;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float p = fast_exp2(sc[kb][qb][i] * c - lse2[qb]);
+          if (decltype(diag)::value) p = i <= lim ? p : 0.f;
+          sc[kb][qb][i] = p * (dp[kb][qb][i] - dlt[qb]);
+        }
+      }
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+      float tmp[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) tmp[j] = sc[j >> 2][qb][j & 3];
+      dsk[qb] = pack8(tmp);
+    }
+  };
+  auto accumulate = [&](const bf16* tk, int ss, const bf16x8 (&dsk)[2]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int mb = 0; mb < 8; ++mb) {
+      const u32x2 a0 = tr_read(tk + to[mb] + 32 * ss * D);
+      const u32x2 a1 = tr_read(tk + to[mb] + (32 * ss + 16) * D);
+      const bf16x8 a = as_bf16x8(u32x4{a0[0], a0[1], a1[0], a1[1]});
+      acc[mb][0] = mfma16(a, dsk[0], acc[mb][0]);
+      acc[mb][1] = mfma16(a, dsk[1], acc[mb][1]);
+    }
+  };
+  // one tile, the halves software-pipelined: half 1's score MFMAs are issued
+  // beside half 0's exponentials, half 0's dQ MFMAs beside half 1's
+  auto tile_body = [&](auto diag, const bf16* tk, const bf16* tv, int kpos, int kt0) __attribute__((always_inline)) {
+    f32x4 sc0[2][2], dp0[2][2], sc1[2][2], dp1[2][2];
+    bf16x8 dsk0[2], dsk1[2];
+    scores(tk, tv, 0, sc0, dp0);
+    __builtin_amdgcn_sched_barrier(0);
+    scores(tk, tv, 1, sc1, dp1);
+    dscores(diag, kpos, kt0, 0, sc0, dp0, dsk0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // the first K/V reads of half 1
+#pragma unroll
+    for (int i = 0; i < 12; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    dscores(diag, kpos, kt0, 1, sc1, dp1, dsk1);
+    accumulate(tk, 0, dsk0);
+    __builtin_amdgcn_sched_group_barrier(0x100, 8, 1);  // K^T reads for dQ of half 0
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+      __builtin_amdgcn_sched_group_barrier(0x002, 4, 1);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+      __builtin_amdgcn_sched_group_barrier(0x002, 4, 1);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    accumulate(tk, 1, dsk1);
+  };
+
   auto step = [&](auto bsel, TileCursor& cur) {
     const int kpos = load_uniform(P.seg_spans, seg.span0 + cur.sp).kpos;
     const int kt0 = cur.kt0;
@@ -244,74 +342,10 @@ __global__ __launch_bounds__(kThreads, 1) void dq_wave_kernel(ts_attn_problem P,
     if (nxt.sp < seg.nspan)
       issue_kv_tile(P, seg, hk, wave, lane, nxt, bsel.value == 0 ? s_k1 : s_k0, bsel.value == 0 ? s_v1 : s_v0);
 
-    const bool diag = kpos + kt0 + BK - 1 > off + q0;
-    // two halves of 32 keys: S^T = K Q^T, dP^T = V dO^T for keys 32 ss .. 32 ss + 31
-    // ([kb][qb] lane holds keys 32 ss + 16 kb + 4 g4 + i, row 16 qb + j16), then
-    // dQ^T += K^T dS^T with slot j <-> key 32 ss + 16 (j >> 2) + 4 g4 + (j & 3)
-#pragma unroll
-    for (int ss = 0; ss < 2; ++ss) {
-      f32x4 sc[2][2], dp[2][2];
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int qb = 0; qb < 2; ++qb) {
-          sc[kb][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
-          dp[kb][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
-        }
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-          const bf16x8 ak = as_bf16x8(ld16(tk + ro[ks] + (32 * ss + 16 * kb) * D));
-          const bf16x8 av = as_bf16x8(ld16(tv + ro[ks] + (32 * ss + 16 * kb) * D));
-#pragma unroll
-          for (int qb = 0; qb < 2; ++qb) {
-            sc[kb][qb] = mfma16(ak, qreg[qb][ks], sc[kb][qb]);
-            dp[kb][qb] = mfma16(av, dreg[qb][ks], dp[kb][qb]);
-          }
-        }
-      // dS^T = P^T (dP^T - delta), P^T = exp2(S^T c - lse2); masked only across the diagonal
-      if (diag) {
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int qb = 0; qb < 2; ++qb) {
-            // row q0 + 16 qb + j16 sees key kt0 + 32 ss + 16 kb + 4 g4 + i iff i <= lim
-            const int lim = off + q0 + 16 * qb + j16 - kpos - kt0 - 32 * ss - 16 * kb - 4 * g4;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const float p = i <= lim ? fast_exp2(sc[kb][qb][i] * c - lse2[qb]) : 0.f;
-              sc[kb][qb][i] = p * (dp[kb][qb][i] - dlt[qb]);
-            }
-          }
-      } else {
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int qb = 0; qb < 2; ++qb)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const float p = fast_exp2(sc[kb][qb][i] * c - lse2[qb]);
-              sc[kb][qb][i] = p * (dp[kb][qb][i] - dlt[qb]);
-            }
-      }
-      bf16x8 dsk[2];
-#pragma unroll
-      for (int qb = 0; qb < 2; ++qb) {
-        float tmp[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) tmp[j] = sc[j >> 2][qb][j & 3];
-        dsk[qb] = pack8(tmp);
-      }
-#pragma unroll
-      for (int mb = 0; mb < 8; ++mb) {
-        const u32x2 a0 = tr_read(tk + to[mb] + 32 * ss * D);
-        const u32x2 a1 = tr_read(tk + to[mb] + (32 * ss + 16) * D);
-        const bf16x8 a = as_bf16x8(u32x4{a0[0], a0[1], a1[0], a1[1]});
-        acc[mb][0] = mfma16(a, dsk[0], acc[mb][0]);
-        acc[mb][1] = mfma16(a, dsk[1], acc[mb][1]);
-      }
-    }
+    if (kpos + kt0 + BK - 1 > off + q0)
+      tile_body(std::true_type{}, tk, tv, kpos, kt0);
+    else
+      tile_body(std::false_type{}, tk, tv, kpos, kt0);
     cur = nxt;
   };
 
