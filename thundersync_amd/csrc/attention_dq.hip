@@ -167,21 +167,24 @@ __global__ __launch_bounds__(kThreads, 1) void dq_kernel(ts_attn_problem P, ts_a
 // backward dQ for GQA groups that are a multiple of 4 (query-stationary)
 //
 // A work-group owns 32 query rows of one segment for the 4 query heads of one
-// quarter of a GQA group (one wave per head).  Q and dO rows stay in
-// registers as B operands, with the rows' (lse * log2 e, delta) pairs.  The
-// segment's key runs stream through 64-key K/V tiles that all four waves
-// share: double-buffered LDS stages filled by buffer_load ... lds (each wave
-// issues a quarter of a tile's instructions; rows past a run's end arrive as
-// zeros and add nothing, because a zero K row contributes zero to dQ), one
-// work-group barrier per tile.  Tiles use the dK/dV kernel's 256-byte rows
+// quarter of a GQA group; wave w takes head w & 3 and 16 NQB of the rows
+// (NQB = 1: eight waves, two per SIMD, so that one wave's LDS and MFMA waits
+// are covered by the other's work; NQB = 2: four waves of 32 rows, one per
+// SIMD).  Q and dO rows stay in registers as B operands, with the rows'
+// (lse * log2 e, delta) pairs.  The segment's key runs stream through 64-key
+// K/V tiles that all waves share: double-buffered LDS stages filled by
+// buffer_load ... lds (each wave issues its share of a tile's instructions;
+// rows past a run's end arrive as zeros and add nothing, because a zero K row
+// contributes zero to dQ), one work-group barrier per tile.  Tiles use the dK/dV kernel's 256-byte rows
 // with chunk c of row r at slot c ^ tile_swizzle(r & 15): K and V rows feed S^T = K Q^T
 // and dP^T = V dO^T as A operands, K^T for dQ^T += K^T dS^T comes from
 // ds_read_b64_tr_b16.  Only tiles that cross the diagonal are masked.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(kThreads, 1) void dq_wave_kernel(ts_attn_problem P, ts_attn_rows Q,
-                                                              ts_attn_rows dO,
-                                                              const float* __restrict__ rowstats,
-                                                              int64_t lse_ld, ts_attn_rows dQ) {
+template <int NQB>
+__global__ __launch_bounds__(64 * 8 / NQB, 1) void dq_wave_kernel(ts_attn_problem P, ts_attn_rows Q, ts_attn_rows dO,
+                                                                 const float* __restrict__ rowstats,
+                                                                 int64_t lse_ld, ts_attn_rows dQ) {
+  constexpr int kWaves = 8 / NQB;
   __shared__ __attribute__((aligned(16))) bf16 s_k0[kKV64];
   __shared__ __attribute__((aligned(16))) bf16 s_v0[kKV64];
   __shared__ __attribute__((aligned(16))) bf16 s_k1[kKV64];
@@ -196,25 +199,26 @@ __global__ __launch_bounds__(kThreads, 1) void dq_wave_kernel(ts_attn_problem P,
   const int group = P.hq / P.hkv;
   const int chunks = group / 4;
   const int hk = yb / chunks;
-  const int h = hk * group + (yb % chunks) * 4 + wave;
+  const int h = hk * group + (yb % chunks) * 4 + (wave & 3);
+  const int qw = q0 + 16 * NQB * (wave >> 2);  // this wave's first row
   const ts_attn_segment seg = load_uniform(P.segs, seg_id);
   const int T = seg.q_len;
   const int off = seg.kv_len - seg.q_len;
   const int last = min(q0 + 32, T) - 1;
   const float c = P.scale * kLog2e;
 
-  // Q / dO rows as B operands: reg[qb][ks] = row q0 + 16 qb + j16, columns 32 ks + 8 g4 ..
-  bf16x8 qreg[2][4], dreg[2][4];
-  const int64_t row0 = seg.q_row0 + q0;
+  // Q / dO rows as B operands: reg[qb][ks] = row qw + 16 qb + j16, columns 32 ks + 8 g4 ..
+  bf16x8 qreg[NQB][4], dreg[NQB][4];
+  const int64_t row0 = seg.q_row0 + qw;
   load_rows_b(qreg, (const bf16*)Q.ptr + row0 * Q.row_stride + (int64_t)h * Q.head_stride, Q.row_stride,
-              T - q0, lane);
+              T - qw, lane);
   load_rows_b(dreg, (const bf16*)dO.ptr + row0 * dO.row_stride + (int64_t)h * dO.head_stride,
-              dO.row_stride, T - q0, lane);
+              dO.row_stride, T - qw, lane);
   // rows past the segment: zero Q and dO with statistics (0, 0) give dS = 0
-  float lse2[2], dlt[2];
+  float lse2[NQB], dlt[NQB];
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb) {
-    const int row = q0 + 16 * qb + j16;
+  for (int qb = 0; qb < NQB; ++qb) {
+    const int row = qw + 16 * qb + j16;
     lse2[qb] = 0.f;
     dlt[qb] = 0.f;
     if (row < T) {
@@ -223,12 +227,11 @@ __global__ __launch_bounds__(kThreads, 1) void dq_wave_kernel(ts_attn_problem P,
       dlt[qb] = rowstats[at + 1];
     }
   }
-  f32x4 acc[8][2];
+  f32x4 acc[8][NQB];
 #pragma unroll
-  for (int mb = 0; mb < 8; ++mb) {
-    acc[mb][0] = f32x4{0.f, 0.f, 0.f, 0.f};
-    acc[mb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-  }
+  for (int mb = 0; mb < 8; ++mb)
+#pragma unroll
+    for (int qb = 0; qb < NQB; ++qb) acc[mb][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   int ro[4], to[8];
   swizzled_offsets(lane, ro, to);
@@ -236,12 +239,12 @@ __global__ __launch_bounds__(kThreads, 1) void dq_wave_kernel(ts_attn_problem P,
   // one 32-key half ss of a tile: S^T = K Q^T, dP^T = V dO^T for keys
   // 32 ss .. 32 ss + 31 ([kb][qb] lane holds keys 32 ss + 16 kb + 4 g4 + i,
   // row 16 qb + j16)
-  auto scores = [&](const bf16* tk, const bf16* tv, int ss, f32x4 (&sc)[2][2], f32x4 (&dp)[2][2])
+  auto scores = [&](const bf16* tk, const bf16* tv, int ss, f32x4 (&sc)[2][NQB], f32x4 (&dp)[2][NQB])
       __attribute__((always_inline)) {
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int qb = 0; qb < 2; ++qb) {
+      for (int qb = 0; qb < NQB; ++qb) {
         sc[kb][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
         dp[kb][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
       }
@@ -252,7 +255,7 @@ __global__ __launch_bounds__(kThreads, 1) void dq_wave_kernel(ts_attn_problem P,
         const bf16x8 ak = as_bf16x8(ld16(tk + ro[ks] + (32 * ss + 16 * kb) * D));
         const bf16x8 av = as_bf16x8(ld16(tv + ro[ks] + (32 * ss + 16 * kb) * D));
 #pragma unroll
-        for (int qb = 0; qb < 2; ++qb) {
+        for (int qb = 0; qb < NQB; ++qb) {
           sc[kb][qb] = mfma16(ak, qreg[qb][ks], sc[kb][qb]);
           dp[kb][qb] = mfma16(av, dreg[qb][ks], dp[kb][qb]);
         }
@@ -261,14 +264,14 @@ __global__ __launch_bounds__(kThreads, 1) void dq_wave_kernel(ts_attn_problem P,
   // dS^T = P^T (dP^T - delta), P^T = exp2(S^T c - lse2), packed as the B
   // operand of dQ^T += K^T dS^T (slot j <-> key 32 ss + 16 (j >> 2) + 4 g4 +
   // (j & 3)); DIAG masks keys past each row's diagonal
-  auto dscores = [&](auto diag, int kpos, int kt0, int ss, f32x4 (&sc)[2][2], const f32x4 (&dp)[2][2],
-                     bf16x8 (&dsk)[2]) __attribute__((always_inline)) {
+  auto dscores = [&](auto diag, int kpos, int kt0, int ss, f32x4 (&sc)[2][NQB], const f32x4 (&dp)[2][NQB],
+                     bf16x8 (&dsk)[NQB]) __attribute__((always_inline)) {
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int qb = 0; qb < 2; ++qb) {
-        // row q0 + 16 qb + j16 sees key kt0 + 32 ss + 16 kb + 4 g4 + i iff i <= lim
-        const int lim = off + q0 + 16 * qb + j16 - kpos - kt0 - 32 * ss - 16 * kb - 4 * g4;
+      for (int qb = 0; qb < NQB; ++qb) {
+        // row qw + 16 qb + j16 sees key kt0 + 32 ss + 16 kb + 4 g4 + i iff i <= lim
+        const int lim = off + qw + 16 * qb + j16 - kpos - kt0 - 32 * ss - 16 * kb - 4 * g4;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           float p = fast_exp2(sc[kb][qb][i] * c - lse2[qb]);
@@ -277,43 +280,44 @@ __global__ __launch_bounds__(kThreads, 1) void dq_wave_kernel(ts_attn_problem P,
         }
       }
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb) {
+    for (int qb = 0; qb < NQB; ++qb) {
       float tmp[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) tmp[j] = sc[j >> 2][qb][j & 3];
       dsk[qb] = pack8(tmp);
     }
   };
-  auto accumulate = [&](const bf16* tk, int ss, const bf16x8 (&dsk)[2]) __attribute__((always_inline)) {
+  auto accumulate = [&](const bf16* tk, int ss, const bf16x8 (&dsk)[NQB]) __attribute__((always_inline)) {
 #pragma unroll
     for (int mb = 0; mb < 8; ++mb) {
       const u32x2 a0 = tr_read(tk + to[mb] + 32 * ss * D);
       const u32x2 a1 = tr_read(tk + to[mb] + (32 * ss + 16) * D);
       const bf16x8 a = as_bf16x8(u32x4{a0[0], a0[1], a1[0], a1[1]});
-      acc[mb][0] = mfma16(a, dsk[0], acc[mb][0]);
-      acc[mb][1] = mfma16(a, dsk[1], acc[mb][1]);
+#pragma unroll
+      for (int qb = 0; qb < NQB; ++qb) acc[mb][qb] = mfma16(a, dsk[qb], acc[mb][qb]);
     }
   };
   // one tile, the halves software-pipelined: half 1's score MFMAs are issued
   // beside half 0's exponentials, half 0's dQ MFMAs beside half 1's
   auto tile_body = [&](auto diag, const bf16* tk, const bf16* tv, int kpos, int kt0) __attribute__((always_inline)) {
-    f32x4 sc0[2][2], dp0[2][2], sc1[2][2], dp1[2][2];
-    bf16x8 dsk0[2], dsk1[2];
+    f32x4 sc0[2][NQB], dp0[2][NQB], sc1[2][NQB], dp1[2][NQB];
+    bf16x8 dsk0[NQB], dsk1[NQB];
     scores(tk, tv, 0, sc0, dp0);
     __builtin_amdgcn_sched_barrier(0);
     scores(tk, tv, 1, sc1, dp1);
     dscores(diag, kpos, kt0, 0, sc0, dp0, dsk0);
+    // 16 K/V reads and 16 NQB MFMAs of half 1 beside ~40 NQB VALU instructions
     __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // the first K/V reads of half 1
 #pragma unroll
     for (int i = 0; i < 12; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, 5, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, NQB, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, NQB == 2 ? 5 : 3, 0);
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, NQB, 0);
+      __builtin_amdgcn_sched_group_barrier(0x002, NQB == 2 ? 4 : 3, 0);
     }
     __builtin_amdgcn_sched_barrier(0);
     dscores(diag, kpos, kt0, 1, sc1, dp1, dsk1);
@@ -322,10 +326,11 @@ __global__ __launch_bounds__(kThreads, 1) void dq_wave_kernel(ts_attn_problem P,
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
-      __builtin_amdgcn_sched_group_barrier(0x002, 4, 1);
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
-      __builtin_amdgcn_sched_group_barrier(0x002, 4, 1);
+#pragma unroll
+      for (int qb = 0; qb < NQB; ++qb) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
+        __builtin_amdgcn_sched_group_barrier(0x002, NQB == 2 ? 4 : 5, 1);
+      }
     }
     __builtin_amdgcn_sched_barrier(0);
     accumulate(tk, 1, dsk1);
@@ -340,9 +345,9 @@ __global__ __launch_bounds__(kThreads, 1) void dq_wave_kernel(ts_attn_problem P,
     const bf16* tk = bsel.value == 0 ? s_k0 : s_k1;
     const bf16* tv = bsel.value == 0 ? s_v0 : s_v1;
     if (nxt.sp < seg.nspan)
-      issue_kv_tile(P, seg, hk, wave, lane, nxt, bsel.value == 0 ? s_k1 : s_k0, bsel.value == 0 ? s_v1 : s_v0);
+      issue_kv_tile<kWaves>(P, seg, hk, wave, lane, nxt, bsel.value == 0 ? s_k1 : s_k0, bsel.value == 0 ? s_v1 : s_v0);
 
-    if (kpos + kt0 + BK - 1 > off + q0)
+    if (kpos + kt0 + BK - 1 > off + qw)
       tile_body(std::true_type{}, tk, tv, kpos, kt0);
     else
       tile_body(std::false_type{}, tk, tv, kpos, kt0);
@@ -350,17 +355,17 @@ __global__ __launch_bounds__(kThreads, 1) void dq_wave_kernel(ts_attn_problem P,
   };
 
   TileCursor cur = next_kv_tile(P, seg, last, TileCursor{0, -BK});
-  if (cur.sp < seg.nspan) issue_kv_tile(P, seg, hk, wave, lane, cur, s_k0, s_v0);
+  if (cur.sp < seg.nspan) issue_kv_tile<kWaves>(P, seg, hk, wave, lane, cur, s_k0, s_v0);
   while (cur.sp < seg.nspan) {
     step(std::integral_constant<int, 0>{}, cur);
     if (cur.sp >= seg.nspan) break;
     step(std::integral_constant<int, 1>{}, cur);
   }
 
-  // dQ^T: acc[mb][qb] lane holds d = 16 mb + 4 g4 + i of row q0 + 16 qb + j16
+  // dQ^T: acc[mb][qb] lane holds d = 16 mb + 4 g4 + i of row qw + 16 qb + j16
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb) {
-    const int row = q0 + 16 * qb + j16;
+  for (int qb = 0; qb < NQB; ++qb) {
+    const int row = qw + 16 * qb + j16;
     if (row >= T) continue;
     bf16* drow = (bf16*)dQ.ptr + (seg.q_row0 + row) * dQ.row_stride + (int64_t)h * dQ.head_stride + 4 * g4;
 #pragma unroll
@@ -380,13 +385,16 @@ int launch_delta(const ts_attn_problem& P, ts_attn_rows out, ts_attn_rows dout, 
   return ts::check_launch("ts_attn_bwd (delta)");
 }
 
+// query rows per wave of the dQ kernel (16: eight waves, two per SIMD; 32: four)
+constexpr int kDqRowsPerWave = 16;
+
 int launch_dq(const ts_attn_problem& P, ts_attn_rows q, ts_attn_rows dout, const float* rowstats,
               int64_t lse_ld, ts_attn_rows dq, hipStream_t s) {
   const int group = P.hq / P.hkv;
   const int gc = heads_per_block(group);
   const dim3 grid((unsigned)(P.n_q_work * P.hkv * (group / gc)));
   if (gc == 4)
-    { ts::TimedLaunch timed_("attention.dq_kernel", s); hipLaunchKernelGGL(dq_wave_kernel, grid, dim3(kThreads), 0, s, P, q, dout, rowstats, lse_ld, dq); }
+    { ts::TimedLaunch timed_("attention.dq_kernel", s); hipLaunchKernelGGL(dq_wave_kernel<kDqRowsPerWave / 16>, grid, dim3(64 * 128 / kDqRowsPerWave), 0, s, P, q, dout, rowstats, lse_ld, dq); }
   else if (gc == 2)
     { ts::TimedLaunch timed_("attention.dq_kernel", s); hipLaunchKernelGGL(dq_kernel<2>, grid, dim3(kThreads), 0, s, P, q, dout, rowstats, lse_ld, dq); }
   else

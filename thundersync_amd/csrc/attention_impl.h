@@ -217,15 +217,18 @@ __device__ __forceinline__ TileCursor next_kv_tile(const ts_attn_problem& P, con
 __device__ __forceinline__ int tile_swizzle(int r) { return r ^ ((r & 1) ? 12 : 0); }
 
 // DMA of one 64-key K/V tile of KV head hk into swizzled LDS tiles (256-byte
-// rows, chunk c of row r at slot c ^ tile_swizzle(r & 15)).  The four waves
-// of a work-group each issue instructions t = wave + 4 u (rows 4 t .. 4 t + 3);
-// lane (g4, j16) fills row 4 t + g4, slot j16 with logical chunk
-// j16 ^ tile_swizzle(4 wave + g4).  Rows past the run arrive as zeros.
+// rows, chunk c of row r at slot c ^ tile_swizzle(r & 15)).  The WAVES waves
+// of a work-group (4 or 8) each issue instructions t = wave + WAVES u (rows
+// 4 t .. 4 t + 3); lane (g4, j16) fills row 4 t + g4, slot j16 with logical
+// chunk j16 ^ tile_swizzle((4 wave + g4) & 15).  Rows past the run arrive as
+// zeros.
+template <int WAVES = 4>
 __device__ __forceinline__ void issue_kv_tile(const ts_attn_problem& P, const ts_attn_segment& seg, int hk,
                                               int wave, int lane, TileCursor tc, bf16* sk, bf16* sv) {
+  static_assert(WAVES == 4 || WAVES == 8, "a tile is 16 instructions of 4 rows");
   const int g4 = lane >> 4, j16 = lane & 15;
   const int dma_row = 4 * wave + g4;
-  const int dma_chunk = (j16 ^ tile_swizzle(4 * wave + g4)) << 3;
+  const int dma_chunk = (j16 ^ tile_swizzle((4 * wave + g4) & 15)) << 3;
   const ts_attn_ref ref = load_uniform(P.seg_spans, seg.span0 + tc.sp);
   const ts_attn_run run = load_uniform(P.runs, ref.index);
   const int nvalid = min(BK, run.len - tc.kt0);
@@ -235,11 +238,11 @@ __device__ __forceinline__ void issue_kv_tile(const ts_attn_problem& P, const ts
   const rsrc_t rv = make_rsrc(vb, (uint32_t)(nvalid * run.v_row_stride * 2));
   const int ko = (int)((dma_row * run.k_row_stride + dma_chunk) * 2);
   const int vo = (int)((dma_row * run.v_row_stride + dma_chunk) * 2);
-  const int kstep = (int)(16 * run.k_row_stride * 2), vstep = (int)(16 * run.v_row_stride * 2);
+  const int kstep = (int)(4 * WAVES * run.k_row_stride * 2), vstep = (int)(4 * WAVES * run.v_row_stride * 2);
 #pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    buffer_dma16(rk, sk + (wave + 4 * u) * 512, ko + u * kstep);
-    buffer_dma16(rv, sv + (wave + 4 * u) * 512, vo + u * vstep);
+  for (int u = 0; u < 16 / WAVES; ++u) {
+    buffer_dma16(rk, sk + (wave + WAVES * u) * 512, ko + u * kstep);
+    buffer_dma16(rv, sv + (wave + WAVES * u) * 512, vo + u * vstep);
   }
 }
 
