@@ -151,7 +151,10 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_kernel(ts_attn_problem P, ts_
 // forward for GQA groups that are a multiple of 4
 //
 // A work-group owns 32 query rows of one segment for the 4 query heads of one
-// quarter of a GQA group (one wave per head); the heads share 64-key K/V
+// quarter of a GQA group; wave w takes head w & 3 and 16 NQB of the rows
+// (NQB = 2: four waves, two work-groups and two waves per SIMD; NQB = 1:
+// eight waves of 16 rows, four waves per SIMD, measured no faster on C2 at
+// 1.32 ms).  The heads share 64-key K/V
 // tiles, streamed by buffer DMA into double-buffered swizzled LDS stages (one
 // work-group barrier per tile).  Q rows stay in registers as B operands of
 // S^T = K Q^T; V^T for O^T += V^T P^T comes from ds_read_b64_tr_b16.  Each
@@ -166,9 +169,12 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_kernel(ts_attn_problem P, ts_
 // ---------------------------------------------------------------------------
 constexpr float kRescaleSlack = 8.f;  // log2 units
 
-__global__ __launch_bounds__(kThreads, 2) void fwd_wave_kernel(ts_attn_problem P, ts_attn_rows Q,
-                                                               ts_attn_rows O, float* __restrict__ lse,
-                                                               int64_t lse_ld) {
+template <int NQB>
+__global__ __launch_bounds__(64 * 8 / NQB, NQB == 1 ? 4 : 2) void fwd_wave_kernel(ts_attn_problem P, ts_attn_rows Q,
+                                                                                  ts_attn_rows O,
+                                                                                  float* __restrict__ lse,
+                                                                                  int64_t lse_ld) {
+  constexpr int kWaves = 8 / NQB;
   __shared__ __attribute__((aligned(16))) bf16 s_k0[kKV64];
   __shared__ __attribute__((aligned(16))) bf16 s_v0[kKV64];
   __shared__ __attribute__((aligned(16))) bf16 s_k1[kKV64];
@@ -183,25 +189,28 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_wave_kernel(ts_attn_problem P
   const int group = P.hq / P.hkv;
   const int chunks = group / 4;
   const int hk = yb / chunks;
-  const int h = hk * group + (yb % chunks) * 4 + wave;
+  const int h = hk * group + (yb % chunks) * 4 + (wave & 3);
+  const int qw = q0 + 16 * NQB * (wave >> 2);  // this wave's first row
   const ts_attn_segment seg = load_uniform(P.segs, seg_id);
   const int T = seg.q_len;
   const int off = seg.kv_len - seg.q_len;
   const int last = min(q0 + 32, T) - 1;
   const float c = P.scale * kLog2e;
 
-  // Q rows as B operands: qreg[qb][ks] = row q0 + 16 qb + j16, columns 32 ks + 8 g4 ..
-  bf16x8 qreg[2][4];
-  load_rows_b(qreg, (const bf16*)Q.ptr + (seg.q_row0 + q0) * Q.row_stride + (int64_t)h * Q.head_stride,
-              Q.row_stride, T - q0, lane);
-  f32x4 acc[8][2];
+  // Q rows as B operands: qreg[qb][ks] = row qw + 16 qb + j16, columns 32 ks + 8 g4 ..
+  bf16x8 qreg[NQB][4];
+  load_rows_b(qreg, (const bf16*)Q.ptr + (seg.q_row0 + qw) * Q.row_stride + (int64_t)h * Q.head_stride,
+              Q.row_stride, T - qw, lane);
+  f32x4 acc[8][NQB];
+  float m[NQB], l[NQB];  // reference point (log2 units) of this lane's column; its part of the
+                         // column's sum of exp2(s c - m)
 #pragma unroll
-  for (int mb = 0; mb < 8; ++mb) {
-    acc[mb][0] = f32x4{0.f, 0.f, 0.f, 0.f};
-    acc[mb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int qb = 0; qb < NQB; ++qb) {
+#pragma unroll
+    for (int mb = 0; mb < 8; ++mb) acc[mb][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    m[qb] = neg_inf();
+    l[qb] = 0.f;
   }
-  float m[2] = {neg_inf(), neg_inf()};  // reference point (log2 units) of this lane's column
-  float l[2] = {0.f, 0.f};              // this lane's part of the column's sum of exp2(s c - m)
   int ro[4], to[8];
   swizzled_offsets(lane, ro, to);
 
@@ -215,40 +224,40 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_wave_kernel(ts_attn_problem P
     const bf16* tk = bsel.value == 0 ? s_k0 : s_k1;
     const bf16* tv = bsel.value == 0 ? s_v0 : s_v1;
     if (nxt.sp < seg.nspan)
-      issue_kv_tile(P, seg, hk, wave, lane, nxt, bsel.value == 0 ? s_k1 : s_k0, bsel.value == 0 ? s_v1 : s_v0);
+      issue_kv_tile<kWaves>(P, seg, hk, wave, lane, nxt, bsel.value == 0 ? s_k1 : s_k0, bsel.value == 0 ? s_v1 : s_v0);
 
-    const bool masked = (ref.kpos + kt0 + BK - 1 > off + q0) | (kt0 + BK > run_len);
+    const bool masked = (ref.kpos + kt0 + BK - 1 > off + qw) | (kt0 + BK > run_len);
     // two halves of 32 keys, each one online-softmax update:
     // S^T = K Q^T with sc[kb][qb] holding keys 32 ss + 16 kb + 4 g4 + i of column
     // 16 qb + j16, then O^T += V^T P^T with slot j <-> key 32 ss + 16 (j >> 2) + 4 g4 + (j & 3)
 #pragma unroll
     for (int ss = 0; ss < 2; ++ss) {
-      f32x4 sc[2][2];
+      f32x4 sc[2][NQB];
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
-        sc[kb][0] = f32x4{0.f, 0.f, 0.f, 0.f};
-        sc[kb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int qb = 0; qb < NQB; ++qb) sc[kb][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
           const bf16x8 ak = as_bf16x8(ld16(tk + ro[ks] + (32 * ss + 16 * kb) * D));
-          sc[kb][0] = mfma16(ak, qreg[0][ks], sc[kb][0]);
-          sc[kb][1] = mfma16(ak, qreg[1][ks], sc[kb][1]);
+#pragma unroll
+          for (int qb = 0; qb < NQB; ++qb) sc[kb][qb] = mfma16(ak, qreg[qb][ks], sc[kb][qb]);
         }
       }
       if (masked) {
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-          for (int qb = 0; qb < 2; ++qb) {
+          for (int qb = 0; qb < NQB; ++qb) {
             const int key0 = kt0 + 32 * ss + 16 * kb + 4 * g4;  // key of element i = key0 + i
-            const int lim = min(off + q0 + 16 * qb + j16 - ref.kpos, run_len - 1) - key0;
+            const int lim = min(off + qw + 16 * qb + j16 - ref.kpos, run_len - 1) - key0;
 #pragma unroll
             for (int i = 0; i < 4; ++i)
               if (i > lim) sc[kb][qb][i] = neg_inf();
           }
       }
 #pragma unroll
-      for (int qb = 0; qb < 2; ++qb) {
+      for (int qb = 0; qb < NQB; ++qb) {
         float mx = fmaxf(fmaxf(fmaxf(sc[0][qb][0], sc[0][qb][1]), fmaxf(sc[0][qb][2], sc[0][qb][3])),
                          fmaxf(fmaxf(sc[1][qb][0], sc[1][qb][1]), fmaxf(sc[1][qb][2], sc[1][qb][3])));
         mx = rows_max4(mx);
@@ -274,9 +283,9 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_wave_kernel(ts_attn_problem P
           }
         l[qb] += ps;
       }
-      bf16x8 pk[2];
+      bf16x8 pk[NQB];
 #pragma unroll
-      for (int qb = 0; qb < 2; ++qb) {
+      for (int qb = 0; qb < NQB; ++qb) {
         float tmp[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) tmp[j] = sc[j >> 2][qb][j & 3];
@@ -287,26 +296,26 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_wave_kernel(ts_attn_problem P
         const u32x2 a0 = tr_read(tv + to[mb] + 32 * ss * D);
         const u32x2 a1 = tr_read(tv + to[mb] + (32 * ss + 16) * D);
         const bf16x8 a = as_bf16x8(u32x4{a0[0], a0[1], a1[0], a1[1]});
-        acc[mb][0] = mfma16(a, pk[0], acc[mb][0]);
-        acc[mb][1] = mfma16(a, pk[1], acc[mb][1]);
+#pragma unroll
+        for (int qb = 0; qb < NQB; ++qb) acc[mb][qb] = mfma16(a, pk[qb], acc[mb][qb]);
       }
     }
     cur = nxt;
   };
 
   TileCursor cur = next_kv_tile(P, seg, last, TileCursor{0, -BK});
-  if (cur.sp < seg.nspan) issue_kv_tile(P, seg, hk, wave, lane, cur, s_k0, s_v0);
+  if (cur.sp < seg.nspan) issue_kv_tile<kWaves>(P, seg, hk, wave, lane, cur, s_k0, s_v0);
   while (cur.sp < seg.nspan) {
     step(std::integral_constant<int, 0>{}, cur);
     if (cur.sp >= seg.nspan) break;
     step(std::integral_constant<int, 1>{}, cur);
   }
 
-  // O = acc / l; acc[mb][qb] lane holds d = 16 mb + 4 g4 + i of row q0 + 16 qb + j16
+  // O = acc / l; acc[mb][qb] lane holds d = 16 mb + 4 g4 + i of row qw + 16 qb + j16
 #pragma unroll
-  for (int qb = 0; qb < 2; ++qb) {
+  for (int qb = 0; qb < NQB; ++qb) {
     const float ls = rows_sum4(l[qb]);
-    const int row = q0 + 16 * qb + j16;
+    const int row = qw + 16 * qb + j16;
     if (row >= T) continue;
     const float inv = ls > 0.f ? 1.f / ls : 0.f;
     bf16* orow = (bf16*)O.ptr + (seg.q_row0 + row) * O.row_stride + (int64_t)h * O.head_stride + 4 * g4;
@@ -320,13 +329,16 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_wave_kernel(ts_attn_problem P
   }
 }
 
+// query rows per wave of the forward kernel (32: four waves per work-group; 16: eight)
+constexpr int kFwdRowsPerWave = 32;
+
 int launch_fwd(const ts_attn_problem& P, ts_attn_rows q, ts_attn_rows out, float* lse, int64_t lse_ld,
                hipStream_t s) {
   const int group = P.hq / P.hkv;
   const int gc = heads_per_block(group);
   const dim3 grid((unsigned)(P.n_q_work * P.hkv * (group / gc)));
   if (gc == 4)
-    { ts::TimedLaunch timed_("attention.fwd_kernel", s); hipLaunchKernelGGL(fwd_wave_kernel, grid, dim3(kThreads), 0, s, P, q, out, lse, lse_ld); }
+    { ts::TimedLaunch timed_("attention.fwd_kernel", s); hipLaunchKernelGGL(fwd_wave_kernel<kFwdRowsPerWave / 16>, grid, dim3(64 * 128 / kFwdRowsPerWave), 0, s, P, q, out, lse, lse_ld); }
   else if (gc == 2)
     { ts::TimedLaunch timed_("attention.fwd_kernel", s); hipLaunchKernelGGL(fwd_kernel<2>, grid, dim3(kThreads), 0, s, P, q, out, lse, lse_ld); }
   else
