@@ -240,28 +240,35 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_wave_kernel(ts_attn_problem 
       dv[mb][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
 
-  // first block at or after (vi, r0); skips visits with no visible rows
-  auto settle = [&](Cursor cur) -> Cursor {
-    while (cur.vi < run.nvisit) {
-      const ts_attn_ref ref = load_uniform(P.run_visits, run.visit0 + cur.vi);
-      const ts_attn_segment seg = load_uniform(P.segs, ref.index);
-      if (cur.r0 < 0) {
-        int rs = ref.kpos + k0 - (seg.kv_len - seg.q_len);
-        rs = rs < 0 ? 0 : rs;
-        cur.r0 = rs & ~31;
-      }
-      if (cur.r0 < seg.q_len) return cur;
-      ++cur.vi;
-      cur.r0 = -1;
-    }
-    return cur;
-  };
-  auto issue = [&](Cursor cur, int h, bf16* buf) {
-    const ts_attn_ref ref = load_uniform(P.run_visits, run.visit0 + cur.vi);
+  // enter visit c.vi (< nvisit): cache its segment's fields and start at the
+  // first 32-row block whose rows can see key k0
+  auto enter = [&](VisitCursor& c) {
+    const ts_attn_ref ref = load_uniform(P.run_visits, run.visit0 + c.vi);
     const ts_attn_segment seg = load_uniform(P.segs, ref.index);
-    const int nrows = min(32, seg.q_len - cur.r0);
+    c.q_len = seg.q_len;
+    c.off = seg.kv_len - seg.q_len;
+    c.kpos = ref.kpos;
+    c.q_row0 = seg.q_row0;
+    const int rs = ref.kpos + k0 - c.off;
+    c.r0 = (rs < 0 ? 0 : rs) & ~31;
+  };
+  // first block at or after c; skips visits with no visible rows
+  auto settle = [&](VisitCursor c) -> VisitCursor {
+    while (c.r0 >= c.q_len) {
+      if (++c.vi >= run.nvisit) break;
+      enter(c);
+    }
+    return c;
+  };
+  auto first = [&]() -> VisitCursor {
+    VisitCursor c{0, 0, 0, 0, 0, 0};
+    if (run.nvisit > 0) enter(c);
+    return settle(c);
+  };
+  auto issue = [&](const VisitCursor& cur, int h, bf16* buf) {
+    const int nrows = min(32, cur.q_len - cur.r0);
     const int n_lo = min(16, nrows), n_hi = nrows - n_lo;
-    const int64_t row0 = seg.q_row0 + cur.r0;
+    const int64_t row0 = cur.q_row0 + cur.r0;
     const bf16* qb = (const bf16*)Q.ptr + row0 * Q.row_stride + (int64_t)h * Q.head_stride;
     const bf16* db = (const bf16*)dO.ptr + row0 * dO.row_stride + (int64_t)h * dO.head_stride;
     const rsrc_t q_lo = make_rsrc(qb, (uint32_t)(n_lo * Q.row_stride * 2));
@@ -281,12 +288,11 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_wave_kernel(ts_attn_problem 
   };
 
   // one 32-row block of the current head; buffer roles fixed per call
-  auto step = [&](auto bsel, Cursor& cur, int h) {
-      const ts_attn_ref ref = load_uniform(P.run_visits, run.visit0 + cur.vi);
-      const ts_attn_segment seg = load_uniform(P.segs, ref.index);
-      const int off = seg.kv_len - seg.q_len;
-      const int r0 = cur.r0;
-      Cursor nxt = settle(Cursor{cur.vi, cur.r0 + 32});
+  auto step = [&](auto bsel, VisitCursor& cur, int h) {
+      const int off = cur.off, r0 = cur.r0, kpos = cur.kpos;
+      VisitCursor nxt = cur;
+      nxt.r0 += 32;
+      nxt = settle(nxt);
       __builtin_amdgcn_s_waitcnt(0);  // this block's tiles have landed
       // static buffer roles: the LDS reads below and the prefetch into the other
       // buffer touch different arrays, so no wait for the prefetch is needed
@@ -335,10 +341,10 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_wave_kernel(ts_attn_problem 
         }
       // P and dS as B operands: slot j = 4 qb + i  <->  row 16 qb + 4 g4 + i
       bf16x8 pk[KB], dsk[KB];
-      if (ref.kpos + k0 + NK - 1 > off + r0) {  // the block crosses the diagonal
+      if (kpos + k0 + NK - 1 > off + r0) {  // the block crosses the diagonal
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) {
-          const int lim = off + r0 - ref.kpos - (k0 + 16 * kb + j16);  // row rl sees the key iff rl >= -lim
+          const int lim = off + r0 - kpos - (k0 + 16 * kb + j16);  // row rl sees the key iff rl >= -lim
           float pv[8], dsv[8];
 #pragma unroll
           for (int qb = 0; qb < 2; ++qb)
@@ -386,7 +392,7 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_wave_kernel(ts_attn_problem 
 
   for (int g = wave; g < group; g += 4) {
     const int h = hk * group + g;
-    Cursor cur = settle(Cursor{0, -1});
+    VisitCursor cur = first();
     if (cur.vi < run.nvisit) issue(cur, h, s_b0[wave]);
     while (cur.vi < run.nvisit) {
       step(std::integral_constant<int, 0>{}, cur, h);

@@ -169,9 +169,16 @@ __device__ __forceinline__ u32x2 tr_read(const bf16* p) {
   return r;
 }
 
-struct Cursor {
-  int vi;  // visit index; == nvisit at the end
-  int r0;  // first row of the block
+// A key run's position in its visit list with the visited segment's fields
+// cached, so that advancing by a row block reads no table unless it moves to
+// the next visit.
+struct VisitCursor {
+  int vi;          // visit index; >= nvisit at the end
+  int r0;          // first row of the block (segment-local)
+  int q_len;       // rows of the visited segment
+  int off;         // its kv_len - q_len
+  int kpos;        // position of the run's first key in the segment's key order
+  int64_t q_row0;  // its first row in the packed Q / dO / statistics
 };
 
 
