@@ -215,8 +215,7 @@ __global__ __launch_bounds__(64 * 8 / NQB, NQB == 1 ? 4 : 2) void fwd_wave_kerne
   swizzled_offsets(lane, ro, to);
 
   auto step = [&](auto bsel, TileCursor& cur) {
-    const ts_attn_ref ref = load_uniform(P.seg_spans, seg.span0 + cur.sp);
-    const int run_len = load_uniform(P.runs, ref.index).len;
+    const int kpos = cur.kpos, run_len = cur.len;
     const int kt0 = cur.kt0;
     const TileCursor nxt = next_kv_tile(P, seg, last, cur);
     __builtin_amdgcn_s_waitcnt(0);  // this wave's part of the tile has landed
@@ -224,9 +223,9 @@ __global__ __launch_bounds__(64 * 8 / NQB, NQB == 1 ? 4 : 2) void fwd_wave_kerne
     const bf16* tk = bsel.value == 0 ? s_k0 : s_k1;
     const bf16* tv = bsel.value == 0 ? s_v0 : s_v1;
     if (nxt.sp < seg.nspan)
-      issue_kv_tile<kWaves>(P, seg, hk, wave, lane, nxt, bsel.value == 0 ? s_k1 : s_k0, bsel.value == 0 ? s_v1 : s_v0);
+      issue_kv_tile<kWaves>(hk, wave, lane, nxt, bsel.value == 0 ? s_k1 : s_k0, bsel.value == 0 ? s_v1 : s_v0);
 
-    const bool masked = (ref.kpos + kt0 + BK - 1 > off + qw) | (kt0 + BK > run_len);
+    const bool masked = (kpos + kt0 + BK - 1 > off + qw) | (kt0 + BK > run_len);
     // two halves of 32 keys, each one online-softmax update:
     // S^T = K Q^T with sc[kb][qb] holding keys 32 ss + 16 kb + 4 g4 + i of column
     // 16 qb + j16, then O^T += V^T P^T with slot j <-> key 32 ss + 16 (j >> 2) + 4 g4 + (j & 3)
@@ -250,7 +249,7 @@ __global__ __launch_bounds__(64 * 8 / NQB, NQB == 1 ? 4 : 2) void fwd_wave_kerne
 #pragma unroll
           for (int qb = 0; qb < NQB; ++qb) {
             const int key0 = kt0 + 32 * ss + 16 * kb + 4 * g4;  // key of element i = key0 + i
-            const int lim = min(off + qw + 16 * qb + j16 - ref.kpos, run_len - 1) - key0;
+            const int lim = min(off + qw + 16 * qb + j16 - kpos, run_len - 1) - key0;
 #pragma unroll
             for (int i = 0; i < 4; ++i)
               if (i > lim) sc[kb][qb][i] = neg_inf();
@@ -303,8 +302,8 @@ __global__ __launch_bounds__(64 * 8 / NQB, NQB == 1 ? 4 : 2) void fwd_wave_kerne
     cur = nxt;
   };
 
-  TileCursor cur = next_kv_tile(P, seg, last, TileCursor{0, -BK});
-  if (cur.sp < seg.nspan) issue_kv_tile<kWaves>(P, seg, hk, wave, lane, cur, s_k0, s_v0);
+  TileCursor cur = first_kv_tile(P, seg, last);
+  if (cur.sp < seg.nspan) issue_kv_tile<kWaves>(hk, wave, lane, cur, s_k0, s_v0);
   while (cur.sp < seg.nspan) {
     step(std::integral_constant<int, 0>{}, cur);
     if (cur.sp >= seg.nspan) break;

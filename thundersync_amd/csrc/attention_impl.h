@@ -185,30 +185,54 @@ struct VisitCursor {
 constexpr int kKV64 = BK * D;  // elements of one 64-key tile
 
 struct TileCursor {
-  int sp;   // span index; == nspan at the end
-  int kt0;  // first run-local key of the tile
+  int sp;    // span index; == nspan at the end
+  int kt0;   // first run-local key of the tile
+  int kpos;  // position of the span's first key in the segment's key order
+  int len;   // keys of the span's run
+  uint64_t k, v;
+  int64_t k_row_stride, k_head_stride, v_row_stride, v_head_stride;
 };
+
+// cache span tc.sp's reference and run fields (tc.sp < nspan)
+__device__ __forceinline__ void enter_span(const ts_attn_problem& P, const ts_attn_segment& seg, TileCursor& tc) {
+  const ts_attn_ref ref = load_uniform(P.seg_spans, seg.span0 + tc.sp);
+  const ts_attn_run run = load_uniform(P.runs, ref.index);
+  tc.kpos = ref.kpos;
+  tc.len = run.len;
+  tc.k = run.k;
+  tc.v = run.v;
+  tc.k_row_stride = run.k_row_stride;
+  tc.k_head_stride = run.k_head_stride;
+  tc.v_row_stride = run.v_row_stride;
+  tc.v_head_stride = run.v_head_stride;
+}
 
 // Next 64-key tile after `tc` in a segment's key order that some row up to
 // `last` (segment-local) can see; sp == nspan when none is left.  Spans are in
 // key order, so once a tile starts past the last visible key so do all later
-// ones.  Start from TileCursor{0, -BK}.
+// ones.  Tables are read only on entering a span.
 __device__ __forceinline__ TileCursor next_kv_tile(const ts_attn_problem& P, const ts_attn_segment& seg,
                                                    int last, TileCursor tc) {
   const int off = seg.kv_len - seg.q_len;
   tc.kt0 += BK;
   while (tc.sp < seg.nspan) {
-    const ts_attn_ref ref = load_uniform(P.seg_spans, seg.span0 + tc.sp);
-    const ts_attn_run run = load_uniform(P.runs, ref.index);
-    if (tc.kt0 >= run.len) {
-      ++tc.sp;
+    if (tc.kt0 >= tc.len) {
+      if (++tc.sp < seg.nspan) enter_span(P, seg, tc);
       tc.kt0 = 0;
       continue;
     }
-    if (ref.kpos + tc.kt0 > off + last) tc.sp = seg.nspan;
+    if (tc.kpos + tc.kt0 > off + last) tc.sp = seg.nspan;
     break;
   }
   return tc;
+}
+
+// the first visible tile of a segment
+__device__ __forceinline__ TileCursor first_kv_tile(const ts_attn_problem& P, const ts_attn_segment& seg,
+                                                    int last) {
+  TileCursor tc{0, -BK, 0, 0, 0, 0, 0, 0, 0, 0};
+  if (seg.nspan > 0) enter_span(P, seg, tc);
+  return next_kv_tile(P, seg, last, tc);
 }
 
 // Row swizzle of the 256-byte-row LDS tiles: 16-byte chunk c of row r sits at
@@ -230,52 +254,24 @@ __device__ __forceinline__ int tile_swizzle(int r) { return r ^ ((r & 1) ? 12 : 
 // chunk j16 ^ tile_swizzle((4 wave + g4) & 15).  Rows past the run arrive as
 // zeros.
 template <int WAVES = 4>
-__device__ __forceinline__ void issue_kv_tile(const ts_attn_problem& P, const ts_attn_segment& seg, int hk,
-                                              int wave, int lane, TileCursor tc, bf16* sk, bf16* sv) {
+__device__ __forceinline__ void issue_kv_tile(int hk, int wave, int lane, const TileCursor& tc, bf16* sk,
+                                              bf16* sv) {
   static_assert(WAVES == 4 || WAVES == 8, "a tile is 16 instructions of 4 rows");
   const int g4 = lane >> 4, j16 = lane & 15;
   const int dma_row = 4 * wave + g4;
   const int dma_chunk = (j16 ^ tile_swizzle((4 * wave + g4) & 15)) << 3;
-  const ts_attn_ref ref = load_uniform(P.seg_spans, seg.span0 + tc.sp);
-  const ts_attn_run run = load_uniform(P.runs, ref.index);
-  const int nvalid = min(BK, run.len - tc.kt0);
-  const bf16* kb = (const bf16*)run.k + (int64_t)tc.kt0 * run.k_row_stride + (int64_t)hk * run.k_head_stride;
-  const bf16* vb = (const bf16*)run.v + (int64_t)tc.kt0 * run.v_row_stride + (int64_t)hk * run.v_head_stride;
-  const rsrc_t rk = make_rsrc(kb, (uint32_t)(nvalid * run.k_row_stride * 2));
-  const rsrc_t rv = make_rsrc(vb, (uint32_t)(nvalid * run.v_row_stride * 2));
-  const int ko = (int)((dma_row * run.k_row_stride + dma_chunk) * 2);
-  const int vo = (int)((dma_row * run.v_row_stride + dma_chunk) * 2);
-  const int kstep = (int)(4 * WAVES * run.k_row_stride * 2), vstep = (int)(4 * WAVES * run.v_row_stride * 2);
+  const int nvalid = min(BK, tc.len - tc.kt0);
+  const bf16* kb = (const bf16*)tc.k + (int64_t)tc.kt0 * tc.k_row_stride + (int64_t)hk * tc.k_head_stride;
+  const bf16* vb = (const bf16*)tc.v + (int64_t)tc.kt0 * tc.v_row_stride + (int64_t)hk * tc.v_head_stride;
+  const rsrc_t rk = make_rsrc(kb, (uint32_t)(nvalid * tc.k_row_stride * 2));
+  const rsrc_t rv = make_rsrc(vb, (uint32_t)(nvalid * tc.v_row_stride * 2));
+  const int ko = (int)((dma_row * tc.k_row_stride + dma_chunk) * 2);
+  const int vo = (int)((dma_row * tc.v_row_stride + dma_chunk) * 2);
+  const int kstep = (int)(4 * WAVES * tc.k_row_stride * 2), vstep = (int)(4 * WAVES * tc.v_row_stride * 2);
 #pragma unroll
   for (int u = 0; u < 16 / WAVES; ++u) {
     buffer_dma16(rk, sk + (wave + WAVES * u) * 512, ko + u * kstep);
     buffer_dma16(rv, sv + (wave + WAVES * u) * 512, vo + u * vstep);
-  }
-}
-
-// issue_kv_tile through untracked inline assembly (the compiler neither sees
-// nor waits for these loads; the caller accounts for them with vmcnt: eight
-// instructions per wave and tile)
-__device__ __forceinline__ void issue_kv_tile_untracked(const ts_attn_problem& P, const ts_attn_segment& seg,
-                                                        int hk, int wave, int lane, TileCursor tc, bf16* sk,
-                                                        bf16* sv) {
-  const int g4 = lane >> 4, j16 = lane & 15;
-  const int dma_row = 4 * wave + g4;
-  const int dma_chunk = (j16 ^ tile_swizzle(4 * wave + g4)) << 3;
-  const ts_attn_ref ref = load_uniform(P.seg_spans, seg.span0 + tc.sp);
-  const ts_attn_run run = load_uniform(P.runs, ref.index);
-  const int nvalid = min(BK, run.len - tc.kt0);
-  const bf16* kb = (const bf16*)run.k + (int64_t)tc.kt0 * run.k_row_stride + (int64_t)hk * run.k_head_stride;
-  const bf16* vb = (const bf16*)run.v + (int64_t)tc.kt0 * run.v_row_stride + (int64_t)hk * run.v_head_stride;
-  const u32x4 rk = raw_descriptor(kb, (uint32_t)(nvalid * run.k_row_stride * 2));
-  const u32x4 rv = raw_descriptor(vb, (uint32_t)(nvalid * run.v_row_stride * 2));
-  const int ko = (int)((dma_row * run.k_row_stride + dma_chunk) * 2);
-  const int vo = (int)((dma_row * run.v_row_stride + dma_chunk) * 2);
-  const int kstep = (int)(16 * run.k_row_stride * 2), vstep = (int)(16 * run.v_row_stride * 2);
-#pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    buffer_dma16_untracked(rk, sk + (wave + 4 * u) * 512, ko + u * kstep);
-    buffer_dma16_untracked(rv, sv + (wave + 4 * u) * 512, vo + u * vstep);
   }
 }
 
