@@ -265,8 +265,10 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_wave_kernel(ts_attn_problem 
     if (run.nvisit > 0) enter(c);
     return settle(c);
   };
+  // DMA of block `cur` (nothing, as zero-size buffer resources, when it is
+  // past the run's last visit)
   auto issue = [&](const VisitCursor& cur, int h, bf16* buf) {
-    const int nrows = min(32, cur.q_len - cur.r0);
+    const int nrows = max(0, min(32, cur.q_len - cur.r0));
     const int n_lo = min(16, nrows), n_hi = nrows - n_lo;
     const int64_t row0 = cur.q_row0 + cur.r0;
     const bf16* qb = (const bf16*)Q.ptr + row0 * Q.row_stride + (int64_t)h * Q.head_stride;
@@ -282,23 +284,24 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_wave_kernel(ts_attn_problem 
       buffer_dma16(d_lo, buf + kTile32 + t * 512, doff[t]);
       buffer_dma16(d_hi, buf + kTile32 + (4 + t) * 512, doff[t]);
     }
-    // 32 rows x 8 bytes of statistics: lanes 0..15, 16 bytes each
+    // 32 rows x 8 bytes of statistics: lanes 0..15, 16 bytes each (the other
+    // lanes read past the resource and write zeros after them)
     const rsrc_t rs = make_rsrc(rowstats + 2 * ((int64_t)h * lse_ld + row0), (uint32_t)(nrows * 8));
-    if (lane < 16) buffer_dma16(rs, buf + 2 * kTile32, lane * 16);
+    buffer_dma16(rs, buf + 2 * kTile32, lane < 16 ? lane * 16 : 0x7ffffff0);
   };
 
   // one 32-row block of the current head; buffer roles fixed per call
-  auto step = [&](auto bsel, VisitCursor& cur, int h) {
+  // `nxt` is the block after `cur`, already settled: the step's body up to the
+  // cursor update is branch-free, so the next block's DMA set-up interleaves
+  // with the MFMAs
+  auto step = [&](auto bsel, VisitCursor& cur, VisitCursor& nxt, int h) {
       const int off = cur.off, r0 = cur.r0, kpos = cur.kpos;
-      VisitCursor nxt = cur;
-      nxt.r0 += 32;
-      nxt = settle(nxt);
       __builtin_amdgcn_s_waitcnt(0);  // this block's tiles have landed
       // static buffer roles: the LDS reads below and the prefetch into the other
       // buffer touch different arrays, so no wait for the prefetch is needed
       bf16* cur_buf = bsel.value == 0 ? s_b0[wave] : s_b1[wave];
       bf16* nxt_buf = bsel.value == 0 ? s_b1[wave] : s_b0[wave];
-      if (nxt.vi < run.nvisit) issue(nxt, h, nxt_buf);
+      issue(nxt, h, nxt_buf);
       const bf16* tq = cur_buf;
       const bf16* td = cur_buf + kTile32;
       const float* sl = reinterpret_cast<const float*>(cur_buf + 2 * kTile32);  // [32] (lse2, delta)
@@ -388,16 +391,22 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_wave_kernel(ts_attn_problem 
         }
       }
       cur = nxt;
+      nxt.r0 += 32;
+      if (nxt.r0 >= nxt.q_len) nxt = settle(nxt);  // tables are read only here
   };
 
   for (int g = wave; g < group; g += 4) {
     const int h = hk * group + g;
     VisitCursor cur = first();
+    VisitCursor nxt = cur;
+    nxt.r0 += 32;
+    nxt = settle(nxt);
+    __builtin_amdgcn_s_waitcnt(0);  // the previous head's last (empty) DMA has landed
     if (cur.vi < run.nvisit) issue(cur, h, s_b0[wave]);
     while (cur.vi < run.nvisit) {
-      step(std::integral_constant<int, 0>{}, cur, h);
+      step(std::integral_constant<int, 0>{}, cur, nxt, h);
       if (cur.vi >= run.nvisit) break;
-      step(std::integral_constant<int, 1>{}, cur, h);
+      step(std::integral_constant<int, 1>{}, cur, nxt, h);
     }
   }
 

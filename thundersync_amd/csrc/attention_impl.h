@@ -160,7 +160,10 @@ __device__ __forceinline__ int task_of(int n_items, int n_long, int& y) {
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kTile32 = 32 * D;              // elements of one 32-row tile (256-byte rows)
-constexpr int kStage32 = 2 * kTile32 + 128;  // Q tile + dO tile + 32 (lse2, delta) pairs
+// Q tile + dO tile + 32 (lse2, delta) pairs in a 1 KB slot: the statistics
+// DMA is issued by all 64 lanes (lanes 16.. with an out-of-range offset write
+// zeros into the rest of the slot), so it needs no lane branch
+constexpr int kStage32 = 2 * kTile32 + 512;
 
 __device__ __forceinline__ u32x2 tr_read(const bf16* p) {
   const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)p);
