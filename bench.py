@@ -50,7 +50,9 @@ def parse():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--seed", type=int, default=0)
-    ap.add_argument("--only", choices=("all", "attention", "chunked", "logprob", "rmsnorm"), default="all")
+    ap.add_argument("--only", choices=("all", "attention", "chunked", "logprob", "rmsnorm", "copy"), default="all",
+                    help="one workload; 'copy' runs only the plain 256 MiB device copy whose FETCH_SIZE / "
+                         "WRITE_SIZE readings calibrate the traffic counters")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     return ap.parse_args()
 
@@ -501,6 +503,19 @@ def bench_rmsnorm(args, device):
     }
 
 
+def calibration_copy(device, nbytes: int = 256 << 20, repeats: int = 3) -> None:
+    """A plain device-to-device copy of `nbytes`, `repeats` times: the reference
+    reading for scaling the FETCH_SIZE / WRITE_SIZE counters to bytes."""
+    import torch
+
+    x = torch.ones(nbytes, dtype=torch.uint8, device=device)
+    y = torch.empty_like(x)
+    for _ in range(repeats):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibration_copy_bytes": nbytes, "repeats": repeats}), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -511,6 +526,9 @@ def main():
 
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)
+    if args.only == "copy":
+        calibration_copy(device)
+        return
     out = {
         "metric": METRIC,
         "value": None,
