@@ -167,7 +167,8 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_kernel(ts_attn_problem P, ts_
 // row sum share the same m the result is unchanged.  Only tiles that cross
 // the diagonal or pass a run's end are masked.
 // ---------------------------------------------------------------------------
-constexpr float kRescaleSlack = 8.f;  // log2 units
+constexpr float kRescaleSlack = 8.f;    // log2 units
+constexpr float kRescaleBound = 256.f;  // 2^kRescaleSlack
 
 template <int NQB>
 __global__ __launch_bounds__(64 * 8 / NQB, NQB == 1 ? 4 : 2) void fwd_wave_kernel(ts_attn_problem P, ts_attn_rows Q,
@@ -255,39 +256,62 @@ __global__ __launch_bounds__(64 * 8 / NQB, NQB == 1 ? 4 : 2) void fwd_wave_kerne
               if (i > lim) sc[kb][qb][i] = neg_inf();
           }
       }
+      // Fast path: the exponentials against the current reference point m.
+      // They stand unless some score exceeds m by more than kRescaleSlack, which
+      // a lane detects as a partial sum above 2^kRescaleSlack (every term is
+      // positive), or m is still -inf; then, rarely, the half is redone on the
+      // slow path: column maxima, the move of m with the rescale of O and the
+      // row sum, and the exponentials again.
+      float pe[2][NQB][4], ps[NQB];
+      bool redo = false;
 #pragma unroll
       for (int qb = 0; qb < NQB; ++qb) {
-        float mx = fmaxf(fmaxf(fmaxf(sc[0][qb][0], sc[0][qb][1]), fmaxf(sc[0][qb][2], sc[0][qb][3])),
-                         fmaxf(fmaxf(sc[1][qb][0], sc[1][qb][1]), fmaxf(sc[1][qb][2], sc[1][qb][3])));
-        mx = rows_max4(mx);
-        const float mt = mx * c;  // maximum in log2 units (-inf if the column sees none of these keys)
-        const bool move = mt > m[qb] + kRescaleSlack;
-        if (__builtin_amdgcn_ballot_w64(move) != 0) {
-          const float mnew = move ? mt : m[qb];
-          const float alpha = fast_exp2(m[qb] - mnew);  // 0 on the first visible keys (m = -inf)
-          l[qb] *= alpha;
-#pragma unroll
-          for (int mb = 0; mb < 8; ++mb) acc[mb][qb] *= alpha;
-          m[qb] = mnew;
-        }
         const float mref = m[qb] == neg_inf() ? 0.f : m[qb];
-        float ps = 0.f;
+        ps[qb] = 0.f;
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const float p = fast_exp2(fmaf(sc[kb][qb][i], c, -mref));
-            sc[kb][qb][i] = p;
-            ps += p;
+            pe[kb][qb][i] = fast_exp2(fmaf(sc[kb][qb][i], c, -mref));
+            ps[qb] += pe[kb][qb][i];
           }
-        l[qb] += ps;
+        redo |= (m[qb] == neg_inf()) | (ps[qb] > kRescaleBound);
       }
+      if (__builtin_amdgcn_ballot_w64(redo) != 0) {
+#pragma unroll
+        for (int qb = 0; qb < NQB; ++qb) {
+          float mx = fmaxf(fmaxf(fmaxf(sc[0][qb][0], sc[0][qb][1]), fmaxf(sc[0][qb][2], sc[0][qb][3])),
+                           fmaxf(fmaxf(sc[1][qb][0], sc[1][qb][1]), fmaxf(sc[1][qb][2], sc[1][qb][3])));
+          mx = rows_max4(mx);
+          const float mt = mx * c;  // maximum in log2 units (-inf if the column sees none of these keys)
+          const bool move = mt > m[qb] + kRescaleSlack;
+          if (__builtin_amdgcn_ballot_w64(move) != 0) {
+            const float mnew = move ? mt : m[qb];
+            const float alpha = fast_exp2(m[qb] - mnew);  // 0 on the first visible keys (m = -inf)
+            l[qb] *= alpha;
+#pragma unroll
+            for (int mb = 0; mb < 8; ++mb) acc[mb][qb] *= alpha;
+            m[qb] = mnew;
+          }
+          const float mref = m[qb] == neg_inf() ? 0.f : m[qb];
+          ps[qb] = 0.f;
+#pragma unroll
+          for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              pe[kb][qb][i] = fast_exp2(fmaf(sc[kb][qb][i], c, -mref));
+              ps[qb] += pe[kb][qb][i];
+            }
+        }
+      }
+#pragma unroll
+      for (int qb = 0; qb < NQB; ++qb) l[qb] += ps[qb];
       bf16x8 pk[NQB];
 #pragma unroll
       for (int qb = 0; qb < NQB; ++qb) {
         float tmp[8];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) tmp[j] = sc[j >> 2][qb][j & 3];
+        for (int j = 0; j < 8; ++j) tmp[j] = pe[j >> 2][qb][j & 3];
         pk[qb] = pack8(tmp);
       }
 #pragma unroll
