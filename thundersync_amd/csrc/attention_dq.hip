@@ -227,6 +227,9 @@ __global__ __launch_bounds__(64 * 8 / NQB, 1) void dq_wave_kernel(ts_attn_proble
       dlt[qb] = rowstats[at + 1];
     }
   }
+  f32x4 ndlt[NQB];  // -delta of the lane's row, the starting value of the dP^T accumulators
+#pragma unroll
+  for (int qb = 0; qb < NQB; ++qb) ndlt[qb] = f32x4{-dlt[qb], -dlt[qb], -dlt[qb], -dlt[qb]};
   f32x4 acc[8][NQB];
 #pragma unroll
   for (int mb = 0; mb < 8; ++mb)
@@ -246,7 +249,7 @@ __global__ __launch_bounds__(64 * 8 / NQB, 1) void dq_wave_kernel(ts_attn_proble
 #pragma unroll
       for (int qb = 0; qb < NQB; ++qb) {
         sc[kb][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
-        dp[kb][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        dp[kb][qb] = ndlt[qb];  // the MFMAs accumulate dP^T - delta
       }
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
@@ -261,7 +264,7 @@ __global__ __launch_bounds__(64 * 8 / NQB, 1) void dq_wave_kernel(ts_attn_proble
         }
       }
   };
-  // dS^T = P^T (dP^T - delta), P^T = exp2(S^T c - lse2), packed as the B
+  // dS^T = P^T (dP^T - delta) (dp holds dP^T - delta), P^T = exp2(S^T c - lse2), packed as the B
   // operand of dQ^T += K^T dS^T (slot j <-> key 32 ss + 16 (j >> 2) + 4 g4 +
   // (j & 3)); DIAG masks keys past each row's diagonal
   auto dscores = [&](auto diag, int kpos, int kt0, int ss, f32x4 (&sc)[2][NQB], const f32x4 (&dp)[2][NQB],
@@ -276,7 +279,7 @@ __global__ __launch_bounds__(64 * 8 / NQB, 1) void dq_wave_kernel(ts_attn_proble
         for (int i = 0; i < 4; ++i) {
           float p = fast_exp2(sc[kb][qb][i] * c - lse2[qb]);
           if (decltype(diag)::value) p = i <= lim ? p : 0.f;
-          sc[kb][qb][i] = p * (dp[kb][qb][i] - dlt[qb]);
+          sc[kb][qb][i] = p * dp[kb][qb][i];
         }
       }
 #pragma unroll
