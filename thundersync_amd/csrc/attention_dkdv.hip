@@ -377,18 +377,34 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_wave_kernel(ts_attn_problem 
           dsk[kb] = pack8(dsv);
         }
       }
-      // dV^T += dO^T P, dK^T += Q^T dS: rows d = 16 mb + 4 g4 + i, column key
-#pragma unroll
-      for (int mb = 0; mb < 8; ++mb) {
+      // dV^T += dO^T P, dK^T += Q^T dS: rows d = 16 mb + 4 g4 + i, column key;
+      // the dO^T / Q^T fragments of block mb + 2 are read while block mb's
+      // MFMAs run
+      bf16x8 a_do[3], a_q[3];
+      auto frag = [&](int mb, bf16x8& fd, bf16x8& fq) __attribute__((always_inline)) {
         const u32x2 a0 = tr_read(td + to[mb]), a1 = tr_read(td + to[mb] + 16 * D);
         const u32x2 b0 = tr_read(tq + to[mb]), b1 = tr_read(tq + to[mb] + 16 * D);
-        const bf16x8 a_do = as_bf16x8(u32x4{a0[0], a0[1], a1[0], a1[1]});
-        const bf16x8 a_q = as_bf16x8(u32x4{b0[0], b0[1], b1[0], b1[1]});
+        fd = as_bf16x8(u32x4{a0[0], a0[1], a1[0], a1[1]});
+        fq = as_bf16x8(u32x4{b0[0], b0[1], b1[0], b1[1]});
+      };
+      frag(0, a_do[0], a_q[0]);
+      frag(1, a_do[1], a_q[1]);
+#pragma unroll
+      for (int mb = 0; mb < 8; ++mb) {
+        if (mb + 2 < 8) frag(mb + 2, a_do[(mb + 2) % 3], a_q[(mb + 2) % 3]);
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) {
-          dv[mb][kb] = mfma16(a_do, pk[kb], dv[mb][kb]);
-          dk[mb][kb] = mfma16(a_q, dsk[kb], dk[mb][kb]);
+          dv[mb][kb] = mfma16(a_do[mb % 3], pk[kb], dv[mb][kb]);
+          dk[mb][kb] = mfma16(a_q[mb % 3], dsk[kb], dk[mb][kb]);
         }
+      }
+      // keep the reads two blocks ahead (the scheduler otherwise pulls them
+      // back to one block ahead, where six MFMAs do not cover their latency)
+      __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+#pragma unroll
+      for (int mb = 0; mb < 8; ++mb) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 2 * KB, 0);
+        if (mb + 2 < 8) __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
       }
       cur = nxt;
       nxt.r0 += 32;
