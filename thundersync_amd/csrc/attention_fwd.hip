@@ -322,6 +322,14 @@ __global__ __launch_bounds__(64 * 8 / NQB, NQB == 1 ? 4 : 2) void fwd_wave_kerne
 #pragma unroll
         for (int qb = 0; qb < NQB; ++qb) acc[mb][qb] = mfma16(a, pk[qb], acc[mb][qb]);
       }
+      // V^T fragment reads kept four blocks ahead of their MFMAs
+      __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+#pragma unroll
+      for (int mb = 0; mb < 8; ++mb) {
+        __builtin_amdgcn_sched_group_barrier(0x008, NQB, 0);
+        if (mb + 4 < 8) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
     cur = nxt;
   };
