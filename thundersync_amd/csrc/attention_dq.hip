@@ -337,6 +337,13 @@ __global__ __launch_bounds__(64 * 8 / NQB, 1) void dq_wave_kernel(ts_attn_proble
     }
     __builtin_amdgcn_sched_barrier(0);
     accumulate(tk, 1, dsk1);
+    // K^T fragment reads of half 1 kept four blocks ahead of their MFMAs
+    __builtin_amdgcn_sched_group_barrier(0x100, 8, 2);
+#pragma unroll
+    for (int mb = 0; mb < 8; ++mb) {
+      __builtin_amdgcn_sched_group_barrier(0x008, NQB, 2);
+      if (mb + 4 < 8) __builtin_amdgcn_sched_group_barrier(0x100, 2, 2);
+    }
   };
 
   auto step = [&](auto bsel, TileCursor& cur) {
