@@ -332,6 +332,13 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_wave_kernel(ts_attn_problem 
           }
         }
       }
+      // Q/dO row reads two k-steps ahead of their MFMAs
+      __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 4 * KB, 0);
+        if (ks + 2 < 4) __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+      }
       // this lane's rows: 16 qb + 4 g4 + i
       float l2[2][4], dl[2][4];
 #pragma unroll
