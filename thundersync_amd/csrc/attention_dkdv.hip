@@ -169,8 +169,12 @@ __global__ __launch_bounds__(kThreads, 2) void dkdv_kernel(ts_attn_problem P, ts
 // lanes i/4, i/4 + 4, i/4 + 8, i/4 + 12, so lane j addressing row kbase +
 // j/4, columns m0 + 4 (j & 3) yields X[kbase + t][m0 + i], t = 0..3 (pinned
 // by the LDS probe test).  The causal mask is applied only to tiles that
-// cross the diagonal.  The per-head partials are summed across waves through
-// LDS in wave order.
+// cross the diagonal.  The next block's DMA is issued without a branch
+// (zero-size resources past the last block) in the same basic block as the
+// score MFMAs, so its scalar set-up interleaves with them, and the visit
+// cursor caches its segment's fields, so a step reads no table unless it
+// enters the next visit.  The per-head partials are summed across waves
+// through LDS in wave order.
 // ---------------------------------------------------------------------------
 template <int KB>
 __global__ __launch_bounds__(kThreads, 1) void dkdv_wave_kernel(ts_attn_problem P, ts_attn_rows Q,
