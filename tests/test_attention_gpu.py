@@ -98,6 +98,50 @@ def test_lse_and_determinism(cuda):
         assert torch.equal(x, y)
 
 
+@pytest.mark.parametrize("slope", [40.0, -40.0])
+def test_drifting_scores(cuda, slope):
+    """Scores that climb (or fall) steeply along the keys: every query row is
+    one direction u plus noise and key j carries slope * j / S along u, so a
+    row's maximum grows by tens of log2 units over its keys.  A rising row
+    exceeds its reference point by more than the forward's slack on most
+    tiles (moving it and rescaling O and the row sum mid-row); a falling row
+    never does, and its late keys underflow to zero weight.  Magnitudes are
+    chosen so that the bf16 rounding of dS before the dQ / dK products (as
+    in flash backward kernels) stays well inside the bar: computed on the
+    CPU, it alone moves dQ by 0.016 of max|dQ| 2.3 here (0.021 of 1.2 with
+    keys of norm 80)."""
+    t, chunks, hq, hkv = 200, [700, 200], 32, 8
+    s_len = sum(chunks)
+    g = torch.Generator().manual_seed(11)
+    u = torch.randn(D, generator=g)
+    u = u / u.norm()
+    q = (8.0 * u + 0.3 * torch.randn(1, t, hq, D, generator=g)).to(torch.bfloat16)
+    ramp = slope * torch.arange(s_len, dtype=torch.float32) / s_len
+    k_all = torch.randn(s_len, hkv, D, generator=g) + ramp[:, None, None] * u
+    v_all = torch.randn(s_len, hkv, D, generator=g)
+    ks = [k.to(torch.bfloat16) for k in k_all.split(chunks)]
+    vs = [v.to(torch.bfloat16) for v in v_all.split(chunks)]
+    dout = torch.randn(1, t, hq, D, generator=g).to(torch.bfloat16)
+    scale = D ** -0.5
+    want, wq, wks, wvs = ref.attention_with_grads(q[0], ks, vs, dout[0], scale)
+    _, want_lse = ref.chained_attention(q[0], ks, vs, scale)
+    layout = hip.chain_layout(t, chunks, hq, hkv)
+    qc = q[0].to(cuda).requires_grad_()
+    kc = [k.to(cuda).requires_grad_() for k in ks]
+    vc = [v.to(cuda).requires_grad_() for v in vs]
+    out, lse = hip.attention(qc, layout, kc, vc, scale)
+    out.backward(dout[0].to(cuda))
+    torch.cuda.synchronize()
+    # the rise of a row's scores along its keys, in log2 units
+    print(f"slope {slope}: scores move by ~{abs(slope) * 8.0 * scale / math.log(2):.0f} log2 units", flush=True)
+    torch.testing.assert_close(lse.cpu(), want_lse, rtol=0, atol=1e-3)
+    close(out, want, "out")
+    close(qc.grad, wq, "dq")
+    for i, (k, v) in enumerate(zip(kc, vc)):
+        close(k.grad, wks[i], f"dk[{i}]")
+        close(v.grad, wvs[i], f"dv[{i}]")
+
+
 # per segment: (own tokens, turn chunks after the shared prompt), as the
 # reference's packed-split test (tests/test_packed_flash_split.py:194-200)
 PACKS = [
