@@ -22,7 +22,9 @@
 // one wave's memory instructions overlap the other's MFMAs; accumulators in
 // the accumulation registers), v_mfma_f32_32x32x16_bf16.  K streams 32 at a
 // time through a 4-stage LDS ring filled by buffer_load ... lds (no register
-// staging), three stages ahead of the MFMAs, one work-group barrier per stage.
+// staging), refilled three stages ahead of the MFMAs, one work-group barrier
+// per stage; each barrier also certifies the next stage, whose first
+// fragments are read during the current stage's last MFMAs.
 // Rows past an operand's valid rows and 8-element K chunks past K arrive as
 // zeros (buffer range checking), so ragged edges need no masking in the loop.
 #include "common.h"
@@ -104,20 +106,19 @@ __device__ __forceinline__ int a_row(int mi, int i, int lane, int wm) {
   return 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3) + 32 * mi + 128 * wm;
 }
 
-// The MFMAs of one stage (two k-steps of 16) in a fixed order: the 6
-// fragment reads of k-step 0, then four groups of {two k-step-0 MFMAs, one or
-// two k-step-1 fragment reads, one refill DMA instruction}, then the 8
-// k-step-1 MFMAs.  Spreading the refill over the MFMAs keeps the wave issuing
-// MFMAs while the DMA is in flight.
+// The MFMAs of one stage (two k-steps of 16) in a fixed order.  The k-step-0
+// fragments a0 / b0 of `st` arrive already in registers (read during the
+// previous stage); four groups of {two k-step-0 MFMAs, one or two k-step-1
+// fragment reads, one refill DMA instruction}, then the 8 k-step-1 MFMAs,
+// beside which the k-step-0 fragments of the next stage `nx` (if any) are
+// read into a0 / b0.  Spreading the refill over the MFMAs keeps the wave
+// issuing MFMAs while the DMA is in flight, and with the next stage's first
+// fragments in registers the MFMAs start right after the stage barrier
+// instead of waiting for LDS reads every wave issues at once.
 template <class Dma>
-__device__ __forceinline__ void mma_stage(f32x16 acc[4][NI], const bf16* st, const int fa[2], const int fb[2],
-                                          Dma&& dma) {
-  bf16x8 a0[4], b0[NI], a1[4], b1[NI];
-#pragma unroll
-  for (int mi = 0; mi < 4; ++mi) a0[mi] = as_bf16x8(ld16(st + fa[0] + 32 * mi * TK));
-#pragma unroll
-  for (int ni = 0; ni < NI; ++ni) b0[ni] = as_bf16x8(ld16(st + fb[0] + 32 * ni * TK));
-  __builtin_amdgcn_sched_barrier(0);
+__device__ __forceinline__ void mma_stage(f32x16 acc[4][NI], const bf16* st, const bf16* nx, const int fa[2],
+                                          const int fb[2], bf16x8 (&a0)[4], bf16x8 (&b0)[NI], Dma&& dma) {
+  bf16x8 a1[4], b1[NI];
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
     acc[g][0] = mfma32(a0[g], b0[0], acc[g][0]);
@@ -132,9 +133,15 @@ __device__ __forceinline__ void mma_stage(f32x16 acc[4][NI], const bf16* st, con
     __builtin_amdgcn_sched_barrier(0);
   }
 #pragma unroll
-  for (int mi = 0; mi < 4; ++mi)
+  for (int mi = 0; mi < 4; ++mi) {
 #pragma unroll
     for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = mfma32(a1[mi], b1[ni], acc[mi][ni]);
+    if (nx != nullptr) {
+      a0[mi] = as_bf16x8(ld16(nx + fa[0] + 32 * mi * TK));
+      if (mi < NI) b0[mi] = as_bf16x8(ld16(nx + fb[0] + 32 * mi * TK));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
 }
 
 // wait until at most 4 * ahead of this wave's DMA instructions are in flight
@@ -184,19 +191,29 @@ __device__ __forceinline__ void gemm_tile(f32x16 acc[4][NI], const bf16* A, int6
   issue(s0, 0);
   if (nk > 1) issue(s1, 1);
   if (nk > 2) issue(s2, 2);
-  // step kt: this wave's DMA of stage kt has landed (later stages may still be
-  // in flight); the barrier makes every wave's share visible and certifies that
-  // all waves are done with the stage refilled next
-  auto step = [&](const bf16* cur, bf16* refill, int kt) {
+  // stage 0 landed everywhere: its k-step-0 fragments into registers
+  bf16x8 a0[4], b0[NI];
+  wait_dma(min(nk - 1, 2));
+  __builtin_amdgcn_s_barrier();
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi) a0[mi] = as_bf16x8(ld16(s0 + fa[0] + 32 * mi * TK));
+#pragma unroll
+  for (int ni = 0; ni < NI; ++ni) b0[ni] = as_bf16x8(ld16(s0 + fb[0] + 32 * ni * TK));
+  // step kt: this wave's DMA of stages kt and kt + 1 has landed (stage kt + 2
+  // may still be in flight); the barrier makes every wave's share of them
+  // visible -- the next stage's first fragments are read during this step --
+  // and certifies that all waves are done with the stage refilled next (read
+  // during step kt - 1 only)
+  auto step = [&](const bf16* cur, const bf16* nxt, bf16* refill, int kt) {
     __builtin_amdgcn_sched_barrier(0);  // keep each stage's loads inside its stage
-    wait_dma(min(nk - 1 - kt, 2));
+    wait_dma(max(min(nk - 2 - kt, 1), 0));
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
     __builtin_amdgcn_s_barrier();
     const bool refill_now = kt + 3 < nk;
     const int k0 = (kt + 3) * TK;
     const u32x4 ra = sa.descriptor(k0), rb = sb.descriptor(k0);
     const bool ka = k0 + sa.kchunk < K, kb = k0 + sb.kchunk < K;
-    mma_stage(acc, cur, fa, fb, [&](int g) {
+    mma_stage(acc, cur, kt + 1 < nk ? nxt : nullptr, fa, fb, a0, b0, [&](int g) {
       if (refill_now) {
         if (g < 2) sa.issue(ra, ka, refill, g, wave);
         else sb.issue(rb, kb, refill + TM * TK, g - 2, wave);
@@ -205,14 +222,14 @@ __device__ __forceinline__ void gemm_tile(f32x16 acc[4][NI], const bf16* A, int6
   };
   int kt = 0;
   for (; kt + 4 <= nk; kt += 4) {
-    step(s0, s3, kt);
-    step(s1, s0, kt + 1);
-    step(s2, s1, kt + 2);
-    step(s3, s2, kt + 3);
+    step(s0, s1, s3, kt);
+    step(s1, s2, s0, kt + 1);
+    step(s2, s3, s1, kt + 2);
+    step(s3, s0, s2, kt + 3);
   }
-  if (kt < nk) step(s0, s3, kt);
-  if (kt + 1 < nk) step(s1, s0, kt + 1);
-  if (kt + 2 < nk) step(s2, s1, kt + 2);
+  if (kt < nk) step(s0, s1, s3, kt);
+  if (kt + 1 < nk) step(s1, s2, s0, kt + 1);
+  if (kt + 2 < nk) step(s2, s3, s1, kt + 2);
   __builtin_amdgcn_sched_barrier(0);
   __syncthreads();
 }
