@@ -98,6 +98,43 @@ def test_lse_and_determinism(cuda):
         assert torch.equal(x, y)
 
 
+def test_fused_projection_views(cuda):
+    """Q, K and V as column slices of one fused projection output
+    [rows, (Hq + 2 Hkv) D] (row stride (Hq + 2 Hkv) D, head stride D): the
+    kernels read them in place through their strides; gradients land in the
+    slices of the fused tensor's gradient."""
+    t, s_len, hq, hkv = 150, 400, 32, 8
+    g = torch.Generator().manual_seed(21)
+    width = (hq + 2 * hkv) * D
+    qkv_q = torch.randn(t, width, generator=g).to(torch.bfloat16)      # rows of the queries
+    qkv_k = torch.randn(s_len, width, generator=g).to(torch.bfloat16)  # rows of the keys
+    dout = torch.randn(t, hq, D, generator=g).to(torch.bfloat16)
+    scale = D ** -0.5
+    split = lambda x: (x[:, : hq * D].view(-1, hq, D), x[:, hq * D : (hq + hkv) * D].view(-1, hkv, D),
+                       x[:, (hq + hkv) * D :].view(-1, hkv, D))
+    q_ref, _, _ = split(qkv_q)
+    _, k_ref, v_ref = split(qkv_k)
+    want, wq, wks, wvs = ref.attention_with_grads(q_ref, [k_ref], [v_ref], dout, scale)
+
+    a = qkv_q.to(cuda).requires_grad_()
+    b = qkv_k.to(cuda).requires_grad_()
+    q, _, _ = split(a)
+    _, k, v = split(b)
+    assert q.stride() == (width, D, 1) and k.stride() == (width, D, 1)
+    out, _ = hip.attention(q, hip.chain_layout(t, [s_len], hq, hkv), [k], [v], scale)
+    out.backward(dout.to(cuda))
+    torch.cuda.synchronize()
+    close(out, want, "out")
+    gq, _, _ = split(a.grad)
+    _, gk, gv = split(b.grad)
+    close(gq, wq, "dq")
+    close(gk, wks[0], "dk")
+    close(gv, wvs[0], "dv")
+    # the unused slices of the fused gradients stay zero
+    assert a.grad[:, hq * D :].abs().max().item() == 0.0
+    assert b.grad[:, : hq * D].abs().max().item() == 0.0
+
+
 @pytest.mark.parametrize("slope", [40.0, -40.0])
 def test_drifting_scores(cuda, slope):
     """Scores that climb (or fall) steeply along the keys: every query row is
