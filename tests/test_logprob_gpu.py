@@ -183,3 +183,21 @@ def test_weight_transpose_exact(cuda, v, d):
     want = torch.zeros(d, vp, dtype=torch.bfloat16)
     want[:, :v] = w.cpu().t()
     assert torch.equal(wt.cpu(), want)
+
+
+def test_repeated_runs_are_bit_identical(cuda):
+    """No atomics and no split reductions: the per-tile partials are merged in
+    a fixed order, so two runs give identical bits (forward, entropy, grad
+    wrt hidden, and the weight gradient's fixed-order fp32 accumulation)."""
+    n, d, v = 2500, 512, 9000
+    h, w, t, g_lp, g_ent = _inputs(n, d, v, seed=41)
+    runs = []
+    for _ in range(2):
+        hc = h.to(cuda).requires_grad_()
+        wc = w.to(cuda).requires_grad_()
+        lp, ent = hip.fused_logprob_entropy(hc, wc, t.to(cuda), chunk=1024)
+        (lp * g_lp.to(cuda) + ent * g_ent.to(cuda)).sum().backward()
+        torch.cuda.synchronize()
+        runs.append((lp.detach(), ent.detach(), hc.grad, wc.grad))
+    for a, b, name in zip(runs[0], runs[1], ("lp", "ent", "grad hidden", "grad weight")):
+        assert torch.equal(a, b), name
