@@ -151,31 +151,41 @@ class AttnLayout:
         for run, vis in enumerate(visits_of):
             visit0.append(len(visit_rows))
             visit_rows.extend(vis)
-        kv_items = []
+        # dK/dV items: every kvb-key block of every visited run; its cost is
+        # the number of query rows that see its first key, over its visits
         kvb = kv_block_keys(self.hq, self.hkv)
+        seg_len = np.array([n for _, n in self.seg_q], np.int64)
+        seg_off = np.array(self.seg_kv, np.int64) - seg_len
+        kv_cost, kv_run, kv_k0 = [], [], []
         for run, vis in enumerate(visits_of):
             if not vis:
                 continue
-            length = self.runs[run].length
-            for k0 in range(0, length, kvb):
-                cost = 0
-                for s, kpos in vis:
-                    off = self.seg_kv[s] - self.seg_q[s][1]
-                    first_row = max(0, kpos + k0 - off)
-                    cost += max(0, self.seg_q[s][1] - first_row)
-                kv_items.append((-cost, run, k0))
+            k0 = np.arange(0, self.runs[run].length, kvb, dtype=np.int64)
+            seg = np.array([s for s, _ in vis], np.int64)
+            kpos = np.array([kp for _, kp in vis], np.int64)
+            q_len, off = seg_len[seg], seg_off[seg]
+            first_row = np.maximum(0, kpos[None, :] + k0[:, None] - off[None, :])
+            kv_cost.append(np.maximum(0, q_len[None, :] - first_row).sum(axis=1))
+            kv_run.append(np.full(k0.shape, run, np.int64))
+            kv_k0.append(k0)
         # longest first; ties keep a deterministic order
         q_items.sort()
-        kv_items.sort()
         q_work = np.array([(s, q0) for _, s, q0 in q_items], np.int32).reshape(-1, 2)
-        kv_work = np.array([(r, k0) for _, r, k0 in kv_items], np.int32).reshape(-1, 2)
+        if kv_cost:
+            cost, run_of, k0_of = (np.concatenate(x) for x in (kv_cost, kv_run, kv_k0))
+            order = np.lexsort((k0_of, run_of, -cost))  # cost descending, then run, then k0
+            kv_work = np.stack([run_of[order], k0_of[order]], axis=1).astype(np.int32)
+            kv_costs = cost[order].tolist()
+        else:
+            kv_work = np.zeros((0, 2), np.int32)
+            kv_costs = []
         group = self.hq // self.hkv
         # rows the forward / dQ work-groups re-read: K and V of every run; the
         # dK/dV work-groups: Q and dO of every row (bf16, all heads)
         kv_bytes = sum(run.length for run in self.runs) * self.hkv * HEAD_DIM * 2 * 2
         q_bytes = self.q_rows * self.hq * HEAD_DIM * 2 * 2
         q_long = _long_items([-c for c, _, _ in q_items], self.hkv * (group // heads_per_block(group)), kv_bytes)
-        kv_long = _long_items([-c for c, _, _ in kv_items], self.hkv, q_bytes)
+        kv_long = _long_items(kv_costs, self.hkv, q_bytes)
         seg_spans = np.array(spans, REF_DTYPE) if spans else np.zeros(0, REF_DTYPE)
         run_visits = np.array(visit_rows, REF_DTYPE) if visit_rows else np.zeros(0, REF_DTYPE)
         return (segs, seg_spans, run_visits, q_work, kv_work, visit0, [len(v) for v in visits_of],
