@@ -244,6 +244,13 @@ __global__ __launch_bounds__(64 * 8 / NQB, NQB == 1 ? 4 : 2) void fwd_wave_kerne
           for (int qb = 0; qb < NQB; ++qb) sc[kb][qb] = mfma16(ak, qreg[qb][ks], sc[kb][qb]);
         }
       }
+      // K fragment reads three (kb, ks) steps ahead of their MFMAs
+      __builtin_amdgcn_sched_group_barrier(0x100, 3, 1);
+#pragma unroll
+      for (int st = 0; st < 8; ++st) {
+        __builtin_amdgcn_sched_group_barrier(0x008, NQB, 1);
+        if (st + 3 < 8) __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
+      }
       if (masked) {
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
