@@ -250,6 +250,30 @@ int ts_logprob_grad_hidden(const void* dlogits, int64_t ld_dlogits,
                            int64_t ld_grad, void* stream);
 
 /* ------------------------------------------------------------------------
+ * Boundary adjoints
+ * ---------------------------------------------------------------------- */
+
+/* Reduction of the consumer adjoints of a shared forest segment into its
+ * parent adjoint: replaces the fused reduction of
+ * engine/boundary_adjoint.py:49-115 (_boundary_adjoint_reduce_kernel, called
+ * by _triton_reduce, :201-225).  out = cast(existing + adjoints[0] + ... +
+ * adjoints[n - 1]), summed in fp32 in that order (without existing: from 0)
+ * and cast once to dtype.  adjoints: host array of n_adjoints (0..16) device
+ * pointers, each n_elements of dtype; existing: device pointer or NULL (at
+ * least one input); every pointer 16-byte aligned; out must not alias an
+ * input; with n_elements == 0 nothing is accessed.  Inputs are not modified. */
+int ts_adjoint_reduce(const void* const* adjoints, int n_adjoints, const void* existing, void* out,
+                      int64_t n_elements, int dtype, void* stream);
+
+/* FP32 adjoint ledger (engine/streaming.py:2647-2665, _ledger_accumulate):
+ * init != 0: ledger = widen(contribution) (the first contribution's widening
+ * copy); init == 0: ledger += widen(contribution) (the mixed-dtype add_).
+ * ledger: n_elements fp32; contribution: n_elements of dtype; both 16-byte
+ * aligned and distinct. */
+int ts_ledger_add(float* ledger, const void* contribution, int64_t n_elements, int dtype, int init,
+                  void* stream);
+
+/* ------------------------------------------------------------------------
  * Diagnostics
  * ------------------------------------------------------------------------ */
 

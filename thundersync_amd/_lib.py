@@ -55,6 +55,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_P, _I64, _P, _I64, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P, _I64, _P],
     ),
     "ts_logprob_grad_hidden": (_INT, [_P, _I64, _P, _I64, _I64, _I64, _I64, _P, _I64, _P]),
+    "ts_adjoint_reduce": (_INT, [ctypes.POINTER(_P), _INT, _P, _P, _I64, _INT, _P]),
+    "ts_ledger_add": (_INT, [_P, _P, _I64, _INT, _INT, _P]),
     "ts_attn_heads_per_block": (_INT, [_INT]),
     "ts_attn_kv_block": (_INT, [_INT]),
     "ts_attn_q_block": (_INT, [_INT]),

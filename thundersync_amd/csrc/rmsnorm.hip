@@ -18,56 +18,6 @@ namespace {
 
 constexpr int kThreads = 256;  // 4 waves
 
-// load / store eight consecutive elements (16 bytes for 16-bit types)
-template <typename T> __device__ __forceinline__ void load8(const T* p, float (&o)[8]);
-template <> __device__ __forceinline__ void load8<bf16>(const bf16* p, float (&o)[8]) {
-  const u32x4 r = *reinterpret_cast<const u32x4*>(p);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    o[2 * i] = __uint_as_float(r[i] << 16);
-    o[2 * i + 1] = __uint_as_float(r[i] & 0xffff0000u);
-  }
-}
-template <> __device__ __forceinline__ void load8<f16>(const f16* p, float (&o)[8]) {
-  typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-  const h8 r = *reinterpret_cast<const h8*>(p);
-#pragma unroll
-  for (int i = 0; i < 8; ++i) o[i] = (float)r[i];
-}
-template <> __device__ __forceinline__ void load8<float>(const float* p, float (&o)[8]) {
-  const f32x4 a = *reinterpret_cast<const f32x4*>(p);
-  const f32x4 b = *reinterpret_cast<const f32x4*>(p + 4);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    o[i] = a[i];
-    o[4 + i] = b[i];
-  }
-}
-template <typename T> __device__ __forceinline__ void store8(T* p, const float (&o)[8]);
-template <> __device__ __forceinline__ void store8<bf16>(bf16* p, const float (&o)[8]) {
-  u32x4 r;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) r[i] = pack_bf2(o[2 * i], o[2 * i + 1]);
-  *reinterpret_cast<u32x4*>(p) = r;
-}
-template <> __device__ __forceinline__ void store8<f16>(f16* p, const float (&o)[8]) {
-  typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-  h8 r;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) r[i] = (f16)o[i];
-  *reinterpret_cast<h8*>(p) = r;
-}
-template <> __device__ __forceinline__ void store8<float>(float* p, const float (&o)[8]) {
-  f32x4 a, b;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    a[i] = o[i];
-    b[i] = o[4 + i];
-  }
-  *reinterpret_cast<f32x4*>(p) = a;
-  *reinterpret_cast<f32x4*>(p + 4) = b;
-}
-
 // eight consecutive elements kept as loaded (16-bit types: four dwords), so a
 // row held across a loop iteration costs half the registers of its floats
 template <typename T> struct Packed8 { u32x4 v; };
