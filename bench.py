@@ -16,6 +16,9 @@ Workloads (synthetic data drawn from fixed seeds):
   and gated before the projection (the reference's production schedule),
   frozen head; scored tokens/s, 6 * N * V * D FLOP.
 * ``secondary[2]``: RMSNorm forward + backward on [16384, 4096] bf16; GB/s.
+* ``secondary[3]``: boundary-adjoint reduction -- an existing parent
+  adjoint plus 16 consumer adjoints of [4096, 4096] bf16 summed in fp32 into
+  a new tensor; GB/s of inputs read plus output written.
 
 A step is one pass of the operator over its whole input, with inputs
 already resident in HBM.  Per-kernel device time comes from the library's
@@ -50,7 +53,7 @@ def parse():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--seed", type=int, default=0)
-    ap.add_argument("--only", choices=("all", "attention", "chunked", "logprob", "rmsnorm", "copy"), default="all",
+    ap.add_argument("--only", choices=("all", "attention", "chunked", "logprob", "rmsnorm", "adjoint", "copy"), default="all",
                     help="one workload; 'copy' runs only the plain 256 MiB device copy whose FETCH_SIZE / "
                          "WRITE_SIZE readings calibrate the traffic counters")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -100,7 +103,7 @@ def measured_traffic(workload, kernel):
     entry = table.get("workloads", {}).get(workload, {}).get(kernel)
     if entry is None:
         return None, None
-    return entry["traffic_bytes"], table.get("measured_at_commit")
+    return entry["traffic_bytes"], entry["measured_at_commit"]
 
 
 def roofline_of(per, work_per_step, unit, peak, workload):
@@ -503,6 +506,76 @@ def bench_rmsnorm(args, device):
     }
 
 
+# ---------------------------------------------------------------------------
+# Boundary-adjoint reduction
+# ---------------------------------------------------------------------------
+ADJOINT_DEGREE = 16
+ADJOINT_SHAPE = (4096, 4096)
+
+
+def bench_adjoint(args, device):
+    import torch
+
+    from thundersync_amd import boundary_adjoint
+
+    g = torch.Generator(device=device).manual_seed(args.seed)
+    adj = [torch.randn(ADJOINT_SHAPE, generator=g, device=device, dtype=torch.bfloat16)
+           for _ in range(ADJOINT_DEGREE)]
+    existing = torch.randn(ADJOINT_SHAPE, generator=g, device=device, dtype=torch.bfloat16)
+
+    def step():
+        boundary_adjoint.reduce_boundary_adjoints(adj, existing=existing)
+
+    kernels = ["adjoint.reduce_kernel"]
+    ms, per = timed(step, args.steps, args.warmup, kernels)
+    n = ADJOINT_SHAPE[0] * ADJOINT_SHAPE[1]
+    nbytes = (ADJOINT_DEGREE + 1) * n * 2 + n * 2  # every input read once, the output written once
+    result = {
+        "metric": "boundary-adjoint reduce GB/s",
+        "value": round(nbytes / (ms * 1e-3) / 1e9, 1),
+        "unit": "GB/s",
+        "ms_per_step": round(ms, 4),
+        "roofline": roofline_of(per, {"adjoint.reduce_kernel": nbytes}, "GB/s", PEAK_HBM_GBS, "adjoint"),
+        "kernels": {k: {"avg_ms": round(x, 4), "launches_per_step": m} for k, (x, m) in per.items()},
+        "config": {"workload": f"boundary adjoint: existing + {ADJOINT_DEGREE} consumer adjoints "
+                               f"[{ADJOINT_SHAPE[0]}, {ADJOINT_SHAPE[1]}] bf16, fp32 accumulation",
+                   "seed": args.seed},
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = adjoint_cpu_baseline(adj, existing, nbytes)
+    return result
+
+
+def adjoint_cpu_baseline(adj, existing, nbytes, rows=1024):
+    """The fused reduction's semantics on the CPU (engine/boundary_adjoint.py:75-115:
+    fp32 accumulation in input order, one cast) over the first `rows` rows."""
+    import torch
+
+    from oracle import boundary_adjoint as ref
+
+    torch.set_num_threads(cpu_threads())
+    a = [x[:rows].cpu() for x in adj]
+    e = existing[:rows].cpu()
+    reps = 0
+    t0 = time.perf_counter()
+    while True:
+        ref.reduce_fp32(a, e)
+        reps += 1
+        dt = time.perf_counter() - t0
+        if dt > 10.0 or reps >= 20000:
+            break
+    sample_bytes = nbytes * rows / ADJOINT_SHAPE[0]
+    return {
+        "value": round(sample_bytes * reps / dt / 1e9, 2),
+        "unit": "GB/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"first {rows} of {ADJOINT_SHAPE[0]} rows, existing + {ADJOINT_DEGREE} bf16 adjoints, "
+                  f"{reps} repetitions",
+        "seconds": round(dt, 3),
+    }
+
+
 def calibration_copy(device, nbytes: int = 256 << 20, repeats: int = 3) -> None:
     """A plain device-to-device copy of `nbytes`, `repeats` times: the reference
     reading for scaling the FETCH_SIZE / WRITE_SIZE counters to bytes."""
@@ -560,6 +633,8 @@ def main():
         out["secondary"].append(bench_logprob(args, device))
     if args.only in ("all", "rmsnorm"):
         out["secondary"].append(bench_rmsnorm(args, device))
+    if args.only in ("all", "adjoint"):
+        out["secondary"].append(bench_adjoint(args, device))
     props = torch.cuda.get_device_properties(device)
     out["device"] = {"name": props.name, "arch": getattr(props, "gcnArchName", ""),
                      "cus": props.multi_processor_count}
