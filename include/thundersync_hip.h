@@ -274,6 +274,39 @@ int ts_ledger_add(float* ledger, const void* contribution, int64_t n_elements, i
                   void* stream);
 
 /* ------------------------------------------------------------------------
+ * Forest metadata (host code: every pointer below is host memory)
+ * ------------------------------------------------------------------------ */
+
+/* The exact shared forest of a batch of trajectories: replaces build_forest
+ * (engine/segments.py:280-346) and its shared-prefix partition (:243-278).
+ * Trajectory i's keys (2 * token + scored) are keys[key_offsets[i] ..
+ * key_offsets[i + 1]) (at least one each) and its group is group_id[i].
+ * Nodes come out numbered in pre-order (groups ascending, children by
+ * ascending first key): node n holds keys[key_offsets[node_src[n]] +
+ * node_offset[n] ..] of length node_len[n] (0 only for a root), its parent
+ * (-1 for a root), depth and group; leaf_of[i] is trajectory i's last node.
+ * Node arrays hold max_nodes >= 2 * n_traj entries. */
+int ts_forest_build(int64_t n_traj, const int64_t* group_id, const int64_t* key_offsets, const int64_t* keys,
+                    int64_t max_nodes, int64_t* n_nodes, int64_t* node_parent, int64_t* node_depth,
+                    int64_t* node_group, int64_t* node_src, int64_t* node_offset, int64_t* node_len,
+                    int64_t* leaf_of);
+
+/* The execution plan of a forest: replaces compile_plan
+ * (engine/plan.py:166-340).  order: the nodes in DFS pre-order (parents
+ * first); node n's keys are keys[node_key_offsets[n] .. + node_len[n]);
+ * traj_leaf / traj_id: each trajectory's leaf node and id, in the forest's
+ * trajectory order.  Outputs: token_ids, position_ids, node_of and
+ * subtree_end of P = sum(node_len) physical rows; node_start / node_end per
+ * node; score_src / score_tgt / score_pos of *n_scored <= P slots;
+ * logical_to_slot / logical_traj of *n_logical <= max_logical entries. */
+int ts_plan_compile(int64_t n_nodes, const int64_t* node_parent, const int64_t* order, const int64_t* node_len,
+                    const int64_t* node_key_offsets, const int64_t* keys, int64_t n_traj, const int64_t* traj_leaf,
+                    const int64_t* traj_id, int64_t max_logical, int64_t* token_ids, int64_t* position_ids,
+                    int64_t* node_of, int64_t* node_start, int64_t* node_end, int64_t* subtree_end,
+                    int64_t* score_src, int64_t* score_tgt, int64_t* score_pos, int64_t* n_scored,
+                    int64_t* logical_to_slot, int64_t* logical_traj, int64_t* n_logical);
+
+/* ------------------------------------------------------------------------
  * Diagnostics
  * ------------------------------------------------------------------------ */
 

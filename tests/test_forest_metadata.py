@@ -151,3 +151,58 @@ def test_pack_layout_cumulative_lengths_and_input_order():
     regrouped = layout.by_segment(tuple(inputs[: len(order)]))
     for s, ks in enumerate(regrouped):
         assert all(a is b for a, b in zip(ks, ancestors[s][0]))
+
+
+@pytest.mark.parametrize("name", sorted(GOLDEN))
+def test_plan_from_node_lists_matches_golden(name):
+    """compile_plan on a forest that does not carry the builder's flat keys
+    (a forest assembled from node lists, as the reference's builder returns)."""
+    case = GOLDEN[name]
+    forest = prod.build_forest(_prod_trajs(case["trajectories"]))
+    forest._flat = None
+    assert _plan_dict(prod.compile_plan(forest)) == case["plan"]
+
+
+def test_empty_batch():
+    forest = prod.build_forest([])
+    assert forest.nodes == [] and forest.roots == [] and forest.leaf_of == {}
+    plan = prod.compile_plan(forest)
+    assert plan.n_physical == 0 and plan.n_scored == 0 and plan.n_nodes == 0
+    assert plan.logical_to_slot.numel() == 0 and plan.key_ranges == []
+
+
+def test_native_builder_rejects_bad_arguments():
+    """The C entry points report bad input as an error status (host code only)."""
+    import ctypes
+
+    import numpy as np
+
+    from thundersync_amd import _lib
+
+    lib = _lib.require_library()
+    p = lambda a: a.ctypes.data
+    keys = np.array([4, 6, 4, 8], np.int64)
+    offsets = np.array([0, 2, 4], np.int64)
+    groups = np.zeros(2, np.int64)
+    out = [np.zeros(4, np.int64) for _ in range(6)]
+    leaf = np.zeros(2, np.int64)
+    count = ctypes.c_int64(0)
+    args = (p(groups), p(offsets), p(keys))
+    assert lib.ts_forest_build(2, *args, 3, ctypes.byref(count), *map(p, out), p(leaf)) == 1
+    assert b"max_nodes" in lib.ts_hip_last_error()
+    assert lib.ts_forest_build(2, *args, 4, ctypes.byref(count), *map(p, out), p(leaf)) == 0
+    assert count.value == 3 and out[0][:3].tolist() == [-1, 0, 0] and leaf.tolist() == [1, 2]
+    empty = np.array([0, 2, 2], np.int64)
+    assert lib.ts_forest_build(2, p(groups), p(empty), p(keys), 4, ctypes.byref(count), *map(p, out), p(leaf)) == 1
+    assert b"empty" in lib.ts_hip_last_error()
+    # a plan whose order lists a child before its parent
+    parent = np.array([-1, 0], np.int64)
+    bad_order = np.array([1, 0], np.int64)
+    lens = np.array([1, 1], np.int64)
+    koff = np.array([0, 1], np.int64)
+    bufs = [np.zeros(4, np.int64) for _ in range(11)]
+    n1, n2 = ctypes.c_int64(0), ctypes.c_int64(0)
+    one = np.array([1], np.int64)
+    status = lib.ts_plan_compile(2, p(parent), p(bad_order), p(lens), p(koff), p(keys), 1, p(one), p(one), 4,
+                                 *map(p, bufs[:9]), ctypes.byref(n1), p(bufs[9]), p(bufs[10]), ctypes.byref(n2))
+    assert status == 1 and b"before its parent" in lib.ts_hip_last_error()

@@ -57,6 +57,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "ts_logprob_grad_hidden": (_INT, [_P, _I64, _P, _I64, _I64, _I64, _I64, _P, _I64, _P]),
     "ts_adjoint_reduce": (_INT, [ctypes.POINTER(_P), _INT, _P, _P, _I64, _INT, _P]),
     "ts_ledger_add": (_INT, [_P, _P, _I64, _INT, _INT, _P]),
+    "ts_forest_build": (_INT, [_I64, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _P, _P, _P]),
+    "ts_plan_compile": (_INT, [_I64, _P, _P, _P, _P, _P, _I64, _P, _P, _I64] + [_P] * 13),
     "ts_attn_heads_per_block": (_INT, [_INT]),
     "ts_attn_kv_block": (_INT, [_INT]),
     "ts_attn_q_block": (_INT, [_INT]),

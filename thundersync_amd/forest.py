@@ -3,10 +3,12 @@
 Same API and bit-identical outputs as the reference's
 ``engine/segments.py`` (``Segment``, ``Trajectory``, ``build_forest``) and
 ``engine/plan.py`` (``ExecutionPlan``, ``compile_plan``,
-``visibility_mask``), built differently: the radix trie is grown with an
-explicit work stack and numpy mismatch scans instead of recursion and binary
-search over slices, and the plan arrays are assembled with numpy over whole
-nodes.  The conventions that make the output bit-exact are kept:
+``visibility_mask``), built differently: the trie and the plan arrays are
+computed in native code (``ts_forest_build``, ``ts_plan_compile``) in one pass
+over flat ``2 * token + scored`` key arrays -- an explicit work stack and
+direct mismatch scans instead of recursion and binary search over slices --
+and this module only packs the keys and wraps the results in the reference's
+objects.  The conventions that make the output bit-exact are kept:
 
 * groups in ascending ``group_id``; a node's children in ascending
   ``(token, scored)`` order of their first key (segments.py:336);
@@ -29,8 +31,12 @@ from collections.abc import Iterable, Sequence
 from dataclasses import dataclass, field
 from enum import Enum
 
+import ctypes
+
 import numpy as np
 import torch
+
+from . import _lib
 
 
 class SegmentKind(str, Enum):
@@ -141,58 +147,60 @@ class SegmentForest:
         return path[::-1]
 
 
-def _shared_prefix(keys: list[np.ndarray], offset: int) -> int:
-    """Length of the prefix all ``keys[i][offset:]`` agree on."""
-    first = keys[0]
-    limit = min(len(k) for k in keys) - offset
-    share = limit
-    for k in keys[1:]:
-        if share == 0:
-            break
-        diff = np.flatnonzero(first[offset : offset + share] != k[offset : offset + share])
-        if diff.size:
-            share = int(diff[0])
-    return max(share, 0)
+def _ptr(a: np.ndarray) -> int:
+    return a.ctypes.data
+
+
+def _flat_keys(trajectories: Sequence[Trajectory]) -> tuple[np.ndarray, np.ndarray]:
+    parts = [t.keys() for t in trajectories]
+    offsets = np.zeros(len(parts) + 1, np.int64)
+    np.cumsum([len(p) for p in parts], out=offsets[1:])
+    keys = np.ascontiguousarray(np.concatenate(parts), np.int64) if parts else np.zeros(1, np.int64)
+    return keys, offsets
 
 
 def build_forest(trajectories: Sequence[Trajectory]) -> SegmentForest:
-    """Compress trajectories into the exact shared forest (segments.py:280-346 semantics)."""
+    """Compress trajectories into the exact shared forest (segments.py:280-346 semantics),
+    on ``ts_forest_build``."""
+    trajs = list(trajectories)
+    lib = _lib.require_library()
+    n = len(trajs)
+    keys, offsets = _flat_keys(trajs)
+    groups = np.array([t.group_id for t in trajs] or [0], np.int64)
+    cap = max(2 * n, 1)
+    parent, depth, group, src, off, length = (np.zeros(cap, np.int64) for _ in range(6))
+    leaf = np.zeros(max(n, 1), np.int64)
+    count = ctypes.c_int64(0)
+    _lib.check(lib.ts_forest_build(n, _ptr(groups), _ptr(offsets), _ptr(keys), cap, ctypes.byref(count),
+                                   _ptr(parent), _ptr(depth), _ptr(group), _ptr(src), _ptr(off), _ptr(length),
+                                   _ptr(leaf)), f"ts_forest_build({n} trajectories)")
+    nn = count.value
+    parents = parent[:nn].tolist()
+    starts = (offsets[src[:nn]] + off[:nn]).tolist()
+    lens = length[:nn].tolist()
+    members: list[list[int]] = [[] for _ in range(nn)]
+    leaf_of: dict[int, int] = {}
+    for i, t in enumerate(trajs):
+        node = int(leaf[i])
+        leaf_of[t.traj_id] = node
+        while node >= 0:
+            members[node].append(t.traj_id)
+            node = parents[node]
     nodes: list[ForestNode] = []
     roots: list[int] = []
-    leaf_of: dict[int, int] = {}
-    groups: dict[int, list[Trajectory]] = {}
-    for t in trajectories:
-        groups.setdefault(t.group_id, []).append(t)
-    for group_id in sorted(groups):
-        members = groups[group_id]
-        keys = {t.traj_id: t.keys() for t in members}
-        # work stack of (trajectory ids, offset, parent, depth); popped in pre-order
-        stack = [([t.traj_id for t in members], 0, None, 0)]
-        while stack:
-            ids, offset, parent, depth = stack.pop()
-            share = _shared_prefix([keys[i] for i in ids], offset)
-            if share == 0 and parent is not None:
-                raise AssertionError("zero-length non-root node: partition is wrong")
-            head = keys[ids[0]][offset : offset + share]
-            idx = len(nodes)
-            nodes.append(ForestNode(
-                tokens=(head >> 1).tolist(), scored=(head & 1).astype(bool).tolist(), parent=parent,
-                depth=depth, trajectories=list(ids), group_id=group_id,
-            ))
-            if parent is None:
-                roots.append(idx)
-            else:
-                nodes[parent].children.append(idx)
-            nxt = offset + share
-            branches: dict[int, list[int]] = {}
-            for i in ids:
-                if len(keys[i]) == nxt:
-                    leaf_of[i] = idx
-                else:
-                    branches.setdefault(int(keys[i][nxt]), []).append(i)
-            for key in sorted(branches, reverse=True):
-                stack.append((branches[key], nxt, idx, depth + 1))
-    return SegmentForest(nodes, roots, list(trajectories), leaf_of)
+    for idx in range(nn):
+        head = keys[starts[idx]:starts[idx] + lens[idx]]
+        p = parents[idx]
+        nodes.append(ForestNode(tokens=(head >> 1).tolist(), scored=(head & 1).astype(bool).tolist(),
+                                parent=None if p < 0 else p, depth=int(depth[idx]), trajectories=members[idx],
+                                group_id=int(group[idx])))
+        if p < 0:
+            roots.append(idx)
+        else:
+            nodes[p].children.append(idx)
+    forest = SegmentForest(nodes, roots, trajs, leaf_of)
+    forest._flat = (keys, np.asarray(starts, np.int64), np.asarray(lens, np.int64))
+    return forest
 
 
 @dataclass
@@ -259,93 +267,67 @@ def _preorder(forest: SegmentForest) -> list[int]:
     return order
 
 
+def _node_keys(forest: SegmentForest) -> tuple[np.ndarray, np.ndarray, np.ndarray]:
+    """(keys, node key offsets, node lengths): the builder's flat keys when the
+    nodes still match them, else the nodes' own token lists packed as keys."""
+    lengths = np.array([len(n.tokens) for n in forest.nodes], np.int64)
+    flat = getattr(forest, "_flat", None)
+    if flat is not None and flat[2].shape == lengths.shape and np.array_equal(flat[2], lengths):
+        return flat[0], flat[1], lengths
+    parts = [np.asarray(n.tokens, np.int64) * 2 + np.asarray(n.scored, np.int64) for n in forest.nodes]
+    offsets = np.zeros(len(parts), np.int64)
+    if parts:
+        np.cumsum(lengths[:-1], out=offsets[1:])
+    keys = np.concatenate(parts) if parts and lengths.sum() else np.zeros(1, np.int64)
+    return np.ascontiguousarray(keys, np.int64), offsets, lengths
+
+
 def compile_plan(forest: SegmentForest, device: torch.device | str = "cpu") -> ExecutionPlan:
-    """Lay the forest out in DFS pre-order and derive every index from it."""
+    """Lay the forest out in DFS pre-order and derive every index from it
+    (plan.py:166-340), on ``ts_plan_compile``."""
+    lib = _lib.require_library()
     nodes = forest.nodes
-    order = _preorder(forest)
     nn = len(nodes)
-    lengths = np.array([len(n.tokens) for n in nodes], np.int64)
-    start = np.zeros(nn, np.int64)
-    end = np.zeros(nn, np.int64)
-    pos0 = np.zeros(nn, np.int64)
-    cursor = 0
-    for n in order:
-        p = nodes[n].parent
-        pos0[n] = 0 if p is None else pos0[p] + lengths[p]
-        start[n] = cursor
-        cursor += lengths[n]
-        end[n] = cursor
-    ordered = [n for n in order if lengths[n]]
-    counts = lengths[ordered] if ordered else np.zeros(0, np.int64)
-    tokens = np.concatenate([np.asarray(nodes[n].tokens, np.int64) for n in ordered]) if ordered else np.zeros(0, np.int64)
-    node_of = np.repeat(np.asarray(ordered, np.int64), counts)
-    node_pos0 = np.repeat(pos0[ordered], counts) if ordered else np.zeros(0, np.int64)
-    within = np.arange(cursor, dtype=np.int64) - np.repeat(start[ordered], counts) if ordered else np.zeros(0, np.int64)
-    positions = node_pos0 + within
+    order_list = _preorder(forest)
+    order = np.asarray(order_list or [0], np.int64)
+    keys, key_off, lengths = _node_keys(forest)
+    parents = np.array([-1 if n.parent is None else n.parent for n in nodes] or [0], np.int64)
+    p_total = int(lengths.sum())
+    trajs = forest.trajectories
+    traj_leaf = np.array([forest.leaf_of[t.traj_id] for t in trajs] or [0], np.int64)
+    traj_ids = np.array([t.traj_id for t in trajs] or [0], np.int64)
+    max_logical = sum(t.n_tokens for t in trajs)
+    cap_p, cap_l = max(p_total, 1), max(max_logical, 1)
+    token_ids, position_ids, node_of, subtree_end, src, tgt, pos = (np.zeros(cap_p, np.int64) for _ in range(7))
+    start, end = np.zeros(max(nn, 1), np.int64), np.zeros(max(nn, 1), np.int64)
+    l2s, ltraj = np.zeros(cap_l, np.int64), np.zeros(cap_l, np.int64)
+    n_scored, n_logical = ctypes.c_int64(0), ctypes.c_int64(0)
+    _lib.check(lib.ts_plan_compile(nn, _ptr(parents), _ptr(order), _ptr(np.ascontiguousarray(lengths if nn else order)),
+                                   _ptr(np.ascontiguousarray(key_off if nn else order)), _ptr(keys), len(trajs),
+                                   _ptr(traj_leaf), _ptr(traj_ids), max_logical, _ptr(token_ids), _ptr(position_ids),
+                                   _ptr(node_of), _ptr(start), _ptr(end), _ptr(subtree_end), _ptr(src), _ptr(tgt),
+                                   _ptr(pos), ctypes.byref(n_scored), _ptr(l2s), _ptr(ltraj), ctypes.byref(n_logical)),
+               f"ts_plan_compile({nn} nodes, {p_total} rows)")
+    ns, nl = n_scored.value, n_logical.value
 
-    sub_end = end.copy()
-    for n in reversed(order):
-        for c in nodes[n].children:
-            sub_end[n] = max(sub_end[n], sub_end[c])
-    subtree_end = np.repeat(sub_end[ordered], counts) if ordered else np.zeros(0, np.int64)
-
+    starts, ends = start[:nn].tolist(), end[:nn].tolist()
     key_ranges: list[list[tuple[int, int]]] = [[] for _ in nodes]
-    for n in order:
+    for n in order_list:
         p = nodes[n].parent
-        inherited = [] if p is None else key_ranges[p][:-1] + [(int(start[p]), int(end[p]))]
-        key_ranges[n] = [(s, e) for s, e in inherited if e > s] + [(int(start[n]), int(end[n]))]
-
-    src, tgt, pos = [], [], []
-    slot_start = np.zeros(nn, np.int64)
-    slot_count = np.zeros(nn, np.int64)
-    slots = 0
-    for n in order:
-        node = nodes[n]
-        slot_start[n] = slots
-        if not node.tokens:
-            continue
-        scored = np.asarray(node.scored, bool).copy()
-        if node.parent is None:
-            scored[0] = False
-        j = np.flatnonzero(scored)
-        if j.size == 0:
-            continue
-        p = j + start[n]
-        s = p - 1
-        if node.parent is not None:
-            s = np.where(j == 0, end[node.parent] - 1, s)
-        src.append(s)
-        pos.append(p)
-        tgt.append(np.asarray(node.tokens, np.int64)[j])
-        slot_count[n] = j.size
-        slots += j.size
-
-    l2s, ltraj = [], []
-    for traj in forest.trajectories:
-        total = 0
-        for n in forest.path_to_root(forest.leaf_of[traj.traj_id]):
-            c = int(slot_count[n])
-            if c:
-                l2s.append(np.arange(slot_start[n], slot_start[n] + c, dtype=np.int64))
-                total += c
-        if total:
-            ltraj.append(np.full(total, traj.traj_id, np.int64))
+        inherited = [] if p is None else key_ranges[p][:-1] + [(starts[p], ends[p])]
+        key_ranges[n] = [(s, e) for s, e in inherited if e > s] + [(starts[n], ends[n])]
 
     dev = torch.device(device)
 
-    def t(a) -> torch.Tensor:
-        arr = np.concatenate(a) if isinstance(a, list) else a
-        if isinstance(a, list) and not a:
-            arr = np.zeros(0, np.int64)
-        return torch.as_tensor(np.ascontiguousarray(arr, dtype=np.int64)).to(dev)
+    def t(a: np.ndarray, count: int) -> torch.Tensor:
+        return torch.from_numpy(a[:count].copy()).to(dev)
 
-    parents = np.array([-1 if n.parent is None else n.parent for n in nodes], np.int64)
     depths = np.array([n.depth for n in nodes], np.int64)
     return ExecutionPlan(
-        token_ids=t(tokens), position_ids=t(positions), node_of=t(node_of),
-        node_start=t(start), node_end=t(end), node_parent=t(parents), node_depth=t(depths),
-        subtree_end=t(subtree_end), score_src=t(src), score_tgt=t(tgt), score_pos=t(pos),
-        logical_to_slot=t(l2s), logical_traj=t(ltraj), key_ranges=key_ranges, forest=forest,
+        token_ids=t(token_ids, p_total), position_ids=t(position_ids, p_total), node_of=t(node_of, p_total),
+        node_start=t(start, nn), node_end=t(end, nn), node_parent=t(parents, nn), node_depth=t(depths, nn),
+        subtree_end=t(subtree_end, p_total), score_src=t(src, ns), score_tgt=t(tgt, ns), score_pos=t(pos, ns),
+        logical_to_slot=t(l2s, nl), logical_traj=t(ltraj, nl), key_ranges=key_ranges, forest=forest,
     )
 
 
