@@ -1,0 +1,51 @@
+"""bench.py's host-side contract (CPU): the one-GPU guard, the roofline
+arithmetic, the traffic table lookup and the CPU-baseline repetition helper."""
+
+from __future__ import annotations
+
+import json
+import subprocess
+import sys
+
+import pytest
+
+from tests.conftest import ROOT
+
+sys.path.insert(0, str(ROOT))
+import bench  # noqa: E402
+
+
+def test_more_than_one_gpu_is_refused_with_a_message():
+    proc = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                          timeout=60)
+    assert proc.returncode == 2
+    assert "one GPU" in proc.stderr and proc.stdout == ""
+
+
+def test_roofline_of_picks_the_kernel_with_the_largest_device_time():
+    per = {"a": (1.0, 1.0), "b": (0.5, 3.0)}  # b: 1.5 ms per step
+    roof = bench.roofline_of(per, {"a": 1e12, "b": 6e12}, "TFLOP/s", 2500.0, "no-such-workload")
+    assert roof["kernel"] == "b" and roof["bound"] == "mfma"
+    assert roof["work_per_launch"] == pytest.approx(2e12)
+    assert roof["achieved"] == pytest.approx(2e12 / 0.5e-3 / 1e12)  # 4000 TFLOP/s
+    assert roof["frac"] == pytest.approx(roof["achieved"] / 2500.0, rel=1e-3)
+    assert roof["traffic"] is None and roof["traffic_source"] is None
+    hbm = bench.roofline_of({"c": (0.1, 1.0)}, {"c": 4e8}, "GB/s", 8000.0, "no-such-workload")
+    assert hbm["bound"] == "hbm" and hbm["achieved"] == pytest.approx(4000.0)
+
+
+def test_traffic_table_entries_name_their_commit():
+    table = json.loads((ROOT / "profiles" / "traffic.json").read_text())
+    for workload, kernels in table["workloads"].items():
+        for kernel, entry in kernels.items():
+            traffic, commit = bench.measured_traffic(workload, kernel)
+            assert abs(traffic - (entry["fetch_bytes"] + entry["write_bytes"])) <= 1  # rounding
+            assert commit and len(commit) >= 7
+
+
+def test_repeat_for_runs_at_least_once_and_stops():
+    calls = []
+    reps, dt = bench.repeat_for(lambda: calls.append(1), seconds=0.0)
+    assert reps == 1 and len(calls) == 1 and dt >= 0.0
+    reps, _ = bench.repeat_for(lambda: None, seconds=100.0, max_reps=7)
+    assert reps == 7
