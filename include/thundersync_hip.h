@@ -3,10 +3,12 @@
  * kernels behind thundersync_amd's operators.
  *
  * Conventions (all entry points):
- *   - every tensor argument is a raw device pointer; sizes and strides are
+ *   - every tensor argument is a raw device pointer (except in the forest
+ *     metadata section: host code over host arrays); sizes and strides are
  *     int64 element counts; `stream` is a hipStream_t passed as void*;
  *   - the caller (PyTorch on the host side) allocates every input, output
- *     and workspace; the library never allocates, frees or retains memory;
+ *     and workspace; the library never allocates, frees or retains device
+ *     memory (the host-side metadata builders use temporary host memory);
  *   - inputs are never written, so a call may be repeated on the same
  *     inputs (activation-checkpoint recompute does exactly that);
  *   - the return value is a status (TS_OK or a TS_ERR_* code); the message
