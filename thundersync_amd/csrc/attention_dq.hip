@@ -19,7 +19,9 @@ __global__ __launch_bounds__(kThreads) void delta_kernel(ts_attn_rows O, ts_attn
   const int64_t row = pair / hq;
   const int h = (int)(pair % hq);
   if (row >= rows) return;
-  const u32x4 a = ld16((const bf16*)O.ptr + row * O.row_stride + (int64_t)h * O.head_stride + 8 * sub);
+  // O is read only here (non-temporal); dO stays cached for the dQ and dK/dV kernels that follow
+  const u32x4 a = __builtin_nontemporal_load(
+      reinterpret_cast<const u32x4*>((const bf16*)O.ptr + row * O.row_stride + (int64_t)h * O.head_stride + 8 * sub));
   const u32x4 b = ld16((const bf16*)dO.ptr + row * dO.row_stride + (int64_t)h * dO.head_stride + 8 * sub);
   float acc = 0.f;
 #pragma unroll

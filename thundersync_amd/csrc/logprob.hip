@@ -576,7 +576,8 @@ __global__ __launch_bounds__(kThreads) void transpose_kernel(const bf16* __restr
   u32x4 in[8], out[8];
 #pragma unroll
   for (int r = 0; r < 8; ++r)
-    in[r] = v0 + r < vocab ? *reinterpret_cast<const u32x4*>(w + (v0 + r) * ldw + d0) : u32x4{0u, 0u, 0u, 0u};
+    in[r] = v0 + r < vocab ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(w + (v0 + r) * ldw + d0))
+                           : u32x4{0u, 0u, 0u, 0u};  // W is read once here: non-temporal
   transpose8x8(in, out);
 #pragma unroll
   for (int e = 0; e < 8; ++e) *reinterpret_cast<u32x4*>(wt + (int64_t)(d0 + e) * ldt + v0) = out[e];
