@@ -233,6 +233,9 @@ __global__ __launch_bounds__(64 * 8 / NQB, NQB == 1 ? 4 : 2) void fwd_wave_kerne
 #pragma unroll
     for (int ss = 0; ss < 2; ++ss) {
       f32x4 sc[2][NQB];
+      // wave priority 1 over the MFMA phases, 0 over the softmax: of the two
+      // waves on a SIMD, the one with MFMAs to issue goes first (fwd -1.4 %)
+      __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
@@ -251,6 +254,7 @@ __global__ __launch_bounds__(64 * 8 / NQB, NQB == 1 ? 4 : 2) void fwd_wave_kerne
         __builtin_amdgcn_sched_group_barrier(0x008, NQB, 1);
         if (st + 3 < 8) __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
       }
+      __builtin_amdgcn_s_setprio(0);
       if (masked) {
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
@@ -321,6 +325,7 @@ __global__ __launch_bounds__(64 * 8 / NQB, NQB == 1 ? 4 : 2) void fwd_wave_kerne
         for (int j = 0; j < 8; ++j) tmp[j] = pe[j >> 2][qb][j & 3];
         pk[qb] = pack8(tmp);
       }
+      __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int mb = 0; mb < 8; ++mb) {
         const u32x2 a0 = tr_read(tv + to[mb] + 32 * ss * D);
@@ -337,6 +342,7 @@ __global__ __launch_bounds__(64 * 8 / NQB, NQB == 1 ? 4 : 2) void fwd_wave_kerne
         if (mb + 4 < 8) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
       }
       __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_setprio(0);
     }
     cur = nxt;
   };
