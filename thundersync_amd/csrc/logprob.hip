@@ -27,6 +27,8 @@
 // fragments are read during the current stage's last MFMAs.
 // Rows past an operand's valid rows and 8-element K chunks past K arrive as
 // zeros (buffer range checking), so ragged edges need no masking in the loop.
+#include <type_traits>
+
 #include "common.h"
 #include "timing.h"
 #include "../../include/thundersync_hip.h"
@@ -43,6 +45,7 @@ constexpr int TK = 32;   // K per LDS stage
 constexpr int kStageElems = (TM + TN) * TK;  // 32 KB: A [TM][TK], then B [TN][TK]
 constexpr int BM = TM;   // vocab rows per forward partial
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
 
 __device__ __forceinline__ float neg_inf() { return -__builtin_huge_valf(); }
 __device__ __forceinline__ u32x4 ld16(const bf16* p) { return *reinterpret_cast<const u32x4*>(p); }
@@ -456,49 +459,56 @@ __global__ __launch_bounds__(kGemmThreads, 1) void dlogits_kernel(DlArgs p) {
   const int wm = wave & 1, wn = wave >> 1;
   // tokens 64 q .. 64 q + 63 of the tile are staged in ring stage q as [64][OPITCH]
   auto quarter = [&](int q) -> bf16* { return q == 0 ? s0 : q == 1 ? s1 : q == 2 ? s2 : s3; };
+  // dl = -p (g_lp + g_H (log p + H)) + g_lp [v = t], with log2 p = l log2 e - lse log2 e as one
+  // FMA and the bracket as one FMA in log2 p: A = g_H ln 2, B = g_lp + g_H H per token.  Tiles
+  // inside the vocabulary and the row range (all but the last of each) skip the bounds tests.
+  auto epilogue = [&](auto full_c) __attribute__((always_inline)) {
+    constexpr bool FULL = decltype(full_c)::value;
 #pragma unroll
-  for (int ni = 0; ni < NI; ++ni) {
-    const int col = 64 * wn + 32 * ni + (lane & 31);  // token within the tile
-    bf16* out = quarter(col >> 6) + (col & 63) * OPITCH;
-    const int n = n0 + col;
-    float lse_n = 0.f, h_n = 0.f, glp = 0.f, gent = 0.f;
-    int64_t t = -1;
-    if (n < p.rows) {
-      lse_n = p.lse[n];
-      glp = p.g_lp[n];
-      if (p.g_ent) {
-        gent = p.g_ent[n];
-        h_n = p.ent[n];
-      }
-      t = p.target[n];
-    }
-#pragma unroll
-    for (int mi = 0; mi < 4; ++mi)
-#pragma unroll
-      for (int i4 = 0; i4 < 4; ++i4) {
-        uint32_t packed[2];
-#pragma unroll
-        for (int j = 0; j < 4; j += 2) {
-          float d2[2];
-#pragma unroll
-          for (int jj = 0; jj < 2; ++jj) {
-            const int i = 4 * i4 + j + jj;
-            const int v = v0 + a_row(mi, i, lane, wm);
-            float d = 0.f;
-            if (v < p.vocab && n < p.rows) {
-              const float logp = acc[mi][ni][i] - lse_n;
-              const float pr = fast_exp2(logp * kLog2e);
-              d = -pr * (glp + gent * (logp + h_n));
-              if (v == t) d += glp;
-            }
-            d2[jj] = d;
-          }
-          packed[j >> 1] = pack_bf2(d2[0], d2[1]);
+    for (int ni = 0; ni < NI; ++ni) {
+      const int col = 64 * wn + 32 * ni + (lane & 31);  // token within the tile
+      bf16* out = quarter(col >> 6) + (col & 63) * OPITCH;
+      const int n = n0 + col;
+      float lse2 = 0.f, coef_a = 0.f, coef_b = 0.f, glp = 0.f;
+      int t = -1;
+      if (FULL || n < p.rows) {
+        lse2 = p.lse[n] * kLog2e;
+        glp = p.g_lp[n];
+        coef_b = glp;
+        if (p.g_ent) {
+          const float gent = p.g_ent[n];
+          coef_a = gent * kLn2;
+          coef_b = fmaf(gent, p.ent[n], glp);
         }
-        // vocab rows a_row(mi, 4 i4 .. 4 i4 + 3) are consecutive: one 8-byte write
-        *reinterpret_cast<u32x2*>(out + a_row(mi, 4 * i4, lane, wm)) = u32x2{packed[0], packed[1]};
+        t = (int)p.target[n];
       }
-  }
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+        for (int i4 = 0; i4 < 4; ++i4) {
+          uint32_t packed[2];
+#pragma unroll
+          for (int j = 0; j < 4; j += 2) {
+            float d2[2];
+#pragma unroll
+            for (int jj = 0; jj < 2; ++jj) {
+              const int i = 4 * i4 + j + jj;
+              const int v = v0 + a_row(mi, i, lane, wm);
+              const float logp2 = fmaf(acc[mi][ni][i], kLog2e, -lse2);
+              float d = -fast_exp2(logp2) * fmaf(coef_a, logp2, coef_b);
+              if (v == t) d += glp;
+              if (!FULL && !(v < p.vocab && n < p.rows)) d = 0.f;
+              d2[jj] = d;
+            }
+            packed[j >> 1] = pack_bf2(d2[0], d2[1]);
+          }
+          // vocab rows a_row(mi, 4 i4 .. 4 i4 + 3) are consecutive: one 8-byte write
+          *reinterpret_cast<u32x2*>(out + a_row(mi, 4 * i4, lane, wm)) = u32x2{packed[0], packed[1]};
+        }
+    }
+  };
+  if (v0 + TM <= p.vocab && n0 + TN <= p.rows) epilogue(std::true_type{});
+  else epilogue(std::false_type{});
   __syncthreads();
   // coalesced store of the [TN tokens][TM vocab] tile
   const int vmax = min(TM, p.vocab_pad - v0);
