@@ -315,28 +315,32 @@ __global__ __launch_bounds__(kGemmThreads, 1) void fwd_stats_kernel(FwdArgs p) {
     for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
       for (int i = 0; i < 16; i += 2) m = fmaxf(m, fmaxf(acc[mi][ni][i], acc[mi][ni][i + 1]));
+    // sum of q = 2^d2 and of q d2 with d2 = (l - m) log2 e as one FMA per logit; the second
+    // sum is taken back to natural-log units once
     float sum = 0.f, e = 0.f;
+    const float m2 = m * kLog2e;
     if (v0 + TM <= p.vocab) {
 #pragma unroll
       for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          const float d = acc[mi][ni][i] - m;
-          const float q = fast_exp2(d * kLog2e);
+          const float d2 = fmaf(acc[mi][ni][i], kLog2e, -m2);
+          const float q = fast_exp2(d2);
           sum += q;
-          e = fmaf(q, d, e);
+          e = fmaf(q, d2, e);
         }
     } else if (m != neg_inf()) {
 #pragma unroll
       for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          const float d = acc[mi][ni][i] - m;  // -inf for rows past the vocabulary: q = 0
-          const float q = fast_exp2(d * kLog2e);
+          const float d2 = fmaf(acc[mi][ni][i], kLog2e, -m2);  // -inf past the vocabulary: q = 0
+          const float q = fast_exp2(d2);
           sum += q;
-          e = q > 0.f ? fmaf(q, d, e) : e;
+          e = q > 0.f ? fmaf(q, d2, e) : e;
         }
     }
+    e *= kLn2;
     // merge with the other half-wave (lane ^ 32 holds the other vocab rows)
     {
       const float mo = shfl_xor(m, 32), so = shfl_xor(sum, 32), eo = shfl_xor(e, 32);
