@@ -306,10 +306,10 @@ __global__ __launch_bounds__(kGemmThreads, 1) void fwd_stats_kernel(FwdArgs p) {
         for (int i = 0; i < 16; ++i)
           if (v0 + a_row(mi, i, lane, wm) >= p.vocab) acc[mi][ni][i] = neg_inf();
   }
+  float mk[NI], sk[NI], ek[NI];  // this lane's column statistics, kept across the exchange
 #pragma unroll
   for (int ni = 0; ni < NI; ++ni) {
     const int col = 64 * wn + 32 * ni + (lane & 31);
-    const int n = n0 + col;
     float m = neg_inf();
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi)
@@ -351,15 +351,22 @@ __global__ __launch_bounds__(kGemmThreads, 1) void fwd_stats_kernel(FwdArgs p) {
       xs[col] = sum;
       xe[col] = e;
     }
-    __syncthreads();
+    mk[ni] = m;
+    sk[ni] = sum;
+    ek[ni] = e;
+  }
+  __syncthreads();  // one exchange for both column groups (their columns differ)
+#pragma unroll
+  for (int ni = 0; ni < NI; ++ni) {
+    const int col = 64 * wn + 32 * ni + (lane & 31);
+    const int n = n0 + col;
     if (wm == 0 && lane < 32 && n < p.rows) {
-      merge_stats(m, sum, e, xm[col], xs[col], xe[col]);
+      merge_stats(mk[ni], sk[ni], ek[ni], xm[col], xs[col], xe[col]);
       const int64_t o = (int64_t)vt * p.rows + n;
-      p.part_m[o] = m;
-      p.part_s[o] = sum;
-      p.part_e[o] = e;
+      p.part_m[o] = mk[ni];
+      p.part_s[o] = sk[ni];
+      p.part_e[o] = ek[ni];
     }
-    __syncthreads();
   }
 }
 
