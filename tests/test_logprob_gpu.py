@@ -122,6 +122,23 @@ def test_gathered_logprobs_and_edge_cases(cuda):
     assert torch.isnan(lp[3]).item() and not torch.isnan(lp[:3]).any().item()
 
 
+def test_out_of_range_targets_match_no_vocabulary_row(cuda):
+    """A target outside [0, vocab) adds no one-hot term to dlogits, however large (no 32-bit wrap)."""
+    g = torch.Generator().manual_seed(11)
+    h = torch.randn(8, 32, generator=g).to(torch.bfloat16)
+    w = (torch.randn(203, 32, generator=g) * 0.05).to(torch.bfloat16)
+    t = torch.randint(0, 203, (8,), generator=g)
+    grads = []
+    for bad in (203, 2**32 + 5, -1):
+        tt = t.clone()
+        tt[2] = bad
+        hc = h.to(cuda).requires_grad_()
+        lp = hip.fused_logprob(hc, w.to(cuda), tt.to(cuda))
+        lp.backward(torch.ones_like(lp))  # row 2 (NaN logprob) still has an upstream gradient
+        grads.append(hc.grad.cpu())
+    assert torch.equal(grads[0], grads[1]) and torch.equal(grads[0], grads[2])
+
+
 def test_validation_errors(cuda):
     h = torch.randn(4, 8, dtype=torch.bfloat16, device=cuda)
     w = torch.randn(16, 8, dtype=torch.bfloat16, device=cuda)

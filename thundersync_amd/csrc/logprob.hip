@@ -491,7 +491,8 @@ __global__ __launch_bounds__(kGemmThreads, 1) void dlogits_kernel(DlArgs p) {
           coef_a = gent * kLn2;
           coef_b = fmaf(gent, p.ent[n], glp);
         }
-        t = (int)p.target[n];
+        const int64_t tt = p.target[n];
+        t = (tt >= 0 && tt < p.vocab) ? (int)tt : -1;  // out-of-range targets match no row
       }
 #pragma unroll
       for (int mi = 0; mi < 4; ++mi)
