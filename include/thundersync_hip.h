@@ -51,6 +51,11 @@ const char* ts_hip_last_error(void);
  *   xf = float(x); rstd = rsqrt(mean(xf^2) + eps);
  *   y = w * T(xf * rstd)            (product rounded to T, as torch does)
  * x, y: [rows, width] of dtype; w: [width] of dtype; rstd: [rows] fp32.
+ * y and rstd are byte-identical to the stock module's on the GPU: mean(xf^2)
+ * is summed in the order torch's reduction kernel uses for a contiguous
+ * [rows, width] fp32 tensor on the device's CU count, and rsqrt is correctly
+ * rounded, as torch.rsqrt is.  TS_ERR_INVALID for a single row wider than
+ * 130560 (torch sums such a row across work-groups). */
  * Replaces FP32RMSNormVJP.forward (accel/rms_norm.py:9-17) and the compiled
  * primal `_primal` / `_CompiledForwardVJP` (grpo/rms_norm.py:12-31). */
 int ts_rmsnorm_fwd(const void* x, const void* w, void* y, float* rstd,

@@ -1,12 +1,11 @@
 """RMSNorm HIP kernels against the CPU oracle (accel/rms_norm.py restated).
 
-Bars: the primal within two units in the last place of the output dtype
-(the fp32 sum of squares is reduced in a different order than torch's, which
-can move rstd by an ulp; the primal rounds twice -- xhat to the dtype, then
-w * xhat -- and each rounding can then land one unit apart); rstd within 2e-6
-relative; dx and dw (fp32 VJP, cast once) within the output dtype's rounding
-of the fp64 closed form.  dW is a fixed-order reduction: two runs are
-bit-identical.
+Bars: the primal and rstd bit-identical (rtol = atol = 0) to the oracle's
+restatement of the GPU forward and to torch's own stock operations on the
+same device -- the reference's "original primal bytes" contract
+(tests/test_rms_norm_precision.py:27-39); dx and dw (fp32 VJP, cast once)
+within the output dtype's rounding of the fp64 closed form.  dW is a
+fixed-order reduction: two runs are bit-identical.
 """
 
 from __future__ import annotations
@@ -20,6 +19,9 @@ from thundersync_amd.rms_norm import FP32RMSNormVJP, rms_norm_backward, rms_norm
 pytestmark = pytest.mark.gpu
 
 SHAPES = [(3, 128), (129, 128), (64, 4096), (257, 4096), (16, 32), (7, 40), (5, 200), (2, 5), (33, 8192), (4, 12288),
+          # forward schedules: one row over 512 threads; 256; 128 threads and a split row; misaligned
+          # rows (width % 4 != 0, >= 128); scalar loads over 64 lanes with a second element
+          (1, 4096), (2, 2048), (4, 12288), (9, 130), (64, 100),
           # backward variants: 8 vectors per lane, part empty (3584); 16 vectors, part empty, four
           # waves (5120); 282 partial rows of 32 (9000 x 1024); 1024 partial rows of 69 rows (70000 x 128)
           (37, 3584), (19, 5120), (9000, 1024), (70000, 128)]
@@ -42,16 +44,21 @@ def make(rows, width, dtype, device, seed):
 def test_forward_matches_oracle(cuda, rows, width, dtype):
     print(f"rmsnorm fwd rows={rows} width={width} {dtype}", flush=True)
     x, w, _ = make(rows, width, dtype, cuda, rows * 31 + width)
-    want, want_rstd = ref.rms_norm_forward(x, w, 1e-6)
+    x[: min(rows, 3)] *= 23.0  # rows far from unit scale
+    want, want_rstd = ref.device_forward(x, w, 1e-6)
     got, rstd = rms_norm_forward(x.to(cuda), w.to(cuda), 1e-6)
+    # torch's own operations on the device (the stock module's forward)
+    xs = x.to(cuda).to(torch.float32)
+    stock_rstd = torch.rsqrt(xs.pow(2).mean(-1, keepdim=True) + 1e-6)
+    stock = w.to(cuda) * (xs * stock_rstd).to(dtype)
     torch.cuda.synchronize()
-    torch.testing.assert_close(rstd.cpu(), want_rstd, rtol=2e-6, atol=0)
-    # two output units for 16-bit outputs; fp32 outputs carry rstd's own
-    # reduction-order difference (a few fp32 ulps)
-    units = 2.02 if dtype != torch.float32 else 8.0
-    tol = want.float().abs() * ulp(dtype) * units + 1e-30
-    err = (got.cpu().float() - want.float()).abs()
-    assert bool((err <= tol).all()), float((err / tol).max())
+    assert torch.equal(rstd, stock_rstd) and torch.equal(got, stock)
+    assert torch.equal(rstd.cpu(), want_rstd) and torch.equal(got.cpu(), want)
+    # and within two output roundings of the fp64 formula
+    closed = w.double() * (x.double() * torch.rsqrt(x.double().pow(2).mean(-1, keepdim=True) + 1e-6))
+    # (plus the absolute spacing of fp16 subnormals, which tiny outputs round to)
+    tol = closed.abs() * ulp(dtype) * 2.02 + torch.finfo(dtype).tiny * ulp(dtype) * 8
+    assert bool(((got.cpu().double() - closed).abs() <= tol).all())
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])

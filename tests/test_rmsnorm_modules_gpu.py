@@ -2,8 +2,8 @@
 
 * ``use_stable_qwen3_rms_norm`` (accel/rms_norm.py:55-70 of the reference):
   every Qwen3RMSNorm of a model is replaced, Parameters keep their identity,
-  and the forward matches the stock module within the bf16 bar of the
-  kernel tests (two roundings).
+  and the forward's bytes equal the stock module's, with and without grad
+  (rtol = atol = 0, the reference's tests/test_rms_norm_precision.py:27-39).
 * ``use_compiled_source_rms_norm`` (grpo/rms_norm.py:44-84,
   grpo/rms_norm_native.py:98-115): bf16 StableQwen3RMSNorm modules become
   NativeSourceRMSNorm once both trials pass; fp32 modules are left alone; the
@@ -62,7 +62,37 @@ def test_stable_swap_keeps_parameters_and_primal(cuda):
         xi = (x if m.weight.numel() == 128 else x[..., :32]).clone().requires_grad_()
         y = m(xi)
         assert y.grad_fn is not None
-        assert (y.float() - stock[n].float()).abs().max().item() <= 2 * 2 ** -7 * 3
+        assert torch.equal(y.detach(), stock[n])
+        with torch.no_grad():
+            assert torch.equal(m(xi), stock[n])
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("record_graph", [False, True])
+@pytest.mark.parametrize("shape", [(64, 128), (3, 7, 4096), (5, 32, 128), (2, 8, 128), (1, 4096), (9, 130)])
+def test_stable_vjp_preserves_primal_bytes(cuda, dtype, record_graph, shape):
+    """The reference's test_stable_vjp_preserves_primal_bytes (seed 71, linspace
+    weights), over its dtypes and grad modes and the C5 norm shapes."""
+    from transformers.models.qwen3.modeling_qwen3 import Qwen3RMSNorm
+
+    from thundersync_amd.rms_norm import use_stable_qwen3_rms_norm
+
+    print(f"stable norm primal bytes {shape} {dtype} grad={record_graph}", flush=True)
+    torch.manual_seed(71)
+    width = shape[-1]
+    model = torch.nn.Sequential(Qwen3RMSNorm(width, eps=1e-6)).to(cuda, dtype)
+    with torch.no_grad():
+        model[0].weight.copy_(torch.linspace(0.4, 3.0, width, device=cuda))
+    x = torch.randn(*shape, device=cuda, dtype=dtype)
+    with torch.set_grad_enabled(record_graph):
+        expected = model(x)
+        assert use_stable_qwen3_rms_norm(model) == 1
+        torch.testing.assert_close(model(x), expected, rtol=0, atol=0)
+    with torch.no_grad():
+        no_grad = model(x)
+    with torch.enable_grad():
+        with_grad = model(x.clone().requires_grad_())
+    assert torch.equal(no_grad, with_grad.detach()) and torch.equal(no_grad, expected.detach())
 
 
 def test_source_swap_and_native_vjp(cuda):

@@ -89,76 +89,292 @@ template <int LPR> __device__ __forceinline__ float row_sum(float v) {
 }
 
 // ---------------------------------------------------------------------------
-// forward, vector path (width % 8 == 0)
+// forward
+//
+// The primal is byte-identical to transformers' Qwen3RMSNorm on this device:
+//   x = float(h); var = x.pow(2).mean(-1); rstd = rsqrt(var + eps);
+//   y = w * T(x * rstd)
+// (accel/rms_norm.py:11-14 restates the same operations).  Two facts make
+// that possible:
+//  * torch sums x.pow(2) along a contiguous row in a fixed order that depends
+//    only on (rows, width) and the CU count: the schedule of its reduction
+//    kernel (ATen/native/hip/Reduce.cuh of the torch 2.10 ROCm build:
+//    setReduceConfig, input_vectorized_thread_reduce_impl / thread_reduce_impl,
+//    block_x_reduce, block_y_reduce; MeanOps::project = sum * factor).
+//    RowReduce below is that schedule; the kernels perform the same fp32
+//    additions on the same operands in the same order (no contraction into
+//    FMAs anywhere on the variance path);
+//  * torch.rsqrt of an fp32 tensor returns the correctly rounded 1/sqrt(x) for
+//    every positive finite float -- equal to float(1.0 / sqrt(double(x))),
+//    checked bit for bit over all 2^31 - 2^23 of them on an MI355X -- so rstd
+//    is computed that way.
 // ---------------------------------------------------------------------------
-template <typename T, int LPR, int NV, bool FULL>
-__global__ __launch_bounds__(kThreads) void rmsnorm_fwd_vec(
+
+// How torch reduces one row of a contiguous [rows, width] fp32 tensor.
+// Thread (x, y) of the row's bw x bh threads sums the loads
+//   idx = x + y * ym, idx + step, idx + 2 step, ...
+// into four accumulators (load element i -> accumulator i for 4-element
+// vector loads; load j -> accumulator j mod 4 for scalar loads), adds them as
+// ((a0 + a1) + a2) + a3, then the threads combine: across x first (pairwise
+// halving from bw/2 down to 64 in LDS, then v += shfl_down(v, 1, 2, 4, ...)),
+// then across y (halving from bh/2 down to 1).
+struct RowReduce {
+  int vec;   // 1: 4-element vector loads (width >= 128); 0: scalar loads
+  int bw;    // threads along the row (power of two, <= 512)
+  int bh;    // thread rows splitting the row's inputs (1: not split)
+  int ym;    // first load of thread row y is x + y * ym
+  int step;  // stride between one thread's loads, in loads
+};
+
+// setReduceConfig (Reduce.cuh) for a reduction over the contiguous last dim
+// of a [rows, width] fp32 tensor; false where torch would split the row over
+// several work-groups (one row wider than 130560), which is not reproduced.
+inline bool torch_row_reduce(int64_t rows, int64_t width, int num_cu, RowReduce& c) {
+  constexpr int64_t kMaxThreads = 512, kWarp = 64;
+  auto last_pow2 = [](int64_t n) {
+    int64_t p = 1;
+    while (p * 2 <= n) p *= 2;
+    return p;
+  };
+  c.vec = width >= 128;
+  const int64_t dim0 = c.vec ? width / 4 : width;
+  const int64_t d0 = dim0 < kMaxThreads ? last_pow2(dim0) : kMaxThreads;
+  const int64_t d1 = rows < kMaxThreads ? last_pow2(rows) : kMaxThreads;
+  int64_t bw = std::min(d0, kWarp);
+  const int64_t block_h = std::min(d1, kMaxThreads / bw);
+  bw = std::min(d0, kMaxThreads / block_h);
+  int64_t step = bw;
+  int64_t per_thread = (width + step - 1) / step;
+  bool split = per_thread >= std::min<int64_t>(block_h * 16, 256);
+  if (rows > 1 && per_thread < 1024 && num_cu < 100) split = false;  // ROCm: force_splitting_output
+  c.bh = 1;
+  c.ym = 0;
+  if (split) {
+    c.ym = (int)step;
+    step *= block_h;
+    c.bh = (int)block_h;
+    per_thread = (width + step - 1) / step;
+    // a single output row whose threads would still sum >= 256 values each is
+    // split across work-groups (global_reduce)
+    if (rows == 1 && per_thread >= 256) return false;
+  }
+  c.bw = (int)bw;
+  c.step = (int)step;
+  return true;
+}
+
+// squares of elements as torch's x.pow(2) of the fp32 copy
+__device__ __forceinline__ float sq_rn(float a) {
+#pragma clang fp contract(off)
+  return a * a;
+}
+__device__ __forceinline__ float add_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a + b;
+}
+// rstd = rsqrt(var + eps) as torch computes it: var = sum * factor, one fp32
+// add of eps, then the correctly rounded reciprocal square root
+__device__ __forceinline__ float torch_rstd(float sum, float factor, float eps) {
+#pragma clang fp contract(off)
+  const float var = sum * factor;
+  const float v = var + eps;
+  return (float)(1.0 / sqrt((double)v));
+}
+
+// four consecutive elements, kept as loaded
+template <typename T> struct Raw4 { u32x2 v; };
+template <> struct Raw4<float> { f32x4 v; };
+template <typename T> __device__ __forceinline__ Raw4<T> load4(const T* p) {
+  return Raw4<T>{*reinterpret_cast<const u32x2*>(p)};
+}
+template <> __device__ __forceinline__ Raw4<float> load4<float>(const float* p) {
+  return Raw4<float>{*reinterpret_cast<const f32x4*>(p)};
+}
+template <typename T> __device__ __forceinline__ void unpack4(const Raw4<T>& r, float (&o)[4]);
+template <> __device__ __forceinline__ void unpack4<bf16>(const Raw4<bf16>& r, float (&o)[4]) {
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    o[2 * i] = __uint_as_float(r.v[i] << 16);
+    o[2 * i + 1] = __uint_as_float(r.v[i] & 0xffff0000u);
+  }
+}
+template <> __device__ __forceinline__ void unpack4<f16>(const Raw4<f16>& r, float (&o)[4]) {
+  typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+  const h4 h = __builtin_bit_cast(h4, r.v);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) o[i] = (float)h[i];
+}
+template <> __device__ __forceinline__ void unpack4<float>(const Raw4<float>& r, float (&o)[4]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) o[i] = r.v[i];
+}
+template <typename T> __device__ __forceinline__ void store4(T* p, const float (&o)[4]);
+template <> __device__ __forceinline__ void store4<bf16>(bf16* p, const float (&o)[4]) {
+  *reinterpret_cast<u32x2*>(p) = u32x2{pack_bf2(o[0], o[1]), pack_bf2(o[2], o[3])};
+}
+template <> __device__ __forceinline__ void store4<f16>(f16* p, const float (&o)[4]) {
+  typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+  const h4 h{(f16)o[0], (f16)o[1], (f16)o[2], (f16)o[3]};
+  *reinterpret_cast<h4*>(p) = h;
+}
+template <> __device__ __forceinline__ void store4<float>(float* p, const float (&o)[4]) {
+  *reinterpret_cast<f32x4*>(p) = f32x4{o[0], o[1], o[2], o[3]};
+}
+
+// y = w * T(x * r): the product rounded to fp32, then to T, then w * that
+// rounded to T, as the module's operations.  The fp32 product is hidden from
+// the optimiser: for fp16 it otherwise folds T(x * r) into one
+// v_fma_mixlo_f16, which rounds the exact product to fp16 once and differs
+// from the two roundings wherever they double-round.
+template <typename T> __device__ __forceinline__ float primal(float w, float x, float r) {
+#pragma clang fp contract(off)
+  float p = x * r;
+  asm("" : "+v"(p));
+  return w * round_t<T>(p);
+}
+
+// Fast form, for rows torch reduces with bw <= 64 threads and no split: lane
+// `sub` of a row is torch's thread x = sub, so the thread sums are formed in
+// place and the shuffle tree is torch's.  64 / bw rows per wave.
+//  VEC: the lane's loads are 4-element vectors x + k bw (width % 4 == 0); NV
+//       bounds their number.  Otherwise (width < 128) the lane sums elements
+//       sub and sub + bw, the only ones its loop reaches.
+template <typename T, bool VEC, int NV>
+__global__ __launch_bounds__(kThreads) void rmsnorm_fwd_lanes(
     const T* __restrict__ x, const T* __restrict__ w, T* __restrict__ y,
-    float* __restrict__ rstd, int64_t rows, int width, float eps) {
-  // FULL: every lane's NV vectors lie inside the row (width == 8 * LPR * NV).
-  // Otherwise a vector past the row end is loaded from the row's last vector
-  // (in bounds) and ignored, so no load sits behind a branch: loads behind
-  // per-vector branches are each waited for before the next is issued.
-  constexpr int kRowsPerWave = kWave / LPR;
+    float* __restrict__ rstd, int64_t rows, int width, int bw, float factor, float eps) {
   const int lane = threadIdx.x & (kWave - 1);
-  const int wave = threadIdx.x / kWave;
-  const int64_t row = ((int64_t)blockIdx.x * (kThreads / kWave) + wave) * kRowsPerWave + lane / LPR;
-  const int sub = lane % LPR;
-  if (row >= rows) return;
-  const int nvec = width / 8;
-  const T* xr = x + row * width;
-  Packed8<T> v[NV];
+  const int rows_per_wave = kWave / bw;
+  const int64_t row = ((int64_t)blockIdx.x * (kThreads / kWave) + threadIdx.x / kWave) * rows_per_wave +
+                      lane / bw;
+  const int sub = lane & (bw - 1);
+  const bool live = row < rows;
+  const T* xr = x + (live ? row : 0) * width;
+  float s;
+  if constexpr (VEC) {
+    const int nvec = width / 4;
+    Raw4<T> v[NV];
 #pragma unroll
-  for (int k = 0; k < NV; ++k) {
-    const int vi = sub + k * LPR;
-    v[k] = load_packed<T>(xr + (FULL ? vi : min(vi, nvec - 1)) * 8);
-  }
-  float ss = 0.f;
+    for (int k = 0; k < NV; ++k) v[k] = load4<T>(xr + min(sub + k * bw, nvec - 1) * 4);
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int k = 0; k < NV; ++k) {
-    if (FULL || sub + k * LPR < nvec) {
-      float f[8];
-      unpack<T>(v[k], f);
+    for (int k = 0; k < NV; ++k) {
+      if (sub + k * bw < nvec) {
+        float f[4];
+        unpack4<T>(v[k], f);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) ss = fmaf(f[i], f[i], ss);
+        for (int i = 0; i < 4; ++i) acc[i] = add_rn(acc[i], sq_rn(f[i]));
+      }
     }
-  }
-  ss = row_sum<LPR>(ss);
-  const float r = __frsqrt_rn(ss / (float)width + eps);
-  if (sub == 0) rstd[row] = r;
-  T* yr = y + row * width;
+    s = add_rn(add_rn(add_rn(acc[0], acc[1]), acc[2]), acc[3]);
+    for (int off = 1; off < bw; off <<= 1) s = add_rn(s, __shfl_down(s, off, kWave));
+    const float r = __shfl(torch_rstd(s, factor, eps), lane - sub, kWave);
+    if (!live) return;
+    if (sub == 0) rstd[row] = r;
+    T* yr = y + row * width;
 #pragma unroll
-  for (int k = 0; k < NV; ++k) {
-    const int vi = sub + k * LPR;
-    float wv[8], f[8], o[8];
-    unpack<T>(load_packed<T>(w + (FULL ? vi : min(vi, nvec - 1)) * 8), wv);
-    unpack<T>(v[k], f);
+    for (int k = 0; k < NV; ++k) {
+      const int vi = sub + k * bw;
+      if (vi < nvec) {
+        float f[4], wv[4], o[4];
+        unpack4<T>(v[k], f);
+        unpack4<T>(load4<T>(w + vi * 4), wv);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) o[i] = wv[i] * round_t<T>(f[i] * r);
-    if (FULL || vi < nvec) store8<T>(yr + vi * 8, o);
+        for (int i = 0; i < 4; ++i) o[i] = primal<T>(wv[i], f[i], r);
+        store4<T>(yr + vi * 4, o);
+      }
+    }
+  } else {
+    const bool second = sub + bw < width;
+    const float a = to_f(xr[sub]);
+    const float b = to_f(xr[second ? sub + bw : sub]);
+    s = add_rn(sq_rn(a), second ? sq_rn(b) : 0.f);
+    for (int off = 1; off < bw; off <<= 1) s = add_rn(s, __shfl_down(s, off, kWave));
+    const float r = __shfl(torch_rstd(s, factor, eps), lane - sub, kWave);
+    if (!live) return;
+    if (sub == 0) rstd[row] = r;
+    T* yr = y + row * width;
+    yr[sub] = from_f<T>(primal<T>(to_f(w[sub]), a, r));
+    if (second) yr[sub + bw] = from_f<T>(primal<T>(to_f(w[sub + bw]), b, r));
   }
 }
 
-// forward, scalar path (any width): one wave per row
+// General form: one wave per row for any RowReduce (more than 64 threads
+// along the row for short row counts, split rows for wide ones, rows that
+// start off a 16-byte boundary when width % 4 != 0).  Lane l forms the sums of
+// torch threads l, l + 64, ... into LDS, then the trees run as torch's do.
+constexpr int kMaxReduceThreads = 512;
+
 template <typename T>
-__global__ __launch_bounds__(kThreads) void rmsnorm_fwd_scalar(
+__global__ __launch_bounds__(kWave) void rmsnorm_fwd_rowwave(
     const T* __restrict__ x, const T* __restrict__ w, T* __restrict__ y,
-    float* __restrict__ rstd, int64_t rows, int width, float eps) {
-  const int lane = threadIdx.x & (kWave - 1);
-  const int64_t row = (int64_t)blockIdx.x * (kThreads / kWave) + threadIdx.x / kWave;
-  if (row >= rows) return;
+    float* __restrict__ rstd, int64_t rows, int width, RowReduce c, float factor, float eps) {
+  __shared__ float part[kMaxReduceThreads];
+  __shared__ float ys[8];
+  __shared__ float rs;
+  const int lane = threadIdx.x;
+  const int64_t row = blockIdx.x;
   const T* xr = x + row * width;
-  float ss = 0.f;
-  for (int i = lane; i < width; i += kWave) {
-    const float a = to_f(xr[i]);
-    ss = fmaf(a, a, ss);
+  const int nthreads = c.bw * c.bh;
+  // torch's fp32 copy of the tensor starts 16-byte aligned, so row `row`
+  // starts (row * width) % 4 elements past a boundary
+  const int shift0 = c.vec ? (int)((row * (int64_t)width) & 3) : 0;
+  auto sq_at = [&](int i) { return sq_rn(to_f(xr[i])); };
+  for (int t = lane; t < nthreads; t += kWave) {
+    const int tx = t % c.bw, ty = t / c.bw;
+    const bool tail_ok = c.bh == 1 || ty == 0;  // should_reduce_tail
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    if (c.vec) {
+      int end = width, d0 = 0, shift = shift0;
+      if (shift > 0) {  // head of a row off the vector boundary
+        d0 = -shift;
+        end = width + shift;
+        if (tx >= shift && tx < 4 && tail_ok) acc[0] = add_rn(0.f, sq_at(d0 + tx));
+        end -= 4;
+        d0 += 4;
+      }
+      for (int idx = tx + ty * c.ym; idx * 4 + 3 < end; idx += c.step)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i] = add_rn(acc[i], sq_at(d0 + idx * 4 + i));
+      const int tail = end - end % 4 + tx;
+      if (tail_ok && tail < end) acc[0] = add_rn(acc[0], sq_at(d0 + tail));
+    } else {
+      int idx = tx + ty * c.ym;
+      for (; idx + 3 * c.step < width; idx += 4 * c.step)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i] = add_rn(acc[i], sq_at(idx + i * c.step));
+      for (int i = 0; i < 4 && idx < width; ++i, idx += c.step) acc[i] = add_rn(acc[i], sq_at(idx));
+    }
+    part[t] = add_rn(add_rn(add_rn(acc[0], acc[1]), acc[2]), acc[3]);
   }
-  ss = wave_sum(ss);
-  const float r = __frsqrt_rn(ss / (float)width + eps);
-  if (lane == 0) rstd[row] = r;
+  __syncthreads();
+  // block_x_reduce: LDS halving down to 64 threads per thread row
+  for (int off = c.bw / 2; off >= kWave; off >>= 1) {
+    for (int i = lane; i < c.bh * off; i += kWave) {
+      const int tx = i % off, ty = i / off;
+      part[ty * c.bw + tx] = add_rn(part[ty * c.bw + tx], part[ty * c.bw + tx + off]);
+    }
+    __syncthreads();
+  }
+  const int dim = min(c.bw, kWave);
+  for (int ty = 0; ty < c.bh; ++ty) {
+    float v = lane < dim ? part[ty * c.bw + lane] : 0.f;
+    for (int off = 1; off < dim; off <<= 1) v = add_rn(v, __shfl_down(v, off, kWave));
+    if (lane == 0) ys[ty] = v;
+  }
+  __syncthreads();
+  if (lane == 0) {
+    // block_y_reduce
+    for (int off = c.bh / 2; off > 0; off >>= 1)
+      for (int ty = 0; ty < off; ++ty) ys[ty] = add_rn(ys[ty], ys[ty + off]);
+    const float r = torch_rstd(ys[0], factor, eps);
+    rs = r;
+    rstd[row] = r;
+  }
+  __syncthreads();
+  const float r = rs;
   T* yr = y + row * width;
-  for (int i = lane; i < width; i += kWave)
-    yr[i] = from_f<T>(to_f(w[i]) * round_t<T>(to_f(xr[i]) * r));
+  for (int i = lane; i < width; i += kWave) yr[i] = from_f<T>(primal<T>(to_f(w[i]), to_f(xr[i]), r));
 }
 
 // ---------------------------------------------------------------------------
@@ -427,35 +643,56 @@ int64_t bwd_parts(int64_t rows, int64_t width) {
   return parts;
 }
 
+// CU count of the device a stream belongs to (torch's schedule consults it)
+int stream_cus(hipStream_t s) {
+  int dev = 0;
+  if (s == nullptr || hipStreamGetDevice(s, &dev) != hipSuccess) (void)hipGetDevice(&dev);
+  static int cached[64] = {0};
+  if (dev >= 0 && dev < 64 && cached[dev] > 0) return cached[dev];
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) n = 256;
+  if (dev >= 0 && dev < 64) cached[dev] = n;
+  return n;
+}
+
 template <typename T>
 int launch_fwd(const void* x, const void* w, void* y, float* rstd, int64_t rows, int width,
                float eps, hipStream_t s) {
-  const Geometry g = pick(width, 0);
-  if (g.lpr == 0) {
-    const int64_t blocks = (rows + 3) / 4;
-    { ts::TimedLaunch timed_("rmsnorm.rmsnorm_fwd_scalar", s); hipLaunchKernelGGL(rmsnorm_fwd_scalar<T>, dim3((unsigned)blocks), dim3(kThreads), 0, s,
-                       (const T*)x, (const T*)w, (T*)y, rstd, rows, width, eps); }
-    return check_launch("ts_rmsnorm_fwd");
+  RowReduce c;
+  if (!torch_row_reduce(rows, width, stream_cus(s), c)) {
+    set_error("ts_rmsnorm_fwd: a single row of width %d is summed across work-groups by torch; "
+              "that order is not reproduced", width);
+    return TS_ERR_INVALID;
   }
-  const int64_t rows_per_block = 4 * (64 / g.lpr);
-  const dim3 grid((unsigned)((rows + rows_per_block - 1) / rows_per_block));
-  const bool full = width == 8 * g.lpr * g.nv;
-#define TS_FWD(LPR, NV)                                                                     \
-  if (g.lpr == LPR && g.nv == NV) {                                                         \
-    ts::TimedLaunch timed_("rmsnorm.rmsnorm_fwd_vec", s);                                   \
-    if (full)                                                                               \
-      hipLaunchKernelGGL((rmsnorm_fwd_vec<T, LPR, NV, true>), grid, dim3(kThreads), 0, s,   \
-                         (const T*)x, (const T*)w, (T*)y, rstd, rows, width, eps);          \
-    else                                                                                    \
-      hipLaunchKernelGGL((rmsnorm_fwd_vec<T, LPR, NV, false>), grid, dim3(kThreads), 0, s,  \
-                         (const T*)x, (const T*)w, (T*)y, rstd, rows, width, eps);          \
-    return check_launch("ts_rmsnorm_fwd");                                                  \
+  // MeanOps' factor: float(outputs) / numel, the division in float
+  const float factor = (float)rows / (float)(rows * (int64_t)width);
+  if (c.bh == 1 && c.bw <= kWave && (!c.vec || width % 4 == 0)) {
+    const int64_t rows_per_block = (kThreads / kWave) * (kWave / c.bw);
+    const dim3 grid((unsigned)((rows + rows_per_block - 1) / rows_per_block));
+    ts::TimedLaunch timed_("rmsnorm.rmsnorm_fwd_lanes", s);
+    if (!c.vec) {
+      hipLaunchKernelGGL((rmsnorm_fwd_lanes<T, false, 1>), grid, dim3(kThreads), 0, s, (const T*)x,
+                         (const T*)w, (T*)y, rstd, rows, width, c.bw, factor, eps);
+      return check_launch("ts_rmsnorm_fwd");
+    }
+    const int loads = (width / 4 + c.bw - 1) / c.bw;
+#define TS_FWD(NV)                                                                             \
+  if (loads <= NV) {                                                                           \
+    hipLaunchKernelGGL((rmsnorm_fwd_lanes<T, true, NV>), grid, dim3(kThreads), 0, s,           \
+                       (const T*)x, (const T*)w, (T*)y, rstd, rows, width, c.bw, factor, eps); \
+    return check_launch("ts_rmsnorm_fwd");                                                     \
   }
-  TS_FWD(4, 1) TS_FWD(8, 1) TS_FWD(16, 1) TS_FWD(32, 1) TS_FWD(64, 1)
-  TS_FWD(4, 2) TS_FWD(8, 2) TS_FWD(16, 2) TS_FWD(32, 2) TS_FWD(64, 2) TS_FWD(64, 4) TS_FWD(64, 8) TS_FWD(64, 16)
+    TS_FWD(1) TS_FWD(2) TS_FWD(4) TS_FWD(8) TS_FWD(16) TS_FWD(32)
 #undef TS_FWD
-  set_error("ts_rmsnorm_fwd: no kernel for width %d", width);
-  return TS_ERR_INVALID;
+  }
+  if (rows > 0x7fffffff) {
+    set_error("ts_rmsnorm_fwd: %lld rows exceed one launch", (long long)rows);
+    return TS_ERR_INVALID;
+  }
+  ts::TimedLaunch timed_("rmsnorm.rmsnorm_fwd_rowwave", s);
+  hipLaunchKernelGGL(rmsnorm_fwd_rowwave<T>, dim3((unsigned)rows), dim3(kWave), 0, s, (const T*)x,
+                     (const T*)w, (T*)y, rstd, rows, width, c, factor, eps);
+  return check_launch("ts_rmsnorm_fwd");
 }
 
 template <typename T>

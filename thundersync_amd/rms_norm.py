@@ -7,6 +7,16 @@ backward is the FP32 VJP from that saved statistic, with ``dx`` cast to the
 hidden dtype and ``dw`` to the weight dtype.  Both directions run in
 ``ts_rmsnorm_fwd`` / ``ts_rmsnorm_bwd`` (include/thundersync_hip.h); there is
 no host path -- a CPU tensor raises.
+
+The forward's bytes equal the stock module's on the GPU (the reference's
+contract, "keep the original primal bytes", accel/rms_norm.py:46-52): the
+kernel sums the squares in the order torch's reduction kernel uses for a
+contiguous row and takes the correctly rounded rsqrt, as torch.rsqrt does.
+That holds for hidden states whose rows are contiguous (a strided input is
+made contiguous first; torch would reduce a dense but permuted one in another
+order).  ``StableQwen3RMSNorm`` therefore runs the HIP forward with and
+without grad alike, so a no-grad pass and the recompute under grad give the
+same bytes.
 """
 
 from __future__ import annotations
@@ -103,16 +113,19 @@ class FP32RMSNormVJP(torch.autograd.Function):
 if Qwen3RMSNorm is not None:
 
     class StableQwen3RMSNorm(Qwen3RMSNorm):
-        """Qwen3RMSNorm whose low-precision training forward runs FP32RMSNormVJP.
+        """Qwen3RMSNorm on the HIP kernels, primal bytes unchanged (accel/rms_norm.py:46-52).
 
-        Dispatch rule of accel/rms_norm.py:46-52: bf16/fp16 inputs under grad
-        take the HIP op; everything else is the stock module's forward.
+        Under grad the forward is FP32RMSNormVJP (the FP32 VJP from the saved
+        rstd); without grad it is the same HIP forward with nothing saved.
+        The reference keeps the stock forward outside bf16/fp16 training;
+        here every forward is the HIP one, whose bytes are the stock
+        module's, so the two modes cannot drift apart.
         """
 
         def forward(self, hidden):
-            if hidden.dtype not in (torch.bfloat16, torch.float16) or not torch.is_grad_enabled():
-                return super().forward(hidden)
-            return FP32RMSNormVJP.apply(hidden, self.weight, self.variance_epsilon)
+            if torch.is_grad_enabled() and (hidden.requires_grad or self.weight.requires_grad):
+                return FP32RMSNormVJP.apply(hidden, self.weight, self.variance_epsilon)
+            return rms_norm_forward(hidden, self.weight, self.variance_epsilon)[0]
 
     def use_stable_qwen3_rms_norm(model: torch.nn.Module) -> int:
         """Swap every Qwen3RMSNorm, keeping Parameter identity (accel/rms_norm.py:55-70)."""
