@@ -55,7 +55,7 @@ const char* ts_hip_last_error(void);
  * is summed in the order torch's reduction kernel uses for a contiguous
  * [rows, width] fp32 tensor on the device's CU count, and rsqrt is correctly
  * rounded, as torch.rsqrt is.  TS_ERR_INVALID for a single row wider than
- * 130560 (torch sums such a row across work-groups). */
+ * 130560 (torch sums such a row across work-groups).
  * Replaces FP32RMSNormVJP.forward (accel/rms_norm.py:9-17) and the compiled
  * primal `_primal` / `_CompiledForwardVJP` (grpo/rms_norm.py:12-31). */
 int ts_rmsnorm_fwd(const void* x, const void* w, void* y, float* rstd,
