@@ -80,6 +80,22 @@ int ts_rmsnorm_bwd(const void* dy, const void* x, const void* w,
                    int64_t workspace_bytes, int64_t rows, int64_t width,
                    int dtype, void* stream);
 
+/* Size of the device array ts_rmsnorm_bwd_noalloc keeps its dW partials in
+ * (one per GPU the library runs on, held until the process ends). */
+#define TS_RMSNORM_BWD_SCRATCH_BYTES (8 << 20)
+
+/* ts_rmsnorm_bwd without a workspace argument and without any allocation:
+ * the dW partials go to a file-scope device array of
+ * TS_RMSNORM_BWD_SCRATCH_BYTES.  No counterpart in the reference; it is for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  TS_ERR_INVALID when
+ * ts_rmsnorm_bwd_workspace(rows, width) exceeds the array (every row count
+ * fits for width <= 8192).  All calls on one GPU share its array: calls that
+ * overlap on one GPU race.  Results are bit-identical to ts_rmsnorm_bwd's. */
+int ts_rmsnorm_bwd_noalloc(const void* dy, const void* x, const void* w,
+                           const float* rstd, void* dx, void* dw, int64_t rows,
+                           int64_t width, int dtype, void* stream);
+
 /* ------------------------------------------------------------------------
  * Forest / packed bottom-right-causal GQA attention (bf16, head_dim 128)
  *
