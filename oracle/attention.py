@@ -87,3 +87,43 @@ def attention_with_grads(q, ks, vs, dout, scale, *, dtype=torch.float32):
     grads = torch.autograd.grad(out, [qq, *kk, *vv], dout.to(dtype))
     n = len(ks)
     return out.detach(), grads[0], list(grads[1 : 1 + n]), list(grads[1 + n :])
+
+
+def prefix_key_grads(q, ks, vs, dout, scale, n_keys, *, rows_per_block=512, dtype=torch.float32):
+    """(dk, dv) of the first ``n_keys`` keys of ``chained_attention(q, ks, vs)``.
+
+    The same bottom-right-causal softmax attention as :func:`chained_attention`,
+    differentiated by hand for the keys of a shared prefix only (the keys a
+    prompt run contributes to every segment that reads it), query rows a block
+    at a time so that long segments fit in memory:
+    ``P = softmax(scale Q K^T)``, ``O = P V``, ``delta = rowsum(dO * O)``,
+    ``dV[:n] = P[:, :n]^T dO``, ``dK[:n] = scale (P[:, :n] * (dO V[:n]^T - delta))^T Q``.
+    Returns fp32/``dtype`` tensors ``[n_keys, Hkv, D]``.
+    """
+    k = torch.cat(list(ks), 0).to(dtype)
+    v = torch.cat(list(vs), 0).to(dtype)
+    t, hq, d = q.shape
+    s, hkv = k.shape[0], k.shape[1]
+    group = hq // hkv
+    # [Hkv, group, rows, D] views of the queries; keys [Hkv, S, D]
+    kh = k.permute(1, 0, 2).contiguous()
+    vh = v.permute(1, 0, 2).contiguous()
+    dk = torch.zeros(hkv, n_keys, d, dtype=dtype)
+    dv = torch.zeros(hkv, n_keys, d, dtype=dtype)
+    for r0 in range(0, t, rows_per_block):
+        r1 = min(t, r0 + rows_per_block)
+        qb = q[r0:r1].to(dtype).reshape(r1 - r0, hkv, group, d).permute(1, 2, 0, 3).contiguous()
+        gb = dout[r0:r1].to(dtype).reshape(r1 - r0, hkv, group, d).permute(1, 2, 0, 3).contiguous()
+        scores = torch.matmul(qb, kh.unsqueeze(1).transpose(-1, -2).contiguous()) * scale
+        rows = torch.arange(r0, r1)[:, None]
+        visible = torch.arange(s)[None, :] <= (s - t) + rows
+        scores = scores.masked_fill(~visible, float("-inf"))
+        p = torch.softmax(scores, dim=-1)
+        out = torch.matmul(p, vh.unsqueeze(1))
+        delta = (gb * out).sum(-1, keepdim=True)
+        pp = p[..., :n_keys]
+        dpp = torch.matmul(gb, vh[:, :n_keys].unsqueeze(1).transpose(-1, -2).contiguous())
+        ds = pp * (dpp - delta)
+        dv += torch.matmul(pp.transpose(-1, -2), gb).sum(1)
+        dk += torch.matmul(ds.transpose(-1, -2), qb).sum(1) * scale
+    return dk.permute(1, 0, 2).contiguous(), dv.permute(1, 0, 2).contiguous()

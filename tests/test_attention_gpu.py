@@ -30,6 +30,7 @@ def close(got, want, what, bar=2e-2):
     assert got.shape == want.shape, (what, got.shape, want.shape)
     err = (got - want).abs().max().item() if got.numel() else 0.0
     scale = max(1.0, want.abs().max().item() if want.numel() else 0.0)
+    print(f"    {what}: max-abs {err:.4g} (bar {bar * scale:.4g} = {bar} x max(1, max|ref| {scale:.3g}))", flush=True)
     assert err <= bar * scale, f"{what}: max-abs {err:.4g} > {bar} x {scale:.3g}"
     return err
 
@@ -239,6 +240,100 @@ def test_packed_matches_per_segment_oracle(cuda, pack, hq, hkv):
         row0 += n
     close(pk.grad, want_pk, "shared prompt dk")
     close(pv.grad, want_pv, "shared prompt dv")
+
+
+@pytest.mark.parametrize("need", ["all", "chunks_only", "query_only"])
+def test_chunked_causal_op(cuda, need):
+    """``ChunkedCausalAttention.apply(query, scale, n_chunks, keep_state, backend,
+    *ks, *vs)`` -- the reference's _ChunkedCausalSDPA call (engine/streaming.py:
+    1354): output and per-chunk dK/dV in input order against the oracle; inputs
+    that do not require grad get None."""
+    t, chunks, hq, hkv = 96, [512, 130, 96], 32, 8
+    q, ks, vs, dout = make(t, chunks, hq, hkv, seed=17)
+    scale = D ** -0.5
+    want, wq, wks, wvs = ref.attention_with_grads(q[0], ks, vs, dout[0], scale)
+    qc = q.to(cuda).requires_grad_(need != "chunks_only")
+    kc = [k.to(cuda).requires_grad_(need != "query_only") for k in ks]
+    vc = [v.to(cuda).requires_grad_(need != "query_only") for v in vs]
+    query = qc.transpose(1, 2)  # [1, Hq, T, D] view
+    out = hip.ChunkedCausalAttention.apply(query, scale, len(kc), True, "auto", *kc, *vc)
+    out.transpose(1, 2).backward(dout.to(cuda))
+    torch.cuda.synchronize()
+    close(out[0].transpose(0, 1), want, "out")
+    if need != "chunks_only":
+        close(qc.grad[0], wq, "dq")
+    else:
+        assert qc.grad is None
+    for i, (k, v) in enumerate(zip(kc, vc)):
+        if need == "query_only":
+            assert k.grad is None and v.grad is None
+        else:
+            close(k.grad, wks[i], f"dk[{i}]")
+            close(v.grad, wvs[i], f"dv[{i}]")
+
+
+def test_chunked_causal_op_callable_backend(cuda):
+    """A callable backend is called as the reference calls it and differentiated
+    by re-running it under autograd (engine/streaming.py:1094-1095, 1384-1399):
+    here an fp32 softmax written with torch ops on the device, whose gradients
+    must then be the oracle's to fp32 accuracy."""
+    calls = []
+
+    def fp32_backend(query, ks, vs, scale):
+        calls.append(torch.is_grad_enabled())
+        q = query[0].float()                                  # [Hq, T, D]
+        k = torch.cat(list(ks), 0).float().transpose(0, 1)    # [Hkv, S, D]
+        v = torch.cat(list(vs), 0).float().transpose(0, 1)
+        rep = q.shape[0] // k.shape[0]
+        k = k.repeat_interleave(rep, 0)
+        v = v.repeat_interleave(rep, 0)
+        s = torch.matmul(q, k.transpose(1, 2).contiguous()) * scale
+        tq, sk = q.shape[1], k.shape[1]
+        visible = torch.arange(sk, device=q.device)[None, :] <= (sk - tq) + torch.arange(tq, device=q.device)[:, None]
+        p = torch.softmax(s.masked_fill(~visible, float("-inf")), -1)
+        return torch.matmul(p, v.contiguous()).to(query.dtype).unsqueeze(0)
+
+    t, chunks, hq, hkv = 40, [64, 40], 8, 2
+    q, ks, vs, dout = make(t, chunks, hq, hkv, seed=5)
+    scale = D ** -0.5
+    want, wq, wks, wvs = ref.attention_with_grads(q[0], ks, vs, dout[0], scale)
+    qc = q.to(cuda).requires_grad_()
+    kc = [k.to(cuda).requires_grad_() for k in ks]
+    vc = [v.to(cuda).requires_grad_() for v in vs]
+    out = hip.ChunkedCausalAttention.apply(qc.transpose(1, 2), scale, 2, False, fp32_backend, *kc, *vc)
+    out.transpose(1, 2).backward(dout.to(cuda))
+    torch.cuda.synchronize()
+    assert calls == [False, True]  # forward without a graph, backward re-run under autograd
+    close(out[0].transpose(0, 1), want, "out")
+    close(qc.grad[0], wq, "dq")
+    for i, (k, v) in enumerate(zip(kc, vc)):
+        close(k.grad, wks[i], f"dk[{i}]")
+        close(v.grad, wvs[i], f"dv[{i}]")
+
+
+def test_ragged_backward(cuda):
+    """``RaggedAttention.apply(scale, n, *qs, *ks, *vs)`` -- the reference's
+    _RaggedAttentionIndependentVJP (engine/streaming.py:1253-1297): outputs and
+    every segment's dQ, dK, dV against the oracle run on that segment alone."""
+    g = torch.Generator().manual_seed(9)
+    lens = [(4, 12), (8, 16), (33, 40), (128, 700), (1, 1)]
+    qs = [torch.randn(1, 32, t, D, generator=g).to(torch.bfloat16) for t, _ in lens]
+    ks = [torch.randn(s, 8, D, generator=g).to(torch.bfloat16) for _, s in lens]
+    vs = [torch.randn(s, 8, D, generator=g).to(torch.bfloat16) for _, s in lens]
+    gs = [torch.randn(1, 32, t, D, generator=g).to(torch.bfloat16) for t, _ in lens]
+    qc = [q.to(cuda).requires_grad_() for q in qs]
+    kc = [k.to(cuda).requires_grad_() for k in ks]
+    vc = [v.to(cuda).requires_grad_() for v in vs]
+    outs = hip.RaggedAttention.apply(D ** -0.5, len(lens), *qc, *kc, *vc)
+    torch.autograd.backward(outs, [x.to(cuda) for x in gs])
+    torch.cuda.synchronize()
+    for i in range(len(lens)):
+        o, gq, gk, gv = ref.attention_with_grads(qs[i][0].transpose(0, 1), [ks[i]], [vs[i]],
+                                                 gs[i][0].transpose(0, 1), D ** -0.5)
+        close(outs[i][0].transpose(0, 1), o, f"seg {i} out")
+        close(qc[i].grad[0].transpose(0, 1), gq, f"seg {i} dq")
+        close(kc[i].grad, gk[0], f"seg {i} dk")
+        close(vc[i].grad, gv[0], f"seg {i} dv")
 
 
 def test_ragged_cohort(cuda):

@@ -10,7 +10,10 @@ against the CPU oracle.
   completions, 21,810 tokens, 32/8 heads) in one launch per direction; the
   prompt's rows and two completions checked against the oracle run on their
   own paths: outputs, dQ, and the dK/dV of a completion's own keys (read by
-  that completion alone).
+  that completion alone); and the shared prompt's dK/dV for KV head 0 in
+  full -- its 2048 keys summed over every row of the forest that reads them
+  (the prompt's own causal rows and all eight completions, 21,810 rows x 4
+  query heads).
 
 Bar: 2e-2 max-abs, scaled by max|ref| where that exceeds 1 (as for the other
 attention tests).
@@ -39,6 +42,7 @@ def close(got, want, what, bar=2e-2):
     assert got.shape == want.shape, (what, got.shape, want.shape)
     err = (got - want).abs().max().item() if got.numel() else 0.0
     scale = max(1.0, want.abs().max().item() if want.numel() else 0.0)
+    print(f"    {what}: max-abs {err:.4g} (bar {bar * scale:.4g} = {bar} x max(1, max|ref| {scale:.3g}))", flush=True)
     assert err <= bar * scale, f"{what}: max-abs {err:.4g} > {bar} x {scale:.3g}"
     return err
 
@@ -145,3 +149,17 @@ def test_c2_full_size_sampled(cuda):
         close(q.grad[s:e], gq, f"dq[node {n}]")
         close(k.grad[s:e], gk[1], f"dk[node {n}]")
         close(v.grad[s:e], gv[1], f"dv[node {n}]")
+
+    # the shared prompt's keys, KV head 0 (query heads 0-3): every node's rows read them
+    want_dk = torch.zeros(2048, 1, D)
+    want_dv = torch.zeros(2048, 1, D)
+    for n in range(9):
+        s, e = starts[n], ends[n]
+        ks = [kc[:2048, :1]] if n == 0 else [kc[:2048, :1], kc[s:e, :1]]
+        vs = [vc[:2048, :1]] if n == 0 else [vc[:2048, :1], vc[s:e, :1]]
+        dk, dv = ref.prefix_key_grads(qc[s:e, :4], ks, vs, dc[s:e, :4], scale, 2048)
+        want_dk += dk
+        want_dv += dv
+    print(f"  shared prompt dK/dV, KV head 0: {ends[8] - starts[0]} rows", flush=True)
+    close(k.grad[:2048, :1], want_dk, "dk[prompt, kv head 0]")
+    close(v.grad[:2048, :1], want_dv, "dv[prompt, kv head 0]")

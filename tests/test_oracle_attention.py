@@ -94,3 +94,18 @@ def test_rms_norm_vjp_oracle_matches_closed_form():
     cdx, cdw = rn.rms_norm_backward_closed_form(dy, x, w, rstd)
     torch.testing.assert_close(dx.double(), cdx, rtol=1e-5, atol=1e-6)
     torch.testing.assert_close(dw.double(), cdw, rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("t,chunks,hq,hkv,n_keys,block", [(7, [9, 7], 8, 2, 9, 3), (40, [16, 40], 4, 1, 16, 512),
+                                                          (5, [20], 2, 2, 11, 2)])
+def test_prefix_key_grads_match_autograd(t, chunks, hq, hkv, n_keys, block):
+    """The hand-written prefix-key VJP against autograd of chained_attention."""
+    g = torch.Generator().manual_seed(t + hq)
+    q = torch.randn(t, hq, 16, generator=g)
+    ks = [torch.randn(n, hkv, 16, generator=g) for n in chunks]
+    vs = [torch.randn(n, hkv, 16, generator=g) for n in chunks]
+    dout = torch.randn(t, hq, 16, generator=g)
+    _, _, gk, gv = ref.attention_with_grads(q, ks, vs, dout, 0.3, dtype=torch.float64)
+    dk, dv = ref.prefix_key_grads(q, ks, vs, dout, 0.3, n_keys, rows_per_block=block, dtype=torch.float64)
+    torch.testing.assert_close(dk, torch.cat(gk, 0)[:n_keys], rtol=1e-10, atol=1e-10)
+    torch.testing.assert_close(dv, torch.cat(gv, 0)[:n_keys], rtol=1e-10, atol=1e-10)

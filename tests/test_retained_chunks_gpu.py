@@ -124,3 +124,22 @@ def test_c4_full_size_sampled(cuda):
         if i == longest:  # its own retained chunk is read by no other query chunk
             close(ks[path[-1]].grad, gk[-1], f"dk[chunk {i}]")
             close(vs[path[-1]].grad, gv[-1], f"dv[chunk {i}]")
+
+    # group 0's first prompt chunk, KV head 0, in full: every query chunk of
+    # the group reads it (the prompt's own chunks and every trajectory's)
+    first = chunks[0][2][0]
+    n_keys = ks[first].shape[0]
+    readers = [c for c in chunks if c[2][0] == first]
+    want_dk = torch.zeros(n_keys, 1, D)
+    want_dv = torch.zeros(n_keys, 1, D)
+    qc, dc = q.detach().cpu(), dout.cpu()
+    for row0, m, path in readers:
+        dk, dv = ref.prefix_key_grads(qc[row0 : row0 + m, :4], [ks[c].detach()[:, :1].cpu() for c in path],
+                                      [vs[c].detach()[:, :1].cpu() for c in path], dc[row0 : row0 + m, :4],
+                                      scale, n_keys)
+        want_dk += dk
+        want_dv += dv
+    print(f"  prompt chunk {first}: {n_keys} keys read by {len(readers)} query chunks "
+          f"({sum(m for _, m, _ in readers)} rows)", flush=True)
+    close(ks[first].grad[:, :1], want_dk, "dk[prompt chunk, kv head 0]")
+    close(vs[first].grad[:, :1], want_dv, "dv[prompt chunk, kv head 0]")

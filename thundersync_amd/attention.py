@@ -26,7 +26,9 @@ Reference entry points mirrored here (same argument meaning):
 * :class:`PackLayout` / :class:`PackedAttention` -- ``_PackedFlashSplit.apply(
   query, key, value, scale, layout, *ancestors)`` (engine/streaming.py:
   1613-1836), with ancestors in the reference's "last segment first" order;
-* :func:`ragged_causal_attention` -- ``_ragged_causal_sdpa`` (:1165-1226);
+* :func:`ragged_causal_attention` -- ``_ragged_causal_sdpa`` (:1165-1226),
+  and :class:`RaggedAttention` -- ``_RaggedAttentionIndependentVJP``
+  (:1253-1297);
 * :func:`forest_attention` -- ``forest_attention(q, k, v, plan, *, scale)``
   (engine/attention.py:186-231);
 * :func:`retained_chunk_layout` / :func:`retained_chunk_attention` -- every
@@ -128,6 +130,16 @@ class AttnLayout:
                 raise ValueError(f"run {r} names source {run.source}")
             if run.length <= 0 or run.offset < 0 or run.offset + run.length > self.source_rows[run.source]:
                 raise ValueError(f"run {r} rows outside its source")
+        # the backward writes each run's dK/dV through its own rows, without
+        # atomics: two runs may not share a row of a source
+        by_source: dict[int, list[tuple[int, int, int]]] = {}
+        for r, run in enumerate(self.runs):
+            by_source.setdefault(run.source, []).append((run.offset, run.offset + run.length, r))
+        for source, spans in by_source.items():
+            spans.sort()
+            for (a0, a1, ra), (b0, _b1, rb) in zip(spans, spans[1:]):
+                if b0 < a1:
+                    raise ValueError(f"runs {ra} and {rb} overlap in source {source} (rows {b0}..{a1 - 1})")
         if max([*self.seg_kv, 0]) >= 2**31 or self.q_rows >= 2**40:
             raise ValueError("attention problem too large")
 
@@ -473,17 +485,33 @@ def causal_attention(query: torch.Tensor, ks: Sequence[torch.Tensor], vs: Sequen
 class ChunkedCausalAttention(torch.autograd.Function):
     """``apply(query, scale, n_chunks, keep_state, backend, *ks, *vs)``.
 
-    Argument order of ``_ChunkedCausalSDPA`` (engine/streaming.py:1354): the
-    op keeps only the query, its output and log-sum-exp plus references to the
-    per-chunk K/V (never a concatenated copy) and returns one dK/dV per chunk
-    in input order.  ``keep_state`` and ``backend`` are accepted for
-    signature compatibility; this op always keeps the output and LSE, which
-    is what the reference's saved-state mode keeps.
+    Argument order and meaning of ``_ChunkedCausalSDPA`` (engine/streaming.py:
+    1314-1423): bottom-right-causal attention of ``query [1, Hq, T, D]`` over
+    the chunk lists as one op that keeps only references to the per-chunk K/V
+    (never a concatenated copy) and returns one dK/dV per chunk in input order.
+
+    * ``backend`` ``"auto"`` or ``"cudnn"`` (the reference's built-in names):
+      the HIP kernels.  The op keeps the query, its output and log-sum-exp --
+      what the reference's saved-state mode keeps -- and its backward runs
+      the HIP backward on them, whatever ``keep_state`` says (the reference's
+      other mode re-runs the forward to reach the same numbers; the HIP
+      forward is deterministic, so keeping them is equivalent).
+    * a callable ``backend(query, ks, vs, scale)``: called as the reference
+      calls it (:1094-1095), and differentiated by re-running it under
+      autograd in the backward (:1384-1399).
+    * any other name raises ``ValueError`` (:1096-1097).
     """
 
     @staticmethod
     def forward(ctx, query, scale, n_chunks, keep_state, backend, *chunks):
-        ks, vs = chunks[:n_chunks], chunks[n_chunks:]
+        ks, vs = list(chunks[:n_chunks]), list(chunks[n_chunks:])
+        ctx.n_chunks, ctx.scale, ctx.backend = n_chunks, scale, backend
+        if callable(backend):
+            ctx.graph = None
+            ctx.save_for_backward(query, *chunks)
+            return backend(query, ks, vs, scale)
+        if backend not in ("auto", "cudnn"):
+            raise ValueError(f"unknown source attention backend: {backend!r}")
         with torch.enable_grad():
             leaves = [c.detach().requires_grad_(c.requires_grad) for c in chunks]
             q = query.detach().requires_grad_(query.requires_grad)
@@ -494,13 +522,27 @@ class ChunkedCausalAttention(torch.autograd.Function):
     @staticmethod
     @torch.autograd.function.once_differentiable
     def backward(ctx, grad_out):
-        q, leaves, out = ctx.graph
-        inputs = [t for t in (q, *leaves) if t.requires_grad]
-        grads = torch.autograd.grad(out, inputs, grad_out, allow_unused=True) if inputs else []
-        it = iter(grads)
-        dq = next(it) if q.requires_grad else None
-        rest = [next(it) if c.requires_grad else None for c in leaves]
-        return (dq, None, None, None, None, *rest)
+        need = ctx.needs_input_grad
+        n = ctx.n_chunks
+        if ctx.graph is None:
+            query, *chunks = ctx.saved_tensors
+            q = query.detach().requires_grad_(True)
+            leaves = [c.detach().requires_grad_(True) for c in chunks]
+            with torch.enable_grad():
+                out = ctx.backend(q, leaves[:n], leaves[n:], ctx.scale)
+            grads = torch.autograd.grad(out, [q, *leaves], grad_out, allow_unused=True)
+            dq, rest = grads[0], list(grads[1:])
+        else:
+            q, leaves, out = ctx.graph
+            inputs = [t for t in (q, *leaves) if t.requires_grad]
+            grads = torch.autograd.grad(out, inputs, grad_out, allow_unused=True) if inputs else []
+            it = iter(grads)
+            dq = next(it) if q.requires_grad else None
+            rest = [next(it) if c.requires_grad else None for c in leaves]
+        return (
+            dq if need[0] else None, None, None, None, None,
+            *(g if need[5 + i] else None for i, g in enumerate(rest)),
+        )
 
 
 @dataclass(eq=False)
@@ -639,31 +681,65 @@ class PackedAttention(torch.autograd.Function):
         return (dq, dks[0], dvs[0], None, None, *anc_k, *anc_v)
 
 
+def _ragged_layout(lengths: Sequence[int], key_rows: Sequence[int], hq: int, hkv: int) -> AttnLayout:
+    """Segment i: ``lengths[i]`` packed query rows over key source i alone."""
+    runs = tuple(Run(i, 0, n) for i, n in enumerate(key_rows))
+    seg_q, row0 = [], 0
+    for n in lengths:
+        seg_q.append((row0, n))
+        row0 += n
+    return AttnLayout(
+        q_rows=row0, hq=hq, hkv=hkv, source_rows=tuple(key_rows), runs=runs,
+        seg_q=tuple(seg_q), seg_spans=tuple(((i, 0),) for i in range(len(key_rows))),
+    )
+
+
 def ragged_causal_attention(queries, keys, values, scale):
-    """``_ragged_causal_sdpa``: per segment ``[1,Hq,T_i,D]`` over ``[S_i,Hkv,D]``."""
+    """``_ragged_causal_sdpa`` (engine/streaming.py:1165-1226): per segment
+    ``[1,Hq,T_i,D]`` over its own ``[S_i,Hkv,D]``, bottom-right causal, all
+    segments in one launch.  Differentiable (one backward launch)."""
     if not queries:
         return []
-    outs = []
-    # one launch for the cohort: each segment is its own key run
     q_rows = [_as_rows(_query_rows(q)) for q in queries]
     lengths = [q.shape[0] for q in q_rows]
     packed = torch.cat(q_rows, 0)
     srcs_k = [_as_rows(k) for k in keys]
     srcs_v = [_as_rows(v) for v in values]
-    runs = tuple(Run(i, 0, k.shape[0]) for i, k in enumerate(srcs_k))
-    seg_q, row0 = [], 0
-    for n in lengths:
-        seg_q.append((row0, n))
-        row0 += n
-    layout = AttnLayout(
-        q_rows=packed.shape[0], hq=packed.shape[1], hkv=srcs_k[0].shape[1],
-        source_rows=tuple(k.shape[0] for k in srcs_k), runs=runs,
-        seg_q=tuple(seg_q), seg_spans=tuple(((i, 0),) for i in range(len(srcs_k))),
-    )
+    layout = _ragged_layout(lengths, [k.shape[0] for k in srcs_k], packed.shape[1], srcs_k[0].shape[1])
     out, _ = attention(packed, layout, srcs_k, srcs_v, scale)
-    for piece in out.split(lengths, 0):
-        outs.append(piece.transpose(0, 1).unsqueeze(0))
-    return outs
+    return [piece.transpose(0, 1).unsqueeze(0) for piece in out.split(lengths, 0)]
+
+
+class RaggedAttention(torch.autograd.Function):
+    """``apply(scale, n_segments, *queries, *keys, *values)`` -> one output per
+    segment, as ``_RaggedAttentionIndependentVJP`` (engine/streaming.py:
+    1253-1297).  The reference runs the cohort through one varlen flash call
+    and recomputes each segment with ``_causal_sdpa`` in its backward; here
+    the forward is one HIP launch for the cohort and the backward one HIP
+    backward launch over the saved output and log-sum-exp, which gives every
+    segment its own independent VJP (segments share no keys)."""
+
+    @staticmethod
+    def forward(ctx, scale, n_segments, *tensors):
+        queries = list(tensors[:n_segments])
+        keys = list(tensors[n_segments : 2 * n_segments])
+        values = list(tensors[2 * n_segments :])
+        with torch.enable_grad():
+            qs = [q.detach().requires_grad_(q.requires_grad) for q in queries]
+            kk = [k.detach().requires_grad_(k.requires_grad) for k in keys]
+            vv = [v.detach().requires_grad_(v.requires_grad) for v in values]
+            outs = ragged_causal_attention(qs, kk, vv, scale)
+        ctx.graph = (qs + kk + vv, outs)
+        return tuple(o.detach() for o in outs)
+
+    @staticmethod
+    @torch.autograd.function.once_differentiable
+    def backward(ctx, *grad_outputs):
+        leaves, outs = ctx.graph
+        inputs = [t for t in leaves if t.requires_grad]
+        grads = torch.autograd.grad(outs, inputs, grad_outputs, allow_unused=True) if inputs else []
+        it = iter(grads)
+        return (None, None, *(next(it) if t.requires_grad else None for t in leaves))
 
 
 # ---------------------------------------------------------------------------
