@@ -425,8 +425,8 @@ def bench_logprob(args, device):
         lp, ent = fused_logprob.fused_logprob_entropy(h, weight, t)
         lp.backward(a)
 
-    kernels = ["logprob.fwd_stats_kernel", "logprob.target_logit_kernel", "logprob.combine_kernel", "logprob.transpose_kernel",
-               "logprob.dlogits_kernel", "logprob.grad_hidden_kernel"]
+    kernels = ["logprob.fwd_stats_kernel", "logprob.target_logit_kernel", "logprob.combine_kernel",
+               "logprob.dlogits_kernel", "logprob.grad_hidden_kernel", "logprob.grad_hidden_reduce_kernel"]
     ms, per = timed(step, args.steps, args.warmup, kernels)
     gemm = 2 * rows * v * d
     work = {
@@ -435,7 +435,7 @@ def bench_logprob(args, device):
         "logprob.grad_hidden_kernel": gemm,
         "logprob.combine_kernel": 0,
         "logprob.target_logit_kernel": 0,
-        "logprob.transpose_kernel": 0,
+        "logprob.grad_hidden_reduce_kernel": 0,
     }
     flop = 3 * gemm
     result = {

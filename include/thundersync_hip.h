@@ -243,12 +243,6 @@ int ts_logprob_fwd(const void* hidden, int64_t ld_hidden, const void* weight,
                    float* lse, void* workspace, int64_t workspace_bytes,
                    void* stream);
 
-/* weight_t [dim, ld_t] = W^T with columns [vocab, ld_t) zero (ld_t % 8 == 0,
- * ld_t >= vocab; dim and ld_weight multiples of 8, both pointers 16-byte
- * aligned): the K-contiguous operand of ts_logprob_grad_hidden. */
-int ts_logprob_weight_t(const void* weight, int64_t ld_weight, int64_t vocab,
-                        int64_t dim, void* weight_t, int64_t ld_t, void* stream);
-
 /* dlogits [rows, ld_dlogits] (bf16) =
  *   -p * (g_lp + g_ent * (log p + H)) + g_lp * onehot(target),
  * p = exp(l - lse), recomputing l on MFMA; columns [vocab, roundup8(vocab))
@@ -263,14 +257,33 @@ int ts_logprob_dlogits(const void* hidden, int64_t ld_hidden, const void* weight
                        int64_t vocab, void* dlogits, int64_t ld_dlogits,
                        void* stream);
 
-/* grad_hidden [rows, dim] (bf16) = dlogits . W, fp32 accumulation on MFMA,
- * with W given as weight_t [dim, ld_t] (vocab_padded = roundup8(vocab)).
- * Replaces the hidden VJP GEMM `_matmul_accum(dlogits, weight)`
- * (accel/fused_logprob.py:175, :297). */
-int ts_logprob_grad_hidden(const void* dlogits, int64_t ld_dlogits,
-                           const void* weight_t, int64_t ld_t, int64_t rows,
-                           int64_t dim, int64_t vocab_padded, void* grad_hidden,
-                           int64_t ld_grad, void* stream);
+/* Workspace bytes ts_logprob_grad_hidden needs for rows x dim x vocab (0
+ * when the row tiles alone fill the device and no vocabulary split is made). */
+int64_t ts_logprob_grad_hidden_workspace(int64_t rows, int64_t dim, int64_t vocab);
+
+/* grad_hidden [rows, dim] (bf16) = dlogits [rows, vocab] . W [vocab, dim],
+ * fp32 accumulation on MFMA, W read in place (as the K-strided operand;
+ * no transposed copy).  When the row tiles alone do not fill the device the
+ * vocabulary is cut into ranges whose fp32 partial sums (the workspace) are
+ * added in range order: deterministic.  Replaces the hidden VJP
+ * `_matmul_accum(dlogits, weight)` of _FusedLinearLogprob.backward and
+ * _FusedLinearLogprobEntropy.backward (accel/fused_logprob.py:167-175,
+ * :297-303). */
+int ts_logprob_grad_hidden(const void* dlogits, int64_t ld_dlogits, const void* weight,
+                           int64_t ld_weight, int64_t rows, int64_t dim, int64_t vocab,
+                           void* grad_hidden, int64_t ld_grad, void* workspace,
+                           int64_t workspace_bytes, void* stream);
+
+/* grad_weight [vocab, ld_grad] (fp32) += dlogits[:rows]^T . hidden[:rows]
+ * on MFMA with fp32 accumulation; called once per dlogits block, it
+ * accumulates the weight gradient across blocks in block order, to be cast to
+ * the weight dtype once (bf16 operands, as the reference's bf16 dlogits and
+ * hidden).  Replaces `_matmul_accum(dlogits.t(), h)` and the fp32
+ * `grad_weight.add_` of _FusedLinearLogprob.backward
+ * (accel/fused_logprob.py:176-193, :304-306). */
+int ts_logprob_grad_weight(const void* dlogits, int64_t ld_dlogits, const void* hidden,
+                           int64_t ld_hidden, int64_t rows, int64_t dim, int64_t vocab,
+                           float* grad_weight, int64_t ld_grad, void* stream);
 
 /* ------------------------------------------------------------------------
  * Boundary adjoints

@@ -183,29 +183,61 @@ def test_c3_full_size_sampled_rows(cuda):
     rel_close(hs.grad[sample], want_gh, 1e-2, "grad hidden (sampled rows)")
 
 
-@pytest.mark.parametrize("v,d", [(1001, 136), (513, 4096), (8, 8)])
-def test_weight_transpose_exact(cuda, v, d):
-    """ts_logprob_weight_t: W^T bit for bit, columns [vocab, ld_t) zero."""
+def test_weight_gradient_c3_head(cuda):
+    """The hand-written weight gradient at the C3 head's shape (151936 x 4096):
+    two 128-row dlogits blocks accumulated in fp32 and cast once, against the
+    oracle's needs_weight_grad path (fused_logprob.py:176-193), every row."""
+    n, d, v = 256, 4096, 151936
+    h, w, t, g_lp, g_ent = _inputs(n, d, v, seed=23)
+    print(f"weight gradient n={n} d={d} v={v} chunk=128", flush=True)
+    _, ent = ref.logprob_entropy_forward(h, w, t, 128)
+    want_gh, want_gw = ref.logprob_entropy_backward(h, w, t, ent, g_lp, g_ent, 128, needs_weight_grad=True)
+    hc, wc = h.to(cuda).requires_grad_(), w.to(cuda).requires_grad_()
+    lp, en = hip.fused_logprob_entropy(hc, wc, t.to(cuda), chunk=128)
+    (lp * g_lp.to(cuda) + en * g_ent.to(cuda)).sum().backward()
+    torch.cuda.synchronize()
+    rel_close(hc.grad, want_gh, 1e-2, "grad hidden")
+    rel_close(wc.grad, want_gw, 1e-2, "grad weight")
+    # the target rows carry the one-hot term: check them on their own scale too
+    rows = t.unique()
+    rel_close(wc.grad[rows.to(cuda)], want_gw[rows], 1e-2, "grad weight (target rows)")
+
+
+def test_backward_memory_is_one_chunk(cuda):
+    """Peak extra device memory of the backward is the [chunk, V] bf16 dlogits
+    block plus the grad_hidden workspace (the reference's O(chunk * V),
+    fused_logprob.py:20-24), not O(N * V)."""
     from thundersync_amd import _lib
 
-    print(f"weight transpose vocab={v} dim={d}", flush=True)
-    lib = _lib.require_library()
-    g = torch.Generator().manual_seed(v + d)
-    w = torch.randn(v, d, generator=g).to(torch.bfloat16).to(cuda)
-    vp = (v + 7) // 8 * 8
-    wt = torch.full((d, vp), 7.0, dtype=torch.bfloat16, device=cuda)  # padding must be overwritten
-    _lib.check(lib.ts_logprob_weight_t(w.data_ptr(), w.stride(0), v, d, wt.data_ptr(), vp, _lib.stream_of(w)),
-               "ts_logprob_weight_t")
+    n, d, v, chunk = 4096, 4096, 151936, 1024
+    g = torch.Generator(device=cuda).manual_seed(3)
+    h = torch.randn(n, d, generator=g, device=cuda, dtype=torch.bfloat16).requires_grad_()
+    w = (torch.randn(v, d, generator=g, device=cuda) * 0.02).to(torch.bfloat16)
+    t = torch.randint(0, v, (n,), generator=g, device=cuda)
+    lp, ent = hip.fused_logprob_entropy(h, w, t, chunk=chunk)
+    upstream = torch.randn(n, generator=g, device=cuda)
+    loss = (lp * upstream).sum()
     torch.cuda.synchronize()
-    want = torch.zeros(d, vp, dtype=torch.bfloat16)
-    want[:, :v] = w.cpu().t()
-    assert torch.equal(wt.cpu(), want)
+    torch.cuda.reset_peak_memory_stats(cuda)
+    before = torch.cuda.memory_allocated(cuda)
+    loss.backward()
+    torch.cuda.synchronize()
+    extra = torch.cuda.max_memory_allocated(cuda) - before
+    block = hip.backward_block_rows(n, chunk)
+    dl_bytes = block * ((v + 7) // 8 * 8) * 2
+    ws_bytes = int(_lib.require_library().ts_logprob_grad_hidden_workspace(block, d, v))
+    grad_hidden = n * d * 2
+    small = 4 << 20  # per-row fp32 coefficients and autograd's scalars
+    print(f"backward extra {extra / 2**20:.1f} MiB: dlogits {dl_bytes / 2**20:.1f} + workspace "
+          f"{ws_bytes / 2**20:.1f} + grad_hidden {grad_hidden / 2**20:.1f} MiB", flush=True)
+    assert extra <= dl_bytes + ws_bytes + grad_hidden + small
+    assert dl_bytes <= chunk * v * 2 + chunk * 16
 
 
 def test_repeated_runs_are_bit_identical(cuda):
-    """No atomics and no split reductions: the per-tile partials are merged in
-    a fixed order, so two runs give identical bits (forward, entropy, grad
-    wrt hidden, and the weight gradient's fixed-order fp32 accumulation)."""
+    """No atomics: the per-tile partials, grad_hidden's vocabulary-range
+    partial sums and the weight gradient's fp32 accumulation are all merged
+    in a fixed order, so two runs give identical bits."""
     n, d, v = 2500, 512, 9000
     h, w, t, g_lp, g_ent = _inputs(n, d, v, seed=41)
     runs = []

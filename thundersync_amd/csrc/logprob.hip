@@ -27,6 +27,7 @@
 // fragments are read during the current stage's last MFMAs.
 // Rows past an operand's valid rows and 8-element K chunks past K arrive as
 // zeros (buffer range checking), so ragged edges need no masking in the loop.
+#include <algorithm>
 #include <type_traits>
 
 #include "common.h"
@@ -102,6 +103,94 @@ struct Streamer {
   }
 };
 
+// An operand stored with its contraction index as the row index ("K-strided":
+// W read as W^T, dlogits or hidden read as their transposes): the tile's 256
+// M values of one K row are contiguous.  A stage holds K rows k0 .. k0 + 31 as
+// [32][256] (512-byte rows), 16-byte chunk c of row k at slot c ^ (4 (k & 3)),
+// so that the transposed fragment reads below touch 16 distinct bank groups
+// per pass.  One instruction moves two K rows: lane i fills row
+// 2 t + (i >> 5), slot i & 31, with logical chunk (i & 31) ^ (4 (row & 3)).
+// K rows past K and chunks past the operand's end arrive as zeros (buffer
+// range checking); chunks past M in earlier rows read the next row, which
+// lands in output rows or columns the epilogue discards.
+struct StreamerT {
+  const bf16* base;  // k 0, m 0 of the tile
+  int64_t ld;        // elements between consecutive K rows
+  int mvalid;        // valid M columns from base (>= 1)
+  int K;
+  int voff[2];
+  __device__ __forceinline__ void init(const bf16* b, int64_t ld_, int mvalid_, int K_, int wave, int lane) {
+    base = b;
+    ld = ld_;
+    mvalid = min(mvalid_, TM);
+    K = K_;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int row = 2 * (wave + 8 * u) + (lane >> 5);
+      const int c = (lane & 31) ^ (4 * (row & 3));
+      voff[u] = (int)((row * ld + 8 * c) * 2);
+    }
+  }
+  __device__ __forceinline__ u32x4 descriptor(int k0) const {
+    const int rows = min(TK, K - k0);
+    return raw_descriptor(base + (int64_t)k0 * ld, (uint32_t)(((int64_t)(rows - 1) * ld + mvalid) * 2));
+  }
+  __device__ __forceinline__ void issue(u32x4 r, bf16* dst, int u, int wave) const {
+    buffer_dma16_untracked(r, dst + (wave + 8 * u) * 512, voff[u]);
+  }
+};
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ u32x2 tr_read(const bf16* p) {
+  const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)p);
+  u32x2 r;
+  __builtin_memcpy(&r, &v, 8);
+  return r;
+}
+
+// Fragment reads of one operand of v_mfma_f32_32x32x16_bf16 from a stage part:
+// lane l holds M row (l & 31) of a 32-row block and the 8 K values
+// 16 kk + 8 (l >> 5) .. + 7 of k-step kk.
+//  K-contiguous part ([256 rows][32 k]): one 16-byte read at row, chunk
+//    2 kk + (l >> 5), slot chunk ^ ((row >> 2) & 3).
+//  K-strided part ([32 k][256 m]): two ds_read_b64_tr_b16.  Within each
+//    16-lane group, lane j addressing K row kb + j / 4 at M columns
+//    m0 + 4 (j & 3) .. + 3 receives the 4 values at K rows kb .. kb + 3 of
+//    column m0 + j (lane semantics pinned by the LDS probe test), so the
+//    group g = l >> 4 takes M columns 16 (g & 1) + 0..15 of the block and K
+//    rows 16 kk + 8 (g >> 1) + {0..3, 4..7}.
+template <bool KS> struct Frag;
+template <> struct Frag<false> {
+  int off[2];  // per kk, block 0
+  __device__ __forceinline__ void init(int lane, int row0) {
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      const int slot = ((2 * kk + (lane >> 5)) ^ ((lane >> 2) & 3)) << 3;
+      off[kk] = (row0 + (lane & 31)) * TK + slot;
+    }
+  }
+  __device__ __forceinline__ bf16x8 read(const bf16* part, int kk, int blk) const {
+    return as_bf16x8(ld16(part + off[kk] + 32 * blk * TK));
+  }
+};
+template <> struct Frag<true> {
+  int off[4];  // per 32-row block (kk = 0, first read)
+  __device__ __forceinline__ void init(int lane, int row0) {
+    const int j = lane & 15, g = lane >> 4;
+    const int k = 8 * (g >> 1) + (j >> 2);  // k & 3 == (j >> 2) & 3
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const int m = row0 + 32 * b + 16 * (g & 1) + 4 * (j & 3);
+      off[b] = k * TM + ((((m >> 3) ^ (4 * (k & 3))) & (TM / 8 - 1)) << 3) + (m & 7);
+    }
+  }
+  __device__ __forceinline__ bf16x8 read(const bf16* part, int kk, int blk) const {
+    const u32x2 lo = tr_read(part + off[blk] + 16 * kk * TM);
+    const u32x2 hi = tr_read(part + off[blk] + (16 * kk + 4) * TM);
+    return as_bf16x8(u32x4{lo[0], lo[1], hi[0], hi[1]});
+  }
+};
+
 // acc[mi][ni]: 32x32 block (A rows 128 wm + 32 mi, B rows 64 wn + 32 ni),
 // wm = wave & 1, wn = wave >> 1.  Lane l holds B row (l & 31) + 32 ni + 64 wn and A rows
 // 8 (i >> 2) + 4 (l >> 5) + (i & 3) + 32 mi + 128 wm, i = 0..15.
@@ -118,19 +207,20 @@ __device__ __forceinline__ int a_row(int mi, int i, int lane, int wm) {
 // issuing MFMAs while the DMA is in flight, and with the next stage's first
 // fragments in registers the MFMAs start right after the stage barrier
 // instead of waiting for LDS reads every wave issues at once.
-template <class Dma>
-__device__ __forceinline__ void mma_stage(f32x16 acc[4][NI], const bf16* st, const bf16* nx, const int fa[2],
-                                          const int fb[2], bf16x8 (&a0)[4], bf16x8 (&b0)[NI], Dma&& dma) {
+template <class FA, class FB, class Dma>
+__device__ __forceinline__ void mma_stage(f32x16 acc[4][NI], const bf16* st, const bf16* nx, const FA& fa,
+                                          const FB& fb, bf16x8 (&a0)[4], bf16x8 (&b0)[NI], Dma&& dma) {
   bf16x8 a1[4], b1[NI];
+  const bf16* sb = st + TM * TK;
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
     acc[g][0] = mfma32(a0[g], b0[0], acc[g][0]);
     acc[g][1] = mfma32(a0[g], b0[1], acc[g][1]);
     if (g < 2) {
-      a1[2 * g] = as_bf16x8(ld16(st + fa[1] + 32 * (2 * g) * TK));
-      a1[2 * g + 1] = as_bf16x8(ld16(st + fa[1] + 32 * (2 * g + 1) * TK));
+      a1[2 * g] = fa.read(st, 1, 2 * g);
+      a1[2 * g + 1] = fa.read(st, 1, 2 * g + 1);
     } else {
-      b1[g - 2] = as_bf16x8(ld16(st + fb[1] + 32 * (g - 2) * TK));
+      b1[g - 2] = fb.read(sb, 1, g - 2);
     }
     dma(g);
     __builtin_amdgcn_sched_barrier(0);
@@ -140,8 +230,8 @@ __device__ __forceinline__ void mma_stage(f32x16 acc[4][NI], const bf16* st, con
 #pragma unroll
     for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = mfma32(a1[mi], b1[ni], acc[mi][ni]);
     if (nx != nullptr) {
-      a0[mi] = as_bf16x8(ld16(nx + fa[0] + 32 * mi * TK));
-      if (mi < NI) b0[mi] = as_bf16x8(ld16(nx + fb[0] + 32 * mi * TK));
+      a0[mi] = fa.read(nx, 0, mi);
+      if (mi < NI) b0[mi] = fb.read(nx + TM * TK, 0, mi);
     }
     __builtin_amdgcn_sched_barrier(0);
   }
@@ -154,9 +244,12 @@ __device__ __forceinline__ void wait_dma(int ahead) {
   else __builtin_amdgcn_s_waitcnt(0x0F70);                  // vmcnt(0)
 }
 
-// C tile = A[256 rows] . B[256 rows]^T over K (both K-contiguous), through the
-// LDS ring s0..s3 (distinct arrays, so the compiler sees that a refill and
-// the reads of another stage never alias).  The ring is free on return.
+// C tile = A . B^T over K through the LDS ring s0..s3 (distinct arrays, so the
+// compiler sees that a refill and the reads of another stage never alias);
+// the ring is free on return.  AKS / BKS: the operand is K-strided (A is then
+// given as its [K][M] storage from the tile's first column, B likewise);
+// otherwise K-contiguous (a_rows / b_rows valid rows of 256 from A / B).
+template <bool AKS, bool BKS>
 __device__ __forceinline__ void gemm_tile(f32x16 acc[4][NI], const bf16* A, int64_t lda, int a_rows,
                                           const bf16* B, int64_t ldb, int b_rows, int K, bf16* s0,
                                           bf16* s1, bf16* s2, bf16* s3) {
@@ -169,26 +262,32 @@ __device__ __forceinline__ void gemm_tile(f32x16 acc[4][NI], const bf16* A, int6
     for (int ni = 0; ni < NI; ++ni)
 #pragma unroll
       for (int i = 0; i < 16; ++i) acc[mi][ni][i] = 0.f;
-  Streamer sa, sb;
+  std::conditional_t<AKS, StreamerT, Streamer> sa;
+  std::conditional_t<BKS, StreamerT, Streamer> sb;
   sa.init(A, lda, a_rows, K, wave, lane);
   sb.init(B, ldb, b_rows, K, wave, lane);
-  // fragment offsets (elements) within a stage: row 128 w + (l & 31) of the A
-  // (B) half, logical chunk 2 kk + (l >> 5) at slot chunk ^ ((row >> 2) & 3)
-  int fa[2], fb[2];
-#pragma unroll
-  for (int kk = 0; kk < 2; ++kk) {
-    const int slot = ((2 * kk + (lane >> 5)) ^ ((lane >> 2) & 3)) << 3;
-    fa[kk] = (128 * wm + (lane & 31)) * TK + slot;
-    fb[kk] = TM * TK + (64 * wn + (lane & 31)) * TK + slot;
-  }
+  Frag<AKS> fa;
+  Frag<BKS> fb;
+  fa.init(lane, 128 * wm);
+  fb.init(lane, 64 * wn);
   const int nk = (K + TK - 1) / TK;
+  // operand s of stage kt: descriptor, and per lane whether its chunk is in K
+  // (K-strided operands bound K by the descriptor's row count instead)
+  auto in_k = [&](const auto& s, int k0) {
+    if constexpr (std::is_same_v<std::decay_t<decltype(s)>, Streamer>) return k0 + s.kchunk < K;
+    else return true;
+  };
+  auto put = [&](const auto& s, u32x4 r, bool ik, bf16* dst, int u) {
+    if constexpr (std::is_same_v<std::decay_t<decltype(s)>, Streamer>) s.issue(r, ik, dst, u, wave);
+    else s.issue(r, dst, u, wave);
+  };
   auto issue = [&](bf16* st, int kt) {
     const u32x4 ra = sa.descriptor(kt * TK), rb = sb.descriptor(kt * TK);
-    const bool ka = kt * TK + sa.kchunk < K, kb = kt * TK + sb.kchunk < K;
+    const bool ka = in_k(sa, kt * TK), kb = in_k(sb, kt * TK);
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-      sa.issue(ra, ka, st, u, wave);
-      sb.issue(rb, kb, st + TM * TK, u, wave);
+      put(sa, ra, ka, st, u);
+      put(sb, rb, kb, st + TM * TK, u);
     }
   };
   issue(s0, 0);
@@ -199,9 +298,9 @@ __device__ __forceinline__ void gemm_tile(f32x16 acc[4][NI], const bf16* A, int6
   wait_dma(min(nk - 1, 2));
   __builtin_amdgcn_s_barrier();
 #pragma unroll
-  for (int mi = 0; mi < 4; ++mi) a0[mi] = as_bf16x8(ld16(s0 + fa[0] + 32 * mi * TK));
+  for (int mi = 0; mi < 4; ++mi) a0[mi] = fa.read(s0, 0, mi);
 #pragma unroll
-  for (int ni = 0; ni < NI; ++ni) b0[ni] = as_bf16x8(ld16(s0 + fb[0] + 32 * ni * TK));
+  for (int ni = 0; ni < NI; ++ni) b0[ni] = fb.read(s0 + TM * TK, 0, ni);
   // step kt: this wave's DMA of stages kt and kt + 1 has landed (stage kt + 2
   // may still be in flight); the barrier makes every wave's share of them
   // visible -- the next stage's first fragments are read during this step --
@@ -214,12 +313,12 @@ __device__ __forceinline__ void gemm_tile(f32x16 acc[4][NI], const bf16* A, int6
     __builtin_amdgcn_s_barrier();
     const bool refill_now = kt + 3 < nk;
     const int k0 = (kt + 3) * TK;
-    const u32x4 ra = sa.descriptor(k0), rb = sb.descriptor(k0);
-    const bool ka = k0 + sa.kchunk < K, kb = k0 + sb.kchunk < K;
+    const u32x4 ra = sa.descriptor(refill_now ? k0 : 0), rb = sb.descriptor(refill_now ? k0 : 0);
+    const bool ka = in_k(sa, k0), kb = in_k(sb, k0);
     mma_stage(acc, cur, kt + 1 < nk ? nxt : nullptr, fa, fb, a0, b0, [&](int g) {
       if (refill_now) {
-        if (g < 2) sa.issue(ra, ka, refill, g, wave);
-        else sb.issue(rb, kb, refill + TM * TK, g - 2, wave);
+        if (g < 2) put(sa, ra, ka, refill, g);
+        else put(sb, rb, kb, refill + TM * TK, g - 2);
       }
     });
   };
@@ -289,8 +388,8 @@ __global__ __launch_bounds__(kGemmThreads, 1) void fwd_stats_kernel(FwdArgs p) {
   grouped_tile(xcd_logical(blockIdx.x, total), p.n_vtiles, p.n_ttiles, vt, tt);
   const int v0 = vt * TM, n0 = tt * TN;
   f32x16 acc[4][NI];
-  gemm_tile(acc, p.w + (int64_t)v0 * p.ldw, p.ldw, min(TM, p.vocab - v0), p.h + (int64_t)n0 * p.ldh,
-            p.ldh, min(TN, p.rows - n0), p.dim, s0, s1, s2, s3);
+  gemm_tile<false, false>(acc, p.w + (int64_t)v0 * p.ldw, p.ldw, min(TM, p.vocab - v0),
+                          p.h + (int64_t)n0 * p.ldh, p.ldh, min(TN, p.rows - n0), p.dim, s0, s1, s2, s3);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave & 1, wn = wave >> 1;
   float* xm = reinterpret_cast<float*>(s0);  // [TN] per token, from the wm = 1 waves
@@ -464,8 +563,8 @@ __global__ __launch_bounds__(kGemmThreads, 1) void dlogits_kernel(DlArgs p) {
   grouped_tile(xcd_logical(blockIdx.x, total), p.n_vtiles, p.n_ttiles, vt, tt);
   const int v0 = vt * TM, n0 = tt * TN;
   f32x16 acc[4][NI];
-  gemm_tile(acc, p.w + (int64_t)v0 * p.ldw, p.ldw, min(TM, p.vocab - v0), p.h + (int64_t)n0 * p.ldh,
-            p.ldh, min(TN, p.rows - n0), p.dim, s0, s1, s2, s3);
+  gemm_tile<false, false>(acc, p.w + (int64_t)v0 * p.ldw, p.ldw, min(TM, p.vocab - v0),
+                          p.h + (int64_t)n0 * p.ldh, p.ldh, min(TN, p.rows - n0), p.dim, s0, s1, s2, s3);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave & 1, wn = wave >> 1;
   // tokens 64 q .. 64 q + 63 of the tile are staged in ring stage q as [64][OPITCH]
@@ -536,28 +635,37 @@ __global__ __launch_bounds__(kGemmThreads, 1) void dlogits_kernel(DlArgs p) {
 }
 
 // ---------------------------------------------------------------------------
-// backward 2: grad_hidden[n][d] = sum_v dl[n][v] W[v][d] as C^T = W^T . dl^T
+// backward 2: grad_hidden[n][d] = sum_v dl[n][v] W[v][d] as C^T = W^T . dl^T,
+// W read in place as a K-strided operand (its rows are the contraction
+// index).  With `ksplit` > 1 the vocabulary is cut into ksplit ranges of
+// whole stages; range s of every tile writes fp32 partial sums to
+// part[s][n][d] and grad_hidden_reduce_kernel adds them in range order.
 // ---------------------------------------------------------------------------
 struct DhArgs {
-  const bf16* wt;   // [dim][ldt]
-  int64_t ldt;
+  const bf16* w;    // [vocab][ldw]
+  int64_t ldw;
   const bf16* dl;   // [rows][ldl]
   int64_t ldl;
-  int rows, dim, kdim;  // kdim = padded vocab
-  int n_ttiles, n_dtiles;
+  int rows, dim, vocab;
+  int n_ttiles, n_dtiles, ksplit, kper;  // kper: vocabulary per range (multiple of TK)
   bf16* dh;
   int64_t ldd;
+  float* part;      // [ksplit][rows][dim] when ksplit > 1
 };
 
 __global__ __launch_bounds__(kGemmThreads, 1) void grad_hidden_kernel(DhArgs p) {
   LP_RING
-  const int total = p.n_ttiles * p.n_dtiles;
+  const int tiles = p.n_ttiles * p.n_dtiles;
+  const int total = tiles * p.ksplit;
+  const int id = xcd_logical(blockIdx.x, total);
+  const int ks = id / tiles;  // vocabulary range: tiles of one range run together
   int dt, tt;
-  grouped_tile(xcd_logical(blockIdx.x, total), p.n_dtiles, p.n_ttiles, dt, tt);
+  grouped_tile(id - ks * tiles, p.n_dtiles, p.n_ttiles, dt, tt);
   const int d0 = dt * TM, n0 = tt * TN;
+  const int kb = ks * p.kper, ke = min(p.vocab, kb + p.kper);
   f32x16 acc[4][NI];
-  gemm_tile(acc, p.wt + (int64_t)d0 * p.ldt, p.ldt, min(TM, p.dim - d0), p.dl + (int64_t)n0 * p.ldl,
-            p.ldl, min(TN, p.rows - n0), p.kdim, s0, s1, s2, s3);
+  gemm_tile<true, false>(acc, p.w + (int64_t)kb * p.ldw + d0, p.ldw, p.dim - d0, p.dl + (int64_t)n0 * p.ldl + kb,
+                         p.ldl, min(TN, p.rows - n0), ke - kb, s0, s1, s2, s3);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave & 1, wn = wave >> 1;
 #pragma unroll
@@ -569,40 +677,93 @@ __global__ __launch_bounds__(kGemmThreads, 1) void grad_hidden_kernel(DhArgs p) 
 #pragma unroll
       for (int i4 = 0; i4 < 4; ++i4) {
         const int d = d0 + a_row(mi, 4 * i4, lane, wm);
-        if (d + 3 < p.dim) {
-          const u32x2 v = {pack_bf2(acc[mi][ni][4 * i4], acc[mi][ni][4 * i4 + 1]),
-                           pack_bf2(acc[mi][ni][4 * i4 + 2], acc[mi][ni][4 * i4 + 3])};
-          *reinterpret_cast<u32x2*>(p.dh + (int64_t)n * p.ldd + d) = v;
+        const float a[4] = {acc[mi][ni][4 * i4], acc[mi][ni][4 * i4 + 1], acc[mi][ni][4 * i4 + 2],
+                            acc[mi][ni][4 * i4 + 3]};
+        if (p.ksplit > 1) {
+          float* q = p.part + ((int64_t)ks * p.rows + n) * p.dim + d;
+          if (d + 3 < p.dim) {
+            *reinterpret_cast<f32x4*>(q) = f32x4{a[0], a[1], a[2], a[3]};
+          } else {
+            for (int j = 0; j < 4; ++j)
+              if (d + j < p.dim) q[j] = a[j];
+          }
+        } else if (d + 3 < p.dim) {
+          *reinterpret_cast<u32x2*>(p.dh + (int64_t)n * p.ldd + d) = u32x2{pack_bf2(a[0], a[1]), pack_bf2(a[2], a[3])};
         } else {
           for (int j = 0; j < 4; ++j)
-            if (d + j < p.dim) p.dh[(int64_t)n * p.ldd + d + j] = from_f<bf16>(acc[mi][ni][4 * i4 + j]);
+            if (d + j < p.dim) p.dh[(int64_t)n * p.ldd + d + j] = from_f<bf16>(a[j]);
         }
       }
   }
 }
 
-// W [vocab][dim] -> W^T [dim][ld] with columns [vocab, ld) zero.  A thread
-// moves an 8 x 8 block through registers: eight 16-byte row loads, an
-// in-register transpose, eight 16-byte column stores.  A work-group covers 64
-// vocabulary rows x 256 dims; lane (td = t >> 3, tv = t & 7) takes rows
-// 8 tv .. 8 tv + 7 and dims 8 td .. 8 td + 7, so every load and every store
-// instruction of a wave covers 128 contiguous bytes in each of 8 rows.
-// Needs dim % 8 == 0, ld % 8 == 0 and 16-byte aligned rows.
-__global__ __launch_bounds__(kThreads) void transpose_kernel(const bf16* __restrict__ w, int64_t ldw,
-                                                             int vocab, int dim, bf16* __restrict__ wt,
-                                                             int64_t ldt) {
-  const int t = threadIdx.x, tv = t & 7, td = t >> 3;
-  const int64_t v0 = (int64_t)blockIdx.x * 64 + 8 * tv;
-  const int d0 = blockIdx.y * 256 + 8 * td;
-  if (d0 >= dim || v0 >= ldt) return;
-  u32x4 in[8], out[8];
+// dh = bf16(sum_s part[s]) in range order; four elements per thread
+__global__ __launch_bounds__(kThreads) void grad_hidden_reduce_kernel(const float* __restrict__ part, int ksplit,
+                                                                      int rows, int dim, bf16* __restrict__ dh,
+                                                                      int64_t ldd) {
+  const int64_t e = ((int64_t)blockIdx.x * kThreads + threadIdx.x) * 4;
+  const int64_t total = (int64_t)rows * dim;
+  if (e >= total) return;
+  const int64_t n = e / dim;
+  const int d = (int)(e - n * dim);
+  f32x4 s = *reinterpret_cast<const f32x4*>(part + e);
+  for (int k = 1; k < ksplit; ++k) s += *reinterpret_cast<const f32x4*>(part + (int64_t)k * total + e);
+  *reinterpret_cast<u32x2*>(dh + n * ldd + d) = u32x2{pack_bf2(s[0], s[1]), pack_bf2(s[2], s[3])};
+}
+
+// ---------------------------------------------------------------------------
+// backward 3 (trainable head): grad_weight[v][d] += sum_n dl[n][v] h[n][d] in
+// fp32, as C = dl^T . h with both operands K-strided (K = the block's rows);
+// the epilogue adds the tile into the fp32 accumulator, so a call per block
+// accumulates across blocks in block order.
+// ---------------------------------------------------------------------------
+struct DwArgs {
+  const bf16* dl;   // [rows][ldl]
+  int64_t ldl;
+  const bf16* h;    // [rows][ldh]
+  int64_t ldh;
+  int rows, dim, vocab;
+  int n_vtiles, n_dtiles;
+  float* gw;        // [vocab][ldg]
+  int64_t ldg;
+};
+
+__global__ __launch_bounds__(kGemmThreads, 1) void grad_weight_kernel(DwArgs p) {
+  LP_RING
+  const int total = p.n_vtiles * p.n_dtiles;
+  int vt, dt;
+  grouped_tile(xcd_logical(blockIdx.x, total), p.n_vtiles, p.n_dtiles, vt, dt);
+  const int v0 = vt * TM, d0 = dt * TN;
+  f32x16 acc[4][NI];
+  gemm_tile<true, true>(acc, p.dl + v0, p.ldl, p.vocab - v0, p.h + d0, p.ldh, p.dim - d0, p.rows, s0, s1, s2,
+                        s3);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave & 1, wn = wave >> 1;
 #pragma unroll
-  for (int r = 0; r < 8; ++r)
-    in[r] = v0 + r < vocab ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(w + (v0 + r) * ldw + d0))
-                           : u32x4{0u, 0u, 0u, 0u};  // W is read once here: non-temporal
-  transpose8x8(in, out);
+  for (int ni = 0; ni < NI; ++ni) {
+    const int d = d0 + 64 * wn + 32 * ni + (lane & 31);
+    if (d >= p.dim) continue;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) *reinterpret_cast<u32x4*>(wt + (int64_t)(d0 + e) * ldt + v0) = out[e];
+    for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int v = v0 + a_row(mi, i, lane, wm);
+        if (v < p.vocab) p.gw[(int64_t)v * p.ldg + d] += acc[mi][ni][i];
+      }
+  }
+}
+
+// ksplit (vocabulary ranges) for grad_hidden: one work-group per CU when the
+// row tiles alone do not give them, each range at least 4096 vocabulary rows
+inline void grad_hidden_split(int64_t rows, int64_t dim, int64_t vocab, int& ksplit, int& kper) {
+  const int64_t tiles = ((rows + TN - 1) / TN) * ((dim + TM - 1) / TM);
+  int64_t k = (256 + tiles - 1) / tiles;
+  k = std::min<int64_t>(k, std::max<int64_t>(1, vocab / 4096));
+  k = std::max<int64_t>(1, std::min<int64_t>(k, 16));
+  int64_t per = (vocab + k - 1) / k;
+  per = (per + TK - 1) / TK * TK;
+  ksplit = (int)((vocab + per - 1) / per);
+  kper = (int)per;
 }
 
 bool ok16(const void* p) { return ((uintptr_t)p & 15) == 0; }
@@ -667,22 +828,6 @@ int ts_logprob_fwd(const void* hidden, int64_t ld_hidden, const void* weight, in
   return ts::check_launch("ts_logprob_fwd (combine)");
 }
 
-int ts_logprob_weight_t(const void* weight, int64_t ld_weight, int64_t vocab, int64_t dim,
-                        void* weight_t, int64_t ld_t, void* stream) {
-  using namespace ts::lp;
-  TS_CHECK_ARG(weight && weight_t && vocab > 0 && dim > 0 && ld_weight >= dim && ld_t >= vocab &&
-                   ld_t % 8 == 0 && vocab < (1 << 30) && dim < (1 << 20),
-               "ts_logprob_weight_t: bad arguments vocab=%lld dim=%lld ld_t=%lld", (long long)vocab,
-               (long long)dim, (long long)ld_t);
-  TS_CHECK_ARG(dim % 8 == 0 && ld_weight % 8 == 0 && ok16(weight) && ok16(weight_t),
-               "ts_logprob_weight_t: alignment (16 bytes, dim and ld_weight %% 8)");
-  const dim3 grid((unsigned)((ld_t + 63) / 64), (unsigned)((dim + 255) / 256));
-  { ts::TimedLaunch timed_("logprob.transpose_kernel", (hipStream_t)stream); hipLaunchKernelGGL(transpose_kernel, grid, dim3(kThreads), 0, (hipStream_t)stream,
-                     (const ts::bf16*)weight, ld_weight, (int)vocab, (int)dim, (ts::bf16*)weight_t,
-                     ld_t); }
-  return ts::check_launch("ts_logprob_weight_t");
-}
-
 int ts_logprob_dlogits(const void* hidden, int64_t ld_hidden, const void* weight, int64_t ld_weight,
                        const int64_t* target, const float* lse, const float* entropy,
                        const float* grad_lp, const float* grad_ent, int64_t rows, int64_t dim,
@@ -722,34 +867,94 @@ int ts_logprob_dlogits(const void* hidden, int64_t ld_hidden, const void* weight
   return ts::check_launch("ts_logprob_dlogits");
 }
 
-int ts_logprob_grad_hidden(const void* dlogits, int64_t ld_dlogits, const void* weight_t,
-                           int64_t ld_t, int64_t rows, int64_t dim, int64_t vocab_padded,
-                           void* grad_hidden, int64_t ld_grad, void* stream) {
+int64_t ts_logprob_grad_hidden_workspace(int64_t rows, int64_t dim, int64_t vocab) {
+  if (rows <= 0 || dim <= 0 || vocab <= 0) return 0;
+  int ksplit, kper;
+  ts::lp::grad_hidden_split(rows, dim, vocab, ksplit, kper);
+  return ksplit > 1 ? (int64_t)ksplit * rows * dim * (int64_t)sizeof(float) : 0;
+}
+
+int ts_logprob_grad_hidden(const void* dlogits, int64_t ld_dlogits, const void* weight, int64_t ld_weight,
+                           int64_t rows, int64_t dim, int64_t vocab, void* grad_hidden, int64_t ld_grad,
+                           void* workspace, int64_t workspace_bytes, void* stream) {
   using namespace ts::lp;
-  TS_CHECK_ARG(rows >= 0 && dim > 0 && vocab_padded > 0 && vocab_padded % 8 == 0 &&
-                   rows < (1 << 30) && dim < (1 << 20) && vocab_padded < (1 << 30),
+  TS_CHECK_ARG(rows >= 0 && dim > 0 && vocab > 0 && rows < (1 << 30) && dim < (1 << 20) && vocab < (1 << 30),
                "ts_logprob_grad_hidden: bad shape");
   if (rows == 0) return TS_OK;
-  TS_CHECK_ARG(dlogits && weight_t && grad_hidden && ok16(dlogits) && ok16(weight_t) &&
-                   ld_dlogits % 8 == 0 && ld_t % 8 == 0 && ld_dlogits >= vocab_padded &&
-                   ld_t >= vocab_padded && ld_grad >= dim && ld_grad % 8 == 0 &&
-                   ok16(grad_hidden),
+  TS_CHECK_ARG(dlogits && weight && grad_hidden && ok16(dlogits) && ok16(weight) && ok16(grad_hidden) &&
+                   ld_dlogits % 8 == 0 && ld_weight % 8 == 0 && ld_grad % 8 == 0 && dim % 8 == 0 &&
+                   ld_dlogits >= (vocab + 7) / 8 * 8 && ld_weight >= dim && ld_grad >= dim,
                "ts_logprob_grad_hidden: alignment or leading dimensions");
+  TS_CHECK_ARG(255 * ld_dlogits < (1ll << 30) && 31 * ld_weight < (1ll << 30),
+               "ts_logprob_grad_hidden: leading dimensions too large for 32-bit tile offsets");
   DhArgs a;
-  a.wt = (const ts::bf16*)weight_t;
-  a.ldt = ld_t;
+  a.w = (const ts::bf16*)weight;
+  a.ldw = ld_weight;
   a.dl = (const ts::bf16*)dlogits;
   a.ldl = ld_dlogits;
   a.rows = (int)rows;
   a.dim = (int)dim;
-  a.kdim = (int)vocab_padded;
+  a.vocab = (int)vocab;
   a.n_ttiles = (int)((rows + TN - 1) / TN);
   a.n_dtiles = (int)((dim + TM - 1) / TM);
+  grad_hidden_split(rows, dim, vocab, a.ksplit, a.kper);
   a.dh = (ts::bf16*)grad_hidden;
   a.ldd = ld_grad;
-  { ts::TimedLaunch timed_("logprob.grad_hidden_kernel", (hipStream_t)stream); hipLaunchKernelGGL(grad_hidden_kernel, dim3((unsigned)(a.n_ttiles * a.n_dtiles)), dim3(kGemmThreads),
-                     0, (hipStream_t)stream, a); }
-  return ts::check_launch("ts_logprob_grad_hidden");
+  a.part = (float*)workspace;
+  if (a.ksplit > 1)
+    TS_CHECK_ARG(workspace && workspace_bytes >= ts_logprob_grad_hidden_workspace(rows, dim, vocab) &&
+                     ok16(workspace),
+                 "ts_logprob_grad_hidden: workspace of %lld bytes, need %lld", (long long)workspace_bytes,
+                 (long long)ts_logprob_grad_hidden_workspace(rows, dim, vocab));
+  hipStream_t s = (hipStream_t)stream;
+  {
+    ts::TimedLaunch timed_("logprob.grad_hidden_kernel", s);
+    hipLaunchKernelGGL(grad_hidden_kernel, dim3((unsigned)(a.n_ttiles * a.n_dtiles * a.ksplit)), dim3(kGemmThreads),
+                       0, s, a);
+  }
+  int st = ts::check_launch("ts_logprob_grad_hidden");
+  if (st != TS_OK || a.ksplit == 1) return st;
+  const int64_t quads = rows * dim / 4;
+  {
+    ts::TimedLaunch timed_("logprob.grad_hidden_reduce_kernel", s);
+    hipLaunchKernelGGL(grad_hidden_reduce_kernel, dim3((unsigned)((quads + kThreads - 1) / kThreads)), dim3(kThreads),
+                       0, s, (const float*)workspace, a.ksplit, (int)rows, (int)dim, (ts::bf16*)grad_hidden, ld_grad);
+  }
+  return ts::check_launch("ts_logprob_grad_hidden (reduce)");
+}
+
+int ts_logprob_grad_weight(const void* dlogits, int64_t ld_dlogits, const void* hidden, int64_t ld_hidden,
+                           int64_t rows, int64_t dim, int64_t vocab, float* grad_weight, int64_t ld_grad,
+                           void* stream) {
+  using namespace ts::lp;
+  TS_CHECK_ARG(rows >= 0 && dim > 0 && vocab > 0 && rows < (1 << 30) && dim < (1 << 20) && vocab < (1 << 30),
+               "ts_logprob_grad_weight: bad shape");
+  if (rows == 0) return TS_OK;
+  TS_CHECK_ARG(dlogits && hidden && grad_weight && ok16(dlogits) && ok16(hidden) && ld_dlogits % 8 == 0 &&
+                   ld_hidden % 8 == 0 && dim % 8 == 0 && ld_dlogits >= vocab && ld_hidden >= dim &&
+                   ld_grad >= dim,
+               "ts_logprob_grad_weight: alignment or leading dimensions");
+  TS_CHECK_ARG(31 * ld_dlogits < (1ll << 30) && 31 * ld_hidden < (1ll << 30),
+               "ts_logprob_grad_weight: leading dimensions too large for 32-bit tile offsets");
+  DwArgs a;
+  a.dl = (const ts::bf16*)dlogits;
+  a.ldl = ld_dlogits;
+  a.h = (const ts::bf16*)hidden;
+  a.ldh = ld_hidden;
+  a.rows = (int)rows;
+  a.dim = (int)dim;
+  a.vocab = (int)vocab;
+  a.n_vtiles = (int)((vocab + TM - 1) / TM);
+  a.n_dtiles = (int)((dim + TN - 1) / TN);
+  a.gw = grad_weight;
+  a.ldg = ld_grad;
+  TS_CHECK_ARG((int64_t)a.n_vtiles * a.n_dtiles < (1ll << 31), "ts_logprob_grad_weight: grid too large");
+  {
+    ts::TimedLaunch timed_("logprob.grad_weight_kernel", (hipStream_t)stream);
+    hipLaunchKernelGGL(grad_weight_kernel, dim3((unsigned)(a.n_vtiles * a.n_dtiles)), dim3(kGemmThreads), 0,
+                       (hipStream_t)stream, a);
+  }
+  return ts::check_launch("ts_logprob_grad_weight");
 }
 
 }  // extern "C"

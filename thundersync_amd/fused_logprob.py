@@ -10,13 +10,16 @@ them in the GEMM epilogue; no ``[N, V]`` or ``[chunk, V]`` logit block is
 ever stored.  It returns logprob, entropy and the per-row log-sum-exp, which
 the backward reuses instead of recomputing the row statistics.
 
-Backward: ``ts_logprob_dlogits`` recomputes the logits and writes bf16
-dlogits for a block of rows (rounded to bf16 as the reference rounds its
-dlogits to the hidden dtype, fused_logprob.py:165 and :295);
-``ts_logprob_grad_hidden`` multiplies them by the weight (read through a
-transposed copy made once per backward call).  The block is
-``max(chunk, 4096)`` rows, so peak memory stays ``O(block * V)`` as in the
-reference, independent of N.
+Backward, per block of ``chunk`` rows (the reference's chunk loop,
+FL:143-193, with its O(chunk * V) memory): ``ts_logprob_dlogits`` recomputes
+the logits and writes the block's bf16 dlogits (rounded to bf16 as the
+reference rounds its dlogits to the hidden dtype, FL:165 and :295);
+``ts_logprob_grad_hidden`` multiplies them by the weight, read in place;
+when the head is trainable ``ts_logprob_grad_weight`` adds ``dl^T h`` into
+an fp32 accumulator, cast once at the end (FL:176-193).  Extra device memory
+is the ``[chunk, V]`` bf16 dlogits block plus a workspace of vocabulary-range
+partial sums for grad_hidden when one block's row tiles do not fill the GPU,
+and the fp32 ``[V, D]`` accumulator when the weight gradient is needed.
 
 bf16 only, GPU only: other dtypes and CPU tensors raise.
 """
@@ -27,8 +30,6 @@ import torch
 
 from . import _lib
 from .operator_profiling import device_role, operator_range
-
-MIN_BACKWARD_ROWS = 4096
 
 
 def _validate(hidden: torch.Tensor, weight: torch.Tensor, target: torch.Tensor) -> None:
@@ -81,6 +82,16 @@ def _forward(hidden, weight, target, with_entropy):
     return lp, ent, lse
 
 
+def backward_block_rows(n: int, chunk: int) -> int:
+    """Rows per dlogits block: ``chunk`` (at least one row), rounded down to a
+    multiple of 256 (whole GEMM tiles) when that stays positive, and never more
+    than the rows there are."""
+    block = max(1, int(chunk))
+    if block >= 256:
+        block -= block % 256
+    return min(block, max(n, 1))
+
+
 def _backward(hidden, weight, target, lse, ent, grad_lp, grad_ent, chunk, needs_weight_grad):
     lib = _lib.require_library()
     d_in = hidden.shape[1]
@@ -94,13 +105,10 @@ def _backward(hidden, weight, target, lse, ent, grad_lp, grad_ent, chunk, needs_
     if n == 0:
         return grad_hidden[:, :d_in], (grad_weight[:, :d_in].to(weight.dtype) if grad_weight is not None else None)
     stream = _lib.stream_of(h)
-    wt = torch.empty(d, vp, dtype=w.dtype, device=w.device)
-    _lib.check(lib.ts_logprob_weight_t(w.data_ptr(), w.stride(0), v, d, wt.data_ptr(), vp, stream),
-               f"ts_logprob_weight_t(vocab={v}, dim={d})")
-    block = max(int(chunk), MIN_BACKWARD_ROWS)
-    block = (block + 127) // 128 * 128
-    block = min(block, (n + 127) // 128 * 128)
+    block = backward_block_rows(n, chunk)
     dl = torch.empty(block, vp, dtype=w.dtype, device=w.device)
+    ws_bytes = int(lib.ts_logprob_grad_hidden_workspace(block, d, v))
+    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=h.device)
     g_lp = grad_lp.to(torch.float32).contiguous()
     g_ent = grad_ent.to(torch.float32).contiguous() if grad_ent is not None else None
     for i in range(0, n, block):
@@ -119,15 +127,21 @@ def _backward(hidden, weight, target, lse, ent, grad_lp, grad_ent, chunk, needs_
         with operator_range("logprob_head_hidden_vjp", role=device_role(h.device), rows=rows, hidden=d, vocab=v):
             _lib.check(
                 lib.ts_logprob_grad_hidden(
-                    dl.data_ptr(), vp, wt.data_ptr(), vp, rows, d, vp,
-                    grad_hidden[i:].data_ptr(), grad_hidden.stride(0), stream,
+                    dl.data_ptr(), vp, w.data_ptr(), w.stride(0), rows, d, v,
+                    grad_hidden[i:].data_ptr(), grad_hidden.stride(0), ws.data_ptr(), ws_bytes, stream,
                 ),
                 f"ts_logprob_grad_hidden(rows={rows}, dim={d}, vocab={v})",
             )
         if grad_weight is not None:
-            # fp32 accumulation across blocks, cast once (fused_logprob.py:176-193)
+            # fp32 accumulation across blocks, cast once (FL:176-193)
             with operator_range("logprob_head_weight_vjp", role=device_role(h.device), rows=rows, hidden=d, vocab=v):
-                grad_weight.add_(torch.mm(dl[:rows, :v].t(), hi, out_dtype=torch.float32))
+                _lib.check(
+                    lib.ts_logprob_grad_weight(
+                        dl.data_ptr(), vp, hi.data_ptr(), h.stride(0), rows, d, v,
+                        grad_weight.data_ptr(), grad_weight.stride(0), stream,
+                    ),
+                    f"ts_logprob_grad_weight(rows={rows}, dim={d}, vocab={v})",
+                )
     if d != d_in:
         grad_hidden = grad_hidden[:, :d_in].contiguous()
         grad_weight = grad_weight[:, :d_in] if grad_weight is not None else None
