@@ -189,6 +189,25 @@ int ts_attn_q_block(int group);
  * group (one wave per query head), else 64. */
 int ts_attn_kv_block(int group);
 
+/* Host-side consistency check of a problem's tables, given as host copies
+ * of the arrays the problem's device pointers name (those pointers are not
+ * read): segment rows inside [0, q_rows) and kv_len >= q_len; each
+ * segment's spans tile its keys in order over runs that exist; every run
+ * non-empty, its K/V (and dK/dV, when set) 16-byte aligned with strides
+ * that are multiples of 8 (row strides below 2^24), its visits in range and
+ * each one a span of the segment it names, as many visits as spans; the work
+ * lists hold every row block (q_block) of every segment and every key block
+ * (kv_block) of every visited run exactly once; the long-item counts within
+ * the lists.  TS_OK, or TS_ERR_INVALID naming the first inconsistency.  The
+ * entry points trust the device tables; the Python layer runs this check
+ * on every call's tables before they are uploaded.  No counterpart in the
+ * reference (its tables are torch tensors checked by the flash kernels'
+ * own argument checks). */
+int ts_attn_check_tables(const ts_attn_problem* problem, const ts_attn_segment* segs,
+                         const ts_attn_ref* seg_spans, int64_t n_spans, const ts_attn_run* runs,
+                         const ts_attn_ref* run_visits, int64_t n_visits, const int32_t* q_work,
+                         const int32_t* kv_work);
+
 typedef struct ts_attn_rows {
   uint64_t ptr; /* device address of row 0, head 0 */
   int64_t row_stride;
@@ -224,7 +243,10 @@ int ts_attn_bwd(const ts_attn_problem* problem, ts_attn_rows q, ts_attn_rows out
  *
  * hidden [rows, dim] (row stride ld_hidden), weight [vocab, dim] (ld_weight),
  * target int64 [rows].  dim and both leading dimensions are multiples of 8
- * and the bases 16-byte aligned.
+ * and the bases 16-byte aligned; leading dimensions are below 2^30 / 255
+ * elements (a 256-row tile's byte offsets fit 32 bits).  A target outside
+ * [0, vocab) is not an error: its logprob is NaN and its dlogits row takes
+ * no one-hot term.
  * ------------------------------------------------------------------------ */
 
 /* Workspace bytes ts_logprob_fwd needs. */

@@ -353,3 +353,27 @@ def test_cpu_and_dtype_refused():
     k = torch.randn(8, 2, D, dtype=torch.bfloat16)
     with pytest.raises(RuntimeError, match="GPU only"):
         hip.causal_attention(q, [k], [k], 0.1)
+
+
+def test_dispatch_trial_and_path_counts(cuda, monkeypatch):
+    """Under auto, the HIP attention is taken after a device trial whose record
+    names the gfx950 device; every forward and backward launch is counted."""
+    from thundersync_amd import _lib, capability, dispatch
+
+    monkeypatch.setenv(_lib.HIP_ENV, "auto")
+    _lib.reset()
+    capability.reset_kernel_probes()
+    q = torch.randn(1, 8, 40, D, device=cuda, dtype=torch.bfloat16)
+    assert dispatch.hip_attention_available(q)
+    assert dispatch.hip_logprob_available(torch.randn(4, 256, device=cuda, dtype=torch.bfloat16))
+    records = {r["kernel"]: r for r in capability.kernel_probe_records()}
+    assert records["hip_attention"]["runs"] and records["hip_logprob"]["runs"], records
+    assert str(records["hip_attention"]["device"]["arch"]).startswith("gfx950")
+    assert not dispatch.hip_attention_available(q.float())
+    before = dispatch.attention_path_counts()
+    k = torch.randn(40, 2, D, device=cuda, dtype=torch.bfloat16, requires_grad=True)
+    qq = q.clone().requires_grad_()
+    hip.causal_attention(qq, [k], [k], D ** -0.5).float().sum().backward()
+    after = dispatch.attention_path_counts()
+    assert after.get("hip", 0) == before.get("hip", 0) + 1
+    assert after.get("hip_backward", 0) == before.get("hip_backward", 0) + 1

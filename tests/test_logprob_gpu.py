@@ -139,6 +139,17 @@ def test_out_of_range_targets_match_no_vocabulary_row(cuda):
     assert torch.equal(grads[0], grads[1]) and torch.equal(grads[0], grads[2])
 
 
+def test_target_check_names_the_row(cuda, monkeypatch):
+    h = torch.randn(6, 8, dtype=torch.bfloat16, device=cuda)
+    w = torch.randn(16, 8, dtype=torch.bfloat16, device=cuda)
+    t = torch.tensor([1, 2, 3, 16, 0, -1], device=cuda)
+    monkeypatch.setenv(hip.CHECK_TARGETS_ENV, "1")
+    with pytest.raises(ValueError, match=r"target\[3\] = 16 is outside the vocabulary \[0, 16\)"):
+        hip.fused_logprob(h, w, t)
+    monkeypatch.setenv(hip.CHECK_TARGETS_ENV, "0")
+    assert torch.isnan(hip.fused_logprob(h, w, t)[3]).item()
+
+
 def test_validation_errors(cuda):
     h = torch.randn(4, 8, dtype=torch.bfloat16, device=cuda)
     w = torch.randn(16, 8, dtype=torch.bfloat16, device=cuda)

@@ -34,3 +34,56 @@ def test_split_by_trajectory_keeps_each_trajectorys_order():
     assert [per[t].numel() for t in range(3)] == [3, 4, 1]
     # logical order is trajectory by trajectory, so each piece is a contiguous run
     assert torch.equal(torch.cat([per[t] for t in range(3)]), logical)
+
+
+def test_assert_supported_refuses_recurrent_layers():
+    from transformers import Qwen3Config, Qwen3ForCausalLM
+
+    from thundersync_amd.step import assert_supported
+
+    cfg = Qwen3Config(vocab_size=32, hidden_size=64, intermediate_size=96, num_hidden_layers=2,
+                      num_attention_heads=2, num_key_value_heads=1, head_dim=32)
+    model = Qwen3ForCausalLM(cfg)
+    assert_supported(model)  # plain attention stack: accepted (and memoised)
+    assert_supported(model)
+    hybrid = Qwen3ForCausalLM(cfg)
+    hybrid.config.layer_types = ["full_attention", "linear_attention"]
+    with pytest.raises(NotImplementedError, match="non-attention layer types"):
+        assert_supported(hybrid)
+
+    class MambaMixer(torch.nn.Module):
+        pass
+
+    recurrent = Qwen3ForCausalLM(cfg)
+    recurrent.model.layers[0].extra = MambaMixer()
+    with pytest.raises(NotImplementedError, match="recurrent state"):
+        assert_supported(recurrent)
+
+
+def test_forest_logprobs_stats_without_a_device(monkeypatch):
+    """The gated and ungated projections and their accounting, with the
+    hidden states and the fused projection stood in for on the CPU."""
+    from thundersync_amd import step
+
+    trajs = [forest.Trajectory([forest.Segment.prompt([1, 2, 3]), forest.Segment.action(body)], group_id=0, traj_id=t)
+             for t, body in enumerate(([4, 5, 6], [4, 5, 7, 8], [9]))]
+    plan = forest.compile_plan(forest.build_forest(trajs))
+    calls = []
+
+    def fake_fused(h, w, t, chunk=1024):
+        calls.append(int(h.shape[0]))
+        return (h[:, 0] * 1000 + t).float()  # identifies (source row, target)
+
+    monkeypatch.setattr(step, "fused_logprob", fake_fused)
+    monkeypatch.setattr(step, "forest_context", lambda plan: __import__("contextlib").nullcontext())
+    hidden = torch.arange(plan.n_physical, dtype=torch.float32)[:, None].repeat(1, 4)
+    model = torch.nn.Linear(4, 4)
+    gated, stats = step.forest_logprobs(model, plan, weight=torch.zeros(16, 4), hidden_fn=lambda i, p: hidden,
+                                        return_stats=True)
+    ungated = step.forest_logprobs(model, plan, weight=torch.zeros(16, 4), hidden_fn=lambda i, p: hidden, gate=False)
+    assert torch.equal(gated, ungated)
+    want = (plan.score_src.float() * 1000 + plan.score_tgt.float()).index_select(0, plan.logical_to_slot)
+    assert torch.equal(gated, want)
+    assert stats.physical_tokens == plan.n_physical and stats.logical_tokens == 3 * 3 + 3 + 4 + 1
+    assert stats.padded_tokens == 3 * 7 and stats.projected_positions == plan.score_src.numel()
+    assert calls[0] == plan.score_src.numel() and calls[1] == plan.n_physical

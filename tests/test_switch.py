@@ -69,3 +69,91 @@ def test_require_with_the_library_resolves_once(unresolved, monkeypatch):
     lib = _lib.library()
     assert lib is not None and _lib.library() is lib
     assert _lib.hip_build().startswith("thundersync_hip")
+
+
+# -- trial-gated dispatch and path counters (engine/streaming.py:355-373, 532-548) --
+
+class _FakeCuda:
+    def __init__(self, dtype, head_dim=128, index=0):
+        import torch
+
+        self.is_cuda = True
+        self.dtype = dtype
+        self.device = torch.device("cuda", index)
+        self.shape = (1, 4, 8, head_dim)
+
+
+@pytest.fixture
+def trial_recorder(monkeypatch):
+    from thundersync_amd import capability, dispatch
+
+    calls = []
+
+    def fake_runs(kernel, like, key, trial):
+        calls.append((kernel, like.device.index, str(like.dtype), key))
+        return like.device.index != 1  # "device 1" fails its trial
+
+    monkeypatch.setattr(dispatch, "kernel_runs", fake_runs)
+    capability.reset_kernel_probes()
+    return calls
+
+
+def test_auto_takes_the_kernels_only_after_a_device_trial(unresolved, monkeypatch, trial_recorder):
+    import torch
+
+    from thundersync_amd import dispatch
+
+    monkeypatch.delenv(_lib.HIP_ENV, raising=False)
+    assert dispatch.hip_attention_available(_FakeCuda(torch.bfloat16))
+    assert trial_recorder == [("hip_attention", 0, "torch.bfloat16", 128)]
+    assert not dispatch.hip_attention_available(_FakeCuda(torch.bfloat16, index=1))
+    # other dtypes and head dims never reach a trial
+    assert not dispatch.hip_attention_available(_FakeCuda(torch.float16))
+    assert not dispatch.hip_attention_available(_FakeCuda(torch.bfloat16, head_dim=64))
+    assert len(trial_recorder) == 2
+    assert dispatch.hip_logprob_available(_FakeCuda(torch.bfloat16))
+    assert trial_recorder[-1] == ("hip_logprob", 0, "torch.bfloat16", 128)
+
+
+def test_require_skips_the_trial_and_off_never_loads(unresolved, monkeypatch, trial_recorder):
+    import torch
+
+    from thundersync_amd import dispatch
+
+    monkeypatch.setenv(_lib.HIP_ENV, "require")
+    assert dispatch.hip_attention_available(_FakeCuda(torch.bfloat16, index=1))
+    assert trial_recorder == []
+    _lib.reset()
+    monkeypatch.setenv(_lib.HIP_ENV, "off")
+    monkeypatch.setattr(_lib, "_load", lambda: (_ for _ in ()).throw(AssertionError("loaded")))
+    assert not dispatch.hip_attention_available(_FakeCuda(torch.bfloat16))
+    assert trial_recorder == []
+
+
+def test_require_without_a_library_raises_at_the_dispatch(unresolved, monkeypatch, trial_recorder):
+    import torch
+
+    from thundersync_amd import dispatch
+
+    monkeypatch.setenv(_lib.HIP_ENV, "require")
+    monkeypatch.setattr(_lib, "_load", lambda: (_ for _ in ()).throw(OSError("not built")))
+    for _ in range(2):
+        with pytest.raises(RuntimeError, match="THUNDERSYNC_HIP=require"):
+            dispatch.hip_attention_available(_FakeCuda(torch.bfloat16))
+
+
+def test_attention_path_counts_are_cumulative_and_thread_safe():
+    import threading
+
+    from thundersync_amd import dispatch
+
+    dispatch.reset_attention_path_counts()
+    threads = [threading.Thread(target=lambda: [dispatch.count_attention_path("hip") for _ in range(500)])
+               for _ in range(4)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    dispatch.count_attention_path("hip_backward", 3)
+    assert dispatch.attention_path_counts() == {"hip": 2000, "hip_backward": 3}
+    dispatch.reset_attention_path_counts()

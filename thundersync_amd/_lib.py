@@ -64,6 +64,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "ts_attn_heads_per_block": (_INT, [_INT]),
     "ts_attn_kv_block": (_INT, [_INT]),
     "ts_attn_q_block": (_INT, [_INT]),
+    "ts_attn_check_tables": (_INT, [ctypes.POINTER(AttnProblem), _P, _P, _I64, _P, _P, _I64, _P, _P]),
     "ts_attn_fwd": (_INT, [ctypes.POINTER(AttnProblem), AttnRows, AttnRows, _P, _I64, _P]),
     "ts_attn_bwd": (
         _INT,
@@ -121,6 +122,11 @@ def library() -> ctypes.CDLL | None:
             lib = None
         _LIB, _SETTING, _RESOLVED = lib, setting, True
         return lib
+
+
+def resolved_setting() -> str | None:
+    """The setting the last completed resolution read, or None before one."""
+    return _SETTING
 
 
 def hip_build() -> str | None:

@@ -52,6 +52,7 @@ import torch
 
 from . import _lib
 from ._abi import REF_DTYPE, RUN_DTYPE, SEG_DTYPE, AttnProblem, AttnRows
+from .dispatch import HIP_BACKWARD_PATH, HIP_PATH, count_attention_path
 from .operator_profiling import operator_range
 
 HEAD_DIM = 128
@@ -228,6 +229,7 @@ class AttnLayout:
                 hit = {
                     "blob": dev,
                     "host": host,
+                    "arrays": (segs, spans, visits, q_work, kv_work),
                     "segs": base + offsets[0],
                     "seg_spans": base + offsets[1],
                     "run_visits": base + offsets[2],
@@ -329,6 +331,28 @@ def _run_table(layout: AttnLayout, keys, values, dkeys=None, dvalues=None) -> to
     return host.to(keys[0].device, non_blocking=True), host
 
 
+def check_tables(layout: AttnLayout, problem: AttnProblem, run_table: np.ndarray | torch.Tensor,
+                 device: torch.device) -> None:
+    """Check the layout's tables for ``device`` and one call's run table on the
+    host (ts_attn_check_tables) before the kernels read their device copies:
+    spans tile every segment's keys, every visit is a span of its segment,
+    the work lists hold every row and key block once, K/V/dK/dV addresses are
+    aligned.  Raises RuntimeError naming the first inconsistency."""
+    segs, spans, visits, q_work, kv_work = layout.device_tables(device)["arrays"]
+    runs = run_table.numpy() if isinstance(run_table, torch.Tensor) else run_table
+    runs = np.ascontiguousarray(runs).view(np.uint8)
+    if runs.size != len(layout.runs) * RUN_DTYPE.itemsize:
+        raise ValueError(f"run table holds {runs.size} bytes, expected {len(layout.runs)} runs")
+    arrays = (segs, spans, runs, visits, q_work, kv_work)
+    segs_p, spans_p, runs_p, visits_p, q_p, kv_p = (a.ctypes.data if a.size else None for a in arrays)
+    lib = _lib.require_library()
+    _lib.check(
+        lib.ts_attn_check_tables(ctypes.byref(problem), segs_p, spans_p, spans.shape[0], runs_p, visits_p,
+                                 visits.shape[0], q_p, kv_p),
+        f"attention tables (rows={layout.q_rows}, segments={len(layout.seg_q)}, runs={len(layout.runs)})",
+    )
+
+
 def _validate_call(layout: AttnLayout, query: torch.Tensor, keys, values) -> None:
     if not query.is_cuda:
         raise RuntimeError("thundersync_amd attention runs on the GPU only; got a CPU tensor")
@@ -360,12 +384,14 @@ class _Attention(torch.autograd.Function):
         lse = torch.empty(layout.hq, max(layout.q_rows, 1), dtype=torch.float32, device=query.device)
         runs, host = _run_table(layout, keys, values)
         problem = layout.problem(query.device, runs.data_ptr(), scale)
+        check_tables(layout, problem, host, query.device)
         with operator_range("hip_attention_forward", rows=layout.q_rows, segments=len(layout.seg_q)):
             _lib.check(
                 lib.ts_attn_fwd(ctypes.byref(problem), _rows(query), _rows(out), lse.data_ptr(),
                                 lse.shape[1], _lib.stream_of(query)),
                 f"ts_attn_fwd(rows={layout.q_rows}, hq={layout.hq}, hkv={layout.hkv})",
             )
+        count_attention_path(HIP_PATH)
         ctx.layout, ctx.scale, ctx.n_sources = layout, scale, n_sources
         ctx.keep = (runs, host)
         ctx.save_for_backward(query, out, lse, *kv)
@@ -399,6 +425,7 @@ class _Attention(torch.autograd.Function):
         runs, host = _run_table(layout, keys, values, dkeys, dvalues)
         rowstats = torch.empty(layout.hq, max(layout.q_rows, 1), 2, dtype=torch.float32, device=query.device)
         problem = layout.problem(query.device, runs.data_ptr(), ctx.scale)
+        check_tables(layout, problem, host, query.device)
         with operator_range("hip_attention_backward", rows=layout.q_rows, segments=len(layout.seg_q)):
             _lib.check(
                 lib.ts_attn_bwd(ctypes.byref(problem), _rows(query), _rows(out), _rows(dout),
@@ -406,6 +433,7 @@ class _Attention(torch.autograd.Function):
                                 _lib.stream_of(query)),
                 f"ts_attn_bwd(rows={layout.q_rows}, hq={layout.hq}, hkv={layout.hkv})",
             )
+        count_attention_path(HIP_BACKWARD_PATH)
         ctx.keep_bwd = (runs, host)
         return (dq, None, None, None, *dkeys, *dvalues)
 

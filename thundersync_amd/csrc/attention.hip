@@ -25,6 +25,8 @@
 //           registers); dV^T += dO^T P and dK^T += Q^T dS with dO^T / Q^T
 //           from LDS rows through the register transpose.
 // Both sides of every contraction use the same slot permutation of the
+#include <vector>
+
 #include "attention_impl.h"
 
 namespace ts {
@@ -106,6 +108,113 @@ int ts_attn_bwd(const ts_attn_problem* problem, ts_attn_rows q, ts_attn_rows out
   }
   if (P.n_kv_work > 0) st = launch_dkdv(P, q, dout, rowstats, lse_ld, s);
   return st;
+}
+
+int ts_attn_check_tables(const ts_attn_problem* problem, const ts_attn_segment* segs,
+                         const ts_attn_ref* seg_spans, int64_t n_spans, const ts_attn_run* runs,
+                         const ts_attn_ref* run_visits, int64_t n_visits, const int32_t* q_work,
+                         const int32_t* kv_work) {
+  using namespace ts::attn;
+  const char* what = "ts_attn_check_tables";
+  int st = validate(problem, what);
+  if (st != TS_OK) return st;
+  const ts_attn_problem& P = *problem;
+  TS_CHECK_ARG(n_spans >= 0 && n_visits >= 0 && (P.n_segs == 0 || (segs && (n_spans == 0 || seg_spans))) &&
+                   (P.n_runs == 0 || runs) && (n_visits == 0 || run_visits) && (P.n_q_work == 0 || q_work) &&
+                   (P.n_kv_work == 0 || kv_work),
+               "%s: null host table", what);
+  // runs: lengths, addressing, visit ranges
+  for (int32_t r = 0; r < P.n_runs; ++r) {
+    const ts_attn_run& u = runs[r];
+    TS_CHECK_ARG(u.len > 0, "%s: run %d has length %d", what, r, u.len);
+    TS_CHECK_ARG(u.k && u.v && u.k % 16 == 0 && u.v % 16 == 0 && u.k_row_stride > 0 && u.v_row_stride > 0 &&
+                     u.k_row_stride % 8 == 0 && u.v_row_stride % 8 == 0 && u.k_head_stride % 8 == 0 &&
+                     u.v_head_stride % 8 == 0 && u.k_row_stride < (1 << 24) && u.v_row_stride < (1 << 24),
+                 "%s: run %d K/V need 16-byte aligned rows, strides multiples of 8 below 2^24", what, r);
+    TS_CHECK_ARG((!u.dk || (u.dk % 16 == 0 && u.dk_row_stride % 8 == 0 && u.dk_head_stride % 8 == 0)) &&
+                     (!u.dv || (u.dv % 16 == 0 && u.dv_row_stride % 8 == 0 && u.dv_head_stride % 8 == 0)),
+                 "%s: run %d dK/dV need 16-byte aligned rows and strides multiples of 8", what, r);
+    TS_CHECK_ARG(u.visit0 >= 0 && u.nvisit >= 0 && (int64_t)u.visit0 + u.nvisit <= n_visits,
+                 "%s: run %d visits [%d, %d) outside the %lld visits", what, r, u.visit0, u.visit0 + u.nvisit,
+                 (long long)n_visits);
+  }
+  // segments and their spans: each span list tiles the segment's keys in order
+  int64_t q_blocks = 0;
+  for (int32_t s = 0; s < P.n_segs; ++s) {
+    const ts_attn_segment& g = segs[s];
+    TS_CHECK_ARG(g.q_row0 >= 0 && g.q_len >= 0 && g.q_row0 + g.q_len <= P.q_rows,
+                 "%s: segment %d rows [%lld, %lld) outside [0, %lld)", what, s, (long long)g.q_row0,
+                 (long long)(g.q_row0 + g.q_len), (long long)P.q_rows);
+    TS_CHECK_ARG(g.q_len == 0 || g.kv_len >= g.q_len, "%s: segment %d has %d rows over %d keys", what, s,
+                 g.q_len, g.kv_len);
+    TS_CHECK_ARG(g.span0 >= 0 && g.nspan >= 0 && (int64_t)g.span0 + g.nspan <= n_spans,
+                 "%s: segment %d spans [%d, %d) outside the %lld spans", what, s, g.span0, g.span0 + g.nspan,
+                 (long long)n_spans);
+    int64_t pos = 0;
+    for (int32_t i = 0; i < g.nspan; ++i) {
+      const ts_attn_ref& r = seg_spans[g.span0 + i];
+      TS_CHECK_ARG(r.index >= 0 && r.index < P.n_runs, "%s: segment %d span %d names run %d of %d", what, s, i,
+                   r.index, P.n_runs);
+      TS_CHECK_ARG(r.kpos == pos, "%s: segment %d span %d at key %d, expected %lld", what, s, i, r.kpos,
+                   (long long)pos);
+      pos += runs[r.index].len;
+    }
+    TS_CHECK_ARG(pos == g.kv_len, "%s: segment %d spans cover %lld keys, kv_len %d", what, s, (long long)pos,
+                 g.kv_len);
+    q_blocks += (g.q_len + P.q_block - 1) / P.q_block;
+  }
+  // visits that match the segments' spans one to one
+  int64_t visits = 0, kv_blocks = 0;
+  std::vector<char> span_seen(n_spans, 0);
+  for (int32_t r = 0; r < P.n_runs; ++r) {
+    const ts_attn_run& u = runs[r];
+    for (int32_t i = 0; i < u.nvisit; ++i) {
+      const ts_attn_ref& v = run_visits[u.visit0 + i];
+      TS_CHECK_ARG(v.index >= 0 && v.index < P.n_segs, "%s: run %d visit %d names segment %d of %d", what, r,
+                   i, v.index, P.n_segs);
+      const ts_attn_segment& g = segs[v.index];
+      int32_t j = 0;
+      while (j < g.nspan && !(seg_spans[g.span0 + j].index == r && seg_spans[g.span0 + j].kpos == v.kpos)) ++j;
+      TS_CHECK_ARG(j < g.nspan, "%s: run %d visit %d (segment %d, key %d) is not a span of that segment", what,
+                   r, i, v.index, v.kpos);
+      TS_CHECK_ARG(!span_seen[g.span0 + j], "%s: run %d visit %d repeats segment %d span %d", what, r, i, v.index,
+                   j);
+      span_seen[g.span0 + j] = 1;
+    }
+    visits += u.nvisit;
+    if (u.nvisit > 0) kv_blocks += (u.len + P.kv_block - 1) / P.kv_block;
+  }
+  int64_t spans_used = 0;
+  for (int32_t s = 0; s < P.n_segs; ++s) spans_used += segs[s].nspan;
+  TS_CHECK_ARG(visits == spans_used, "%s: %lld visits for %lld spans", what, (long long)visits,
+               (long long)spans_used);
+  // work lists: every row block and every visited run's key block exactly once
+  TS_CHECK_ARG(P.n_q_work == q_blocks && P.n_kv_work == kv_blocks,
+               "%s: %d forward items for %lld row blocks, %d dK/dV items for %lld key blocks", what, P.n_q_work,
+               (long long)q_blocks, P.n_kv_work, (long long)kv_blocks);
+  std::vector<int64_t> first_q(P.n_segs + 1, 0), first_k(P.n_runs + 1, 0);
+  for (int32_t s = 0; s < P.n_segs; ++s) first_q[s + 1] = first_q[s] + (segs[s].q_len + P.q_block - 1) / P.q_block;
+  for (int32_t r = 0; r < P.n_runs; ++r)
+    first_k[r + 1] = first_k[r] + (runs[r].nvisit > 0 ? (runs[r].len + P.kv_block - 1) / P.kv_block : 0);
+  std::vector<char> seen_q(q_blocks, 0), seen_k(kv_blocks, 0);
+  for (int32_t i = 0; i < P.n_q_work; ++i) {
+    const int32_t s = q_work[2 * i], q0 = q_work[2 * i + 1];
+    TS_CHECK_ARG(s >= 0 && s < P.n_segs && q0 >= 0 && q0 < segs[s].q_len && q0 % P.q_block == 0,
+                 "%s: forward item %d (segment %d, row %d) is not a row block", what, i, s, q0);
+    char& once = seen_q[first_q[s] + q0 / P.q_block];
+    TS_CHECK_ARG(!once, "%s: forward item %d repeats segment %d row %d", what, i, s, q0);
+    once = 1;
+  }
+  for (int32_t i = 0; i < P.n_kv_work; ++i) {
+    const int32_t r = kv_work[2 * i], k0 = kv_work[2 * i + 1];
+    TS_CHECK_ARG(r >= 0 && r < P.n_runs && runs[r].nvisit > 0 && k0 >= 0 && k0 < runs[r].len &&
+                     k0 % P.kv_block == 0,
+                 "%s: dK/dV item %d (run %d, key %d) is not a key block of a visited run", what, i, r, k0);
+    char& once = seen_k[first_k[r] + k0 / P.kv_block];
+    TS_CHECK_ARG(!once, "%s: dK/dV item %d repeats run %d key %d", what, i, r, k0);
+    once = 1;
+  }
+  return TS_OK;
 }
 
 }  // extern "C"

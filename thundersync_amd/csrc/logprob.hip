@@ -793,6 +793,8 @@ int ts_logprob_fwd(const void* hidden, int64_t ld_hidden, const void* weight, in
   TS_CHECK_ARG(dim % 8 == 0 && ld_hidden % 8 == 0 && ld_weight % 8 == 0 && ld_hidden >= dim &&
                    ld_weight >= dim && ok16(hidden) && ok16(weight),
                "ts_logprob_fwd: hidden/weight rows must be 16-byte aligned with dim %% 8 == 0");
+  TS_CHECK_ARG(255 * ld_hidden < (1ll << 30) && 255 * ld_weight < (1ll << 30),
+               "ts_logprob_fwd: leading dimensions too large for 32-bit tile offsets");
   TS_CHECK_ARG(workspace && workspace_bytes >= ts_logprob_fwd_workspace(rows, vocab),
                "ts_logprob_fwd: workspace of %lld bytes, need %lld", (long long)workspace_bytes,
                (long long)ts_logprob_fwd_workspace(rows, vocab));
@@ -843,6 +845,8 @@ int ts_logprob_dlogits(const void* hidden, int64_t ld_hidden, const void* weight
   TS_CHECK_ARG(dim % 8 == 0 && ld_hidden % 8 == 0 && ld_weight % 8 == 0 && ok16(hidden) &&
                    ok16(weight) && ok16(dlogits) && ld_dlogits % 8 == 0 && ld_dlogits >= vocab,
                "ts_logprob_dlogits: alignment (16 bytes, dims %% 8) or ld_dlogits");
+  TS_CHECK_ARG(255 * ld_hidden < (1ll << 30) && 255 * ld_weight < (1ll << 30),
+               "ts_logprob_dlogits: leading dimensions too large for 32-bit tile offsets");
   DlArgs a;
   a.h = (const ts::bf16*)hidden;
   a.ldh = ld_hidden;

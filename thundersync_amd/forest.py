@@ -138,6 +138,11 @@ class SegmentForest:
     def logical_tokens(self) -> int:
         return sum(t.n_tokens for t in self.trajectories)
 
+    @property
+    def padded_tokens(self) -> int:
+        """Tokens of the [trajectories, longest] rectangle a padded batch would hold."""
+        return len(self.trajectories) * max((t.n_tokens for t in self.trajectories), default=0)
+
     def path_to_root(self, node: int) -> list[int]:
         path = []
         cur: int | None = node

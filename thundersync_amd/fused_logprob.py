@@ -32,6 +32,27 @@ from . import _lib
 from .operator_profiling import device_role, operator_range
 
 
+CHECK_TARGETS_ENV = "THUNDERSYNC_CHECK_TARGETS"
+
+
+def _check_targets(target: torch.Tensor, vocab: int) -> None:
+    """With THUNDERSYNC_CHECK_TARGETS=1, refuse targets outside [0, vocab),
+    naming the first offending row (costs one device synchronisation).
+
+    Without it an out-of-range target is not an error, as it is in the
+    reference's gather: its logprob comes back NaN and its dlogits row gets
+    no one-hot term (every vocabulary entry takes its -p g part), so a bad
+    token id surfaces as a NaN loss."""
+    import os
+
+    if os.environ.get(CHECK_TARGETS_ENV, "0") in ("", "0") or target.numel() == 0:
+        return
+    bad = ((target < 0) | (target >= vocab)).nonzero()
+    if bad.numel():
+        row = int(bad[0, 0])
+        raise ValueError(f"target[{row}] = {int(target[row])} is outside the vocabulary [0, {vocab})")
+
+
 def _validate(hidden: torch.Tensor, weight: torch.Tensor, target: torch.Tensor) -> None:
     # the reference's contract, accel/fused_logprob.py:209-216
     if hidden.dim() != 2:
@@ -46,6 +67,7 @@ def _validate(hidden: torch.Tensor, weight: torch.Tensor, target: torch.Tensor) 
         raise TypeError(
             f"thundersync_amd fused logprob takes bf16 hidden and weight, got {hidden.dtype}/{weight.dtype}"
         )
+    _check_targets(target, weight.shape[0])
 
 
 def _pad_dim(t: torch.Tensor) -> torch.Tensor:

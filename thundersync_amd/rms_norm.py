@@ -127,18 +127,27 @@ if Qwen3RMSNorm is not None:
                 return FP32RMSNormVJP.apply(hidden, self.weight, self.variance_epsilon)
             return rms_norm_forward(hidden, self.weight, self.variance_epsilon)[0]
 
-    def use_stable_qwen3_rms_norm(model: torch.nn.Module) -> int:
-        """Swap every Qwen3RMSNorm, keeping Parameter identity (accel/rms_norm.py:55-70)."""
+    def replace_norms(model: torch.nn.Module, select, make) -> int:
+        """Replace every named submodule ``m`` with ``select(m)`` true by
+        ``make(m)``, a module built on the meta device that then takes ``m``'s
+        own weight Parameter and training flag (no weight copy: optimizers
+        and state dicts keep the original Parameter).  Returns the count."""
         count = 0
         for name, module in list(model.named_modules()):
-            if not name or not isinstance(module, Qwen3RMSNorm):
-                continue
-            if isinstance(module, StableQwen3RMSNorm):
+            if not name or not select(module):
                 continue
             with torch.device("meta"):
-                replacement = StableQwen3RMSNorm(module.weight.numel(), eps=module.variance_epsilon)
+                replacement = make(module)
             replacement.weight = module.weight
             replacement.train(module.training)
             model.set_submodule(name, replacement)
             count += 1
         return count
+
+    def use_stable_qwen3_rms_norm(model: torch.nn.Module) -> int:
+        """Swap every Qwen3RMSNorm for StableQwen3RMSNorm (accel/rms_norm.py:55-70)."""
+        return replace_norms(
+            model,
+            lambda m: isinstance(m, Qwen3RMSNorm) and not isinstance(m, StableQwen3RMSNorm),
+            lambda m: StableQwen3RMSNorm(m.weight.numel(), eps=m.variance_epsilon),
+        )
