@@ -15,10 +15,16 @@ Workloads (synthetic data drawn from fixed seeds):
   hidden -- hidden [16384, 4096], head [151936, 4096], 70% of rows scored
   and gated before the projection (the reference's production schedule),
   frozen head; scored tokens/s, 6 * N * V * D FLOP.
-* ``secondary[2]``: RMSNorm forward + backward on [16384, 4096] bf16; GB/s.
-* ``secondary[3]``: boundary-adjoint reduction -- an existing parent
+* ``secondary[2]``: C3 ungated -- the same operator over all 16,384 rows;
+  projected tokens/s.
+* ``secondary[3]``: RMSNorm forward + backward on [16384, 4096] bf16; GB/s.
+* ``secondary[4]``: boundary-adjoint reduction -- an existing parent
   adjoint plus 16 consumer adjoints of [4096, 4096] bf16 summed in fp32 into
   a new tensor; GB/s of inputs read plus output written.
+
+The MFMA peak is derived from the device's CU count and peak engine clock
+(4096 dense bf16 FLOP per CU per clock), the HBM peak is the published
+8 TB/s; both, with their inputs, are in ``peaks``.
 
 A step is one pass of the operator over its whole input, with inputs
 already resident in HBM.  Per-kernel device time comes from the library's
@@ -26,7 +32,8 @@ own HIP-event brackets (ts_timing_*), recorded on the stream each kernel is
 launched on, over the timed steps; ``roofline`` names the kernel with the
 largest share.  ``cpu_baseline`` times the CPU oracle (the build's op-for-op
 restatement of the reference's eager path) on a bounded sample of the same
-workload, on the host cores.
+workload, on every core the process may run on (``cores``, with
+``cpu_model``).
 """
 
 from __future__ import annotations
@@ -43,8 +50,33 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 METRIC = "forest-attn fwd+bwd TFLOP/s; fused-logprob fwd+bwd tokens/s (1 MI355X)"
-PEAK_BF16_TFLOPS = 2500.0  # dense bf16 MFMA, MI355X
-PEAK_HBM_GBS = 8000.0
+# Dense bf16 MFMA work per compute unit per engine clock on CDNA4: the
+# published 2.5 PFLOP/s of MI355X over its 256 CUs at 2.4 GHz.  The bf16 peak
+# is this times the CU count and peak engine clock the device reports.
+BF16_FLOP_PER_CU_CLOCK = 4096
+PUBLISHED_BF16_TFLOPS = 2500.0
+PEAK_HBM_GBS = 8000.0  # published HBM3E bandwidth, MI355X
+PEAKS: dict = {}
+
+
+def device_peaks(device) -> dict:
+    """MFMA peak from the device's CU count and engine clock (hipDeviceGetAttribute),
+    with the inputs; the HBM peak is the published figure (the reported memory
+    clock and bus width are recorded beside it)."""
+    from thundersync_amd import _lib
+
+    c = _lib.device_clocks(device.index or 0)
+    bf16 = c["cus"] * c["clock_khz"] * 1e3 * BF16_FLOP_PER_CU_CLOCK / 1e12
+    return {
+        "bf16_tflops": round(bf16, 1),
+        "cus": c["cus"],
+        "clock_mhz": c["clock_khz"] / 1e3,
+        "bf16_flop_per_cu_clock": BF16_FLOP_PER_CU_CLOCK,
+        "published_bf16_tflops": PUBLISHED_BF16_TFLOPS,
+        "hbm_gbs": PEAK_HBM_GBS,
+        "mem_clock_mhz": c["mem_clock_khz"] / 1e3,
+        "mem_bus_bits": c["mem_bus_bits"],
+    }
 
 
 def parse():
@@ -53,7 +85,8 @@ def parse():
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--seed", type=int, default=0)
-    ap.add_argument("--only", choices=("all", "attention", "chunked", "logprob", "rmsnorm", "adjoint", "copy"), default="all",
+    ap.add_argument("--only", choices=("all", "attention", "chunked", "logprob", "logprob_ungated", "rmsnorm", "adjoint",
+                                       "copy"), default="all",
                     help="one workload; 'copy' runs only the plain 256 MiB device copy whose FETCH_SIZE / "
                          "WRITE_SIZE readings calibrate the traffic counters")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -61,11 +94,23 @@ def parse():
 
 
 def cpu_threads() -> int:
+    """Every core this process may run on."""
     try:
-        n = len(os.sched_getaffinity(0))
+        return max(1, len(os.sched_getaffinity(0)))
     except AttributeError:  # pragma: no cover
-        n = os.cpu_count() or 1
-    return max(1, min(n, 16))
+        return os.cpu_count() or 1
+
+
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:  # pragma: no cover
+        pass
+    import platform
+
+    return platform.processor() or "unknown"
 
 
 CPU_BASELINE_SECONDS = 10.0
@@ -201,7 +246,7 @@ def bench_attention(args, device):
         "value": round(flop / (ms * 1e-3) / 1e12, 2),
         "unit": "TFLOP/s",
         "ms_per_step": round(ms, 4),
-        "roofline": roofline_of(per, work, "TFLOP/s", PEAK_BF16_TFLOPS, "attention"),
+        "roofline": roofline_of(per, work, "TFLOP/s", PEAKS["bf16_tflops"], "attention"),
         "kernels": {k: {"avg_ms": round(a, 4), "launches_per_step": n} for k, (a, n) in per.items()},
         "config": {
             "workload": "C2 forest attention fwd+bwd: 2048-token shared prompt + 8 completions "
@@ -249,6 +294,7 @@ def attention_cpu_baseline(plan, q, k, v, dout, lengths):
         "value": round(14 * 128 * 32 * pairs * reps / dt / 1e12, 4),
         "unit": "TFLOP/s",
         "cores": torch.get_num_threads(),
+        "cpu_model": cpu_model(),
         "kind": "port",
         "sample": f"prompt node (2048 rows) + first completion node ({lengths[0]} rows) of the same C2 "
                   f"forest, {pairs} visible pairs, fp32 masked SDPA fwd+bwd on the host, {reps} passes",
@@ -337,7 +383,7 @@ def bench_chunked(args, device):
         "value": round(flop / (ms * 1e-3) / 1e12, 2),
         "unit": "TFLOP/s",
         "ms_per_step": round(ms, 4),
-        "roofline": roofline_of(per, work, "TFLOP/s", PEAK_BF16_TFLOPS, "chunked"),
+        "roofline": roofline_of(per, work, "TFLOP/s", PEAKS["bf16_tflops"], "chunked"),
         "kernels": {k: {"avg_ms": round(a, 4), "launches_per_step": n} for k, (a, n) in per.items()},
         "config": {
             "workload": "C4 chunked retained-KV attention fwd+bwd: 4 groups x (1024-token prompt + 4 "
@@ -392,6 +438,7 @@ def chunked_cpu_baseline(chunks, lengths, q, ks, vs, dout, chunk=512, prompt=102
         "value": round(14 * 128 * 32 * pairs * reps / dt / 1e12, 4),
         "unit": "TFLOP/s",
         "cores": torch.get_num_threads(),
+        "cpu_model": cpu_model(),
         "kind": "port",
         "sample": f"the {len(sample)} query chunks of the first C4 trajectory ({pairs} visible pairs), "
                   f"fp32 masked SDPA fwd+bwd over the concatenated retained K/V on the host, {reps} passes",
@@ -402,7 +449,10 @@ def chunked_cpu_baseline(chunks, lengths, q, ks, vs, dout, chunk=512, prompt=102
 # ---------------------------------------------------------------------------
 # C3 fused logprob
 # ---------------------------------------------------------------------------
-def bench_logprob(args, device):
+def bench_logprob(args, device, gate: bool = True):
+    """C3: ``gate`` projects only the scored rows (70%), the reference's
+    production schedule; ``gate=False`` projects all 16,384 rows, the
+    ungated form."""
     import torch
 
     from thundersync_amd import fused_logprob
@@ -414,7 +464,7 @@ def bench_logprob(args, device):
     target = torch.randint(0, v, (n,), generator=g, device=device)
     adv = torch.randn(n, generator=g, device=device)
     mask = torch.rand(n, generator=g, device=device) < 0.7
-    idx = mask.nonzero(as_tuple=True)[0]
+    idx = mask.nonzero(as_tuple=True)[0] if gate else torch.arange(n, device=device)
     h = hidden.index_select(0, idx).requires_grad_()
     t = target.index_select(0, idx)
     a = adv.index_select(0, idx)
@@ -438,19 +488,21 @@ def bench_logprob(args, device):
         "logprob.grad_hidden_reduce_kernel": 0,
     }
     flop = 3 * gemm
+    form = ("70% scored rows gated first" if gate else "all 16384 rows projected (ungated)")
     result = {
-        "metric": "fused-logprob fwd+bwd tokens/s",
+        "metric": "fused-logprob fwd+bwd tokens/s" + ("" if gate else " (ungated)"),
         "value": round(rows / (ms * 1e-3), 1),
         "unit": "tokens/s",
         "tflops": round(flop / (ms * 1e-3) / 1e12, 2),
-        "mfma_frac": round(flop / (ms * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+        "mfma_frac": round(flop / (ms * 1e-3) / 1e12 / PEAKS["bf16_tflops"], 4),
         "ms_per_step": round(ms, 4),
-        "roofline": roofline_of({k: x for k, x in per.items() if work[k]}, work, "TFLOP/s", PEAK_BF16_TFLOPS, "logprob"),
+        "roofline": roofline_of({k: x for k, x in per.items() if work[k]}, work, "TFLOP/s", PEAKS["bf16_tflops"],
+                                "logprob" if gate else "logprob_ungated"),
         "kernels": {k: {"avg_ms": round(x, 4), "launches_per_step": m} for k, (x, m) in per.items()},
         "config": {
             "workload": "C3 fused logprob+entropy fwd + grad wrt hidden: hidden [16384,4096] bf16, "
-                        "head [151936,4096] bf16 N(0,0.02), 70% scored rows gated first, frozen head",
-            "scored_rows": rows,
+                        f"head [151936,4096] bf16 N(0,0.02), {form}, frozen head",
+            "projected_rows": rows,
             "flop_per_step": flop,
             "seed": args.seed,
         },
@@ -481,6 +533,7 @@ def logprob_cpu_baseline(h, weight, t, a, rows=96):
         "value": round(rows * reps / dt, 2),
         "unit": "tokens/s",
         "cores": torch.get_num_threads(),
+        "cpu_model": cpu_model(),
         "kind": "port",
         "sample": f"{rows} scored rows of C3 (dim 4096, vocab 151936), chunk 1024, fwd + grad wrt hidden, "
                   f"{reps} passes",
@@ -507,20 +560,51 @@ def bench_rmsnorm(args, device):
         y = rms_norm.FP32RMSNormVJP.apply(x, w, 1e-6)
         y.backward(dy)
 
-    kernels = ["rmsnorm.rmsnorm_fwd_vec", "rmsnorm.rmsnorm_bwd_vec", "rmsnorm.rmsnorm_dw_reduce"]
+    kernels = ["rmsnorm.rmsnorm_fwd_lanes", "rmsnorm.rmsnorm_fwd_rowwave", "rmsnorm.rmsnorm_bwd_vec",
+               "rmsnorm.rmsnorm_dw_reduce"]
     ms, per = timed(step, args.steps, args.warmup, kernels)
     fwd_bytes = 4 * r * w_ + 4 * r + 2 * w_
     bwd_bytes = 6 * r * w_ + 4 * r + 2 * w_ + 4 * w_
-    work = {"rmsnorm.rmsnorm_fwd_vec": fwd_bytes, "rmsnorm.rmsnorm_bwd_vec": bwd_bytes,
-            "rmsnorm.rmsnorm_dw_reduce": 0}
-    return {
+    work = {"rmsnorm.rmsnorm_fwd_lanes": fwd_bytes, "rmsnorm.rmsnorm_fwd_rowwave": fwd_bytes,
+            "rmsnorm.rmsnorm_bwd_vec": bwd_bytes, "rmsnorm.rmsnorm_dw_reduce": 0}
+    result = {
         "metric": "RMSNorm fwd+bwd GB/s",
         "value": round((fwd_bytes + bwd_bytes) / (ms * 1e-3) / 1e9, 1),
         "unit": "GB/s",
         "ms_per_step": round(ms, 4),
-        "roofline": roofline_of({k: x for k, x in per.items() if work[k]}, work, "GB/s", PEAK_HBM_GBS, "rmsnorm"),
+        "roofline": roofline_of({k: x for k, x in per.items() if work[k]}, work, "GB/s", PEAKS["hbm_gbs"], "rmsnorm"),
         "kernels": {k: {"avg_ms": round(x, 4), "launches_per_step": m} for k, (x, m) in per.items()},
         "config": {"workload": "RMSNorm fwd+bwd [16384, 4096] bf16, FP32 VJP with dW", "seed": args.seed},
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = rmsnorm_cpu_baseline(x, w, dy, (fwd_bytes + bwd_bytes) / r)
+    return result
+
+
+def rmsnorm_cpu_baseline(x, w, dy, bytes_per_row, rows=2048):
+    """The reference's eager forward (accel/rms_norm.py:11-14) and FP32 VJP
+    (:33-38) on the CPU over the first `rows` rows; GB/s of the same
+    algorithmic bytes per row as the device figure."""
+    import torch
+
+    from oracle import rms_norm as ref
+
+    torch.set_num_threads(cpu_threads())
+    xs, ws, gs = x.detach()[:rows].cpu(), w.detach().cpu(), dy[:rows].cpu()
+
+    def one_pass():
+        ref.rms_norm_forward(xs, ws, 1e-6)
+        ref.rms_norm_backward(gs, xs, ws, 1e-6)
+
+    reps, dt = repeat_for(one_pass)
+    return {
+        "value": round(bytes_per_row * rows * reps / dt / 1e9, 2),
+        "unit": "GB/s",
+        "cores": torch.get_num_threads(),
+        "cpu_model": cpu_model(),
+        "kind": "port",
+        "sample": f"first {rows} of 16384 rows of [16384, 4096] bf16, eager fp32 forward + VJP, {reps} passes",
+        "seconds": round(dt, 3),
     }
 
 
@@ -553,7 +637,7 @@ def bench_adjoint(args, device):
         "value": round(nbytes / (ms * 1e-3) / 1e9, 1),
         "unit": "GB/s",
         "ms_per_step": round(ms, 4),
-        "roofline": roofline_of(per, {"adjoint.reduce_kernel": nbytes}, "GB/s", PEAK_HBM_GBS, "adjoint"),
+        "roofline": roofline_of(per, {"adjoint.reduce_kernel": nbytes}, "GB/s", PEAKS["hbm_gbs"], "adjoint"),
         "kernels": {k: {"avg_ms": round(x, 4), "launches_per_step": m} for k, (x, m) in per.items()},
         "config": {"workload": f"boundary adjoint: existing + {ADJOINT_DEGREE} consumer adjoints "
                                f"[{ADJOINT_SHAPE[0]}, {ADJOINT_SHAPE[1]}] bf16, fp32 accumulation",
@@ -580,6 +664,7 @@ def adjoint_cpu_baseline(adj, existing, nbytes, rows=1024):
         "value": round(sample_bytes * reps / dt / 1e9, 2),
         "unit": "GB/s",
         "cores": torch.get_num_threads(),
+        "cpu_model": cpu_model(),
         "kind": "port",
         "sample": f"first {rows} of {ADJOINT_SHAPE[0]} rows, existing + {ADJOINT_DEGREE} bf16 adjoints, "
                   f"{reps} passes",
@@ -610,6 +695,7 @@ def main():
 
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)
+    PEAKS.update(device_peaks(device))
     if args.only == "copy":
         calibration_copy(device)
         return
@@ -642,6 +728,8 @@ def main():
         out["secondary"].append(bench_chunked(args, device))
     if args.only in ("all", "logprob"):
         out["secondary"].append(bench_logprob(args, device))
+    if args.only in ("all", "logprob_ungated"):
+        out["secondary"].append(bench_logprob(args, device, gate=False))
     if args.only in ("all", "rmsnorm"):
         out["secondary"].append(bench_rmsnorm(args, device))
     if args.only in ("all", "adjoint"):
@@ -649,6 +737,7 @@ def main():
     props = torch.cuda.get_device_properties(device)
     out["device"] = {"name": props.name, "arch": getattr(props, "gcnArchName", ""),
                      "cus": props.multi_processor_count}
+    out["peaks"] = dict(PEAKS)
     print(json.dumps(out), flush=True)
 
 

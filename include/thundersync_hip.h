@@ -380,6 +380,12 @@ int ts_timing_enable(int enable);
 int ts_timing_reset(void);
 int ts_timing_read(const char* kernel, double* total_ms, int64_t* launches);
 
+/* The device's compute-unit count, peak engine clock (kHz), memory clock
+ * (kHz) and memory bus width (bits), from hipDeviceGetAttribute.  bench.py
+ * derives its MFMA peak from the first two.  No counterpart in the
+ * reference. */
+int ts_device_clocks(int device, int* cus, int* clock_khz, int* mem_clock_khz, int* mem_bus_bits);
+
 /* Runs one v_mfma_f32_16x16x32_bf16 and one v_mfma_f32_32x32x16_bf16 on
  * operands the caller lays out per lane (a, b: 64 lanes x 8 bf16 each), and
  * the 8x8 16-bit register transpose on `t_in` (64 lanes x 8 x 8 bf16).

@@ -49,3 +49,25 @@ def test_repeat_for_runs_at_least_once_and_stops():
     assert reps == 1 and len(calls) == 1 and dt >= 0.0
     reps, _ = bench.repeat_for(lambda: None, seconds=100.0, max_reps=7)
     assert reps == 7
+
+
+def test_cpu_baseline_uses_every_affinity_core_and_names_the_cpu():
+    import os
+
+    assert bench.cpu_threads() == len(os.sched_getaffinity(0))
+    model = bench.cpu_model()
+    assert isinstance(model, str) and model
+
+
+def test_mfma_peak_follows_cus_and_clock(monkeypatch):
+    import torch
+
+    from thundersync_amd import _lib
+
+    monkeypatch.setattr(_lib, "device_clocks",
+                        lambda i: {"cus": 256, "clock_khz": 2_400_000, "mem_clock_khz": 2_000_000,
+                                   "mem_bus_bits": 8192})
+    peaks = bench.device_peaks(torch.device("cuda", 0))
+    # 256 CUs x 2.4 GHz x 4096 FLOP per CU per clock: the published 2.5 PFLOP/s
+    assert peaks["bf16_tflops"] == pytest.approx(2516.6, abs=0.1)
+    assert peaks["cus"] == 256 and peaks["clock_mhz"] == 2400.0 and peaks["hbm_gbs"] == 8000.0

@@ -45,6 +45,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "ts_probe_layouts": (_INT, [_P, _P, _P, _P, _P, _P, _P]),
     "ts_probe_lds": (_INT, [_P, _P, _P, _P, _P, _INT, _P]),
     "ts_probe_lanes": (_INT, [_P, _P, _P]),
+    "ts_device_clocks": (_INT, [_INT, ctypes.POINTER(_INT), ctypes.POINTER(_INT), ctypes.POINTER(_INT),
+                                ctypes.POINTER(_INT)]),
     "ts_timing_enable": (_INT, [_INT]),
     "ts_timing_reset": (_INT, []),
     "ts_timing_read": (_INT, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_I64)]),
@@ -183,6 +185,15 @@ def stream_of(tensor) -> int:
 
 def ptr(tensor) -> int | None:
     return None if tensor is None else tensor.data_ptr()
+
+
+def device_clocks(device: int = 0) -> dict[str, int]:
+    """Compute units, peak engine clock, memory clock (kHz) and memory bus
+    width (bits) of a device, from hipDeviceGetAttribute (ts_device_clocks)."""
+    lib = require_library()
+    vals = [ctypes.c_int() for _ in range(4)]
+    check(lib.ts_device_clocks(int(device), *(ctypes.byref(v) for v in vals)), "ts_device_clocks")
+    return dict(zip(("cus", "clock_khz", "mem_clock_khz", "mem_bus_bits"), (v.value for v in vals)))
 
 
 class KernelTimer:

@@ -104,6 +104,24 @@ const char* ts_hip_version(void) { return "thundersync_hip 0.1.0 gfx950"; }
 
 const char* ts_hip_last_error(void) { return ts::g_error; }
 
+int ts_device_clocks(int device, int* cus, int* clock_khz, int* mem_clock_khz, int* mem_bus_bits) {
+  TS_CHECK_ARG(cus && clock_khz && mem_clock_khz && mem_bus_bits, "ts_device_clocks: null pointer");
+  const struct {
+    hipDeviceAttribute_t attr;
+    int* out;
+  } want[] = {{hipDeviceAttributeMultiprocessorCount, cus},
+              {hipDeviceAttributeClockRate, clock_khz},
+              {hipDeviceAttributeMemoryClockRate, mem_clock_khz},
+              {hipDeviceAttributeMemoryBusWidth, mem_bus_bits}};
+  for (const auto& w : want) {
+    if (hipDeviceGetAttribute(w.out, w.attr, device) != hipSuccess) {
+      ts::set_error("ts_device_clocks: hipDeviceGetAttribute failed on device %d", device);
+      return TS_ERR_LAUNCH;
+    }
+  }
+  return TS_OK;
+}
+
 int ts_probe_layouts(const void* a, const void* b, float* d16, float* d32,
                      const void* t_in, void* t_out, void* stream) {
   TS_CHECK_ARG(a && b && d16 && d32 && t_in && t_out, "ts_probe_layouts: null pointer");
