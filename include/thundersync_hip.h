@@ -308,6 +308,35 @@ int ts_logprob_grad_weight(const void* dlogits, int64_t ld_dlogits, const void* 
                            float* grad_weight, int64_t ld_grad, void* stream);
 
 /* ------------------------------------------------------------------------
+ * Merged-weight LoRA linear (bf16 operands, fp32 accumulation)
+ *
+ * The caller has merged the adapters into the weight (W_eff = W + s B A,
+ * [out, in]); lora_a is A [rank, in] and lora_b_t is B transposed,
+ * [rank, out], both bf16 with rows of in / out elements.  Rows of x, y, g
+ * and the weight are 16-byte aligned, in and out multiples of 8.
+ * ------------------------------------------------------------------------ */
+
+/* y [rows, out] = x [rows, in] . W_eff^T.
+ * Replaces FusedLoRALinear.forward (accel/fused_lora.py:29-33). */
+int ts_lora_fwd(const void* x, int64_t ld_x, const void* weight, int64_t ld_weight, int64_t rows,
+                int64_t in_features, int64_t out_features, void* y, int64_t ld_y, void* stream);
+
+/* Workspace bytes ts_lora_bwd needs. */
+int64_t ts_lora_bwd_workspace(int64_t rows, int64_t in_features, int64_t out_features, int64_t rank);
+
+/* grad_x [rows, in] (bf16) = g W_eff; grad_a [rank, in] (fp32) =
+ * s (g B)^T x; grad_b [out, rank] (fp32) = s g^T (x A^T), with g = grad_out
+ * [rows, out].  g B and x A^T are rounded to bf16 (the reference forms them
+ * as activation-dtype products); the adapter gradients are fp32 sums over
+ * fixed row ranges added in range order, then scaled: the same bytes on
+ * every call.  A null grad_x / grad_a / grad_b is not computed.  rank <= 256.
+ * Replaces FusedLoRALinear.backward (accel/fused_lora.py:35-48). */
+int ts_lora_bwd(const void* grad_out, int64_t ld_grad_out, const void* x, int64_t ld_x, const void* weight,
+                int64_t ld_weight, const void* lora_a, const void* lora_b_t, int64_t rank, float scaling,
+                int64_t rows, int64_t in_features, int64_t out_features, void* grad_x, int64_t ld_grad_x,
+                float* grad_a, float* grad_b, void* workspace, int64_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
  * Boundary adjoints
  * ---------------------------------------------------------------------- */
 

@@ -261,3 +261,46 @@ def test_repeated_runs_are_bit_identical(cuda):
         runs.append((lp.detach(), ent.detach(), hc.grad, wc.grad))
     for a, b, name in zip(runs[0], runs[1], ("lp", "ent", "grad hidden", "grad weight")):
         assert torch.equal(a, b), name
+
+
+@pytest.mark.parametrize("first_scored", [True, False])
+def test_predictor_logprobs_match_the_streaming_gather(cuda, first_scored):
+    """engine/streaming.py:4113-4130 / 5318-5349: predictors are
+    cat([boundary, hidden[:-1]]) at the scored positions; the helper gathers
+    only those rows.  Values and gradients (hidden, boundary) against the
+    oracle applied to the reference's concatenation."""
+    print(f"predictor_logprobs first_scored={first_scored}", flush=True)
+    t, d, v = 300, 256, 4099
+    g = torch.Generator().manual_seed(41 + first_scored)
+    hidden = torch.randn(t, d, generator=g).to(torch.bfloat16)
+    boundary = torch.randn(d, generator=g).to(torch.bfloat16)
+    w = (torch.randn(v, d, generator=g) * 0.02).to(torch.bfloat16)
+    tokens = torch.randint(0, v, (t,), generator=g).tolist()
+    scored = (torch.rand(t, generator=g) < 0.6).tolist()
+    scored[0] = first_scored
+    pos = [j for j, s in enumerate(scored) if s]
+    src = torch.cat([boundary.unsqueeze(0), hidden[:-1]])
+    rows = src.index_select(0, torch.tensor(pos))
+    tgt = torch.tensor([tokens[j] for j in pos])
+    g_lp = torch.randn(len(pos), generator=g)
+    want = ref.logprob_forward(rows, w, tgt, 1024)
+    want_rows, _ = ref.logprob_backward(rows, w, tgt, g_lp, 1024)
+    # scatter the per-row gradient back through the concatenation
+    want_src = torch.zeros(t, d)
+    want_src.index_add_(0, torch.tensor(pos), want_rows.float())
+    hc = hidden.to(cuda).requires_grad_()
+    bc = boundary.to(cuda).requires_grad_()
+    lp = hip.predictor_logprobs(bc, hc, tokens, scored, w.to(cuda), chunk=64)
+    (lp * g_lp.to(cuda)).sum().backward()
+    torch.testing.assert_close(lp.cpu(), want, rtol=0, atol=1e-3)
+    rel_close(hc.grad[:-1], want_src[1:], 1e-2, "grad hidden")
+    assert torch.count_nonzero(hc.grad[-1]) == 0  # the last hidden predicts nothing here
+    if first_scored:
+        rel_close(bc.grad, want_src[0], 1e-2, "grad boundary")
+    else:
+        assert bc.grad is None or torch.count_nonzero(bc.grad) == 0
+    # nothing scored: empty, on the weight's device
+    empty = hip.predictor_logprobs(bc, hc, tokens, [False] * t, w.to(cuda))
+    assert empty.shape == (0,) and empty.device == w.to(cuda).device
+    with pytest.raises(ValueError, match="one entry per position"):
+        hip.predictor_logprobs(bc, hc, tokens[:-1], scored, w.to(cuda))

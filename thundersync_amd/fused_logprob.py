@@ -239,3 +239,39 @@ def gathered_logprobs(hidden: torch.Tensor, weight: torch.Tensor, token_ids: tor
     lp = fused_logprob(hidden[idx - 1], weight, token_ids[idx], chunk=chunk)
     out = torch.zeros(n, dtype=lp.dtype, device=lp.device)
     return out.index_put((idx,), lp)
+
+
+def predictor_logprobs(boundary_hidden: torch.Tensor, hidden: torch.Tensor, tokens, scored, weight: torch.Tensor,
+                       *, chunk: int = 1024) -> torch.Tensor:
+    """Logprobs of a chunk's scored tokens, each predicted by the hidden state
+    one position earlier; the chunk's first position by ``boundary_hidden``,
+    the last hidden state of what precedes the chunk.
+
+    The logprob gathers of the reference's streaming engine: appended turns
+    (engine/streaming.py:4113-4130, the previous chunk's last hidden) and
+    suffix rebuilds (:5318-5349, the prompt's last hidden).  There the
+    predictors are ``cat([boundary, hidden[:-1]])`` indexed at the scored
+    positions; here only the scored predictor rows are gathered (no ``[T, D]``
+    copy), and gradients reach ``hidden``, ``boundary_hidden`` and, when it
+    requires them, ``weight``.  ``tokens`` and ``scored`` are per-position
+    sequences (Python or 1-D tensors); the result is fp32 ``[n_scored]`` in
+    position order, empty when nothing is scored.
+    """
+    t = hidden.shape[0]
+    if boundary_hidden.shape != hidden.shape[1:]:
+        raise ValueError(f"boundary_hidden {tuple(boundary_hidden.shape)} must be one row of {tuple(hidden.shape)}")
+    scored_t = torch.as_tensor(scored, dtype=torch.bool).cpu()
+    tokens_t = torch.as_tensor(tokens, dtype=torch.long).cpu()
+    if scored_t.shape != (t,) or tokens_t.shape != (t,):
+        raise ValueError(f"tokens and scored need one entry per position ({t})")
+    positions = scored_t.nonzero(as_tuple=True)[0]
+    if positions.numel() == 0:
+        return torch.zeros(0, dtype=torch.float32, device=weight.device)
+    dev = hidden.device
+    first = bool(positions[0] == 0)
+    rest = positions[1:] if first else positions
+    rows = hidden.index_select(0, (rest - 1).to(dev, non_blocking=True))
+    if first:
+        rows = torch.cat([boundary_hidden.unsqueeze(0), rows], dim=0)
+    target = tokens_t.index_select(0, positions).to(dev, non_blocking=True)
+    return fused_logprob(rows, weight, target, chunk=chunk)
