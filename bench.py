@@ -21,6 +21,11 @@ Workloads (synthetic data drawn from fixed seeds):
 * ``secondary[4]``: boundary-adjoint reduction -- an existing parent
   adjoint plus 16 consumer adjoints of [4096, 4096] bf16 summed in fp32 into
   a new tensor; GB/s of inputs read plus output written.
+* ``secondary[5]``: merged-weight LoRA linear, forward + backward (dx, dA,
+  dB) at a C5 q_proj slice: 16384 tokens, 4096 -> 4096, rank 16.
+* ``--only c5`` (not in the default run): one GRPO-shaped update of the
+  Qwen3-8B-shaped C5 decoder through every operator of the build, wall time
+  and per-kernel breakdown.
 
 The MFMA peak is derived from the device's CU count and peak engine clock
 (4096 dense bf16 FLOP per CU per clock), the HBM peak is the published
@@ -86,7 +91,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--only", choices=("all", "attention", "chunked", "logprob", "logprob_ungated", "rmsnorm", "adjoint",
-                                       "copy"), default="all",
+                                       "lora", "c5", "copy"), default="all",
                     help="one workload; 'copy' runs only the plain 256 MiB device copy whose FETCH_SIZE / "
                          "WRITE_SIZE readings calibrate the traffic counters")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -672,6 +677,213 @@ def adjoint_cpu_baseline(adj, existing, nbytes, rows=1024):
     }
 
 
+# ---------------------------------------------------------------------------
+# Merged-weight LoRA linear
+# ---------------------------------------------------------------------------
+LORA_SHAPE = (16384, 4096, 4096, 16)  # tokens, in, out, rank: a C5 q_proj over 16384 tokens
+
+
+def bench_lora(args, device):
+    import torch
+
+    from thundersync_amd import fused_lora
+
+    t, fin, fout, r = LORA_SHAPE
+    g = torch.Generator(device=device).manual_seed(args.seed)
+    x = torch.randn(t, fin, generator=g, device=device, dtype=torch.bfloat16).requires_grad_()
+    w = (torch.randn(fout, fin, generator=g, device=device) * fin ** -0.5).to(torch.bfloat16)
+    a = (torch.randn(r, fin, generator=g, device=device) * fin ** -0.5).requires_grad_()
+    b = (torch.randn(fout, r, generator=g, device=device) * 0.01).requires_grad_()
+    dy = torch.randn(t, fout, generator=g, device=device, dtype=torch.bfloat16)
+
+    def step():
+        x.grad = a.grad = b.grad = None
+        fused_lora.FusedLoRALinear.apply(x, w, a, b, 2.0).backward(dy)
+
+    kernels = ["lora.fwd_kernel", "lora.grad_x_kernel", "lora.grad_x_reduce_kernel", "lora.rank_kernel",
+               "lora.grad_a_kernel", "lora.grad_b_kernel", "lora.reduce_kernel"]
+    ms, per = timed(step, args.steps, args.warmup, kernels)
+    gemm = 2 * t * fin * fout
+    adapter = 2 * t * r * (fin + fout)  # g B and x A^T, then u^T x and g^T t: the same count again
+    work = {"lora.fwd_kernel": gemm, "lora.grad_x_kernel": gemm, "lora.rank_kernel": adapter,
+            "lora.grad_a_kernel": 2 * t * r * fin, "lora.grad_b_kernel": 2 * t * r * fout,
+            "lora.grad_x_reduce_kernel": 0, "lora.reduce_kernel": 0}
+    flop = 2 * gemm + 2 * adapter
+    # the adapter products read g and x (bf16) twice over the backward
+    adapter_bytes = 2 * 2 * t * (fin + fout)
+    adapter_ms = sum(per[k][0] * per[k][1] for k in ("lora.rank_kernel", "lora.grad_a_kernel",
+                                                      "lora.grad_b_kernel", "lora.reduce_kernel") if k in per)
+    result = {
+        "metric": "merged-weight LoRA linear fwd+bwd TFLOP/s",
+        "value": round(flop / (ms * 1e-3) / 1e12, 2),
+        "unit": "TFLOP/s",
+        "ms_per_step": round(ms, 4),
+        "roofline": roofline_of({k: v for k, v in per.items() if work[k]}, work, "TFLOP/s", PEAKS["bf16_tflops"],
+                                "lora"),
+        "adapter_gradients": {"ms": round(adapter_ms, 4), "bytes": adapter_bytes,
+                              "gbs": round(adapter_bytes / (adapter_ms * 1e-3) / 1e9, 1) if adapter_ms else None},
+        "kernels": {k: {"avg_ms": round(v, 4), "launches_per_step": n} for k, (v, n) in per.items()},
+        "config": {"workload": f"FusedLoRALinear fwd + bwd (dx, dA, dB): x [{t}, {fin}] bf16, W_eff [{fout}, {fin}] "
+                               f"bf16, rank {r} fp32 adapters, scaling 2 (a C5 q_proj slice)",
+                   "flop_per_step": flop, "seed": args.seed},
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = lora_cpu_baseline(x, w, a, b, dy, flop / t)
+    return result
+
+
+def lora_cpu_baseline(x, w, a, b, dy, flop_per_row, rows=512):
+    """The reference layer's forward + backward (accel/fused_lora.py:29-48) on
+    the CPU in fp32 over the first `rows` rows."""
+    import torch
+
+    from oracle import lora as ref
+
+    torch.set_num_threads(cpu_threads())
+    xs, ws, gs = x.detach()[:rows].float().cpu(), w.float().cpu(), dy[:rows].float().cpu()
+    as_, bs = a.detach().cpu(), b.detach().cpu()
+    reps, dt = repeat_for(lambda: ref.reference_step(xs, ws, as_, bs, gs, 2.0))
+    return {
+        "value": round(flop_per_row * rows * reps / dt / 1e12, 4),
+        "unit": "TFLOP/s",
+        "cores": torch.get_num_threads(),
+        "cpu_model": cpu_model(),
+        "kind": "port",
+        "sample": f"first {rows} of {LORA_SHAPE[0]} rows, fp32 eager forward + backward, {reps} passes",
+        "seconds": round(dt, 3),
+    }
+
+
+# ---------------------------------------------------------------------------
+# C5: one GRPO-shaped update of a Qwen3-8B-shaped decoder (opt-in: --only c5)
+# ---------------------------------------------------------------------------
+def c5_model(device):
+    import torch
+    from transformers import Qwen3Config, Qwen3ForCausalLM
+
+    from thundersync_amd.attention import HIP_FOREST_ATTENTION_NAME, register_attention
+    from thundersync_amd.lora_layers import add_lora
+    from thundersync_amd.rms_norm import use_stable_qwen3_rms_norm
+
+    cfg = Qwen3Config(vocab_size=151936, hidden_size=4096, intermediate_size=12288, num_hidden_layers=36,
+                      num_attention_heads=32, num_key_value_heads=8, head_dim=128, tie_word_embeddings=False,
+                      max_position_embeddings=40960, rms_norm_eps=1e-6)
+    default = torch.get_default_dtype()
+    torch.set_default_dtype(torch.bfloat16)
+    try:
+        with torch.device(device):
+            model = Qwen3ForCausalLM(cfg)
+    finally:
+        torch.set_default_dtype(default)
+    assert register_attention()
+    model.set_attn_implementation(HIP_FOREST_ATTENTION_NAME)
+    use_stable_qwen3_rms_norm(model)
+    add_lora(model, ["q_proj", "k_proj", "v_proj", "o_proj"], rank=16, alpha=32)
+    model.gradient_checkpointing_enable(gradient_checkpointing_kwargs={"use_reentrant": False})
+    model.train()
+    return model
+
+
+def c5_rollouts(seed, device):
+    import torch
+
+    from thundersync_amd import forest
+
+    g = torch.Generator().manual_seed(seed)
+    trajs, rewards = [], []
+    for grp in range(2):
+        prompt = torch.randint(0, 151936, (1024,), generator=g).tolist()
+        lengths = torch.randint(512, 8193, (8,), generator=g).tolist()
+        for i, n in enumerate(lengths):
+            body = torch.randint(0, 151936, (n,), generator=g).tolist()
+            trajs.append(forest.Trajectory([forest.Segment.prompt(prompt), forest.Segment.action(body)],
+                                           group_id=grp, traj_id=8 * grp + i))
+        rewards.append(torch.randn(8, generator=g))
+    r = torch.stack(rewards)
+    adv = ((r - r.mean(1, keepdim=True)) / r.std(1, unbiased=False, keepdim=True).clamp_min(1e-6)).flatten()
+    plan = forest.compile_plan(forest.build_forest(trajs)).to(device)
+    return plan, {i: float(adv[i]) for i in range(16)}
+
+
+def bench_c5(args, device):
+    import torch
+
+    from thundersync_amd import attention as att
+    from thundersync_amd.attention import forest_context
+    from thundersync_amd.fused_lora import fuse_merged_lora_forward, unfuse_merged_lora_forward
+    from thundersync_amd.step import forest_logprobs, split_by_trajectory
+
+    t0 = time.perf_counter()
+    model = c5_model(device)
+    plan, adv = c5_rollouts(args.seed, device)
+    build_s = time.perf_counter() - t0
+    params = [p for p in model.parameters() if p.requires_grad]
+    opt = torch.optim.AdamW(params, lr=1e-5)
+    scored = int(plan.score_src.numel())
+
+    def update():
+        fuse_merged_lora_forward(model)
+        with forest_context(plan):
+            lp = forest_logprobs(model, plan)
+            per = split_by_trajectory(plan, lp)
+            loss = -sum(adv[tid] * v.sum() for tid, v in per.items()) / lp.numel()
+            loss.backward()
+        unfuse_merged_lora_forward(model)
+        opt.step()
+        opt.zero_grad(set_to_none=True)
+
+    kernels = ["attention.fwd_kernel", "attention.delta_kernel", "attention.dq_kernel", "attention.dkdv_kernel",
+               "logprob.fwd_stats_kernel", "logprob.target_logit_kernel", "logprob.combine_kernel",
+               "logprob.dlogits_kernel", "logprob.grad_hidden_kernel", "logprob.grad_hidden_reduce_kernel",
+               "rmsnorm.rmsnorm_fwd_lanes", "rmsnorm.rmsnorm_fwd_rowwave", "rmsnorm.rmsnorm_bwd_vec",
+               "rmsnorm.rmsnorm_bwd_scalar", "rmsnorm.rmsnorm_dw_reduce",
+               "lora.fwd_kernel", "lora.grad_x_kernel", "lora.grad_x_reduce_kernel", "lora.rank_kernel",
+               "lora.grad_a_kernel", "lora.grad_b_kernel", "lora.reduce_kernel"]
+    steps, warmup = max(1, min(args.steps, 3)), max(1, min(args.warmup, 1))
+    ms, per = timed(update, steps, warmup, kernels)
+    p, layers, d, hq = plan.n_physical, 36, 128, 32
+    pairs = att.forest_layout(plan, 32, 8).visible_pairs()
+    proj = 2 * p * (4096 * 4096 * 2 + 4096 * 1024 * 2)  # q, k, v, o of one layer
+    v, dim = 151936, 4096
+    work = {  # per update; the forward of every layer runs twice (checkpoint recompute)
+        "attention.fwd_kernel": 2 * layers * 4 * d * hq * pairs,
+        "attention.dq_kernel": layers * 2 * d * hq * pairs,
+        "attention.dkdv_kernel": layers * 8 * d * hq * pairs,
+        "lora.fwd_kernel": 2 * layers * proj,
+        "lora.grad_x_kernel": layers * proj,
+        "logprob.fwd_stats_kernel": 2 * scored * v * dim,
+        "logprob.dlogits_kernel": 2 * scored * v * dim,
+        "logprob.grad_hidden_kernel": 2 * scored * v * dim,
+    }
+    kern = {}
+    for k, (avg, n) in per.items():
+        entry = {"avg_ms": round(avg, 4), "launches_per_update": n, "ms_per_update": round(avg * n, 3)}
+        if k in work:
+            tf = work[k] / (avg * n * 1e-3) / 1e12
+            entry.update(tflops=round(tf, 1), frac=round(tf / PEAKS["bf16_tflops"], 4))
+        kern[k] = entry
+    ours = sum(e["ms_per_update"] for e in kern.values())
+    model_flop = 6 * 6.95e9 * p  # dense linears fwd + recompute + dx, order of magnitude only
+    return {
+        "metric": "C5 GRPO update wall time (one MI355X)",
+        "value": round(ms / 1e3, 3),
+        "unit": "s",
+        "higher_is_better": False,
+        "ms_per_step": round(ms, 1),
+        "library_kernel_ms": round(ours, 1),
+        "other_ms": round(ms - ours, 1),
+        "kernels": kern,
+        "config": {"workload": "Qwen3-8B-shaped decoder (36 layers, 4096, 32/8 heads, MLP 12288, vocab 151936), "
+                               "random-init bf16, LoRA rank 16 on q/k/v/o (fp32 adapters, merged-weight path), "
+                               "2 groups x 8 trajectories, prompt 1024, completions U[512,8192], forest attention, "
+                               "fused logprob, HIP RMSNorm, per-layer activation checkpointing, AdamW on the adapters",
+                   "physical_tokens": p, "logical_tokens": plan.forest.logical_tokens, "scored_tokens": scored,
+                   "visible_pairs_per_layer": pairs, "build_seconds": round(build_s, 1),
+                   "steps": steps, "warmup": warmup, "seed": args.seed,
+                   "approx_dense_linear_flop": model_flop},
+    }
+
+
 def calibration_copy(device, nbytes: int = 256 << 20, repeats: int = 3) -> None:
     """A plain device-to-device copy of `nbytes`, `repeats` times: the reference
     reading for scaling the FETCH_SIZE / WRITE_SIZE counters to bytes."""
@@ -734,6 +946,10 @@ def main():
         out["secondary"].append(bench_rmsnorm(args, device))
     if args.only in ("all", "adjoint"):
         out["secondary"].append(bench_adjoint(args, device))
+    if args.only in ("all", "lora"):
+        out["secondary"].append(bench_lora(args, device))
+    if args.only == "c5":
+        out["secondary"].append(bench_c5(args, device))
     props = torch.cuda.get_device_properties(device)
     out["device"] = {"name": props.name, "arch": getattr(props, "gcnArchName", ""),
                      "cus": props.multi_processor_count}

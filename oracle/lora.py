@@ -49,3 +49,16 @@ def fused_backward(grad_out, x, weight_eff, lora_a, lora_b, scaling, *, round_ra
     da = scaling * (u.t() @ xx)
     db = scaling * (g.t() @ t)
     return dx, da, db
+
+
+def reference_step(x, weight, lora_a, lora_b, grad_out, scaling):
+    """The reference layer's forward and backward as its own code computes them
+    (accel/fused_lora.py:32-47: products in the activation dtype, the scale
+    applied after, gradients cast to each adapter's dtype): the eager CPU path
+    bench.py times as the baseline.  Returns (y, dx, dA, dB)."""
+    y = x @ weight.t()
+    a, b = lora_a.to(x.dtype), lora_b.to(x.dtype)
+    dx = grad_out @ weight
+    da = ((grad_out @ b).transpose(-2, -1) @ x * scaling).to(lora_a.dtype)
+    db = (grad_out.transpose(-2, -1) @ (x @ a.t()) * scaling).to(lora_b.dtype)
+    return y, dx, da, db

@@ -45,3 +45,14 @@ def test_rank_rounding_only_moves_adapter_gradients():
     for e, r in zip(exact[1:], rounded[1:]):
         assert not torch.equal(e, r)
         torch.testing.assert_close(r, e, rtol=2e-2, atol=2e-2 * e.abs().max().item())
+
+
+def test_reference_step_agrees_with_the_fp64_restatement():
+    g = torch.Generator().manual_seed(8)
+    x, dy = torch.randn(33, 48, generator=g), torch.randn(33, 40, generator=g)
+    w, a, b = torch.randn(40, 48, generator=g), torch.randn(6, 48, generator=g), torch.randn(40, 6, generator=g)
+    y, dx, da, db = ref.reference_step(x, w, a, b, dy, 1.5)
+    want = ref.fused_backward(dy, x, w, a, b, 1.5)
+    torch.testing.assert_close(y.double(), ref.fused_forward(x, w), rtol=1e-5, atol=1e-4)
+    for got, exp in zip((dx, da, db), want):
+        torch.testing.assert_close(got.double(), exp, rtol=1e-5, atol=1e-4)

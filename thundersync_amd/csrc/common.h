@@ -283,6 +283,14 @@ template <> __device__ __forceinline__ void store8<float>(float* p, const float 
 void set_error(const char* fmt, ...);
 int check_launch(const char* what);
 
+// out [rows, dim] (bf16) = lhs [rows, vocab] . W [vocab, dim] on the MFMA core
+// (the logprob grad-hidden GEMM), launches timed under `label` and, for the
+// split-sum pass, `reduce_label`.  Defined in logprob.hip; the C entry
+// ts_logprob_grad_hidden documents the arguments.
+int grad_hidden_launch(const void* dlogits, int64_t ld_dlogits, const void* weight, int64_t ld_weight, int64_t rows,
+                       int64_t dim, int64_t vocab, void* grad_hidden, int64_t ld_grad, void* workspace,
+                       int64_t workspace_bytes, void* stream, const char* label, const char* reduce_label);
+
 }  // namespace ts
 
 #define TS_CHECK_ARG(cond, ...)            \

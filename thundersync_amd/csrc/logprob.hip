@@ -572,9 +572,13 @@ int64_t ts_logprob_grad_hidden_workspace(int64_t rows, int64_t dim, int64_t voca
   return ksplit > 1 ? (int64_t)ksplit * rows * dim * (int64_t)sizeof(float) : 0;
 }
 
-int ts_logprob_grad_hidden(const void* dlogits, int64_t ld_dlogits, const void* weight, int64_t ld_weight,
-                           int64_t rows, int64_t dim, int64_t vocab, void* grad_hidden, int64_t ld_grad,
-                           void* workspace, int64_t workspace_bytes, void* stream) {
+}  // extern "C"
+
+namespace ts {
+
+int grad_hidden_launch(const void* dlogits, int64_t ld_dlogits, const void* weight, int64_t ld_weight, int64_t rows,
+                       int64_t dim, int64_t vocab, void* grad_hidden, int64_t ld_grad, void* workspace,
+                       int64_t workspace_bytes, void* stream, const char* label, const char* reduce_label) {
   using namespace ts::lp;
   TS_CHECK_ARG(rows >= 0 && dim > 0 && vocab > 0 && rows < (1 << 30) && dim < (1 << 20) && vocab < (1 << 30),
                "ts_logprob_grad_hidden: bad shape");
@@ -606,7 +610,7 @@ int ts_logprob_grad_hidden(const void* dlogits, int64_t ld_dlogits, const void* 
                  (long long)ts_logprob_grad_hidden_workspace(rows, dim, vocab));
   hipStream_t s = (hipStream_t)stream;
   {
-    ts::TimedLaunch timed_("logprob.grad_hidden_kernel", s);
+    ts::TimedLaunch timed_(label, s);
     hipLaunchKernelGGL(grad_hidden_kernel, dim3((unsigned)(a.n_ttiles * a.n_dtiles * a.ksplit)), dim3(kGemmThreads),
                        0, s, a);
   }
@@ -614,11 +618,23 @@ int ts_logprob_grad_hidden(const void* dlogits, int64_t ld_dlogits, const void* 
   if (st != TS_OK || a.ksplit == 1) return st;
   const int64_t quads = rows * dim / 4;
   {
-    ts::TimedLaunch timed_("logprob.grad_hidden_reduce_kernel", s);
+    ts::TimedLaunch timed_(reduce_label, s);
     hipLaunchKernelGGL(grad_hidden_reduce_kernel, dim3((unsigned)((quads + kThreads - 1) / kThreads)), dim3(kThreads),
                        0, s, (const float*)workspace, a.ksplit, (int)rows, (int)dim, (ts::bf16*)grad_hidden, ld_grad);
   }
   return ts::check_launch("ts_logprob_grad_hidden (reduce)");
+}
+
+}  // namespace ts
+
+extern "C" {
+
+int ts_logprob_grad_hidden(const void* dlogits, int64_t ld_dlogits, const void* weight, int64_t ld_weight,
+                           int64_t rows, int64_t dim, int64_t vocab, void* grad_hidden, int64_t ld_grad,
+                           void* workspace, int64_t workspace_bytes, void* stream) {
+  return ts::grad_hidden_launch(dlogits, ld_dlogits, weight, ld_weight, rows, dim, vocab, grad_hidden, ld_grad,
+                                workspace, workspace_bytes, stream, "logprob.grad_hidden_kernel",
+                                "logprob.grad_hidden_reduce_kernel");
 }
 
 int ts_logprob_grad_weight(const void* dlogits, int64_t ld_dlogits, const void* hidden, int64_t ld_hidden,

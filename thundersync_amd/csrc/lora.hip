@@ -341,8 +341,9 @@ int ts_lora_bwd(const void* grad_out, int64_t ld_grad_out, const void* x, int64_
   float* part_b = reinterpret_cast<float*>(ws + 2 * L.rank_bytes + L.part_a);
   void* dx_ws = ws + 2 * L.rank_bytes + L.part_a + L.part_b;
   if (grad_x) {
-    const int st = ts_logprob_grad_hidden(grad_out, ld_grad_out, weight, ld_weight, rows, in_features,
-                                          out_features, grad_x, ld_grad_x, dx_ws, L.dx, stream);
+    const int st = ts::grad_hidden_launch(grad_out, ld_grad_out, weight, ld_weight, rows, in_features, out_features,
+                                          grad_x, ld_grad_x, dx_ws, L.dx, stream, "lora.grad_x_kernel",
+                                          "lora.grad_x_reduce_kernel");
     if (st != TS_OK) return st;
   }
   if (!want_a && !want_b) return TS_OK;
