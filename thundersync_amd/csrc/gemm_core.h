@@ -20,8 +20,17 @@
 namespace ts {
 namespace gemm {
 
-constexpr int kGemmThreads = 512;  // GEMM work-groups: 8 waves, 2 per SIMD
-constexpr int NI = 2;              // 32-column B blocks per wave (wave tile 128 x 64)
+#ifndef TS_GEMM_WAVES
+#define TS_GEMM_WAVES 8
+#endif
+// waves per work-group: 8 (two per SIMD, wave tile 128 x 64) or 4 (one per
+// SIMD, wave tile 128 x 128); wave w covers A rows 128 (w & 1) .. and B rows
+// 32 NI (w >> 1) ..
+constexpr int kWaves = TS_GEMM_WAVES;
+static_assert(kWaves == 8 || kWaves == 4, "8 or 4 waves per GEMM work-group");
+constexpr int kGemmThreads = 64 * kWaves;
+constexpr int NI = 16 / kWaves;         // 32-column B blocks per wave
+constexpr int kDmaPerWave = 16 / kWaves;  // DMA instructions per operand, wave and stage
 constexpr int TM = 256;  // A rows (vocab rows, or hidden dims) per work-group
 constexpr int TN = 256;  // B rows (tokens) per work-group
 constexpr int TK = 32;   // K per LDS stage
@@ -50,7 +59,7 @@ __device__ __forceinline__ void grouped_tile(int id, int n_a, int n_b, int& ta, 
 }
 
 // One operand's share of a stage: 256 rows x 64 bytes = 16 instructions of 16
-// rows each, issued by the 8 waves as t = wave + 8 u.  Lane i of an
+// rows each, issued by the waves as t = wave + kWaves u.  Lane i of an
 // instruction fills row 16 t + i / 4, slot i & 3 with the logical 16-byte
 // chunk c = (i & 3) ^ (i >> 4): row r's chunk c sits at slot c ^ ((r >> 2) & 3),
 // so the 16 rows of a fragment read at one chunk hit 16 distinct bank groups.
@@ -59,7 +68,7 @@ struct Streamer {
   int64_t ld;
   int rows;          // valid rows from base (>= 1)
   int K;
-  int voff[2];       // byte offset of this lane's row and chunk within a stage, per u
+  int voff[kDmaPerWave];  // byte offset of this lane's row and chunk within a stage, per u
   int kchunk;        // this lane's chunk start within a stage (elements)
   __device__ __forceinline__ void init(const bf16* b, int64_t ld_, int rows_, int K_, int wave, int lane) {
     base = b;
@@ -68,7 +77,8 @@ struct Streamer {
     K = K_;
     kchunk = 8 * ((lane & 3) ^ (lane >> 4));
 #pragma unroll
-    for (int u = 0; u < 2; ++u) voff[u] = (int)(((16 * (wave + 8 * u) + (lane >> 2)) * ld + kchunk) * 2);
+    for (int u = 0; u < kDmaPerWave; ++u)
+      voff[u] = (int)(((16 * (wave + kWaves * u) + (lane >> 2)) * ld + kchunk) * 2);
   }
   // descriptor and this lane's chunk validity for K columns [k0, k0 + TK)
   __device__ __forceinline__ u32x4 descriptor(int k0) const {
@@ -77,7 +87,7 @@ struct Streamer {
   // instruction u of this wave's share of the stage into dst (wave-uniform);
   // a chunk past K reads nothing: zeros
   __device__ __forceinline__ void issue(u32x4 r, bool in_k, bf16* dst, int u, int wave) const {
-    buffer_dma16_untracked(r, dst + (wave + 8 * u) * 512, in_k ? voff[u] : 0x7ffffff0);
+    buffer_dma16_untracked(r, dst + (wave + kWaves * u) * 512, in_k ? voff[u] : 0x7ffffff0);
   }
 };
 
@@ -96,15 +106,15 @@ struct StreamerT {
   int64_t ld;        // elements between consecutive K rows
   int mvalid;        // valid M columns from base (>= 1)
   int K;
-  int voff[2];
+  int voff[kDmaPerWave];
   __device__ __forceinline__ void init(const bf16* b, int64_t ld_, int mvalid_, int K_, int wave, int lane) {
     base = b;
     ld = ld_;
     mvalid = min(mvalid_, TM);
     K = K_;
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int row = 2 * (wave + 8 * u) + (lane >> 5);
+    for (int u = 0; u < kDmaPerWave; ++u) {
+      const int row = 2 * (wave + kWaves * u) + (lane >> 5);
       const int c = (lane & 31) ^ (4 * (row & 3));
       voff[u] = (int)((row * ld + 8 * c) * 2);
     }
@@ -114,7 +124,7 @@ struct StreamerT {
     return raw_descriptor(base + (int64_t)k0 * ld, (uint32_t)(((int64_t)(rows - 1) * ld + mvalid) * 2));
   }
   __device__ __forceinline__ void issue(u32x4 r, bf16* dst, int u, int wave) const {
-    buffer_dma16_untracked(r, dst + (wave + 8 * u) * 512, voff[u]);
+    buffer_dma16_untracked(r, dst + (wave + kWaves * u) * 512, voff[u]);
   }
 };
 
@@ -169,12 +179,13 @@ template <> struct Frag<true> {
   }
 };
 
-// acc[mi][ni]: 32x32 block (A rows 128 wm + 32 mi, B rows 64 wn + 32 ni),
-// wm = wave & 1, wn = wave >> 1.  Lane l holds B row (l & 31) + 32 ni + 64 wn and A rows
-// 8 (i >> 2) + 4 (l >> 5) + (i & 3) + 32 mi + 128 wm, i = 0..15.
+// acc[mi][ni]: 32x32 block (A rows 128 wm + 32 mi, B rows 32 NI wn + 32 ni),
+// wm = wave & 1, wn = wave >> 1.  Lane l holds B row b_row(ni, l, wn) and A rows
+// a_row(mi, i, l, wm), i = 0..15.
 __device__ __forceinline__ int a_row(int mi, int i, int lane, int wm) {
   return 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3) + 32 * mi + 128 * wm;
 }
+__device__ __forceinline__ int b_row(int ni, int lane, int wn) { return 32 * NI * wn + 32 * ni + (lane & 31); }
 
 // The MFMAs of one stage (two k-steps of 16) in a fixed order.  The k-step-0
 // fragments a0 / b0 of `st` arrive already in registers (read during the
@@ -185,20 +196,25 @@ __device__ __forceinline__ int a_row(int mi, int i, int lane, int wm) {
 // issuing MFMAs while the DMA is in flight, and with the next stage's first
 // fragments in registers the MFMAs start right after the stage barrier
 // instead of waiting for LDS reads every wave issues at once.
-template <class FA, class FB, class Dma>
+template <bool HAS_NEXT, class FA, class FB, class Dma>
 __device__ __forceinline__ void mma_stage(f32x16 acc[4][NI], const bf16* st, const bf16* nx, const FA& fa,
                                           const FB& fb, bf16x8 (&a0)[4], bf16x8 (&b0)[NI], Dma&& dma) {
   bf16x8 a1[4], b1[NI];
   const bf16* sb = st + TM * TK;
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
-    acc[g][0] = mfma32(a0[g], b0[0], acc[g][0]);
-    acc[g][1] = mfma32(a0[g], b0[1], acc[g][1]);
-    if (g < 2) {
-      a1[2 * g] = fa.read(st, 1, 2 * g);
-      a1[2 * g + 1] = fa.read(st, 1, 2 * g + 1);
+#pragma unroll
+    for (int ni = 0; ni < NI; ++ni) acc[g][ni] = mfma32(a0[g], b0[ni], acc[g][ni]);
+    if constexpr (NI == 2) {
+      if (g < 2) {
+        a1[2 * g] = fa.read(st, 1, 2 * g);
+        a1[2 * g + 1] = fa.read(st, 1, 2 * g + 1);
+      } else {
+        b1[g - 2] = fb.read(sb, 1, g - 2);
+      }
     } else {
-      b1[g - 2] = fb.read(sb, 1, g - 2);
+      a1[g] = fa.read(st, 1, g);
+      b1[g] = fb.read(sb, 1, g);
     }
     dma(g);
     __builtin_amdgcn_sched_barrier(0);
@@ -207,7 +223,7 @@ __device__ __forceinline__ void mma_stage(f32x16 acc[4][NI], const bf16* st, con
   for (int mi = 0; mi < 4; ++mi) {
 #pragma unroll
     for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = mfma32(a1[mi], b1[ni], acc[mi][ni]);
-    if (nx != nullptr) {
+    if (HAS_NEXT || nx != nullptr) {
       a0[mi] = fa.read(nx, 0, mi);
       if (mi < NI) b0[mi] = fb.read(nx + TM * TK, 0, mi);
     }
@@ -215,11 +231,18 @@ __device__ __forceinline__ void mma_stage(f32x16 acc[4][NI], const bf16* st, con
   }
 }
 
-// wait until at most 4 * ahead of this wave's DMA instructions are in flight
+// wait until at most `ahead` stages of this wave's DMA instructions are in
+// flight (2 kDmaPerWave instructions per stage)
 __device__ __forceinline__ void wait_dma(int ahead) {
-  if (ahead >= 2) __builtin_amdgcn_s_waitcnt(0x0F78);       // vmcnt(8)
-  else if (ahead == 1) __builtin_amdgcn_s_waitcnt(0x0F74);  // vmcnt(4)
-  else __builtin_amdgcn_s_waitcnt(0x0F70);                  // vmcnt(0)
+  if constexpr (kDmaPerWave == 2) {
+    if (ahead >= 2) __builtin_amdgcn_s_waitcnt(0x0F78);       // vmcnt(8)
+    else if (ahead == 1) __builtin_amdgcn_s_waitcnt(0x0F74);  // vmcnt(4)
+    else __builtin_amdgcn_s_waitcnt(0x0F70);                  // vmcnt(0)
+  } else {
+    if (ahead >= 2) __builtin_amdgcn_s_waitcnt(0x4F70);       // vmcnt(16)
+    else if (ahead == 1) __builtin_amdgcn_s_waitcnt(0x0F78);  // vmcnt(8)
+    else __builtin_amdgcn_s_waitcnt(0x0F70);                  // vmcnt(0)
+  }
 }
 
 // C tile = A . B^T over K through the LDS ring s0..s3 (distinct arrays, so the
@@ -247,7 +270,7 @@ __device__ __forceinline__ void gemm_tile(f32x16 acc[4][NI], const bf16* A, int6
   Frag<AKS> fa;
   Frag<BKS> fb;
   fa.init(lane, 128 * wm);
-  fb.init(lane, 64 * wn);
+  fb.init(lane, 32 * NI * wn);
   const int nk = (K + TK - 1) / TK;
   // operand s of stage kt: descriptor, and per lane whether its chunk is in K
   // (K-strided operands bound K by the descriptor's row count instead)
@@ -263,7 +286,7 @@ __device__ __forceinline__ void gemm_tile(f32x16 acc[4][NI], const bf16* A, int6
     const u32x4 ra = sa.descriptor(kt * TK), rb = sb.descriptor(kt * TK);
     const bool ka = in_k(sa, kt * TK), kb = in_k(sb, kt * TK);
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
+    for (int u = 0; u < kDmaPerWave; ++u) {
       put(sa, ra, ka, st, u);
       put(sb, rb, kb, st + TM * TK, u);
     }
@@ -284,32 +307,51 @@ __device__ __forceinline__ void gemm_tile(f32x16 acc[4][NI], const bf16* A, int6
   // visible -- the next stage's first fragments are read during this step --
   // and certifies that all waves are done with the stage refilled next (read
   // during step kt - 1 only)
-  auto step = [&](const bf16* cur, const bf16* nxt, bf16* refill, int kt) {
+  // A FULL step (kt + 4 < nk) has a next stage and refills a stage that lies
+  // wholly inside K, so its body has no branch: the refill DMA and the next
+  // stage's fragment reads sit in the MFMAs' basic block.  The last steps
+  // take the general form.
+  auto step = [&](auto full, const bf16* cur, const bf16* nxt, bf16* refill, int kt) {
+    constexpr bool FULL = decltype(full)::value;
     __builtin_amdgcn_sched_barrier(0);  // keep each stage's loads inside its stage
-    wait_dma(max(min(nk - 2 - kt, 1), 0));
+    if constexpr (FULL) wait_dma(1);
+    else wait_dma(max(min(nk - 2 - kt, 1), 0));
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
     __builtin_amdgcn_s_barrier();
-    const bool refill_now = kt + 3 < nk;
+    const bool refill_now = FULL || kt + 3 < nk;
     const int k0 = (kt + 3) * TK;
     const u32x4 ra = sa.descriptor(refill_now ? k0 : 0), rb = sb.descriptor(refill_now ? k0 : 0);
-    const bool ka = in_k(sa, k0), kb = in_k(sb, k0);
-    mma_stage(acc, cur, kt + 1 < nk ? nxt : nullptr, fa, fb, a0, b0, [&](int g) {
+    const bool ka = FULL || in_k(sa, k0), kb = FULL || in_k(sb, k0);
+    mma_stage<FULL>(acc, cur, (FULL || kt + 1 < nk) ? nxt : nullptr, fa, fb, a0, b0, [&](int g) {
       if (refill_now) {
-        if (g < 2) put(sa, ra, ka, refill, g);
-        else put(sb, rb, kb, refill + TM * TK, g - 2);
+        if constexpr (kDmaPerWave == 2) {
+          if (g < 2) put(sa, ra, ka, refill, g);
+          else put(sb, rb, kb, refill + TM * TK, g - 2);
+        } else {
+          put(sa, ra, ka, refill, g);
+          put(sb, rb, kb, refill + TM * TK, g);
+        }
       }
     });
   };
+  constexpr std::true_type full{};
+  constexpr std::false_type general{};
   int kt = 0;
-  for (; kt + 4 <= nk; kt += 4) {
-    step(s0, s1, s3, kt);
-    step(s1, s2, s0, kt + 1);
-    step(s2, s3, s1, kt + 2);
-    step(s3, s0, s2, kt + 3);
+  for (; kt + 7 < nk; kt += 4) {
+    step(full, s0, s1, s3, kt);
+    step(full, s1, s2, s0, kt + 1);
+    step(full, s2, s3, s1, kt + 2);
+    step(full, s3, s0, s2, kt + 3);
   }
-  if (kt < nk) step(s0, s1, s3, kt);
-  if (kt + 1 < nk) step(s1, s2, s0, kt + 1);
-  if (kt + 2 < nk) step(s2, s3, s1, kt + 2);
+  for (; kt + 4 <= nk; kt += 4) {
+    step(general, s0, s1, s3, kt);
+    step(general, s1, s2, s0, kt + 1);
+    step(general, s2, s3, s1, kt + 2);
+    step(general, s3, s0, s2, kt + 3);
+  }
+  if (kt < nk) step(general, s0, s1, s3, kt);
+  if (kt + 1 < nk) step(general, s1, s2, s0, kt + 1);
+  if (kt + 2 < nk) step(general, s2, s3, s1, kt + 2);
   __builtin_amdgcn_sched_barrier(0);
   __syncthreads();
 }

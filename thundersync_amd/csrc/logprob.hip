@@ -102,7 +102,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void fwd_stats_kernel(FwdArgs p) {
   float mk[NI], sk[NI], ek[NI];  // this lane's column statistics, kept across the exchange
 #pragma unroll
   for (int ni = 0; ni < NI; ++ni) {
-    const int col = 64 * wn + 32 * ni + (lane & 31);
+    const int col = b_row(ni, lane, wn);
     float m = neg_inf();
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi)
@@ -151,7 +151,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void fwd_stats_kernel(FwdArgs p) {
   __syncthreads();  // one exchange for both column groups (their columns differ)
 #pragma unroll
   for (int ni = 0; ni < NI; ++ni) {
-    const int col = 64 * wn + 32 * ni + (lane & 31);
+    const int col = b_row(ni, lane, wn);
     const int n = n0 + col;
     if (wm == 0 && lane < 32 && n < p.rows) {
       merge_stats(mk[ni], sk[ni], ek[ni], xm[col], xs[col], xe[col]);
@@ -270,7 +270,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void dlogits_kernel(DlArgs p) {
     constexpr bool FULL = decltype(full_c)::value;
 #pragma unroll
     for (int ni = 0; ni < NI; ++ni) {
-      const int col = 64 * wn + 32 * ni + (lane & 31);  // token within the tile
+      const int col = b_row(ni, lane, wn);  // token within the tile
       bf16* out = quarter(col >> 6) + (col & 63) * OPITCH;
       const int n = n0 + col;
       float lse2 = 0.f, coef_a = 0.f, coef_b = 0.f, glp = 0.f;
@@ -364,7 +364,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void grad_hidden_kernel(DhArgs p) 
   const int wm = wave & 1, wn = wave >> 1;
 #pragma unroll
   for (int ni = 0; ni < NI; ++ni) {
-    const int n = n0 + 64 * wn + 32 * ni + (lane & 31);
+    const int n = n0 + b_row(ni, lane, wn);
     if (n >= p.rows) continue;
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi)
@@ -435,7 +435,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void grad_weight_kernel(DwArgs p) 
   const int wm = wave & 1, wn = wave >> 1;
 #pragma unroll
   for (int ni = 0; ni < NI; ++ni) {
-    const int d = d0 + 64 * wn + 32 * ni + (lane & 31);
+    const int d = d0 + b_row(ni, lane, wn);
     if (d >= p.dim) continue;
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi)

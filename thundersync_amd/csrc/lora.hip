@@ -69,7 +69,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void lora_fwd_kernel(FwdArgs p) {
   auto quarter = [&](int q) -> bf16* { return q == 0 ? s0 : q == 1 ? s1 : q == 2 ? s2 : s3; };
 #pragma unroll
   for (int ni = 0; ni < NI; ++ni) {
-    const int col = 64 * wn + 32 * ni + (lane & 31);  // row of x / y within the tile
+    const int col = b_row(ni, lane, wn);  // row of x / y within the tile
     bf16* o = quarter(col >> 6) + (col & 63) * OPITCH;
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi)
@@ -129,7 +129,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void lora_rank_kernel(RankArgs p) 
   // padding columns of out^T are written from them
 #pragma unroll
   for (int ni = 0; ni < NI; ++ni) {
-    const int r = 64 * wn + 32 * ni + (lane & 31);
+    const int r = b_row(ni, lane, wn);
     if (r >= p.rank) continue;
     bf16* o = job.out + (int64_t)r * p.ld_out;
 #pragma unroll
@@ -173,7 +173,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void lora_grad_a_kernel(AdapterArg
   float* part = p.part + (int64_t)s * p.rank * p.width;
 #pragma unroll
   for (int ni = 0; ni < NI; ++ni) {
-    const int k = k0 + 64 * wn + 32 * ni + (lane & 31);
+    const int k = k0 + b_row(ni, lane, wn);
     if (k >= p.width) continue;
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi)
@@ -198,7 +198,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void lora_grad_b_kernel(AdapterArg
   float* part = p.part + (int64_t)s * p.width * p.rank;
 #pragma unroll
   for (int ni = 0; ni < NI; ++ni) {
-    const int r = 64 * wn + 32 * ni + (lane & 31);
+    const int r = b_row(ni, lane, wn);
     if (r >= p.rank) continue;
 #pragma unroll
     for (int mi = 0; mi < 4; ++mi)
