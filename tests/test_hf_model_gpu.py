@@ -10,8 +10,10 @@
   log-softmax.  Gated and ungated projection agree.
 
 Bars: relative Frobenius error 3e-2 for hidden states and gradients (bf16
-weights and activations through two layers against fp32); 0.1 nat absolute for
-log-probabilities of a near-uniform random model (|log p| ~ 5).
+weights and activations through two layers against fp32); 2e-2 nat absolute
+for log-probabilities of a near-uniform random model (|log p| ~ 5) against the
+fp32 CPU model (measured: under 5e-3), and 5e-3 nat against the same bf16 model
+run on each trajectory alone, where only the packing differs (measured: 0).
 """
 
 from __future__ import annotations
@@ -109,4 +111,20 @@ def test_forest_logprobs_in_model(cuda):
         assert got.shape == want.shape, (i, got.shape, want.shape)
         err = (got - want).abs().max().item()
         print(f"  trajectory {i}: {got.numel()} scored tokens, max |diff| {err:.3e}", flush=True)
-        assert err < 0.1
+        assert err < 2e-2
+    # the same bf16 model on the GPU, each trajectory alone through the causal
+    # adapter and the fused head: only the packing differs, so the forest's
+    # logprobs agree to the bf16 rounding of the attention outputs
+    from thundersync_amd.attention import HIP_ATTENTION_NAME
+    from thundersync_amd.fused_logprob import fused_logprob
+    from thundersync_amd.step import unembedding
+
+    gpu.set_attn_implementation(HIP_ATTENTION_NAME)
+    for i, body in enumerate(bodies):
+        ids = torch.tensor(prompt + body, device=cuda)
+        with torch.no_grad():
+            hidden = gpu.model(input_ids=ids[None]).last_hidden_state[0]
+            alone = fused_logprob(hidden[len(prompt) - 1 : -1], unembedding(gpu), ids[len(prompt):])
+        err = (per[i] - alone).abs().max().item()
+        print(f"  trajectory {i}: forest vs alone (same bf16 model) max |diff| {err:.3e}", flush=True)
+        assert err < 5e-3
