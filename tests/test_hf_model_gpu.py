@@ -128,3 +128,79 @@ def test_forest_logprobs_in_model(cuda):
         err = (per[i] - alone).abs().max().item()
         print(f"  trajectory {i}: forest vs alone (same bf16 model) max |diff| {err:.3e}", flush=True)
         assert err < 5e-3
+
+
+def test_lora_grpo_update_through_the_build(cuda):
+    """The C5 update's path at small scale: a bf16 Qwen3 with fp32 LoRA adapters
+    on q/k/v/o, the forest attention adapter, the HIP RMSNorm modules, per-layer
+    activation checkpointing, the merged-weight LoRA layers and the fused head,
+    one reward-linear loss over a shared-prompt forest -- against the unmerged
+    fp32 model on the CPU, trajectory by trajectory with its stock attention.
+    Bars: the loss within 1e-2 relative, every adapter gradient within 3e-2
+    relative Frobenius error (bf16 weights, merged weight and activations
+    through two layers, forward and backward, against fp32)."""
+    from thundersync_amd import forest
+    from thundersync_amd.attention import HIP_FOREST_ATTENTION_NAME, forest_context, register_attention
+    from thundersync_amd.fused_lora import fuse_merged_lora_forward, unfuse_merged_lora_forward
+    from thundersync_amd.lora_layers import LoraLinear, add_lora
+    from thundersync_amd.rms_norm import use_stable_qwen3_rms_norm
+    from thundersync_amd.step import forest_logprobs, split_by_trajectory
+
+    print("LoRA GRPO update through the build vs the unmerged fp32 model", flush=True)
+    assert register_attention()
+    ref = tiny_model(seed=5)
+    assert add_lora(ref, ["q_proj", "k_proj", "v_proj", "o_proj"], rank=8, alpha=16) == 8
+    g = torch.Generator().manual_seed(6)
+    with torch.no_grad():
+        for m in ref.modules():
+            if isinstance(m, LoraLinear):
+                for p in (m.lora_A["default"].weight, m.lora_B["default"].weight):
+                    p.copy_((torch.randn(p.shape, generator=g) * 0.05).to(torch.bfloat16).float())
+    gpu = copy.deepcopy(ref).to(device=cuda, dtype=torch.bfloat16)
+    for m in gpu.modules():
+        if isinstance(m, LoraLinear):
+            m.lora_A.float()
+            m.lora_B.float()
+    gpu.set_attn_implementation(HIP_FOREST_ATTENTION_NAME)
+    use_stable_qwen3_rms_norm(gpu)
+    gpu.gradient_checkpointing_enable(gradient_checkpointing_kwargs={"use_reentrant": False})
+    gpu.train()
+
+    prompt = torch.randint(0, 96, (40,), generator=g).tolist()
+    bodies = [torch.randint(0, 96, (n,), generator=g).tolist() for n in (25, 31, 17)]
+    adv = {0: 1.0, 1: -0.25, 2: -0.75}
+    trajs = [forest.Trajectory([forest.Segment.prompt(prompt), forest.Segment.action(b)], group_id=0, traj_id=i)
+             for i, b in enumerate(bodies)]
+    plan = forest.compile_plan(forest.build_forest(trajs)).to(cuda)
+    n_tokens = sum(len(b) for b in bodies)
+
+    assert fuse_merged_lora_forward(gpu) == 8
+    with forest_context(plan):
+        lp = forest_logprobs(gpu, plan)
+        per = split_by_trajectory(plan, lp)
+        loss = -sum(adv[t] * v.sum() for t, v in per.items()) / lp.numel()
+        loss.backward()
+    torch.cuda.synchronize()
+    assert unfuse_merged_lora_forward(gpu) == 8
+    assert lp.numel() == n_tokens
+
+    want = torch.zeros(())
+    for i, body in enumerate(bodies):
+        tokens = torch.tensor(prompt + body)
+        logits = ref(input_ids=tokens[None]).logits[0]
+        lp_i = torch.log_softmax(logits, -1)[len(prompt) - 1 : -1].gather(1, tokens[len(prompt):, None])[:, 0]
+        want = want - adv[i] * lp_i.sum() / n_tokens
+    want.backward()
+    err = abs(loss.item() - want.item()) / abs(want.item())
+    print(f"  loss {loss.item():.6f} vs {want.item():.6f} (relative {err:.2e})", flush=True)
+    assert err < 1e-2
+    got = {n: p.grad for n, p in gpu.named_parameters() if p.grad is not None}
+    exp = {n: p.grad for n, p in ref.named_parameters() if p.grad is not None}
+    assert set(got) == set(exp) and len(got) == 16
+    worst = 0.0
+    for name in sorted(exp):
+        assert got[name].dtype == torch.float32, name
+        e = rel(got[name], exp[name])
+        worst = max(worst, e)
+        assert e < 3e-2, (name, e)
+    print(f"  16 adapter gradients: worst relative error {worst:.2e}", flush=True)
