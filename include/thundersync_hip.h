@@ -97,7 +97,7 @@ int ts_rmsnorm_bwd_noalloc(const void* dy, const void* x, const void* w,
                            int64_t width, int dtype, void* stream);
 
 /* ------------------------------------------------------------------------
- * Forest / packed bottom-right-causal GQA attention (bf16, head_dim 128)
+ * Forest / packed bottom-right-causal GQA attention (bf16 or fp16, head_dim 128)
  *
  * A problem is a set of query SEGMENTS and key RUNS.  Segment s owns query
  * rows [q_row0, q_row0 + q_len) of the packed Q/O/dO/dQ tensors
@@ -175,6 +175,7 @@ typedef struct ts_attn_problem {
    * last-level cache).  0 <= n_*_long <= n_*_work. */
   int32_t n_q_long;
   int32_t n_kv_long;
+  int32_t dtype;  /* element type of Q/K/V/O/dO/dQ/dK/dV: TS_BF16 or TS_F16 */
 } ts_attn_problem;
 
 /* Query heads one forward/dQ work-group processes for a GQA group size
@@ -239,10 +240,11 @@ int ts_attn_bwd(const ts_attn_problem* problem, ts_attn_rows q, ts_attn_rows out
                 ts_attn_rows dq, void* stream);
 
 /* ------------------------------------------------------------------------
- * Fused chunked-vocab logprob / entropy (bf16 operands, fp32 results)
+ * Fused chunked-vocab logprob / entropy (bf16 or fp16 operands, fp32 results)
  *
  * hidden [rows, dim] (row stride ld_hidden), weight [vocab, dim] (ld_weight),
- * target int64 [rows].  dim and both leading dimensions are multiples of 8
+ * target int64 [rows]; hidden, weight, dlogits and grad_hidden share the
+ * element type `dtype` (TS_BF16 or TS_F16).  dim and both leading dimensions are multiples of 8
  * and the bases 16-byte aligned; leading dimensions are below 2^30 / 255
  * elements (a 256-row tile's byte offsets fit 32 bits).  A target outside
  * [0, vocab) is not an error: its logprob is NaN and its dlogits row takes
@@ -263,7 +265,7 @@ int ts_logprob_fwd(const void* hidden, int64_t ld_hidden, const void* weight,
                    int64_t ld_weight, const int64_t* target, int64_t rows,
                    int64_t dim, int64_t vocab, float* logprob, float* entropy,
                    float* lse, void* workspace, int64_t workspace_bytes,
-                   void* stream);
+                   int dtype, void* stream);
 
 /* dlogits [rows, ld_dlogits] (bf16) =
  *   -p * (g_lp + g_ent * (log p + H)) + g_lp * onehot(target),
@@ -277,7 +279,7 @@ int ts_logprob_dlogits(const void* hidden, int64_t ld_hidden, const void* weight
                        const float* entropy, const float* grad_lp,
                        const float* grad_ent, int64_t rows, int64_t dim,
                        int64_t vocab, void* dlogits, int64_t ld_dlogits,
-                       void* stream);
+                       int dtype, void* stream);
 
 /* Workspace bytes ts_logprob_grad_hidden needs for rows x dim x vocab (0
  * when the row tiles alone fill the device and no vocabulary split is made). */
@@ -294,7 +296,7 @@ int64_t ts_logprob_grad_hidden_workspace(int64_t rows, int64_t dim, int64_t voca
 int ts_logprob_grad_hidden(const void* dlogits, int64_t ld_dlogits, const void* weight,
                            int64_t ld_weight, int64_t rows, int64_t dim, int64_t vocab,
                            void* grad_hidden, int64_t ld_grad, void* workspace,
-                           int64_t workspace_bytes, void* stream);
+                           int64_t workspace_bytes, int dtype, void* stream);
 
 /* grad_weight [vocab, ld_grad] (fp32) += dlogits[:rows]^T . hidden[:rows]
  * on MFMA with fp32 accumulation; called once per dlogits block, it
@@ -305,21 +307,23 @@ int ts_logprob_grad_hidden(const void* dlogits, int64_t ld_dlogits, const void* 
  * (accel/fused_logprob.py:176-193, :304-306). */
 int ts_logprob_grad_weight(const void* dlogits, int64_t ld_dlogits, const void* hidden,
                            int64_t ld_hidden, int64_t rows, int64_t dim, int64_t vocab,
-                           float* grad_weight, int64_t ld_grad, void* stream);
+                           float* grad_weight, int64_t ld_grad, int dtype, void* stream);
 
 /* ------------------------------------------------------------------------
- * Merged-weight LoRA linear (bf16 operands, fp32 accumulation)
+ * Merged-weight LoRA linear (bf16 or fp16 operands, fp32 accumulation)
  *
  * The caller has merged the adapters into the weight (W_eff = W + s B A,
  * [out, in]); lora_a is A [rank, in] and lora_b_t is B transposed,
- * [rank, out], both bf16 with rows of in / out elements.  Rows of x, y, g
+ * [rank, out], both in the activations' dtype with rows of in / out
+ * elements; `dtype` (TS_BF16 or TS_F16) is that of x, the weight, the
+ * adapters, y, grad_out and grad_x.  Rows of x, y, g
  * and the weight are 16-byte aligned, in and out multiples of 8.
  * ------------------------------------------------------------------------ */
 
 /* y [rows, out] = x [rows, in] . W_eff^T.
  * Replaces FusedLoRALinear.forward (accel/fused_lora.py:29-33). */
 int ts_lora_fwd(const void* x, int64_t ld_x, const void* weight, int64_t ld_weight, int64_t rows,
-                int64_t in_features, int64_t out_features, void* y, int64_t ld_y, void* stream);
+                int64_t in_features, int64_t out_features, void* y, int64_t ld_y, int dtype, void* stream);
 
 /* Workspace bytes ts_lora_bwd needs. */
 int64_t ts_lora_bwd_workspace(int64_t rows, int64_t in_features, int64_t out_features, int64_t rank);
@@ -334,7 +338,8 @@ int64_t ts_lora_bwd_workspace(int64_t rows, int64_t in_features, int64_t out_fea
 int ts_lora_bwd(const void* grad_out, int64_t ld_grad_out, const void* x, int64_t ld_x, const void* weight,
                 int64_t ld_weight, const void* lora_a, const void* lora_b_t, int64_t rank, float scaling,
                 int64_t rows, int64_t in_features, int64_t out_features, void* grad_x, int64_t ld_grad_x,
-                float* grad_a, float* grad_b, void* workspace, int64_t workspace_bytes, void* stream);
+                float* grad_a, float* grad_b, void* workspace, int64_t workspace_bytes, int dtype,
+                void* stream);
 
 /* ------------------------------------------------------------------------
  * Boundary adjoints

@@ -45,6 +45,7 @@ class AttnProblem(ctypes.Structure):
         ("q_rows", ctypes.c_int64),
         ("n_q_long", ctypes.c_int32),
         ("n_kv_long", ctypes.c_int32),
+        ("dtype", ctypes.c_int32),
     ]
 
 
@@ -55,4 +56,4 @@ class AttnRows(ctypes.Structure):
 
 
 assert SEG_DTYPE.itemsize == 24 and REF_DTYPE.itemsize == 8 and RUN_DTYPE.itemsize == 112
-assert ctypes.sizeof(AttnProblem) == 104 and ctypes.sizeof(AttnRows) == 24
+assert ctypes.sizeof(AttnProblem) == 112 and ctypes.sizeof(AttnRows) == 24

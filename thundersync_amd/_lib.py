@@ -51,20 +51,20 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "ts_timing_reset": (_INT, []),
     "ts_timing_read": (_INT, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_I64)]),
     "ts_logprob_fwd_workspace": (_I64, [_I64, _I64]),
-    "ts_logprob_fwd": (_INT, [_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _P, _P, _P, _P, _I64, _P]),
+    "ts_logprob_fwd": (_INT, [_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _P, _P, _P, _P, _I64, _INT, _P]),
     "ts_logprob_dlogits": (
         _INT,
-        [_P, _I64, _P, _I64, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P, _I64, _P],
+        [_P, _I64, _P, _I64, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P, _I64, _INT, _P],
     ),
     "ts_logprob_grad_hidden_workspace": (_I64, [_I64, _I64, _I64]),
-    "ts_logprob_grad_hidden": (_INT, [_P, _I64, _P, _I64, _I64, _I64, _I64, _P, _I64, _P, _I64, _P]),
-    "ts_logprob_grad_weight": (_INT, [_P, _I64, _P, _I64, _I64, _I64, _I64, _P, _I64, _P]),
-    "ts_lora_fwd": (_INT, [_P, _I64, _P, _I64, _I64, _I64, _I64, _P, _I64, _P]),
+    "ts_logprob_grad_hidden": (_INT, [_P, _I64, _P, _I64, _I64, _I64, _I64, _P, _I64, _P, _I64, _INT, _P]),
+    "ts_logprob_grad_weight": (_INT, [_P, _I64, _P, _I64, _I64, _I64, _I64, _P, _I64, _INT, _P]),
+    "ts_lora_fwd": (_INT, [_P, _I64, _P, _I64, _I64, _I64, _I64, _P, _I64, _INT, _P]),
     "ts_lora_bwd_workspace": (_I64, [_I64, _I64, _I64, _I64]),
     "ts_lora_bwd": (
         _INT,
         [_P, _I64, _P, _I64, _P, _I64, _P, _P, _I64, ctypes.c_float, _I64, _I64, _I64, _P, _I64, _P, _P, _P, _I64,
-         _P],
+         _INT, _P],
     ),
     "ts_adjoint_reduce": (_INT, [ctypes.POINTER(_P), _INT, _P, _P, _I64, _INT, _P]),
     "ts_ledger_add": (_INT, [_P, _P, _I64, _INT, _INT, _P]),

@@ -36,7 +36,8 @@ Reference entry points mirrored here (same argument meaning):
   launch, each chunk being the call ``_ChunkedCausalSDPA`` makes
   (engine/streaming.py:1314-1423).
 
-There is no host path: CPU tensors, unsupported dtypes or head dims raise.
+Element types: bf16 and fp16 (Q, K, V of one call share one), head dim 128.
+There is no host path: CPU tensors, other dtypes or head dims raise.
 """
 
 from __future__ import annotations
@@ -56,6 +57,7 @@ from .dispatch import HIP_BACKWARD_PATH, HIP_PATH, count_attention_path
 from .operator_profiling import operator_range
 
 HEAD_DIM = 128
+ELEMENT_DTYPES = (torch.bfloat16, torch.float16)
 
 
 def heads_per_block(group: int) -> int:
@@ -194,7 +196,7 @@ class AttnLayout:
             kv_costs = []
         group = self.hq // self.hkv
         # rows the forward / dQ work-groups re-read: K and V of every run; the
-        # dK/dV work-groups: Q and dO of every row (bf16, all heads)
+        # dK/dV work-groups: Q and dO of every row (2-byte elements, all heads)
         kv_bytes = sum(run.length for run in self.runs) * self.hkv * HEAD_DIM * 2 * 2
         q_bytes = self.q_rows * self.hq * HEAD_DIM * 2 * 2
         q_long = _long_items([-c for c, _, _ in q_items], self.hkv * (group // heads_per_block(group)), kv_bytes)
@@ -245,13 +247,13 @@ class AttnLayout:
                 self._tables[key] = hit
         return hit
 
-    def problem(self, device, runs_ptr: int, scale: float) -> AttnProblem:
+    def problem(self, device, runs_ptr: int, scale: float, dtype: torch.dtype = torch.bfloat16) -> AttnProblem:
         t = self.device_tables(device)
         return AttnProblem(
             t["segs"], t["seg_spans"], runs_ptr, t["run_visits"], t["q_work"], t["kv_work"],
             t["n_q_work"], t["n_kv_work"], len(self.seg_q), len(self.runs), self.hq, self.hkv,
             HEAD_DIM, float(scale), q_block_rows(self.hq, self.hkv), kv_block_keys(self.hq, self.hkv), self.q_rows,
-            t["n_q_long"], t["n_kv_long"],
+            t["n_q_long"], t["n_kv_long"], _lib.dtype_code(dtype),
         )
 
     # -- reference diagnostics ---------------------------------------------
@@ -356,8 +358,8 @@ def check_tables(layout: AttnLayout, problem: AttnProblem, run_table: np.ndarray
 def _validate_call(layout: AttnLayout, query: torch.Tensor, keys, values) -> None:
     if not query.is_cuda:
         raise RuntimeError("thundersync_amd attention runs on the GPU only; got a CPU tensor")
-    if query.dtype != torch.bfloat16:
-        raise TypeError(f"thundersync_amd attention takes bf16, got {query.dtype}")
+    if query.dtype not in ELEMENT_DTYPES:
+        raise TypeError(f"thundersync_amd attention takes bf16 or fp16, got {query.dtype}")
     _check_rows_tensor(query, "query", layout.hq)
     if query.shape[0] != layout.q_rows:
         raise ValueError(f"query has {query.shape[0]} rows, layout {layout.q_rows}")
@@ -383,7 +385,7 @@ class _Attention(torch.autograd.Function):
         out = torch.empty(query.shape, dtype=query.dtype, device=query.device)
         lse = torch.empty(layout.hq, max(layout.q_rows, 1), dtype=torch.float32, device=query.device)
         runs, host = _run_table(layout, keys, values)
-        problem = layout.problem(query.device, runs.data_ptr(), scale)
+        problem = layout.problem(query.device, runs.data_ptr(), scale, query.dtype)
         check_tables(layout, problem, host, query.device)
         with operator_range("hip_attention_forward", rows=layout.q_rows, segments=len(layout.seg_q)):
             _lib.check(
@@ -424,7 +426,7 @@ class _Attention(torch.autograd.Function):
                 dvalues[i].zero_()
         runs, host = _run_table(layout, keys, values, dkeys, dvalues)
         rowstats = torch.empty(layout.hq, max(layout.q_rows, 1), 2, dtype=torch.float32, device=query.device)
-        problem = layout.problem(query.device, runs.data_ptr(), ctx.scale)
+        problem = layout.problem(query.device, runs.data_ptr(), ctx.scale, query.dtype)
         check_tables(layout, problem, host, query.device)
         with operator_range("hip_attention_backward", rows=layout.q_rows, segments=len(layout.seg_q)):
             _lib.check(
@@ -440,7 +442,7 @@ class _Attention(torch.autograd.Function):
 
 def attention(query: torch.Tensor, layout: AttnLayout, keys: Sequence[torch.Tensor],
               values: Sequence[torch.Tensor], scale: float) -> tuple[torch.Tensor, torch.Tensor]:
-    """Core op: query ``[R, Hq, 128]`` bf16 -> (out ``[R, Hq, 128]``, lse ``[Hq, R]`` fp32)."""
+    """Core op: query ``[R, Hq, 128]`` bf16 or fp16 -> (out ``[R, Hq, 128]``, lse ``[Hq, R]`` fp32)."""
     return _Attention.apply(query, layout, float(scale), len(keys), *keys, *values)
 
 

@@ -29,6 +29,9 @@
 
 #include "attention_impl.h"
 
+// the host mirrors (thundersync_amd/_abi.py) assume these sizes
+static_assert(sizeof(ts_attn_problem) == 112 && sizeof(ts_attn_rows) == 24, "ts_attn ABI layout");
+
 namespace ts {
 namespace attn {
 
@@ -43,6 +46,7 @@ bool aligned_rows(const ts_attn_rows& r) {
 int validate(const ts_attn_problem* p, const char* what) {
   TS_CHECK_ARG(p != nullptr, "%s: null problem", what);
   TS_CHECK_ARG(p->head_dim == D, "%s: head_dim %d unsupported (128 only)", what, p->head_dim);
+  TS_CHECK_ARG(p->dtype == kBF16 || p->dtype == kF16, "%s: dtype %d unsupported (bf16 or fp16)", what, p->dtype);
   TS_CHECK_ARG(p->hq > 0 && p->hkv > 0 && p->hq % p->hkv == 0, "%s: hq %d not a multiple of hkv %d",
                what, p->hq, p->hkv);
   const int gc = heads_per_block(p->hq / p->hkv);

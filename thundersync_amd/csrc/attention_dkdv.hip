@@ -7,6 +7,7 @@ namespace attn {
 // ---------------------------------------------------------------------------
 // backward dK / dV (key-stationary)
 // ---------------------------------------------------------------------------
+template <typename E>
 __global__ __launch_bounds__(kThreads, 2) void dkdv_kernel(ts_attn_problem P, ts_attn_rows Q,
                                                            ts_attn_rows dO, const float* __restrict__ rowstats,
                                                            int64_t lse_ld) {
@@ -95,8 +96,8 @@ __global__ __launch_bounds__(kThreads, 2) void dkdv_kernel(ts_attn_problem P, ts
             const int r = 16 * qb + (lane & 15);
             const bf16x8 aq = as_bf16x8(ld16(sq + r * PITCH + 32 * ks + 8 * (lane >> 4)));
             const bf16x8 ad = as_bf16x8(ld16(sd + r * PITCH + 32 * ks + 8 * (lane >> 4)));
-            s[qb] = mfma16(aq, kreg[ks], s[qb]);
-            dp[qb] = mfma16(ad, vreg[ks], dp[qb]);
+            s[qb] = mma16<E>(aq, kreg[ks], s[qb]);
+            dp[qb] = mma16<E>(ad, vreg[ks], dp[qb]);
           }
         }
         float pv[8], dsv[8];
@@ -110,17 +111,17 @@ __global__ __launch_bounds__(kThreads, 2) void dkdv_kernel(ts_attn_problem P, ts
             pv[4 * qb + i] = p;
             dsv[4 * qb + i] = p * (dp[qb][i] - s_dlt[rl]);
           }
-        const bf16x8 pk = pack8(pv);
-        const bf16x8 dsk = pack8(dsv);
+        const bf16x8 pk = pack8<E>(pv);
+        const bf16x8 dsk = pack8<E>(dsv);
         int rows[8];
         slot_rows(lane >> 4, 0, rows);
         bf16x8 at[8];
         lds_rows_transposed(sd, rows, 8 * (lane & 15), at);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) dv[e] = mfma16(at[e], pk, dv[e]);
+        for (int e = 0; e < 8; ++e) dv[e] = mma16<E>(at[e], pk, dv[e]);
         lds_rows_transposed(sq, rows, 8 * (lane & 15), at);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) dk[e] = mfma16(at[e], dsk, dk[e]);
+        for (int e = 0; e < 8; ++e) dk[e] = mma16<E>(at[e], dsk, dk[e]);
       }
     }
   }
@@ -133,7 +134,7 @@ __global__ __launch_bounds__(kThreads, 2) void dkdv_kernel(ts_attn_problem P, ts
       float tmp[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) tmp[e] = dk[e][i] * P.scale;
-      st16(p + 8 * i, as_u32x4(pack8(tmp)));
+      st16(p + 8 * i, as_u32x4(pack8<E>(tmp)));
     }
   }
   if (run.dv) {
@@ -144,7 +145,7 @@ __global__ __launch_bounds__(kThreads, 2) void dkdv_kernel(ts_attn_problem P, ts
       float tmp[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) tmp[e] = dv[e][i];
-      st16(p + 8 * i, as_u32x4(pack8(tmp)));
+      st16(p + 8 * i, as_u32x4(pack8<E>(tmp)));
     }
   }
 }
@@ -176,7 +177,7 @@ __global__ __launch_bounds__(kThreads, 2) void dkdv_kernel(ts_attn_problem P, ts
 // enters the next visit.  The per-head partials are summed across waves
 // through LDS in wave order.
 // ---------------------------------------------------------------------------
-template <int KB>
+template <typename E, int KB>
 __global__ __launch_bounds__(kThreads, 1) void dkdv_wave_kernel(ts_attn_problem P, ts_attn_rows Q,
                                                                 ts_attn_rows dO,
                                                                 const float* __restrict__ rowstats,
@@ -331,8 +332,8 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_wave_kernel(ts_attn_problem 
         for (int kb = 0; kb < KB; ++kb) {
   #pragma unroll
           for (int qb = 0; qb < 2; ++qb) {
-            sc[qb][kb] = mfma16(aq[qb], kreg[kb][ks], sc[qb][kb]);
-            dp[qb][kb] = mfma16(ad[qb], vreg[kb][ks], dp[qb][kb]);
+            sc[qb][kb] = mma16<E>(aq[qb], kreg[kb][ks], sc[qb][kb]);
+            dp[qb][kb] = mma16<E>(ad[qb], vreg[kb][ks], dp[qb][kb]);
           }
         }
       }
@@ -369,8 +370,8 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_wave_kernel(ts_attn_problem 
               pv[4 * qb + i] = p;
               dsv[4 * qb + i] = p * (dp[qb][kb][i] - dl[qb][i]);
             }
-          pk[kb] = pack8(pv);
-          dsk[kb] = pack8(dsv);
+          pk[kb] = pack8<E>(pv);
+          dsk[kb] = pack8<E>(dsv);
         }
       } else {
 #pragma unroll
@@ -384,8 +385,8 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_wave_kernel(ts_attn_problem 
               pv[4 * qb + i] = p;
               dsv[4 * qb + i] = p * (dp[qb][kb][i] - dl[qb][i]);
             }
-          pk[kb] = pack8(pv);
-          dsk[kb] = pack8(dsv);
+          pk[kb] = pack8<E>(pv);
+          dsk[kb] = pack8<E>(dsv);
         }
       }
       // dV^T += dO^T P, dK^T += Q^T dS: rows d = 16 mb + 4 g4 + i, column key;
@@ -405,8 +406,8 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_wave_kernel(ts_attn_problem 
         if (mb + 2 < 8) frag(mb + 2, a_do[(mb + 2) % 3], a_q[(mb + 2) % 3]);
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) {
-          dv[mb][kb] = mfma16(a_do[mb % 3], pk[kb], dv[mb][kb]);
-          dk[mb][kb] = mfma16(a_q[mb % 3], dsk[kb], dk[mb][kb]);
+          dv[mb][kb] = mma16<E>(a_do[mb % 3], pk[kb], dv[mb][kb]);
+          dk[mb][kb] = mma16<E>(a_q[mb % 3], dsk[kb], dk[mb][kb]);
         }
       }
       // keep the reads two blocks ahead (the scheduler otherwise pulls them
@@ -479,21 +480,28 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_wave_kernel(ts_attn_problem 
         for (int q = 0; q < 4; ++q) acc8[4 * hc + q] = sum[q] * mult;
       }
       if (base && key < nkeys)
-        st16((bf16*)base + (int64_t)(k0 + key) * rs + (int64_t)hk * hs + d8, as_u32x4(pack8(acc8)));
+        st16((bf16*)base + (int64_t)(k0 + key) * rs + (int64_t)hk * hs + d8, as_u32x4(pack8<E>(acc8)));
     }
     __syncthreads();
   }
 }
 
-int launch_dkdv(const ts_attn_problem& P, ts_attn_rows q, ts_attn_rows dout, const float* rowstats,
+template <typename E>
+int launch_dkdv_t(const ts_attn_problem& P, ts_attn_rows q, ts_attn_rows dout, const float* rowstats,
                 int64_t lse_ld, hipStream_t s) {
   const int group = P.hq / P.hkv;
   const dim3 grid((unsigned)(P.n_kv_work * P.hkv));
   if (group % 4 == 0)
-    { ts::TimedLaunch timed_("attention.dkdv_kernel", s); hipLaunchKernelGGL(dkdv_wave_kernel<3>, grid, dim3(kThreads), 0, s, P, q, dout, rowstats, lse_ld); }
+    { ts::TimedLaunch timed_("attention.dkdv_kernel", s); hipLaunchKernelGGL((dkdv_wave_kernel<E, 3>), grid, dim3(kThreads), 0, s, P, q, dout, rowstats, lse_ld); }
   else
-    { ts::TimedLaunch timed_("attention.dkdv_kernel", s); hipLaunchKernelGGL(dkdv_kernel, grid, dim3(kThreads), 0, s, P, q, dout, rowstats, lse_ld); }
+    { ts::TimedLaunch timed_("attention.dkdv_kernel", s); hipLaunchKernelGGL(dkdv_kernel<E>, grid, dim3(kThreads), 0, s, P, q, dout, rowstats, lse_ld); }
   return ts::check_launch("ts_attn_bwd (dkdv)");
+}
+
+int launch_dkdv(const ts_attn_problem& P, ts_attn_rows q, ts_attn_rows dout, const float* rowstats,
+                int64_t lse_ld, hipStream_t s) {
+  return P.dtype == kF16 ? launch_dkdv_t<f16>(P, q, dout, rowstats, lse_ld, s)
+                         : launch_dkdv_t<bf16>(P, q, dout, rowstats, lse_ld, s);
 }
 
 }  // namespace attn

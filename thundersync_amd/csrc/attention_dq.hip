@@ -10,6 +10,7 @@ namespace attn {
 // so that exp2(s * scale * log2(e) - lse2) is 0.  The two values of a row are
 // adjacent so the backward kernels fetch a tile's statistics in one load.
 // ---------------------------------------------------------------------------
+template <typename E>
 __global__ __launch_bounds__(kThreads) void delta_kernel(ts_attn_rows O, ts_attn_rows dO,
                                                          const float* __restrict__ lse,
                                                          float* __restrict__ rowstats, int64_t lse_ld,
@@ -26,8 +27,8 @@ __global__ __launch_bounds__(kThreads) void delta_kernel(ts_attn_rows O, ts_attn
   float acc = 0.f;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    acc = fmaf(bf_bits_to_f(a[i] & 0xffffu), bf_bits_to_f(b[i] & 0xffffu), acc);
-    acc = fmaf(bf_bits_to_f(a[i] >> 16), bf_bits_to_f(b[i] >> 16), acc);
+    acc = fmaf(bits_to_f<E>(a[i] & 0xffffu), bits_to_f<E>(b[i] & 0xffffu), acc);
+    acc = fmaf(bits_to_f<E>(a[i] >> 16), bits_to_f<E>(b[i] >> 16), acc);
   }
 #pragma unroll
   for (int msk = 8; msk >= 1; msk >>= 1) acc += shfl_xor(acc, msk);
@@ -42,7 +43,7 @@ __global__ __launch_bounds__(kThreads) void delta_kernel(ts_attn_rows O, ts_attn
 // ---------------------------------------------------------------------------
 // backward dQ (query-stationary)
 // ---------------------------------------------------------------------------
-template <int GC>
+template <typename E, int GC>
 __global__ __launch_bounds__(kThreads, 1) void dq_kernel(ts_attn_problem P, ts_attn_rows Q,
                                                          ts_attn_rows dO, const float* __restrict__ rowstats,
                                                          int64_t lse_ld, ts_attn_rows dQ) {
@@ -108,8 +109,8 @@ __global__ __launch_bounds__(kThreads, 1) void dq_kernel(ts_attn_problem P, ts_a
       if (!active || ref.kpos + kt0 > off + w_last) continue;
 
       f32x4 s[4][2], dp[4][2];
-      tile_scores(s, sk, qreg, lane);
-      tile_scores(dp, sv, dreg, lane);  // dP^T = V dO^T, same shape as S^T
+      tile_scores<E>(s, sk, qreg, lane);
+      tile_scores<E>(dp, sv, dreg, lane);  // dP^T = V dO^T, same shape as S^T
       const bool need_mask = (kt0 + BK > run.len) || (ref.kpos + kt0 + BK - 1 > off + wq0);
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
@@ -134,7 +135,7 @@ __global__ __launch_bounds__(kThreads, 1) void dq_kernel(ts_attn_problem P, ts_a
           float tmp[8];
 #pragma unroll
           for (int j = 0; j < 8; ++j) tmp[j] = s[2 * ss + (j >> 2)][qb][j & 3];
-          dsk[qb] = pack8(tmp);
+          dsk[qb] = pack8<E>(tmp);
         }
         int rows[8];
         slot_rows(lane >> 4, 32 * ss, rows);
@@ -142,8 +143,8 @@ __global__ __launch_bounds__(kThreads, 1) void dq_kernel(ts_attn_problem P, ts_a
         lds_rows_transposed(sk, rows, 8 * (lane & 15), kt);
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          acc[0][e] = mfma16(kt[e], dsk[0], acc[0][e]);
-          acc[1][e] = mfma16(kt[e], dsk[1], acc[1][e]);
+          acc[0][e] = mma16<E>(kt[e], dsk[0], acc[0][e]);
+          acc[1][e] = mma16<E>(kt[e], dsk[1], acc[1][e]);
         }
       }
     }
@@ -160,7 +161,7 @@ __global__ __launch_bounds__(kThreads, 1) void dq_kernel(ts_attn_problem P, ts_a
       float tmp[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) tmp[e] = acc[qb][e][i] * P.scale;
-      st16(drow + 8 * i, as_u32x4(pack8(tmp)));
+      st16(drow + 8 * i, as_u32x4(pack8<E>(tmp)));
     }
   }
 }
@@ -182,7 +183,7 @@ __global__ __launch_bounds__(kThreads, 1) void dq_kernel(ts_attn_problem P, ts_a
 // and dP^T = V dO^T as A operands, K^T for dQ^T += K^T dS^T comes from
 // ds_read_b64_tr_b16.  Only tiles that cross the diagonal are masked.
 // ---------------------------------------------------------------------------
-template <int NQB>
+template <typename E, int NQB>
 __global__ __launch_bounds__(64 * 8 / NQB, 1) void dq_wave_kernel(ts_attn_problem P, ts_attn_rows Q, ts_attn_rows dO,
                                                                  const float* __restrict__ rowstats,
                                                                  int64_t lse_ld, ts_attn_rows dQ) {
@@ -261,8 +262,8 @@ __global__ __launch_bounds__(64 * 8 / NQB, 1) void dq_wave_kernel(ts_attn_proble
         const bf16x8 av = as_bf16x8(ld16(tv + ro[ks] + (32 * ss + 16 * kb) * D));
 #pragma unroll
         for (int qb = 0; qb < NQB; ++qb) {
-          sc[kb][qb] = mfma16(ak, qreg[qb][ks], sc[kb][qb]);
-          dp[kb][qb] = mfma16(av, dreg[qb][ks], dp[kb][qb]);
+          sc[kb][qb] = mma16<E>(ak, qreg[qb][ks], sc[kb][qb]);
+          dp[kb][qb] = mma16<E>(av, dreg[qb][ks], dp[kb][qb]);
         }
       }
   };
@@ -289,7 +290,7 @@ __global__ __launch_bounds__(64 * 8 / NQB, 1) void dq_wave_kernel(ts_attn_proble
       float tmp[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) tmp[j] = sc[j >> 2][qb][j & 3];
-      dsk[qb] = pack8(tmp);
+      dsk[qb] = pack8<E>(tmp);
     }
   };
   auto accumulate = [&](const bf16* tk, int ss, const bf16x8 (&dsk)[NQB]) __attribute__((always_inline)) {
@@ -299,7 +300,7 @@ __global__ __launch_bounds__(64 * 8 / NQB, 1) void dq_wave_kernel(ts_attn_proble
       const u32x2 a1 = tr_read(tk + to[mb] + (32 * ss + 16) * D);
       const bf16x8 a = as_bf16x8(u32x4{a0[0], a0[1], a1[0], a1[1]});
 #pragma unroll
-      for (int qb = 0; qb < NQB; ++qb) acc[mb][qb] = mfma16(a, dsk[qb], acc[mb][qb]);
+      for (int qb = 0; qb < NQB; ++qb) acc[mb][qb] = mma16<E>(a, dsk[qb], acc[mb][qb]);
     }
   };
   // one tile, the halves software-pipelined: half 1's score MFMAs are issued
@@ -383,16 +384,17 @@ __global__ __launch_bounds__(64 * 8 / NQB, 1) void dq_wave_kernel(ts_attn_proble
 #pragma unroll
     for (int mb = 0; mb < 8; ++mb) {
       const f32x4 v = acc[mb][qb] * P.scale;
-      *reinterpret_cast<u32x2*>(drow + 16 * mb) = u32x2{pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3])};
+      *reinterpret_cast<u32x2*>(drow + 16 * mb) = u32x2{pack2<E>(v[0], v[1]), pack2<E>(v[2], v[3])};
     }
   }
 }
 
-int launch_delta(const ts_attn_problem& P, ts_attn_rows out, ts_attn_rows dout, const float* lse,
+template <typename E>
+int launch_delta_t(const ts_attn_problem& P, ts_attn_rows out, ts_attn_rows dout, const float* lse,
                  float* rowstats, int64_t lse_ld, hipStream_t s) {
   const int64_t pairs = P.q_rows * P.hq;
   if (pairs == 0) return TS_OK;
-  { ts::TimedLaunch timed_("attention.delta_kernel", s); hipLaunchKernelGGL(delta_kernel, dim3((unsigned)((pairs + 15) / 16)), dim3(kThreads), 0, s, out,
+  { ts::TimedLaunch timed_("attention.delta_kernel", s); hipLaunchKernelGGL(delta_kernel<E>, dim3((unsigned)((pairs + 15) / 16)), dim3(kThreads), 0, s, out,
                      dout, lse, rowstats, lse_ld, P.q_rows, P.hq); }
   return ts::check_launch("ts_attn_bwd (delta)");
 }
@@ -400,18 +402,31 @@ int launch_delta(const ts_attn_problem& P, ts_attn_rows out, ts_attn_rows dout, 
 // query rows per wave of the dQ kernel (16: eight waves, two per SIMD; 32: four)
 constexpr int kDqRowsPerWave = 16;
 
-int launch_dq(const ts_attn_problem& P, ts_attn_rows q, ts_attn_rows dout, const float* rowstats,
+template <typename E>
+int launch_dq_t(const ts_attn_problem& P, ts_attn_rows q, ts_attn_rows dout, const float* rowstats,
               int64_t lse_ld, ts_attn_rows dq, hipStream_t s) {
   const int group = P.hq / P.hkv;
   const int gc = heads_per_block(group);
   const dim3 grid((unsigned)(P.n_q_work * P.hkv * (group / gc)));
   if (gc == 4)
-    { ts::TimedLaunch timed_("attention.dq_kernel", s); hipLaunchKernelGGL(dq_wave_kernel<kDqRowsPerWave / 16>, grid, dim3(64 * 128 / kDqRowsPerWave), 0, s, P, q, dout, rowstats, lse_ld, dq); }
+    { ts::TimedLaunch timed_("attention.dq_kernel", s); hipLaunchKernelGGL((dq_wave_kernel<E, kDqRowsPerWave / 16>), grid, dim3(64 * 128 / kDqRowsPerWave), 0, s, P, q, dout, rowstats, lse_ld, dq); }
   else if (gc == 2)
-    { ts::TimedLaunch timed_("attention.dq_kernel", s); hipLaunchKernelGGL(dq_kernel<2>, grid, dim3(kThreads), 0, s, P, q, dout, rowstats, lse_ld, dq); }
+    { ts::TimedLaunch timed_("attention.dq_kernel", s); hipLaunchKernelGGL((dq_kernel<E, 2>), grid, dim3(kThreads), 0, s, P, q, dout, rowstats, lse_ld, dq); }
   else
-    { ts::TimedLaunch timed_("attention.dq_kernel", s); hipLaunchKernelGGL(dq_kernel<1>, grid, dim3(kThreads), 0, s, P, q, dout, rowstats, lse_ld, dq); }
+    { ts::TimedLaunch timed_("attention.dq_kernel", s); hipLaunchKernelGGL((dq_kernel<E, 1>), grid, dim3(kThreads), 0, s, P, q, dout, rowstats, lse_ld, dq); }
   return ts::check_launch("ts_attn_bwd (dq)");
+}
+
+int launch_delta(const ts_attn_problem& P, ts_attn_rows out, ts_attn_rows dout, const float* lse,
+                 float* rowstats, int64_t lse_ld, hipStream_t s) {
+  return P.dtype == kF16 ? launch_delta_t<f16>(P, out, dout, lse, rowstats, lse_ld, s)
+                         : launch_delta_t<bf16>(P, out, dout, lse, rowstats, lse_ld, s);
+}
+
+int launch_dq(const ts_attn_problem& P, ts_attn_rows q, ts_attn_rows dout, const float* rowstats,
+              int64_t lse_ld, ts_attn_rows dq, hipStream_t s) {
+  return P.dtype == kF16 ? launch_dq_t<f16>(P, q, dout, rowstats, lse_ld, dq, s)
+                         : launch_dq_t<bf16>(P, q, dout, rowstats, lse_ld, dq, s);
 }
 
 }  // namespace attn

@@ -7,7 +7,7 @@ namespace attn {
 // ---------------------------------------------------------------------------
 // forward
 // ---------------------------------------------------------------------------
-template <int GC>
+template <typename E, int GC>
 __global__ __launch_bounds__(kThreads, 2) void fwd_kernel(ts_attn_problem P, ts_attn_rows Q,
                                                           ts_attn_rows O, float* __restrict__ lse,
                                                           int64_t lse_ld) {
@@ -61,7 +61,7 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_kernel(ts_attn_problem P, ts_
       if (!active || ref.kpos + kt0 > off + w_last) continue;
 
       f32x4 s[4][2];
-      tile_scores(s, sk, qreg, lane);
+      tile_scores<E>(s, sk, qreg, lane);
       const bool need_mask = (kt0 + BK > run.len) || (ref.kpos + kt0 + BK - 1 > off + wq0);
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
@@ -112,7 +112,7 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_kernel(ts_attn_problem P, ts_
           float tmp[8];
 #pragma unroll
           for (int j = 0; j < 8; ++j) tmp[j] = s[2 * ss + (j >> 2)][qb][j & 3];
-          pk[qb] = pack8(tmp);
+          pk[qb] = pack8<E>(tmp);
         }
         int rows[8];
         slot_rows(lane >> 4, 32 * ss, rows);
@@ -120,8 +120,8 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_kernel(ts_attn_problem P, ts_
         lds_rows_transposed(sv, rows, 8 * (lane & 15), vt);
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          o[0][e] = mfma16(vt[e], pk[0], o[0][e]);
-          o[1][e] = mfma16(vt[e], pk[1], o[1][e]);
+          o[0][e] = mma16<E>(vt[e], pk[0], o[0][e]);
+          o[1][e] = mma16<E>(vt[e], pk[1], o[1][e]);
         }
       }
     }
@@ -140,7 +140,7 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_kernel(ts_attn_problem P, ts_
       float tmp[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) tmp[e] = o[qb][e][i] * inv;
-      st16(orow + 8 * i, as_u32x4(pack8(tmp)));
+      st16(orow + 8 * i, as_u32x4(pack8<E>(tmp)));
     }
     if ((lane >> 4) == 0)
       lse[(int64_t)h * lse_ld + seg.q_row0 + row] = l > 0.f ? (m[qb] + fast_log2(l)) * kLn2 : neg_inf();
@@ -170,7 +170,7 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_kernel(ts_attn_problem P, ts_
 constexpr float kRescaleSlack = 8.f;    // log2 units
 constexpr float kRescaleBound = 256.f;  // 2^kRescaleSlack
 
-template <int NQB>
+template <typename E, int NQB>
 __global__ __launch_bounds__(64 * 8 / NQB, NQB == 1 ? 4 : 2) void fwd_wave_kernel(ts_attn_problem P, ts_attn_rows Q,
                                                                                   ts_attn_rows O,
                                                                                   float* __restrict__ lse,
@@ -244,7 +244,7 @@ __global__ __launch_bounds__(64 * 8 / NQB, NQB == 1 ? 4 : 2) void fwd_wave_kerne
         for (int ks = 0; ks < 4; ++ks) {
           const bf16x8 ak = as_bf16x8(ld16(tk + ro[ks] + (32 * ss + 16 * kb) * D));
 #pragma unroll
-          for (int qb = 0; qb < NQB; ++qb) sc[kb][qb] = mfma16(ak, qreg[qb][ks], sc[kb][qb]);
+          for (int qb = 0; qb < NQB; ++qb) sc[kb][qb] = mma16<E>(ak, qreg[qb][ks], sc[kb][qb]);
         }
       }
       // K fragment reads three (kb, ks) steps ahead of their MFMAs
@@ -323,7 +323,7 @@ __global__ __launch_bounds__(64 * 8 / NQB, NQB == 1 ? 4 : 2) void fwd_wave_kerne
         float tmp[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) tmp[j] = pe[j >> 2][qb][j & 3];
-        pk[qb] = pack8(tmp);
+        pk[qb] = pack8<E>(tmp);
       }
       __builtin_amdgcn_s_setprio(1);
 #pragma unroll
@@ -332,7 +332,7 @@ __global__ __launch_bounds__(64 * 8 / NQB, NQB == 1 ? 4 : 2) void fwd_wave_kerne
         const u32x2 a1 = tr_read(tv + to[mb] + (32 * ss + 16) * D);
         const bf16x8 a = as_bf16x8(u32x4{a0[0], a0[1], a1[0], a1[1]});
 #pragma unroll
-        for (int qb = 0; qb < NQB; ++qb) acc[mb][qb] = mfma16(a, pk[qb], acc[mb][qb]);
+        for (int qb = 0; qb < NQB; ++qb) acc[mb][qb] = mma16<E>(a, pk[qb], acc[mb][qb]);
       }
       // V^T fragment reads kept four blocks ahead of their MFMAs
       __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
@@ -366,7 +366,7 @@ __global__ __launch_bounds__(64 * 8 / NQB, NQB == 1 ? 4 : 2) void fwd_wave_kerne
 #pragma unroll
     for (int mb = 0; mb < 8; ++mb) {
       const f32x4 v = acc[mb][qb] * inv;
-      *reinterpret_cast<u32x2*>(orow + 16 * mb) = u32x2{pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3])};
+      *reinterpret_cast<u32x2*>(orow + 16 * mb) = u32x2{pack2<E>(v[0], v[1]), pack2<E>(v[2], v[3])};
     }
     if (g4 == 0)
       lse[(int64_t)h * lse_ld + seg.q_row0 + row] = ls > 0.f ? (m[qb] + fast_log2(ls)) * kLn2 : neg_inf();
@@ -376,18 +376,24 @@ __global__ __launch_bounds__(64 * 8 / NQB, NQB == 1 ? 4 : 2) void fwd_wave_kerne
 // query rows per wave of the forward kernel (32: four waves per work-group; 16: eight)
 constexpr int kFwdRowsPerWave = 32;
 
-int launch_fwd(const ts_attn_problem& P, ts_attn_rows q, ts_attn_rows out, float* lse, int64_t lse_ld,
+template <typename E>
+int launch_fwd_t(const ts_attn_problem& P, ts_attn_rows q, ts_attn_rows out, float* lse, int64_t lse_ld,
                hipStream_t s) {
   const int group = P.hq / P.hkv;
   const int gc = heads_per_block(group);
   const dim3 grid((unsigned)(P.n_q_work * P.hkv * (group / gc)));
   if (gc == 4)
-    { ts::TimedLaunch timed_("attention.fwd_kernel", s); hipLaunchKernelGGL(fwd_wave_kernel<kFwdRowsPerWave / 16>, grid, dim3(64 * 128 / kFwdRowsPerWave), 0, s, P, q, out, lse, lse_ld); }
+    { ts::TimedLaunch timed_("attention.fwd_kernel", s); hipLaunchKernelGGL((fwd_wave_kernel<E, kFwdRowsPerWave / 16>), grid, dim3(64 * 128 / kFwdRowsPerWave), 0, s, P, q, out, lse, lse_ld); }
   else if (gc == 2)
-    { ts::TimedLaunch timed_("attention.fwd_kernel", s); hipLaunchKernelGGL(fwd_kernel<2>, grid, dim3(kThreads), 0, s, P, q, out, lse, lse_ld); }
+    { ts::TimedLaunch timed_("attention.fwd_kernel", s); hipLaunchKernelGGL((fwd_kernel<E, 2>), grid, dim3(kThreads), 0, s, P, q, out, lse, lse_ld); }
   else
-    { ts::TimedLaunch timed_("attention.fwd_kernel", s); hipLaunchKernelGGL(fwd_kernel<1>, grid, dim3(kThreads), 0, s, P, q, out, lse, lse_ld); }
+    { ts::TimedLaunch timed_("attention.fwd_kernel", s); hipLaunchKernelGGL((fwd_kernel<E, 1>), grid, dim3(kThreads), 0, s, P, q, out, lse, lse_ld); }
   return ts::check_launch("ts_attn_fwd");
+}
+
+int launch_fwd(const ts_attn_problem& P, ts_attn_rows q, ts_attn_rows out, float* lse, int64_t lse_ld,
+               hipStream_t s) {
+  return P.dtype == kF16 ? launch_fwd_t<f16>(P, q, out, lse, lse_ld, s) : launch_fwd_t<bf16>(P, q, out, lse, lse_ld, s);
 }
 
 }  // namespace attn

@@ -83,10 +83,11 @@ __device__ __forceinline__ void slot_rows(int g, int base, int rows[8]) {
   for (int j = 0; j < 8; ++j) rows[j] = base + 4 * g + (j & 3) + 16 * (j >> 2);
 }
 
-__device__ __forceinline__ bf16x8 pack8(const float* x) {
+// eight floats as eight T values (an operand container; see mma16)
+template <typename T> __device__ __forceinline__ bf16x8 pack8(const float* x) {
   u32x4 r;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) r[i] = pack_bf2(x[2 * i], x[2 * i + 1]);
+  for (int i = 0; i < 4; ++i) r[i] = pack2<T>(x[2 * i], x[2 * i + 1]);
   return as_bf16x8(r);
 }
 
@@ -109,6 +110,7 @@ __device__ __forceinline__ void load_rows_b(bf16x8 (&reg)[NQB][4], const bf16* b
 
 // S^T tile (64 keys x 32 rows) = K_lds Q^T: s[kb][qb] lane holds keys
 // 16 kb + 4 (lane >> 4) + i, row 16 qb + (lane & 15).
+template <typename E>
 __device__ __forceinline__ void tile_scores(f32x4 s[4][2], const bf16* sk, const bf16x8 qreg[2][4],
                                             int lane) {
 #pragma unroll
@@ -118,8 +120,8 @@ __device__ __forceinline__ void tile_scores(f32x4 s[4][2], const bf16* sk, const
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       const bf16x8 a = as_bf16x8(ld16(sk + (16 * kb + (lane & 15)) * PITCH + 32 * ks + 8 * (lane >> 4)));
-      s[kb][0] = mfma16(a, qreg[0][ks], s[kb][0]);
-      s[kb][1] = mfma16(a, qreg[1][ks], s[kb][1]);
+      s[kb][0] = mma16<E>(a, qreg[0][ks], s[kb][0]);
+      s[kb][1] = mma16<E>(a, qreg[1][ks], s[kb][1]);
     }
   }
 }

@@ -7,6 +7,7 @@
 
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <type_traits>
 #include <string.h>
 #include <stdio.h>
 #include <stdarg.h>
@@ -17,6 +18,7 @@ typedef __bf16 bf16;
 typedef _Float16 f16;
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -80,6 +82,44 @@ __device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
 //   D: lane l holds col (l & 31), rows 8*(i >> 2) + 4*(l >> 5) + (i & 3)
 __device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// The same products for a 16-bit element type T (bf16 or f16).  Operands
+// travel as bf16x8 bit containers whatever T is (loads, LDS and DMA move bits);
+// for f16 they are reinterpreted here, at the instruction that reads them.
+template <typename T> __device__ __forceinline__ f32x4 mma16(bf16x8 a, bf16x8 b, f32x4 c) {
+  if constexpr (std::is_same_v<T, f16>)
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c,
+                                                  0, 0, 0);
+  else
+    return mfma16(a, b, c);
+}
+template <typename T> __device__ __forceinline__ f32x16 mma32(bf16x8 a, bf16x8 b, f32x16 c) {
+  if constexpr (std::is_same_v<T, f16>)
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c,
+                                                  0, 0, 0);
+  else
+    return mfma32(a, b, c);
+}
+
+// two floats as one dword of two T values (lo = a, hi = b), rounded to nearest even
+template <typename T> __device__ __forceinline__ uint32_t pack2(float a, float b) {
+  if constexpr (std::is_same_v<T, f16>) {
+    typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    const f16x2 h = __builtin_convertvector((f32x2{a, b}), f16x2);
+    uint32_t r;
+    __builtin_memcpy(&r, &h, 4);
+    return r;
+  } else {
+    return pack_bf2(a, b);
+  }
+}
+
+// the float value of 16 bits of T
+template <typename T> __device__ __forceinline__ float bits_to_f(uint32_t h) {
+  if constexpr (std::is_same_v<T, f16>) return (float)__builtin_bit_cast(f16, (uint16_t)h);
+  else return bf_bits_to_f(h);
 }
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) {
@@ -283,13 +323,21 @@ template <> __device__ __forceinline__ void store8<float>(float* p, const float 
 void set_error(const char* fmt, ...);
 int check_launch(const char* what);
 
+// launch kernel<f16> or kernel<bf16> by a DType code (kF16: f16, otherwise bf16)
+#define TS_LAUNCH_E(dtype, kernel, ...)                                  \
+  do {                                                                   \
+    if ((dtype) == ::ts::kF16) hipLaunchKernelGGL((kernel<::ts::f16>), __VA_ARGS__);  \
+    else hipLaunchKernelGGL((kernel<::ts::bf16>), __VA_ARGS__);          \
+  } while (0)
+
 // out [rows, dim] (bf16) = lhs [rows, vocab] . W [vocab, dim] on the MFMA core
 // (the logprob grad-hidden GEMM), launches timed under `label` and, for the
 // split-sum pass, `reduce_label`.  Defined in logprob.hip; the C entry
 // ts_logprob_grad_hidden documents the arguments.
 int grad_hidden_launch(const void* dlogits, int64_t ld_dlogits, const void* weight, int64_t ld_weight, int64_t rows,
                        int64_t dim, int64_t vocab, void* grad_hidden, int64_t ld_grad, void* workspace,
-                       int64_t workspace_bytes, void* stream, const char* label, const char* reduce_label);
+                       int64_t workspace_bytes, int dtype, void* stream, const char* label,
+                       const char* reduce_label);
 
 }  // namespace ts
 

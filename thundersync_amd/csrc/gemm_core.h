@@ -1,5 +1,5 @@
 // MFMA GEMM core for gfx950: one 256 x 256 work-group tile of C = A . B^T
-// (bf16 operands, fp32 accumulation), shared by the logprob and LoRA kernels.
+// (bf16 or fp16 operands E, fp32 accumulation), shared by the logprob and LoRA kernels.
 //
 // 8 waves of 128 x 64 (two per SIMD, so one wave's memory instructions overlap
 // the other's MFMAs), v_mfma_f32_32x32x16_bf16.  K streams 32 at a time
@@ -196,7 +196,7 @@ __device__ __forceinline__ int b_row(int ni, int lane, int wn) { return 32 * NI 
 // issuing MFMAs while the DMA is in flight, and with the next stage's first
 // fragments in registers the MFMAs start right after the stage barrier
 // instead of waiting for LDS reads every wave issues at once.
-template <bool HAS_NEXT, class FA, class FB, class Dma>
+template <typename E, bool HAS_NEXT, class FA, class FB, class Dma>
 __device__ __forceinline__ void mma_stage(f32x16 acc[4][NI], const bf16* st, const bf16* nx, const FA& fa,
                                           const FB& fb, bf16x8 (&a0)[4], bf16x8 (&b0)[NI], Dma&& dma) {
   bf16x8 a1[4], b1[NI];
@@ -204,7 +204,7 @@ __device__ __forceinline__ void mma_stage(f32x16 acc[4][NI], const bf16* st, con
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
 #pragma unroll
-    for (int ni = 0; ni < NI; ++ni) acc[g][ni] = mfma32(a0[g], b0[ni], acc[g][ni]);
+    for (int ni = 0; ni < NI; ++ni) acc[g][ni] = mma32<E>(a0[g], b0[ni], acc[g][ni]);
     if constexpr (NI == 2) {
       if (g < 2) {
         a1[2 * g] = fa.read(st, 1, 2 * g);
@@ -222,7 +222,7 @@ __device__ __forceinline__ void mma_stage(f32x16 acc[4][NI], const bf16* st, con
 #pragma unroll
   for (int mi = 0; mi < 4; ++mi) {
 #pragma unroll
-    for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = mfma32(a1[mi], b1[ni], acc[mi][ni]);
+    for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = mma32<E>(a1[mi], b1[ni], acc[mi][ni]);
     if (HAS_NEXT || nx != nullptr) {
       a0[mi] = fa.read(nx, 0, mi);
       if (mi < NI) b0[mi] = fb.read(nx + TM * TK, 0, mi);
@@ -250,7 +250,7 @@ __device__ __forceinline__ void wait_dma(int ahead) {
 // the ring is free on return.  AKS / BKS: the operand is K-strided (A is then
 // given as its [K][M] storage from the tile's first column, B likewise);
 // otherwise K-contiguous (a_rows / b_rows valid rows of 256 from A / B).
-template <bool AKS, bool BKS>
+template <typename E, bool AKS, bool BKS>
 __device__ __forceinline__ void gemm_tile(f32x16 acc[4][NI], const bf16* A, int64_t lda, int a_rows,
                                           const bf16* B, int64_t ldb, int b_rows, int K, bf16* s0,
                                           bf16* s1, bf16* s2, bf16* s3) {
@@ -322,7 +322,7 @@ __device__ __forceinline__ void gemm_tile(f32x16 acc[4][NI], const bf16* A, int6
     const int k0 = (kt + 3) * TK;
     const u32x4 ra = sa.descriptor(refill_now ? k0 : 0), rb = sb.descriptor(refill_now ? k0 : 0);
     const bool ka = FULL || in_k(sa, k0), kb = FULL || in_k(sb, k0);
-    mma_stage<FULL>(acc, cur, (FULL || kt + 1 < nk) ? nxt : nullptr, fa, fb, a0, b0, [&](int g) {
+    mma_stage<E, FULL>(acc, cur, (FULL || kt + 1 < nk) ? nxt : nullptr, fa, fb, a0, b0, [&](int g) {
       if (refill_now) {
         if constexpr (kDmaPerWave == 2) {
           if (g < 2) put(sa, ra, ka, refill, g);

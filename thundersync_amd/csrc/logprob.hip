@@ -75,6 +75,7 @@ struct FwdArgs {
   float* tgt;      // [rows] target logit
 };
 
+template <typename E>
 __global__ __launch_bounds__(kGemmThreads, 1) void fwd_stats_kernel(FwdArgs p) {
   GEMM_RING
   const int total = p.n_ttiles * p.n_vtiles;
@@ -82,7 +83,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void fwd_stats_kernel(FwdArgs p) {
   grouped_tile(xcd_logical(blockIdx.x, total), p.n_vtiles, p.n_ttiles, vt, tt);
   const int v0 = vt * TM, n0 = tt * TN;
   f32x16 acc[4][NI];
-  gemm_tile<false, false>(acc, p.w + (int64_t)v0 * p.ldw, p.ldw, min(TM, p.vocab - v0),
+  gemm_tile<E, false, false>(acc, p.w + (int64_t)v0 * p.ldw, p.ldw, min(TM, p.vocab - v0),
                           p.h + (int64_t)n0 * p.ldh, p.ldh, min(TN, p.rows - n0), p.dim, s0, s1, s2, s3);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave & 1, wn = wave >> 1;
@@ -166,6 +167,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void fwd_stats_kernel(FwdArgs p) {
 // target logit l[n, t] = sum_d h[n, d] W[t, d] (fp32 sum of exact bf16
 // products), one wave per row; rows with t outside [0, vocab) are skipped
 // (the combine kernel writes NaN for them)
+template <typename E>
 __global__ __launch_bounds__(kThreads) void target_logit_kernel(const bf16* __restrict__ h, int64_t ldh,
                                                                 const bf16* __restrict__ w, int64_t ldw,
                                                                 const int64_t* __restrict__ target, int rows,
@@ -182,8 +184,8 @@ __global__ __launch_bounds__(kThreads) void target_logit_kernel(const bf16* __re
     const u32x4 a = ld16(hr + d), b = ld16(wr + d);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      acc = fmaf(bf_bits_to_f(a[i] & 0xffffu), bf_bits_to_f(b[i] & 0xffffu), acc);
-      acc = fmaf(bf_bits_to_f(a[i] >> 16), bf_bits_to_f(b[i] >> 16), acc);
+      acc = fmaf(bits_to_f<E>(a[i] & 0xffffu), bits_to_f<E>(b[i] & 0xffffu), acc);
+      acc = fmaf(bits_to_f<E>(a[i] >> 16), bits_to_f<E>(b[i] >> 16), acc);
     }
   }
   acc = wave_sum(acc);
@@ -250,6 +252,7 @@ struct DlArgs {
 constexpr int OPITCH = TM + 8;  // staging pitch (bf16) of [64 tokens][TM vocab] quarter tiles
 static_assert(64 * OPITCH <= kRingElems, "a quarter of the dlogits tile fits one ring stage");
 
+template <typename E>
 __global__ __launch_bounds__(kGemmThreads, 1) void dlogits_kernel(DlArgs p) {
   GEMM_RING
   const int total = p.n_ttiles * p.n_vtiles;
@@ -257,7 +260,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void dlogits_kernel(DlArgs p) {
   grouped_tile(xcd_logical(blockIdx.x, total), p.n_vtiles, p.n_ttiles, vt, tt);
   const int v0 = vt * TM, n0 = tt * TN;
   f32x16 acc[4][NI];
-  gemm_tile<false, false>(acc, p.w + (int64_t)v0 * p.ldw, p.ldw, min(TM, p.vocab - v0),
+  gemm_tile<E, false, false>(acc, p.w + (int64_t)v0 * p.ldw, p.ldw, min(TM, p.vocab - v0),
                           p.h + (int64_t)n0 * p.ldh, p.ldh, min(TN, p.rows - n0), p.dim, s0, s1, s2, s3);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave & 1, wn = wave >> 1;
@@ -305,7 +308,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void dlogits_kernel(DlArgs p) {
               if (!FULL && !(v < p.vocab && n < p.rows)) d = 0.f;
               d2[jj] = d;
             }
-            packed[j >> 1] = pack_bf2(d2[0], d2[1]);
+            packed[j >> 1] = pack2<E>(d2[0], d2[1]);
           }
           // vocab rows a_row(mi, 4 i4 .. 4 i4 + 3) are consecutive: one 8-byte write
           *reinterpret_cast<u32x2*>(out + a_row(mi, 4 * i4, lane, wm)) = u32x2{packed[0], packed[1]};
@@ -347,6 +350,7 @@ struct DhArgs {
   float* part;      // [ksplit][rows][dim] when ksplit > 1
 };
 
+template <typename E>
 __global__ __launch_bounds__(kGemmThreads, 1) void grad_hidden_kernel(DhArgs p) {
   GEMM_RING
   const int tiles = p.n_ttiles * p.n_dtiles;
@@ -358,7 +362,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void grad_hidden_kernel(DhArgs p) 
   const int d0 = dt * TM, n0 = tt * TN;
   const int kb = ks * p.kper, ke = min(p.vocab, kb + p.kper);
   f32x16 acc[4][NI];
-  gemm_tile<true, false>(acc, p.w + (int64_t)kb * p.ldw + d0, p.ldw, p.dim - d0, p.dl + (int64_t)n0 * p.ldl + kb,
+  gemm_tile<E, true, false>(acc, p.w + (int64_t)kb * p.ldw + d0, p.ldw, p.dim - d0, p.dl + (int64_t)n0 * p.ldl + kb,
                          p.ldl, min(TN, p.rows - n0), ke - kb, s0, s1, s2, s3);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave & 1, wn = wave >> 1;
@@ -382,16 +386,17 @@ __global__ __launch_bounds__(kGemmThreads, 1) void grad_hidden_kernel(DhArgs p) 
               if (d + j < p.dim) q[j] = a[j];
           }
         } else if (d + 3 < p.dim) {
-          *reinterpret_cast<u32x2*>(p.dh + (int64_t)n * p.ldd + d) = u32x2{pack_bf2(a[0], a[1]), pack_bf2(a[2], a[3])};
+          *reinterpret_cast<u32x2*>(p.dh + (int64_t)n * p.ldd + d) = u32x2{pack2<E>(a[0], a[1]), pack2<E>(a[2], a[3])};
         } else {
           for (int j = 0; j < 4; ++j)
-            if (d + j < p.dim) p.dh[(int64_t)n * p.ldd + d + j] = from_f<bf16>(a[j]);
+            if (d + j < p.dim) reinterpret_cast<E*>(p.dh)[(int64_t)n * p.ldd + d + j] = from_f<E>(a[j]);
         }
       }
   }
 }
 
 // dh = bf16(sum_s part[s]) in range order; four elements per thread
+template <typename E>
 __global__ __launch_bounds__(kThreads) void grad_hidden_reduce_kernel(const float* __restrict__ part, int ksplit,
                                                                       int rows, int dim, bf16* __restrict__ dh,
                                                                       int64_t ldd) {
@@ -402,7 +407,7 @@ __global__ __launch_bounds__(kThreads) void grad_hidden_reduce_kernel(const floa
   const int d = (int)(e - n * dim);
   f32x4 s = *reinterpret_cast<const f32x4*>(part + e);
   for (int k = 1; k < ksplit; ++k) s += *reinterpret_cast<const f32x4*>(part + (int64_t)k * total + e);
-  *reinterpret_cast<u32x2*>(dh + n * ldd + d) = u32x2{pack_bf2(s[0], s[1]), pack_bf2(s[2], s[3])};
+  *reinterpret_cast<u32x2*>(dh + n * ldd + d) = u32x2{pack2<E>(s[0], s[1]), pack2<E>(s[2], s[3])};
 }
 
 // ---------------------------------------------------------------------------
@@ -422,6 +427,7 @@ struct DwArgs {
   int64_t ldg;
 };
 
+template <typename E>
 __global__ __launch_bounds__(kGemmThreads, 1) void grad_weight_kernel(DwArgs p) {
   GEMM_RING
   const int total = p.n_vtiles * p.n_dtiles;
@@ -429,7 +435,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void grad_weight_kernel(DwArgs p) 
   grouped_tile(xcd_logical(blockIdx.x, total), p.n_vtiles, p.n_dtiles, vt, dt);
   const int v0 = vt * TM, d0 = dt * TN;
   f32x16 acc[4][NI];
-  gemm_tile<true, true>(acc, p.dl + v0, p.ldl, p.vocab - v0, p.h + d0, p.ldh, p.dim - d0, p.rows, s0, s1, s2,
+  gemm_tile<E, true, true>(acc, p.dl + v0, p.ldl, p.vocab - v0, p.h + d0, p.ldh, p.dim - d0, p.rows, s0, s1, s2,
                         s3);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave & 1, wn = wave >> 1;
@@ -475,9 +481,10 @@ int64_t ts_logprob_fwd_workspace(int64_t rows, int64_t vocab) {
 
 int ts_logprob_fwd(const void* hidden, int64_t ld_hidden, const void* weight, int64_t ld_weight,
                    const int64_t* target, int64_t rows, int64_t dim, int64_t vocab, float* logprob,
-                   float* entropy, float* lse, void* workspace, int64_t workspace_bytes,
+                   float* entropy, float* lse, void* workspace, int64_t workspace_bytes, int dtype,
                    void* stream) {
   using namespace ts::lp;
+  TS_CHECK_ARG(dtype == ts::kBF16 || dtype == ts::kF16, "ts_logprob_fwd: dtype %d (bf16 or fp16)", dtype);
   TS_CHECK_ARG(rows >= 0 && dim > 0 && vocab > 0 && rows < (1 << 30) && vocab < (1 << 30) &&
                    dim < (1 << 20),
                "ts_logprob_fwd: bad shape rows=%lld dim=%lld vocab=%lld", (long long)rows,
@@ -510,11 +517,11 @@ int ts_logprob_fwd(const void* hidden, int64_t ld_hidden, const void* weight, in
   a.tgt = ws + 3 * (int64_t)a.n_vtiles * rows;
   TS_CHECK_ARG((int64_t)a.n_ttiles * a.n_vtiles < (1ll << 31), "ts_logprob_fwd: grid too large");
   hipStream_t s = (hipStream_t)stream;
-  { ts::TimedLaunch timed_("logprob.fwd_stats_kernel", s); hipLaunchKernelGGL(fwd_stats_kernel, dim3((unsigned)(a.n_ttiles * a.n_vtiles)), dim3(kGemmThreads),
+  { ts::TimedLaunch timed_("logprob.fwd_stats_kernel", s); TS_LAUNCH_E(dtype, fwd_stats_kernel, dim3((unsigned)(a.n_ttiles * a.n_vtiles)), dim3(kGemmThreads),
                      0, s, a); }
   int st = ts::check_launch("ts_logprob_fwd (tiles)");
   if (st != TS_OK) return st;
-  { ts::TimedLaunch timed_("logprob.target_logit_kernel", s); hipLaunchKernelGGL(target_logit_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(kThreads),
+  { ts::TimedLaunch timed_("logprob.target_logit_kernel", s); TS_LAUNCH_E(dtype, target_logit_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(kThreads),
                      0, s, a.h, a.ldh, a.w, a.ldw, target, (int)rows, (int)dim, (int)vocab, a.tgt); }
   st = ts::check_launch("ts_logprob_fwd (target logits)");
   if (st != TS_OK) return st;
@@ -527,8 +534,9 @@ int ts_logprob_fwd(const void* hidden, int64_t ld_hidden, const void* weight, in
 int ts_logprob_dlogits(const void* hidden, int64_t ld_hidden, const void* weight, int64_t ld_weight,
                        const int64_t* target, const float* lse, const float* entropy,
                        const float* grad_lp, const float* grad_ent, int64_t rows, int64_t dim,
-                       int64_t vocab, void* dlogits, int64_t ld_dlogits, void* stream) {
+                       int64_t vocab, void* dlogits, int64_t ld_dlogits, int dtype, void* stream) {
   using namespace ts::lp;
+  TS_CHECK_ARG(dtype == ts::kBF16 || dtype == ts::kF16, "ts_logprob_dlogits: dtype %d (bf16 or fp16)", dtype);
   TS_CHECK_ARG(rows >= 0 && dim > 0 && vocab > 0 && rows < (1 << 30) && vocab < (1 << 30) &&
                    dim < (1 << 20),
                "ts_logprob_dlogits: bad shape");
@@ -560,7 +568,7 @@ int ts_logprob_dlogits(const void* hidden, int64_t ld_hidden, const void* weight
   a.dl = (ts::bf16*)dlogits;
   a.ldl = ld_dlogits;
   TS_CHECK_ARG(a.vocab_pad <= ld_dlogits, "ts_logprob_dlogits: ld_dlogits below padded vocab");
-  { ts::TimedLaunch timed_("logprob.dlogits_kernel", (hipStream_t)stream); hipLaunchKernelGGL(dlogits_kernel, dim3((unsigned)(a.n_ttiles * a.n_vtiles)), dim3(kGemmThreads),
+  { ts::TimedLaunch timed_("logprob.dlogits_kernel", (hipStream_t)stream); TS_LAUNCH_E(dtype, dlogits_kernel, dim3((unsigned)(a.n_ttiles * a.n_vtiles)), dim3(kGemmThreads),
                      0, (hipStream_t)stream, a); }
   return ts::check_launch("ts_logprob_dlogits");
 }
@@ -578,8 +586,10 @@ namespace ts {
 
 int grad_hidden_launch(const void* dlogits, int64_t ld_dlogits, const void* weight, int64_t ld_weight, int64_t rows,
                        int64_t dim, int64_t vocab, void* grad_hidden, int64_t ld_grad, void* workspace,
-                       int64_t workspace_bytes, void* stream, const char* label, const char* reduce_label) {
+                       int64_t workspace_bytes, int dtype, void* stream, const char* label,
+                       const char* reduce_label) {
   using namespace ts::lp;
+  TS_CHECK_ARG(dtype == ts::kBF16 || dtype == ts::kF16, "ts_logprob_grad_hidden: dtype %d (bf16 or fp16)", dtype);
   TS_CHECK_ARG(rows >= 0 && dim > 0 && vocab > 0 && rows < (1 << 30) && dim < (1 << 20) && vocab < (1 << 30),
                "ts_logprob_grad_hidden: bad shape");
   if (rows == 0) return TS_OK;
@@ -611,7 +621,7 @@ int grad_hidden_launch(const void* dlogits, int64_t ld_dlogits, const void* weig
   hipStream_t s = (hipStream_t)stream;
   {
     ts::TimedLaunch timed_(label, s);
-    hipLaunchKernelGGL(grad_hidden_kernel, dim3((unsigned)(a.n_ttiles * a.n_dtiles * a.ksplit)), dim3(kGemmThreads),
+    TS_LAUNCH_E(dtype, grad_hidden_kernel, dim3((unsigned)(a.n_ttiles * a.n_dtiles * a.ksplit)), dim3(kGemmThreads),
                        0, s, a);
   }
   int st = ts::check_launch("ts_logprob_grad_hidden");
@@ -619,7 +629,7 @@ int grad_hidden_launch(const void* dlogits, int64_t ld_dlogits, const void* weig
   const int64_t quads = rows * dim / 4;
   {
     ts::TimedLaunch timed_(reduce_label, s);
-    hipLaunchKernelGGL(grad_hidden_reduce_kernel, dim3((unsigned)((quads + kThreads - 1) / kThreads)), dim3(kThreads),
+    TS_LAUNCH_E(dtype, grad_hidden_reduce_kernel, dim3((unsigned)((quads + kThreads - 1) / kThreads)), dim3(kThreads),
                        0, s, (const float*)workspace, a.ksplit, (int)rows, (int)dim, (ts::bf16*)grad_hidden, ld_grad);
   }
   return ts::check_launch("ts_logprob_grad_hidden (reduce)");
@@ -631,16 +641,17 @@ extern "C" {
 
 int ts_logprob_grad_hidden(const void* dlogits, int64_t ld_dlogits, const void* weight, int64_t ld_weight,
                            int64_t rows, int64_t dim, int64_t vocab, void* grad_hidden, int64_t ld_grad,
-                           void* workspace, int64_t workspace_bytes, void* stream) {
+                           void* workspace, int64_t workspace_bytes, int dtype, void* stream) {
   return ts::grad_hidden_launch(dlogits, ld_dlogits, weight, ld_weight, rows, dim, vocab, grad_hidden, ld_grad,
-                                workspace, workspace_bytes, stream, "logprob.grad_hidden_kernel",
+                                workspace, workspace_bytes, dtype, stream, "logprob.grad_hidden_kernel",
                                 "logprob.grad_hidden_reduce_kernel");
 }
 
 int ts_logprob_grad_weight(const void* dlogits, int64_t ld_dlogits, const void* hidden, int64_t ld_hidden,
                            int64_t rows, int64_t dim, int64_t vocab, float* grad_weight, int64_t ld_grad,
-                           void* stream) {
+                           int dtype, void* stream) {
   using namespace ts::lp;
+  TS_CHECK_ARG(dtype == ts::kBF16 || dtype == ts::kF16, "ts_logprob_grad_weight: dtype %d (bf16 or fp16)", dtype);
   TS_CHECK_ARG(rows >= 0 && dim > 0 && vocab > 0 && rows < (1 << 30) && dim < (1 << 20) && vocab < (1 << 30),
                "ts_logprob_grad_weight: bad shape");
   if (rows == 0) return TS_OK;
@@ -665,7 +676,7 @@ int ts_logprob_grad_weight(const void* dlogits, int64_t ld_dlogits, const void* 
   TS_CHECK_ARG((int64_t)a.n_vtiles * a.n_dtiles < (1ll << 31), "ts_logprob_grad_weight: grid too large");
   {
     ts::TimedLaunch timed_("logprob.grad_weight_kernel", (hipStream_t)stream);
-    hipLaunchKernelGGL(grad_weight_kernel, dim3((unsigned)(a.n_vtiles * a.n_dtiles)), dim3(kGemmThreads), 0,
+    TS_LAUNCH_E(dtype, grad_weight_kernel, dim3((unsigned)(a.n_vtiles * a.n_dtiles)), dim3(kGemmThreads), 0,
                        (hipStream_t)stream, a);
   }
   return ts::check_launch("ts_logprob_grad_weight");

@@ -1,4 +1,4 @@
-// Merged-weight LoRA linear for gfx950 (bf16 operands, fp32 accumulation).
+// Merged-weight LoRA linear for gfx950 (bf16 or fp16 operands, fp32 accumulation).
 //
 // Reference: accel/fused_lora.py:26-48 (FusedLoRALinear).  The adapters are
 // merged into the base weight by the caller (W_eff = W + s B A), so the
@@ -54,6 +54,7 @@ struct FwdArgs {
   int64_t ldy;
 };
 
+template <typename E>
 __global__ __launch_bounds__(kGemmThreads, 1) void lora_fwd_kernel(FwdArgs p) {
   GEMM_RING
   const int total = p.n_mtiles * p.n_ntiles;
@@ -61,7 +62,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void lora_fwd_kernel(FwdArgs p) {
   grouped_tile(xcd_logical(blockIdx.x, total), p.n_ntiles, p.n_mtiles, nt, mt);
   const int n0 = nt * TM, m0 = mt * TN;
   f32x16 acc[4][NI];
-  gemm_tile<false, false>(acc, p.w + (int64_t)n0 * p.ldw, p.ldw, min(TM, p.out - n0),
+  gemm_tile<E, false, false>(acc, p.w + (int64_t)n0 * p.ldw, p.ldw, min(TM, p.out - n0),
                           p.x + (int64_t)m0 * p.ldx, p.ldx, min(TN, p.rows - m0), p.in, s0, s1, s2, s3);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave & 1, wn = wave >> 1;
@@ -78,7 +79,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void lora_fwd_kernel(FwdArgs p) {
         const f32x16& a = acc[mi][ni];
         // output columns a_row(mi, 4 i4 .. 4 i4 + 3) are consecutive: one 8-byte write
         *reinterpret_cast<u32x2*>(o + a_row(mi, 4 * i4, lane, wm)) =
-            u32x2{pack_bf2(a[4 * i4], a[4 * i4 + 1]), pack_bf2(a[4 * i4 + 2], a[4 * i4 + 3])};
+            u32x2{pack2<E>(a[4 * i4], a[4 * i4 + 1]), pack2<E>(a[4 * i4 + 2], a[4 * i4 + 3])};
       }
   }
   __syncthreads();
@@ -114,6 +115,7 @@ struct RankArgs {
   int64_t ld_out;  // rows rounded up to a multiple of 8; columns rows .. ld_out - 1 are written as zeros
 };
 
+template <typename E>
 __global__ __launch_bounds__(kGemmThreads, 1) void lora_rank_kernel(RankArgs p) {
   GEMM_RING
   const int id = xcd_logical(blockIdx.x, p.n_mtiles * p.n_jobs);
@@ -121,7 +123,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void lora_rank_kernel(RankArgs p) 
   const RankJob& job = p.job[j];
   const int m0 = (id - j * p.n_mtiles) * TM;
   f32x16 acc[4][NI];
-  gemm_tile<false, false>(acc, job.src + (int64_t)m0 * job.ld_src, job.ld_src, min(TM, p.rows - m0), job.proj,
+  gemm_tile<E, false, false>(acc, job.src + (int64_t)m0 * job.ld_src, job.ld_src, min(TM, p.rows - m0), job.proj,
                           job.ld_proj, p.rank, job.k, s0, s1, s2, s3);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave & 1, wn = wave >> 1;
@@ -140,7 +142,7 @@ __global__ __launch_bounds__(kGemmThreads, 1) void lora_rank_kernel(RankArgs p) 
         const f32x16& a = acc[mi][ni];
         if (m + 3 < p.ld_out)
           *reinterpret_cast<u32x2*>(o + m) =
-              u32x2{pack_bf2(a[4 * i4], a[4 * i4 + 1]), pack_bf2(a[4 * i4 + 2], a[4 * i4 + 3])};
+              u32x2{pack2<E>(a[4 * i4], a[4 * i4 + 1]), pack2<E>(a[4 * i4 + 2], a[4 * i4 + 3])};
       }
   }
 }
@@ -160,13 +162,14 @@ struct AdapterArgs {
   float* part;      // A side [msplit][rank][width]; B side [msplit][width][rank]
 };
 
+template <typename E>
 __global__ __launch_bounds__(kGemmThreads, 1) void lora_grad_a_kernel(AdapterArgs p) {
   GEMM_RING
   const int id = xcd_logical(blockIdx.x, p.n_tiles * p.msplit);
   const int s = id / p.n_tiles, kt = id - s * p.n_tiles;
   const int k0 = kt * TN, kb = s * p.kper, ke = min(p.rows, kb + p.kper);
   f32x16 acc[4][NI];
-  gemm_tile<false, true>(acc, p.uT + kb, p.ld_rt, p.rank, p.big + (int64_t)kb * p.ld_big + k0, p.ld_big,
+  gemm_tile<E, false, true>(acc, p.uT + kb, p.ld_rt, p.rank, p.big + (int64_t)kb * p.ld_big + k0, p.ld_big,
                          p.width - k0, ke - kb, s0, s1, s2, s3);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave & 1, wn = wave >> 1;
@@ -185,13 +188,14 @@ __global__ __launch_bounds__(kGemmThreads, 1) void lora_grad_a_kernel(AdapterArg
   }
 }
 
+template <typename E>
 __global__ __launch_bounds__(kGemmThreads, 1) void lora_grad_b_kernel(AdapterArgs p) {
   GEMM_RING
   const int id = xcd_logical(blockIdx.x, p.n_tiles * p.msplit);
   const int s = id / p.n_tiles, nt = id - s * p.n_tiles;
   const int n0 = nt * TM, kb = s * p.kper, ke = min(p.rows, kb + p.kper);
   f32x16 acc[4][NI];
-  gemm_tile<true, false>(acc, p.big + (int64_t)kb * p.ld_big + n0, p.ld_big, p.width - n0, p.uT + kb, p.ld_rt,
+  gemm_tile<E, true, false>(acc, p.big + (int64_t)kb * p.ld_big + n0, p.ld_big, p.width - n0, p.uT + kb, p.ld_rt,
                          p.rank, ke - kb, s0, s1, s2, s3);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave & 1, wn = wave >> 1;
@@ -265,9 +269,10 @@ inline BwdLayout bwd_layout(int64_t rows, int64_t in, int64_t out, int64_t rank)
 extern "C" {
 
 int ts_lora_fwd(const void* x, int64_t ld_x, const void* weight, int64_t ld_weight, int64_t rows,
-                int64_t in_features, int64_t out_features, void* y, int64_t ld_y, void* stream) {
+                int64_t in_features, int64_t out_features, void* y, int64_t ld_y, int dtype, void* stream) {
   using namespace ts::lora;
   using ts::bf16;
+  TS_CHECK_ARG(dtype == ts::kBF16 || dtype == ts::kF16, "ts_lora_fwd: dtype %d (bf16 or fp16)", dtype);
   TS_CHECK_ARG(rows >= 0 && in_features > 0 && out_features > 0 && rows < (1 << 30) &&
                    in_features < (1 << 20) && out_features < (1 << 24),
                "ts_lora_fwd: bad shape rows=%lld in=%lld out=%lld", (long long)rows, (long long)in_features,
@@ -286,7 +291,7 @@ int ts_lora_fwd(const void* x, int64_t ld_x, const void* weight, int64_t ld_weig
   hipStream_t s = static_cast<hipStream_t>(stream);
   {
     ts::TimedLaunch timed_("lora.fwd_kernel", s);
-    hipLaunchKernelGGL(lora_fwd_kernel, dim3((unsigned)(p.n_mtiles * p.n_ntiles)), dim3(kGemmThreads), 0, s, p);
+    TS_LAUNCH_E(dtype, lora_fwd_kernel, dim3((unsigned)(p.n_mtiles * p.n_ntiles)), dim3(kGemmThreads), 0, s, p);
   }
   return ts::check_launch("ts_lora_fwd");
 }
@@ -300,9 +305,11 @@ int64_t ts_lora_bwd_workspace(int64_t rows, int64_t in_features, int64_t out_fea
 int ts_lora_bwd(const void* grad_out, int64_t ld_grad_out, const void* x, int64_t ld_x, const void* weight,
                 int64_t ld_weight, const void* lora_a, const void* lora_b_t, int64_t rank, float scaling,
                 int64_t rows, int64_t in_features, int64_t out_features, void* grad_x, int64_t ld_grad_x,
-                float* grad_a, float* grad_b, void* workspace, int64_t workspace_bytes, void* stream) {
+                float* grad_a, float* grad_b, void* workspace, int64_t workspace_bytes, int dtype,
+                void* stream) {
   using namespace ts::lora;
   using ts::bf16;
+  TS_CHECK_ARG(dtype == ts::kBF16 || dtype == ts::kF16, "ts_lora_bwd: dtype %d (bf16 or fp16)", dtype);
   TS_CHECK_ARG(rows >= 0 && in_features > 0 && out_features > 0 && rank > 0 && rank <= TN &&
                    rows < (1 << 30) && in_features < (1 << 20) && out_features < (1 << 20),
                "ts_lora_bwd: bad shape rows=%lld in=%lld out=%lld rank=%lld (rank at most %d)", (long long)rows,
@@ -342,7 +349,7 @@ int ts_lora_bwd(const void* grad_out, int64_t ld_grad_out, const void* x, int64_
   void* dx_ws = ws + 2 * L.rank_bytes + L.part_a + L.part_b;
   if (grad_x) {
     const int st = ts::grad_hidden_launch(grad_out, ld_grad_out, weight, ld_weight, rows, in_features, out_features,
-                                          grad_x, ld_grad_x, dx_ws, L.dx, stream, "lora.grad_x_kernel",
+                                          grad_x, ld_grad_x, dx_ws, L.dx, dtype, stream, "lora.grad_x_kernel",
                                           "lora.grad_x_reduce_kernel");
     if (st != TS_OK) return st;
   }
@@ -359,7 +366,7 @@ int ts_lora_bwd(const void* grad_out, int64_t ld_grad_out, const void* x, int64_
                                             in_features, (int)in_features, tT};
   {
     ts::TimedLaunch timed_("lora.rank_kernel", s);
-    hipLaunchKernelGGL(lora_rank_kernel, dim3((unsigned)(rk.n_mtiles * rk.n_jobs)), dim3(kGemmThreads), 0, s, rk);
+    TS_LAUNCH_E(dtype, lora_rank_kernel, dim3((unsigned)(rk.n_mtiles * rk.n_jobs)), dim3(kGemmThreads), 0, s, rk);
   }
   int st = ts::check_launch("ts_lora_bwd rank");
   if (st != TS_OK) return st;
@@ -368,7 +375,7 @@ int ts_lora_bwd(const void* grad_out, int64_t ld_grad_out, const void* x, int64_
                   (int)((in_features + TN - 1) / TN), L.msplit_a, L.kper_a, part_a};
     {
       ts::TimedLaunch timed_("lora.grad_a_kernel", s);
-      hipLaunchKernelGGL(lora_grad_a_kernel, dim3((unsigned)(a.n_tiles * a.msplit)), dim3(kGemmThreads), 0, s, a);
+      TS_LAUNCH_E(dtype, lora_grad_a_kernel, dim3((unsigned)(a.n_tiles * a.msplit)), dim3(kGemmThreads), 0, s, a);
     }
     const int64_t n = rank * in_features;
     {
@@ -384,7 +391,7 @@ int ts_lora_bwd(const void* grad_out, int64_t ld_grad_out, const void* x, int64_
                   (int)out_features, (int)((out_features + TM - 1) / TM), L.msplit_b, L.kper_b, part_b};
     {
       ts::TimedLaunch timed_("lora.grad_b_kernel", s);
-      hipLaunchKernelGGL(lora_grad_b_kernel, dim3((unsigned)(b.n_tiles * b.msplit)), dim3(kGemmThreads), 0, s, b);
+      TS_LAUNCH_E(dtype, lora_grad_b_kernel, dim3((unsigned)(b.n_tiles * b.msplit)), dim3(kGemmThreads), 0, s, b);
     }
     const int64_t n = out_features * rank;
     {

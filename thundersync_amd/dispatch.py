@@ -86,7 +86,7 @@ def logprob_trial(device: torch.device, dtype: torch.dtype, dim: int) -> None:
 
 
 def _available(like: torch.Tensor, kernel: str, key: int, trial) -> bool:
-    if not like.is_cuda or like.dtype != torch.bfloat16:
+    if not like.is_cuda or like.dtype not in (torch.bfloat16, torch.float16):
         return False
     if _lib.library() is None:  # off, or auto without a library; require raises
         return False

@@ -32,6 +32,7 @@ from . import _lib
 from .operator_profiling import device_role, operator_range
 
 
+ELEMENT_DTYPES = (torch.bfloat16, torch.float16)
 CHECK_TARGETS_ENV = "THUNDERSYNC_CHECK_TARGETS"
 
 
@@ -63,9 +64,10 @@ def _validate(hidden: torch.Tensor, weight: torch.Tensor, target: torch.Tensor) 
         raise ValueError(f"weight {tuple(weight.shape)} does not match hidden dim {hidden.shape[1]}")
     if not hidden.is_cuda or not weight.is_cuda or not target.is_cuda:
         raise RuntimeError("thundersync_amd fused logprob runs on the GPU only; got a CPU tensor")
-    if hidden.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
+    if hidden.dtype not in ELEMENT_DTYPES or weight.dtype != hidden.dtype:
         raise TypeError(
-            f"thundersync_amd fused logprob takes bf16 hidden and weight, got {hidden.dtype}/{weight.dtype}"
+            "thundersync_amd fused logprob takes bf16 or fp16 hidden and weight of one dtype, got "
+            f"{hidden.dtype}/{weight.dtype}"
         )
     _check_targets(target, weight.shape[0])
 
@@ -97,7 +99,7 @@ def _forward(hidden, weight, target, with_entropy):
         lib.ts_logprob_fwd(
             h.data_ptr(), h.stride(0), w.data_ptr(), w.stride(0), t.data_ptr(), n, d, v,
             lp.data_ptr(), _lib.ptr(ent), lse.data_ptr(), ws.data_ptr(), ws_bytes,
-            _lib.stream_of(h),
+            _lib.dtype_code(h.dtype), _lib.stream_of(h),
         ),
         f"ts_logprob_fwd(rows={n}, dim={d}, vocab={v})",
     )
@@ -127,6 +129,7 @@ def _backward(hidden, weight, target, lse, ent, grad_lp, grad_ent, chunk, needs_
     if n == 0:
         return grad_hidden[:, :d_in], (grad_weight[:, :d_in].to(weight.dtype) if grad_weight is not None else None)
     stream = _lib.stream_of(h)
+    code = _lib.dtype_code(h.dtype)
     block = backward_block_rows(n, chunk)
     dl = torch.empty(block, vp, dtype=w.dtype, device=w.device)
     ws_bytes = int(lib.ts_logprob_grad_hidden_workspace(block, d, v))
@@ -142,7 +145,7 @@ def _backward(hidden, weight, target, lse, ent, grad_lp, grad_ent, chunk, needs_
                     hi.data_ptr(), h.stride(0), w.data_ptr(), w.stride(0), t[i:].data_ptr(),
                     lse[i:].data_ptr(), ent[i:].data_ptr() if ent is not None else None,
                     g_lp[i:].data_ptr(), g_ent[i:].data_ptr() if g_ent is not None else None,
-                    rows, d, v, dl.data_ptr(), vp, stream,
+                    rows, d, v, dl.data_ptr(), vp, code, stream,
                 ),
                 f"ts_logprob_dlogits(rows={rows}, dim={d}, vocab={v})",
             )
@@ -150,7 +153,7 @@ def _backward(hidden, weight, target, lse, ent, grad_lp, grad_ent, chunk, needs_
             _lib.check(
                 lib.ts_logprob_grad_hidden(
                     dl.data_ptr(), vp, w.data_ptr(), w.stride(0), rows, d, v,
-                    grad_hidden[i:].data_ptr(), grad_hidden.stride(0), ws.data_ptr(), ws_bytes, stream,
+                    grad_hidden[i:].data_ptr(), grad_hidden.stride(0), ws.data_ptr(), ws_bytes, code, stream,
                 ),
                 f"ts_logprob_grad_hidden(rows={rows}, dim={d}, vocab={v})",
             )
@@ -160,7 +163,7 @@ def _backward(hidden, weight, target, lse, ent, grad_lp, grad_ent, chunk, needs_
                 _lib.check(
                     lib.ts_logprob_grad_weight(
                         dl.data_ptr(), vp, hi.data_ptr(), h.stride(0), rows, d, v,
-                        grad_weight.data_ptr(), grad_weight.stride(0), stream,
+                        grad_weight.data_ptr(), grad_weight.stride(0), code, stream,
                     ),
                     f"ts_logprob_grad_weight(rows={rows}, dim={d}, vocab={v})",
                 )

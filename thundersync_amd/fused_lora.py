@@ -8,13 +8,14 @@ GEMM and the backward the exact derivative of the unmerged layer:
 
     y = x W_eff^T      dx = g W_eff      dA = s (g B)^T x      dB = s g^T (x A^T)
 
-Every product runs in the library (``ts_lora_fwd`` / ``ts_lora_bwd``, bf16
-operands on MFMA with fp32 accumulation); the adapter gradients come back as
+Every product runs in the library (``ts_lora_fwd`` / ``ts_lora_bwd``, bf16 or
+fp16 operands on MFMA with fp32 accumulation); the adapter gradients come back as
 fp32 sums over fixed row ranges added in order, so a call gives the same
 bytes every time, and are cast to each adapter's own dtype.  The adapters
 are cast to the activation dtype before the products, as the reference does.
 
-Activations must be bf16 CUDA tensors with ``in`` and ``out`` multiples of 8;
+Activations must be bf16 or fp16 CUDA tensors (the weight of the same dtype)
+with ``in`` and ``out`` multiples of 8;
 anything else raises -- there is no host fallback.  The caller merges before
 and unmerges after (the optimizer step moves A and B and leaves the merged
 weight stale), which the two module-level functions do through the layer's
@@ -50,8 +51,9 @@ def _rows_view(t: torch.Tensor, features: int, name: str) -> torch.Tensor:
 def _check(x: torch.Tensor, weight: torch.Tensor) -> None:
     if not x.is_cuda:
         raise RuntimeError("thundersync_amd FusedLoRALinear runs on the GPU only; got a CPU tensor")
-    if x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
-        raise TypeError(f"FusedLoRALinear takes bf16 activations and weight, got {x.dtype} / {weight.dtype}")
+    if x.dtype not in (torch.bfloat16, torch.float16) or weight.dtype != x.dtype:
+        raise TypeError(f"FusedLoRALinear takes bf16 or fp16 activations and a weight of the same dtype, got "
+                        f"{x.dtype} / {weight.dtype}")
     if weight.dim() != 2:
         raise ValueError(f"weight must be [out, in], got {tuple(weight.shape)}")
     out_f, in_f = weight.shape
@@ -83,7 +85,7 @@ class FusedLoRALinear(torch.autograd.Function):
                             out=out_f):
             _lib.check(
                 lib.ts_lora_fwd(rows.data_ptr(), rows.stride(0), w.data_ptr(), w.stride(0), rows.shape[0], in_f,
-                                out_f, y.data_ptr(), y.stride(0), _lib.stream_of(x)),
+                                out_f, y.data_ptr(), y.stride(0), _lib.dtype_code(x.dtype), _lib.stream_of(x)),
                 f"ts_lora_fwd(rows={rows.shape[0]}, in={in_f}, out={out_f})",
             )
         ctx.save_for_backward(x, weight, lora_a, lora_b)
@@ -121,7 +123,7 @@ class FusedLoRALinear(torch.autograd.Function):
                                 w.stride(0) if w is not None else 0, _lib.ptr(a), _lib.ptr(b_t), rank,
                                 ctypes.c_float(ctx.scaling), n, in_f, out_f, _lib.ptr(dx),
                                 dx.stride(0) if dx is not None else 0, _lib.ptr(da), _lib.ptr(db), ws.data_ptr(),
-                                ws_bytes, _lib.stream_of(x)),
+                                ws_bytes, _lib.dtype_code(x.dtype), _lib.stream_of(x)),
                 f"ts_lora_bwd(rows={n}, in={in_f}, out={out_f}, rank={rank})",
             )
         grad_x = dx.view(x.shape) if dx is not None else None
