@@ -97,16 +97,17 @@ int ts_rmsnorm_bwd_noalloc(const void* dy, const void* x, const void* w,
                            int64_t width, int dtype, void* stream);
 
 /* ------------------------------------------------------------------------
- * Forest / packed bottom-right-causal GQA attention (bf16 or fp16, head_dim 128)
+ * Forest / packed bottom-right-causal GQA attention (bf16 or fp16; head_dim
+ * D = 32, 64, 96, 128, 192 or 256)
  *
  * A problem is a set of query SEGMENTS and key RUNS.  Segment s owns query
  * rows [q_row0, q_row0 + q_len) of the packed Q/O/dO/dQ tensors
- * ([rows, Hq, 128], any row/head stride) and attends to a virtual key
+ * ([rows, Hq, D], any row/head stride) and attends to a virtual key
  * sequence of kv_len keys assembled from runs: seg_spans[span0 .. span0 +
  * nspan) lists (run, kpos) -- run `index` supplies keys [kpos, kpos + len)
  * of that sequence.  Visibility is bottom-right causal over the sequence:
  * query row i sees key position j iff j <= kv_len - q_len + i.  A run is
- * one contiguous [len, Hkv, 128] block of K/V rows (a retained chunk, a
+ * one contiguous [len, Hkv, D] block of K/V rows (a retained chunk, a
  * forest node, a prefix), read in place through its own pointers and
  * strides, never concatenated; run_visits[visit0 .. visit0 + nvisit) lists
  * (segment, kpos) -- every segment that reads it -- and the backward writes
@@ -163,7 +164,7 @@ typedef struct ts_attn_problem {
   int32_t n_runs;
   int32_t hq;
   int32_t hkv;
-  int32_t head_dim;
+  int32_t head_dim; /* 32, 64, 96, 128, 192 or 256 */
   float scale;
   int32_t q_block;  /* rows per q_work item: ts_attn_q_block(hq / hkv) */
   int32_t kv_block; /* keys per kv_work item: ts_attn_kv_block(hq / hkv) */

@@ -4,11 +4,11 @@ One differentiable core op, :func:`attention`, serves every shape the
 reference's streaming engine produces.  A call is described by an
 :class:`AttnLayout`:
 
-* **key sources** -- the K/V tensors the call reads, each ``[N, Hkv, 128]``
+* **key sources** -- the K/V tensors the call reads, each ``[N, Hkv, D]``
   (a retained chunk, a pack's own K/V, a forest's whole K/V), read in place;
 * **runs** -- contiguous row ranges of a source (a whole chunk, one forest
   node);
-* **segments** -- blocks of query rows of the packed ``[R, Hq, 128]`` query,
+* **segments** -- blocks of query rows of the packed ``[R, Hq, D]`` query,
   each attending bottom-right-causally to the concatenation of its runs.
 
 The layout is integer metadata only (no pointers), so one layout serves every
@@ -36,7 +36,9 @@ Reference entry points mirrored here (same argument meaning):
   launch, each chunk being the call ``_ChunkedCausalSDPA`` makes
   (engine/streaming.py:1314-1423).
 
-Element types: bf16 and fp16 (Q, K, V of one call share one), head dim 128.
+Element types: bf16 and fp16 (Q, K, V of one call share one).  Head dims D:
+32, 64, 96, 128, 192 and 256 (128 with GQA groups that are a multiple of 4 runs
+the one-wave-per-head kernels, every other case the register-staged ones).
 There is no host path: CPU tensors, other dtypes or head dims raise.
 """
 
@@ -56,7 +58,8 @@ from ._abi import REF_DTYPE, RUN_DTYPE, SEG_DTYPE, AttnProblem, AttnRows
 from .dispatch import HIP_BACKWARD_PATH, HIP_PATH, count_attention_path
 from .operator_profiling import operator_range
 
-HEAD_DIM = 128
+HEAD_DIMS = (32, 64, 96, 128, 192, 256)
+HEAD_DIM = 128  # the head dim the tuned kernels take; also the launch-order estimate's row width
 ELEMENT_DTYPES = (torch.bfloat16, torch.float16)
 
 
@@ -247,12 +250,13 @@ class AttnLayout:
                 self._tables[key] = hit
         return hit
 
-    def problem(self, device, runs_ptr: int, scale: float, dtype: torch.dtype = torch.bfloat16) -> AttnProblem:
+    def problem(self, device, runs_ptr: int, scale: float, dtype: torch.dtype = torch.bfloat16,
+                head_dim: int = HEAD_DIM) -> AttnProblem:
         t = self.device_tables(device)
         return AttnProblem(
             t["segs"], t["seg_spans"], runs_ptr, t["run_visits"], t["q_work"], t["kv_work"],
             t["n_q_work"], t["n_kv_work"], len(self.seg_q), len(self.runs), self.hq, self.hkv,
-            HEAD_DIM, float(scale), q_block_rows(self.hq, self.hkv), kv_block_keys(self.hq, self.hkv), self.q_rows,
+            int(head_dim), float(scale), q_block_rows(self.hq, self.hkv), kv_block_keys(self.hq, self.hkv), self.q_rows,
             t["n_q_long"], t["n_kv_long"], _lib.dtype_code(dtype),
         )
 
@@ -295,9 +299,9 @@ def _long_items(costs: Sequence[int], heads: int, reread_bytes: int, slots: int 
     return n
 
 
-def _check_rows_tensor(t: torch.Tensor, name: str, heads: int, max_row_stride: int = 1 << 24) -> None:
-    if t.dim() != 3 or t.shape[1] != heads or t.shape[2] != HEAD_DIM:
-        raise ValueError(f"{name} must be [rows, {heads}, {HEAD_DIM}], got {tuple(t.shape)}")
+def _check_rows_tensor(t: torch.Tensor, name: str, heads: int, head_dim: int, max_row_stride: int = 1 << 24) -> None:
+    if t.dim() != 3 or t.shape[1] != heads or t.shape[2] != head_dim:
+        raise ValueError(f"{name} must be [rows, {heads}, {head_dim}], got {tuple(t.shape)}")
     if t.stride(2) != 1 or t.stride(0) % 8 or t.stride(1) % 8 or t.data_ptr() % 16:
         raise ValueError(f"{name} needs a contiguous head dim, 16-byte alignment and 8-element strides")
     if t.stride(0) >= max_row_stride:
@@ -360,7 +364,10 @@ def _validate_call(layout: AttnLayout, query: torch.Tensor, keys, values) -> Non
         raise RuntimeError("thundersync_amd attention runs on the GPU only; got a CPU tensor")
     if query.dtype not in ELEMENT_DTYPES:
         raise TypeError(f"thundersync_amd attention takes bf16 or fp16, got {query.dtype}")
-    _check_rows_tensor(query, "query", layout.hq)
+    head_dim = query.shape[-1] if query.dim() == 3 else -1
+    if head_dim not in HEAD_DIMS:
+        raise ValueError(f"thundersync_amd attention takes head dims {HEAD_DIMS}, got query {tuple(query.shape)}")
+    _check_rows_tensor(query, "query", layout.hq, head_dim)
     if query.shape[0] != layout.q_rows:
         raise ValueError(f"query has {query.shape[0]} rows, layout {layout.q_rows}")
     if len(keys) != len(layout.source_rows) or len(values) != len(layout.source_rows):
@@ -369,7 +376,7 @@ def _validate_call(layout: AttnLayout, query: torch.Tensor, keys, values) -> Non
         for name, t in (("key", k), ("value", v)):
             if t.device != query.device or t.dtype != query.dtype:
                 raise ValueError(f"{name} source {i} must be {query.dtype} on {query.device}")
-            _check_rows_tensor(t, f"{name} source {i}", layout.hkv)
+            _check_rows_tensor(t, f"{name} source {i}", layout.hkv, head_dim)
             if t.shape[0] != layout.source_rows[i]:
                 raise ValueError(f"{name} source {i} has {t.shape[0]} rows, layout {layout.source_rows[i]}")
 
@@ -385,7 +392,7 @@ class _Attention(torch.autograd.Function):
         out = torch.empty(query.shape, dtype=query.dtype, device=query.device)
         lse = torch.empty(layout.hq, max(layout.q_rows, 1), dtype=torch.float32, device=query.device)
         runs, host = _run_table(layout, keys, values)
-        problem = layout.problem(query.device, runs.data_ptr(), scale, query.dtype)
+        problem = layout.problem(query.device, runs.data_ptr(), scale, query.dtype, query.shape[2])
         check_tables(layout, problem, host, query.device)
         with operator_range("hip_attention_forward", rows=layout.q_rows, segments=len(layout.seg_q)):
             _lib.check(
@@ -426,7 +433,7 @@ class _Attention(torch.autograd.Function):
                 dvalues[i].zero_()
         runs, host = _run_table(layout, keys, values, dkeys, dvalues)
         rowstats = torch.empty(layout.hq, max(layout.q_rows, 1), 2, dtype=torch.float32, device=query.device)
-        problem = layout.problem(query.device, runs.data_ptr(), ctx.scale, query.dtype)
+        problem = layout.problem(query.device, runs.data_ptr(), ctx.scale, query.dtype, query.shape[2])
         check_tables(layout, problem, host, query.device)
         with operator_range("hip_attention_backward", rows=layout.q_rows, segments=len(layout.seg_q)):
             _lib.check(
@@ -442,7 +449,7 @@ class _Attention(torch.autograd.Function):
 
 def attention(query: torch.Tensor, layout: AttnLayout, keys: Sequence[torch.Tensor],
               values: Sequence[torch.Tensor], scale: float) -> tuple[torch.Tensor, torch.Tensor]:
-    """Core op: query ``[R, Hq, 128]`` bf16 or fp16 -> (out ``[R, Hq, 128]``, lse ``[Hq, R]`` fp32)."""
+    """Core op: query ``[R, Hq, D]`` bf16 or fp16 -> (out ``[R, Hq, D]``, lse ``[Hq, R]`` fp32)."""
     return _Attention.apply(query, layout, float(scale), len(keys), *keys, *values)
 
 
@@ -804,8 +811,8 @@ def retained_chunk_layout(q_rows: int, chunk_rows: Sequence[int], chunks: Sequen
 
 def retained_chunk_attention(query: torch.Tensor, ks: Sequence[torch.Tensor], vs: Sequence[torch.Tensor],
                              layout: AttnLayout, scale: float) -> torch.Tensor:
-    """``query`` ``[R, Hq, 128]`` over retained chunks ``ks``/``vs`` (each
-    ``[S_c, Hkv, 128]``) as described by :func:`retained_chunk_layout`;
+    """``query`` ``[R, Hq, D]`` over retained chunks ``ks``/``vs`` (each
+    ``[S_c, Hkv, D]``) as described by :func:`retained_chunk_layout`;
     differentiable wrt the query and every retained chunk."""
     out, _ = attention(_as_rows(query), layout, [_as_rows(k) for k in ks], [_as_rows(v) for v in vs], scale)
     return out

@@ -45,7 +45,8 @@ bool aligned_rows(const ts_attn_rows& r) {
 
 int validate(const ts_attn_problem* p, const char* what) {
   TS_CHECK_ARG(p != nullptr, "%s: null problem", what);
-  TS_CHECK_ARG(p->head_dim == D, "%s: head_dim %d unsupported (128 only)", what, p->head_dim);
+  TS_CHECK_ARG(head_dim_supported(p->head_dim), "%s: head_dim %d unsupported (32, 64, 96, 128, 192 or 256)", what,
+               p->head_dim);
   TS_CHECK_ARG(p->dtype == kBF16 || p->dtype == kF16, "%s: dtype %d unsupported (bf16 or fp16)", what, p->dtype);
   TS_CHECK_ARG(p->hq > 0 && p->hkv > 0 && p->hq % p->hkv == 0, "%s: hq %d not a multiple of hkv %d",
                what, p->hq, p->hkv);

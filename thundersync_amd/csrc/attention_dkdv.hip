@@ -7,12 +7,20 @@ namespace attn {
 // ---------------------------------------------------------------------------
 // backward dK / dV (key-stationary)
 // ---------------------------------------------------------------------------
-template <typename E>
-__global__ __launch_bounds__(kThreads, 2) void dkdv_kernel(ts_attn_problem P, ts_attn_rows Q,
+// Register-staged dK/dV for any supported head dim HD and GQA groups that are
+// not a multiple of 4 (and, at head dims other than 128, those that are): a
+// work-group owns P.kv_block keys (48 or 64) of one run and one KV head, wave
+// w keys 16 w .. 16 w + 15 (a wave past the block only helps stage the
+// tiles), and loops over every query head of the group and every visible
+// 32-row block; Q and dO rows pass through registers into padded LDS rows,
+// dO^T and Q^T come from register transposes of 8 x 8 blocks.
+template <typename E, int HD>
+__global__ __launch_bounds__(kThreads, HD > 128 ? 1 : 2) void dkdv_kernel(ts_attn_problem P, ts_attn_rows Q,
                                                            ts_attn_rows dO, const float* __restrict__ rowstats,
                                                            int64_t lse_ld) {
-  __shared__ __attribute__((aligned(16))) bf16 sq[32 * PITCH];
-  __shared__ __attribute__((aligned(16))) bf16 sd[32 * PITCH];
+  constexpr int NH = col_blocks<HD>();
+  __shared__ __attribute__((aligned(16))) bf16 sq[32 * pitch_of<HD>()];
+  __shared__ __attribute__((aligned(16))) bf16 sd[32 * pitch_of<HD>()];
   __shared__ float s_lse2[32];
   __shared__ float s_dlt[32];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -24,18 +32,20 @@ __global__ __launch_bounds__(kThreads, 2) void dkdv_kernel(ts_attn_problem P, ts
   const ts_attn_run run = load_uniform(P.runs, run_id);
   const int wk0 = k0 + 16 * wave;                 // first key (run-local) of this wave
   const int mykey = wk0 + (lane & 15);            // key column this lane holds
-  const bool wave_has_keys = wk0 < run.len;
+  const bool in_block = 16 * wave < P.kv_block;   // the wave's keys belong to this work item
+  const bool wave_has_keys = in_block && wk0 < run.len;
+  const bool key_valid = in_block && mykey < run.len;
   const float c = P.scale * kLog2e;
 
   // K^T / V^T B operands: key (lane & 15), d = 32 ks + 8 (lane >> 4) .. +7
-  bf16x8 kreg[4], vreg[4];
+  bf16x8 kreg[HD / 32], vreg[HD / 32];
   {
     const bf16* kp = (const bf16*)run.k + (int64_t)mykey * run.k_row_stride + (int64_t)hk * run.k_head_stride;
     const bf16* vp = (const bf16*)run.v + (int64_t)mykey * run.v_row_stride + (int64_t)hk * run.v_head_stride;
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
+    for (int ks = 0; ks < HD / 32; ++ks) {
       u32x4 a = u32x4{0u, 0u, 0u, 0u}, b = u32x4{0u, 0u, 0u, 0u};
-      if (mykey < run.len) {
+      if (key_valid) {
         a = ld16(kp + 32 * ks + 8 * (lane >> 4));
         b = ld16(vp + 32 * ks + 8 * (lane >> 4));
       }
@@ -43,12 +53,14 @@ __global__ __launch_bounds__(kThreads, 2) void dkdv_kernel(ts_attn_problem P, ts
       vreg[ks] = as_bf16x8(b);
     }
   }
-  f32x4 dk[8], dv[8];
+  f32x4 dk[NH][8], dv[NH][8];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    dk[e] = f32x4{0.f, 0.f, 0.f, 0.f};
-    dv[e] = f32x4{0.f, 0.f, 0.f, 0.f};
-  }
+  for (int hh = 0; hh < NH; ++hh)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      dk[hh][e] = f32x4{0.f, 0.f, 0.f, 0.f};
+      dv[hh][e] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
 
   for (int vi = 0; vi < run.nvisit; ++vi) {
     const ts_attn_ref ref = load_uniform(P.run_visits, run.visit0 + vi);
@@ -68,10 +80,10 @@ __global__ __launch_bounds__(kThreads, 2) void dkdv_kernel(ts_attn_problem P, ts
         const int h = hk * group + g;
         __syncthreads();
         const int64_t row0 = seg.q_row0 + r0;
-        rows32_to_lds(sq, (const bf16*)Q.ptr + row0 * Q.row_stride + (int64_t)h * Q.head_stride,
-                      Q.row_stride, nrows, tid);
-        rows32_to_lds(sd, (const bf16*)dO.ptr + row0 * dO.row_stride + (int64_t)h * dO.head_stride,
-                      dO.row_stride, nrows, tid);
+        rows32_to_lds<HD>(sq, (const bf16*)Q.ptr + row0 * Q.row_stride + (int64_t)h * Q.head_stride,
+                          Q.row_stride, nrows, tid);
+        rows32_to_lds<HD>(sd, (const bf16*)dO.ptr + row0 * dO.row_stride + (int64_t)h * dO.head_stride,
+                          dO.row_stride, nrows, tid);
         if (tid < 32) {
           float l2 = __builtin_huge_valf(), dl = 0.f;
           if (tid < nrows) {
@@ -92,10 +104,10 @@ __global__ __launch_bounds__(kThreads, 2) void dkdv_kernel(ts_attn_problem P, ts
           s[qb] = f32x4{0.f, 0.f, 0.f, 0.f};
           dp[qb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-          for (int ks = 0; ks < 4; ++ks) {
+          for (int ks = 0; ks < HD / 32; ++ks) {
             const int r = 16 * qb + (lane & 15);
-            const bf16x8 aq = as_bf16x8(ld16(sq + r * PITCH + 32 * ks + 8 * (lane >> 4)));
-            const bf16x8 ad = as_bf16x8(ld16(sd + r * PITCH + 32 * ks + 8 * (lane >> 4)));
+            const bf16x8 aq = as_bf16x8(ld16(sq + r * pitch_of<HD>() + 32 * ks + 8 * (lane >> 4)));
+            const bf16x8 ad = as_bf16x8(ld16(sd + r * pitch_of<HD>() + 32 * ks + 8 * (lane >> 4)));
             s[qb] = mma16<E>(aq, kreg[ks], s[qb]);
             dp[qb] = mma16<E>(ad, vreg[ks], dp[qb]);
           }
@@ -107,7 +119,7 @@ __global__ __launch_bounds__(kThreads, 2) void dkdv_kernel(ts_attn_problem P, ts
           for (int i = 0; i < 4; ++i) {
             const int rl = 16 * qb + 4 * (lane >> 4) + i;
             float p = fast_exp2(s[qb][i] * c - s_lse2[rl]);
-            if (rl >= nrows || mykey >= run.len || ref.kpos + mykey > off + r0 + rl) p = 0.f;
+            if (rl >= nrows || !key_valid || ref.kpos + mykey > off + r0 + rl) p = 0.f;
             pv[4 * qb + i] = p;
             dsv[4 * qb + i] = p * (dp[qb][i] - s_dlt[rl]);
           }
@@ -115,38 +127,48 @@ __global__ __launch_bounds__(kThreads, 2) void dkdv_kernel(ts_attn_problem P, ts
         const bf16x8 dsk = pack8<E>(dsv);
         int rows[8];
         slot_rows(lane >> 4, 0, rows);
-        bf16x8 at[8];
-        lds_rows_transposed(sd, rows, 8 * (lane & 15), at);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) dv[e] = mma16<E>(at[e], pk, dv[e]);
-        lds_rows_transposed(sq, rows, 8 * (lane & 15), at);
+        for (int hh = 0; hh < NH; ++hh) {
+          const int c0 = col_start<HD>(hh, lane);
+          bf16x8 at[8];
+          lds_rows_transposed<HD>(sd, rows, c0, at);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) dk[e] = mma16<E>(at[e], dsk, dk[e]);
+          for (int e = 0; e < 8; ++e) dv[hh][e] = mma16<E>(at[e], pk, dv[hh][e]);
+          lds_rows_transposed<HD>(sq, rows, c0, at);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) dk[hh][e] = mma16<E>(at[e], dsk, dk[hh][e]);
+        }
       }
     }
   }
-  if (mykey >= run.len) return;
+  if (!key_valid) return;
   if (run.dk) {
     bf16* p = (bf16*)run.dk + (int64_t)mykey * run.dk_row_stride + (int64_t)hk * run.dk_head_stride +
               32 * (lane >> 4);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float tmp[8];
+    for (int hh = 0; hh < NH; ++hh)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) tmp[e] = dk[e][i] * P.scale;
-      st16(p + 8 * i, as_u32x4(pack8<E>(tmp)));
-    }
+      for (int i = 0; i < 4; ++i) {
+        if (!col_valid<HD>(hh, lane >> 4, i)) continue;
+        float tmp[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) tmp[e] = dk[hh][e][i] * P.scale;
+        st16(p + 128 * hh + 8 * i, as_u32x4(pack8<E>(tmp)));
+      }
   }
   if (run.dv) {
     bf16* p = (bf16*)run.dv + (int64_t)mykey * run.dv_row_stride + (int64_t)hk * run.dv_head_stride +
               32 * (lane >> 4);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float tmp[8];
+    for (int hh = 0; hh < NH; ++hh)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) tmp[e] = dv[e][i];
-      st16(p + 8 * i, as_u32x4(pack8<E>(tmp)));
-    }
+      for (int i = 0; i < 4; ++i) {
+        if (!col_valid<HD>(hh, lane >> 4, i)) continue;
+        float tmp[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) tmp[e] = dv[hh][e][i];
+        st16(p + 128 * hh + 8 * i, as_u32x4(pack8<E>(tmp)));
+      }
   }
 }
 
@@ -486,15 +508,32 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_wave_kernel(ts_attn_problem 
   }
 }
 
+template <typename E, int HD>
+void launch_dkdv_generic(dim3 grid, const ts_attn_problem& P, ts_attn_rows q, ts_attn_rows dout,
+                         const float* rowstats, int64_t lse_ld, hipStream_t s) {
+  ts::TimedLaunch timed_("attention.dkdv_kernel", s);
+  hipLaunchKernelGGL((dkdv_kernel<E, HD>), grid, dim3(kThreads), 0, s, P, q, dout, rowstats, lse_ld);
+}
+
 template <typename E>
 int launch_dkdv_t(const ts_attn_problem& P, ts_attn_rows q, ts_attn_rows dout, const float* rowstats,
                 int64_t lse_ld, hipStream_t s) {
   const int group = P.hq / P.hkv;
   const dim3 grid((unsigned)(P.n_kv_work * P.hkv));
-  if (group % 4 == 0)
-    { ts::TimedLaunch timed_("attention.dkdv_kernel", s); hipLaunchKernelGGL((dkdv_wave_kernel<E, 3>), grid, dim3(kThreads), 0, s, P, q, dout, rowstats, lse_ld); }
-  else
-    { ts::TimedLaunch timed_("attention.dkdv_kernel", s); hipLaunchKernelGGL(dkdv_kernel<E>, grid, dim3(kThreads), 0, s, P, q, dout, rowstats, lse_ld); }
+  switch (P.head_dim) {
+    case 32: launch_dkdv_generic<E, 32>(grid, P, q, dout, rowstats, lse_ld, s); break;
+    case 64: launch_dkdv_generic<E, 64>(grid, P, q, dout, rowstats, lse_ld, s); break;
+    case 96: launch_dkdv_generic<E, 96>(grid, P, q, dout, rowstats, lse_ld, s); break;
+    case 192: launch_dkdv_generic<E, 192>(grid, P, q, dout, rowstats, lse_ld, s); break;
+    case 256: launch_dkdv_generic<E, 256>(grid, P, q, dout, rowstats, lse_ld, s); break;
+    default:
+      if (group % 4 == 0) {
+        ts::TimedLaunch timed_("attention.dkdv_kernel", s);
+        hipLaunchKernelGGL((dkdv_wave_kernel<E, 3>), grid, dim3(kThreads), 0, s, P, q, dout, rowstats, lse_ld);
+      } else {
+        launch_dkdv_generic<E, D>(grid, P, q, dout, rowstats, lse_ld, s);
+      }
+  }
   return ts::check_launch("ts_attn_bwd (dkdv)");
 }
 

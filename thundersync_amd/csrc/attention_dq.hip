@@ -10,7 +10,7 @@ namespace attn {
 // so that exp2(s * scale * log2(e) - lse2) is 0.  The two values of a row are
 // adjacent so the backward kernels fetch a tile's statistics in one load.
 // ---------------------------------------------------------------------------
-template <typename E>
+template <typename E, int HD>
 __global__ __launch_bounds__(kThreads) void delta_kernel(ts_attn_rows O, ts_attn_rows dO,
                                                          const float* __restrict__ lse,
                                                          float* __restrict__ rowstats, int64_t lse_ld,
@@ -20,15 +20,30 @@ __global__ __launch_bounds__(kThreads) void delta_kernel(ts_attn_rows O, ts_attn
   const int64_t row = pair / hq;
   const int h = (int)(pair % hq);
   if (row >= rows) return;
-  // O is read only here (non-temporal); dO stays cached for the dQ and dK/dV kernels that follow
-  const u32x4 a = __builtin_nontemporal_load(
-      reinterpret_cast<const u32x4*>((const bf16*)O.ptr + row * O.row_stride + (int64_t)h * O.head_stride + 8 * sub));
-  const u32x4 b = ld16((const bf16*)dO.ptr + row * dO.row_stride + (int64_t)h * dO.head_stride + 8 * sub);
+  // 16 lanes per (row, head), HD / 16 elements each.  O is read only here
+  // (non-temporal); dO stays cached for the dQ and dK/dV kernels that follow
+  constexpr int PER = HD / 16;
+  const bf16* op = (const bf16*)O.ptr + row * O.row_stride + (int64_t)h * O.head_stride + PER * sub;
+  const bf16* dp = (const bf16*)dO.ptr + row * dO.row_stride + (int64_t)h * dO.head_stride + PER * sub;
   float acc = 0.f;
+  auto add2 = [&](uint32_t a, uint32_t b) {
+    acc = fmaf(bits_to_f<E>(a & 0xffffu), bits_to_f<E>(b & 0xffffu), acc);
+    acc = fmaf(bits_to_f<E>(a >> 16), bits_to_f<E>(b >> 16), acc);
+  };
+  if constexpr (PER % 8 == 0) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    acc = fmaf(bits_to_f<E>(a[i] & 0xffffu), bits_to_f<E>(b[i] & 0xffffu), acc);
-    acc = fmaf(bits_to_f<E>(a[i] >> 16), bits_to_f<E>(b[i] >> 16), acc);
+    for (int c = 0; c < PER / 8; ++c) {
+      const u32x4 a = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(op + 8 * c));
+      const u32x4 b = ld16(dp + 8 * c);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) add2(a[i], b[i]);
+    }
+  } else {
+    // PER = 2, 4 or 6: 4-byte loads
+#pragma unroll
+    for (int c = 0; c < PER / 2; ++c)
+      add2(__builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(op) + c),
+           reinterpret_cast<const uint32_t*>(dp)[c]);
   }
 #pragma unroll
   for (int msk = 8; msk >= 1; msk >>= 1) acc += shfl_xor(acc, msk);
@@ -43,12 +58,16 @@ __global__ __launch_bounds__(kThreads) void delta_kernel(ts_attn_rows O, ts_attn
 // ---------------------------------------------------------------------------
 // backward dQ (query-stationary)
 // ---------------------------------------------------------------------------
-template <typename E, int GC>
+// Register-staged dQ for any supported head dim HD (the forward's work split:
+// wave w takes head w % GC and rows 32 (w / GC) ..); K^T for dQ^T += K^T dS^T
+// from register transposes of 8 x 8 blocks.
+template <typename E, int GC, int HD>
 __global__ __launch_bounds__(kThreads, 1) void dq_kernel(ts_attn_problem P, ts_attn_rows Q,
                                                          ts_attn_rows dO, const float* __restrict__ rowstats,
                                                          int64_t lse_ld, ts_attn_rows dQ) {
-  __shared__ __attribute__((aligned(16))) bf16 sk[BK * PITCH];
-  __shared__ __attribute__((aligned(16))) bf16 sv[BK * PITCH];
+  constexpr int NH = col_blocks<HD>();
+  __shared__ __attribute__((aligned(16))) bf16 sk[BK * pitch_of<HD>()];
+  __shared__ __attribute__((aligned(16))) bf16 sv[BK * pitch_of<HD>()];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   int yb;
   const int item = task_of(P.n_q_work, P.n_q_long, yb);
@@ -67,12 +86,12 @@ __global__ __launch_bounds__(kThreads, 1) void dq_kernel(ts_attn_problem P, ts_a
   const int w_last = min(wq0 + 32, T) - 1;
   const float c = P.scale * kLog2e;
 
-  bf16x8 qreg[2][4], dreg[2][4];
+  bf16x8 qreg[2][HD / 32], dreg[2][HD / 32];
   const int64_t qoff = (seg.q_row0 + wq0);
-  load_rows_b(qreg, (const bf16*)Q.ptr + qoff * Q.row_stride + (int64_t)h * Q.head_stride, Q.row_stride,
-              active ? T - wq0 : 0, lane);
-  load_rows_b(dreg, (const bf16*)dO.ptr + qoff * dO.row_stride + (int64_t)h * dO.head_stride,
-              dO.row_stride, active ? T - wq0 : 0, lane);
+  load_rows_b<2, HD>(qreg, (const bf16*)Q.ptr + qoff * Q.row_stride + (int64_t)h * Q.head_stride, Q.row_stride,
+                     active ? T - wq0 : 0, lane);
+  load_rows_b<2, HD>(dreg, (const bf16*)dO.ptr + qoff * dO.row_stride + (int64_t)h * dO.head_stride,
+                     dO.row_stride, active ? T - wq0 : 0, lane);
   float lse2[2], dlt[2];
 #pragma unroll
   for (int qb = 0; qb < 2; ++qb) {
@@ -85,11 +104,13 @@ __global__ __launch_bounds__(kThreads, 1) void dq_kernel(ts_attn_problem P, ts_a
       dlt[qb] = rowstats[at + 1];
     }
   }
-  f32x4 acc[2][8];
+  f32x4 acc[2][NH][8];
 #pragma unroll
   for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc[qb][e] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int hh = 0; hh < NH; ++hh)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[qb][hh][e] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   for (int sp = 0; sp < seg.nspan; ++sp) {
     const ts_attn_ref ref = load_uniform(P.seg_spans, seg.span0 + sp);
@@ -99,18 +120,13 @@ __global__ __launch_bounds__(kThreads, 1) void dq_kernel(ts_attn_problem P, ts_a
     for (int kt0 = 0; kt0 < run.len; kt0 += BK) {
       if (ref.kpos + kt0 > off + wg_last) break;
       const int nvalid = min(BK, run.len - kt0);
-      Tile tk, tv;
-      tile_load(tk, kb0 + (int64_t)kt0 * run.k_row_stride, run.k_row_stride, nvalid, tid);
-      tile_load(tv, vb0 + (int64_t)kt0 * run.v_row_stride, run.v_row_stride, nvalid, tid);
-      __syncthreads();
-      tile_store(tk, sk, tid);
-      tile_store(tv, sv, tid);
-      __syncthreads();
+      stage_kv<HD>(sk, sv, kb0 + (int64_t)kt0 * run.k_row_stride, run.k_row_stride,
+                   vb0 + (int64_t)kt0 * run.v_row_stride, run.v_row_stride, nvalid, tid);
       if (!active || ref.kpos + kt0 > off + w_last) continue;
 
       f32x4 s[4][2], dp[4][2];
-      tile_scores<E>(s, sk, qreg, lane);
-      tile_scores<E>(dp, sv, dreg, lane);  // dP^T = V dO^T, same shape as S^T
+      tile_scores<E, HD>(s, sk, qreg, lane);
+      tile_scores<E, HD>(dp, sv, dreg, lane);  // dP^T = V dO^T, same shape as S^T
       const bool need_mask = (kt0 + BK > run.len) || (ref.kpos + kt0 + BK - 1 > off + wq0);
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
@@ -139,12 +155,15 @@ __global__ __launch_bounds__(kThreads, 1) void dq_kernel(ts_attn_problem P, ts_a
         }
         int rows[8];
         slot_rows(lane >> 4, 32 * ss, rows);
-        bf16x8 kt[8];
-        lds_rows_transposed(sk, rows, 8 * (lane & 15), kt);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          acc[0][e] = mma16<E>(kt[e], dsk[0], acc[0][e]);
-          acc[1][e] = mma16<E>(kt[e], dsk[1], acc[1][e]);
+        for (int hh = 0; hh < NH; ++hh) {
+          bf16x8 kt[8];
+          lds_rows_transposed<HD>(sk, rows, col_start<HD>(hh, lane), kt);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            acc[0][hh][e] = mma16<E>(kt[e], dsk[0], acc[0][hh][e]);
+            acc[1][hh][e] = mma16<E>(kt[e], dsk[1], acc[1][hh][e]);
+          }
         }
       }
     }
@@ -157,12 +176,15 @@ __global__ __launch_bounds__(kThreads, 1) void dq_kernel(ts_attn_problem P, ts_a
     bf16* drow = (bf16*)dQ.ptr + (seg.q_row0 + row) * dQ.row_stride + (int64_t)h * dQ.head_stride +
                  32 * (lane >> 4);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float tmp[8];
+    for (int hh = 0; hh < NH; ++hh)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) tmp[e] = acc[qb][e][i] * P.scale;
-      st16(drow + 8 * i, as_u32x4(pack8<E>(tmp)));
-    }
+      for (int i = 0; i < 4; ++i) {
+        if (!col_valid<HD>(hh, lane >> 4, i)) continue;
+        float tmp[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) tmp[e] = acc[qb][hh][e][i] * P.scale;
+        st16(drow + 128 * hh + 8 * i, as_u32x4(pack8<E>(tmp)));
+      }
   }
 }
 
@@ -389,18 +411,48 @@ __global__ __launch_bounds__(64 * 8 / NQB, 1) void dq_wave_kernel(ts_attn_proble
   }
 }
 
+template <typename E, int HD>
+void launch_delta_hd(const ts_attn_problem& P, ts_attn_rows out, ts_attn_rows dout, const float* lse, float* rowstats,
+                     int64_t lse_ld, int64_t pairs, hipStream_t s) {
+  ts::TimedLaunch timed_("attention.delta_kernel", s);
+  hipLaunchKernelGGL((delta_kernel<E, HD>), dim3((unsigned)((pairs + 15) / 16)), dim3(kThreads), 0, s, out, dout, lse,
+                     rowstats, lse_ld, P.q_rows, P.hq);
+}
+
 template <typename E>
 int launch_delta_t(const ts_attn_problem& P, ts_attn_rows out, ts_attn_rows dout, const float* lse,
                  float* rowstats, int64_t lse_ld, hipStream_t s) {
   const int64_t pairs = P.q_rows * P.hq;
   if (pairs == 0) return TS_OK;
-  { ts::TimedLaunch timed_("attention.delta_kernel", s); hipLaunchKernelGGL(delta_kernel<E>, dim3((unsigned)((pairs + 15) / 16)), dim3(kThreads), 0, s, out,
-                     dout, lse, rowstats, lse_ld, P.q_rows, P.hq); }
+  switch (P.head_dim) {
+    case 32: launch_delta_hd<E, 32>(P, out, dout, lse, rowstats, lse_ld, pairs, s); break;
+    case 64: launch_delta_hd<E, 64>(P, out, dout, lse, rowstats, lse_ld, pairs, s); break;
+    case 96: launch_delta_hd<E, 96>(P, out, dout, lse, rowstats, lse_ld, pairs, s); break;
+    case 192: launch_delta_hd<E, 192>(P, out, dout, lse, rowstats, lse_ld, pairs, s); break;
+    case 256: launch_delta_hd<E, 256>(P, out, dout, lse, rowstats, lse_ld, pairs, s); break;
+    default: launch_delta_hd<E, D>(P, out, dout, lse, rowstats, lse_ld, pairs, s);
+  }
   return ts::check_launch("ts_attn_bwd (delta)");
 }
 
 // query rows per wave of the dQ kernel (16: eight waves, two per SIMD; 32: four)
 constexpr int kDqRowsPerWave = 16;
+
+template <typename E, int HD>
+void launch_dq_generic(const ts_attn_problem& P, int gc, dim3 grid, ts_attn_rows q, ts_attn_rows dout,
+                       const float* rowstats, int64_t lse_ld, ts_attn_rows dq, hipStream_t s) {
+  ts::TimedLaunch timed_("attention.dq_kernel", s);
+  if constexpr (HD != D) {
+    if (gc == 4) {
+      hipLaunchKernelGGL((dq_kernel<E, 4, HD>), grid, dim3(kThreads), 0, s, P, q, dout, rowstats, lse_ld, dq);
+      return;
+    }
+  }
+  if (gc == 2)
+    hipLaunchKernelGGL((dq_kernel<E, 2, HD>), grid, dim3(kThreads), 0, s, P, q, dout, rowstats, lse_ld, dq);
+  else
+    hipLaunchKernelGGL((dq_kernel<E, 1, HD>), grid, dim3(kThreads), 0, s, P, q, dout, rowstats, lse_ld, dq);
+}
 
 template <typename E>
 int launch_dq_t(const ts_attn_problem& P, ts_attn_rows q, ts_attn_rows dout, const float* rowstats,
@@ -408,12 +460,21 @@ int launch_dq_t(const ts_attn_problem& P, ts_attn_rows q, ts_attn_rows dout, con
   const int group = P.hq / P.hkv;
   const int gc = heads_per_block(group);
   const dim3 grid((unsigned)(P.n_q_work * P.hkv * (group / gc)));
-  if (gc == 4)
-    { ts::TimedLaunch timed_("attention.dq_kernel", s); hipLaunchKernelGGL((dq_wave_kernel<E, kDqRowsPerWave / 16>), grid, dim3(64 * 128 / kDqRowsPerWave), 0, s, P, q, dout, rowstats, lse_ld, dq); }
-  else if (gc == 2)
-    { ts::TimedLaunch timed_("attention.dq_kernel", s); hipLaunchKernelGGL((dq_kernel<E, 2>), grid, dim3(kThreads), 0, s, P, q, dout, rowstats, lse_ld, dq); }
-  else
-    { ts::TimedLaunch timed_("attention.dq_kernel", s); hipLaunchKernelGGL((dq_kernel<E, 1>), grid, dim3(kThreads), 0, s, P, q, dout, rowstats, lse_ld, dq); }
+  switch (P.head_dim) {
+    case 32: launch_dq_generic<E, 32>(P, gc, grid, q, dout, rowstats, lse_ld, dq, s); break;
+    case 64: launch_dq_generic<E, 64>(P, gc, grid, q, dout, rowstats, lse_ld, dq, s); break;
+    case 96: launch_dq_generic<E, 96>(P, gc, grid, q, dout, rowstats, lse_ld, dq, s); break;
+    case 192: launch_dq_generic<E, 192>(P, gc, grid, q, dout, rowstats, lse_ld, dq, s); break;
+    case 256: launch_dq_generic<E, 256>(P, gc, grid, q, dout, rowstats, lse_ld, dq, s); break;
+    default:
+      if (gc == 4) {
+        ts::TimedLaunch timed_("attention.dq_kernel", s);
+        hipLaunchKernelGGL((dq_wave_kernel<E, kDqRowsPerWave / 16>), grid, dim3(64 * 128 / kDqRowsPerWave), 0, s, P, q,
+                           dout, rowstats, lse_ld, dq);
+      } else {
+        launch_dq_generic<E, D>(P, gc, grid, q, dout, rowstats, lse_ld, dq, s);
+      }
+  }
   return ts::check_launch("ts_attn_bwd (dq)");
 }
 

@@ -7,12 +7,18 @@ namespace attn {
 // ---------------------------------------------------------------------------
 // forward
 // ---------------------------------------------------------------------------
-template <typename E, int GC>
-__global__ __launch_bounds__(kThreads, 2) void fwd_kernel(ts_attn_problem P, ts_attn_rows Q,
+// Register-staged forward for any supported head dim HD and GQA groups that
+// are not a multiple of 4 (and, at head dims other than 128, those that are):
+// a work-group owns 32 4 / GC query rows of GC query heads (wave w: head
+// w % GC, rows 32 (w / GC) ..); K/V tiles of 64 keys pass through registers
+// into padded LDS rows; V^T comes from register transposes of 8 x 8 blocks.
+template <typename E, int GC, int HD>
+__global__ __launch_bounds__(kThreads, HD > 128 ? 1 : 2) void fwd_kernel(ts_attn_problem P, ts_attn_rows Q,
                                                           ts_attn_rows O, float* __restrict__ lse,
                                                           int64_t lse_ld) {
-  __shared__ __attribute__((aligned(16))) bf16 sk[BK * PITCH];
-  __shared__ __attribute__((aligned(16))) bf16 sv[BK * PITCH];
+  constexpr int NH = col_blocks<HD>();
+  __shared__ __attribute__((aligned(16))) bf16 sk[BK * pitch_of<HD>()];
+  __shared__ __attribute__((aligned(16))) bf16 sv[BK * pitch_of<HD>()];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   int yb;
   const int item = task_of(P.n_q_work, P.n_q_long, yb);
@@ -31,15 +37,17 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_kernel(ts_attn_problem P, ts_
   const int w_last = min(wq0 + 32, T) - 1;
   const float c = P.scale * kLog2e;
 
-  bf16x8 qreg[2][4];
+  bf16x8 qreg[2][HD / 32];
   const bf16* qbase = (const bf16*)Q.ptr + (seg.q_row0 + wq0) * Q.row_stride + (int64_t)h * Q.head_stride;
-  load_rows_b(qreg, qbase, Q.row_stride, active ? T - wq0 : 0, lane);
+  load_rows_b<2, HD>(qreg, qbase, Q.row_stride, active ? T - wq0 : 0, lane);
 
-  f32x4 o[2][8];
+  f32x4 o[2][NH][8];
 #pragma unroll
   for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) o[qb][e] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int hh = 0; hh < NH; ++hh)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[qb][hh][e] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m[2] = {neg_inf(), neg_inf()};
   float lsum[2] = {0.f, 0.f};
 
@@ -51,17 +59,12 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_kernel(ts_attn_problem P, ts_
     for (int kt0 = 0; kt0 < run.len; kt0 += BK) {
       if (ref.kpos + kt0 > off + wg_last) break;  // later keys are invisible to every row
       const int nvalid = min(BK, run.len - kt0);
-      Tile tk, tv;
-      tile_load(tk, kb0 + (int64_t)kt0 * run.k_row_stride, run.k_row_stride, nvalid, tid);
-      tile_load(tv, vb0 + (int64_t)kt0 * run.v_row_stride, run.v_row_stride, nvalid, tid);
-      __syncthreads();
-      tile_store(tk, sk, tid);
-      tile_store(tv, sv, tid);
-      __syncthreads();
+      stage_kv<HD>(sk, sv, kb0 + (int64_t)kt0 * run.k_row_stride, run.k_row_stride,
+                   vb0 + (int64_t)kt0 * run.v_row_stride, run.v_row_stride, nvalid, tid);
       if (!active || ref.kpos + kt0 > off + w_last) continue;
 
       f32x4 s[4][2];
-      tile_scores<E>(s, sk, qreg, lane);
+      tile_scores<E, HD>(s, sk, qreg, lane);
       const bool need_mask = (kt0 + BK > run.len) || (ref.kpos + kt0 + BK - 1 > off + wq0);
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
@@ -101,7 +104,9 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_kernel(ts_attn_problem P, ts_
           }
         lsum[qb] = lsum[qb] * alpha + ps;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) o[qb][e] *= alpha;
+        for (int hh = 0; hh < NH; ++hh)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) o[qb][hh][e] *= alpha;
       }
       // O^T += V^T P^T, 32 keys per k-step
 #pragma unroll
@@ -116,12 +121,15 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_kernel(ts_attn_problem P, ts_
         }
         int rows[8];
         slot_rows(lane >> 4, 32 * ss, rows);
-        bf16x8 vt[8];
-        lds_rows_transposed(sv, rows, 8 * (lane & 15), vt);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          o[0][e] = mma16<E>(vt[e], pk[0], o[0][e]);
-          o[1][e] = mma16<E>(vt[e], pk[1], o[1][e]);
+        for (int hh = 0; hh < NH; ++hh) {
+          bf16x8 vt[8];
+          lds_rows_transposed<HD>(sv, rows, col_start<HD>(hh, lane), vt);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            o[0][hh][e] = mma16<E>(vt[e], pk[0], o[0][hh][e]);
+            o[1][hh][e] = mma16<E>(vt[e], pk[1], o[1][hh][e]);
+          }
         }
       }
     }
@@ -136,12 +144,15 @@ __global__ __launch_bounds__(kThreads, 2) void fwd_kernel(ts_attn_problem P, ts_
     bf16* orow = (bf16*)O.ptr + (seg.q_row0 + row) * O.row_stride + (int64_t)h * O.head_stride +
                  32 * (lane >> 4);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float tmp[8];
+    for (int hh = 0; hh < NH; ++hh)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) tmp[e] = o[qb][e][i] * inv;
-      st16(orow + 8 * i, as_u32x4(pack8<E>(tmp)));
-    }
+      for (int i = 0; i < 4; ++i) {
+        if (!col_valid<HD>(hh, lane >> 4, i)) continue;
+        float tmp[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) tmp[e] = o[qb][hh][e][i] * inv;
+        st16(orow + 128 * hh + 8 * i, as_u32x4(pack8<E>(tmp)));
+      }
     if ((lane >> 4) == 0)
       lse[(int64_t)h * lse_ld + seg.q_row0 + row] = l > 0.f ? (m[qb] + fast_log2(l)) * kLn2 : neg_inf();
   }
@@ -376,18 +387,43 @@ __global__ __launch_bounds__(64 * 8 / NQB, NQB == 1 ? 4 : 2) void fwd_wave_kerne
 // query rows per wave of the forward kernel (32: four waves per work-group; 16: eight)
 constexpr int kFwdRowsPerWave = 32;
 
+template <typename E, int HD>
+void launch_fwd_generic(const ts_attn_problem& P, int gc, dim3 grid, ts_attn_rows q, ts_attn_rows out, float* lse,
+                        int64_t lse_ld, hipStream_t s) {
+  ts::TimedLaunch timed_("attention.fwd_kernel", s);
+  if constexpr (HD != D) {
+    if (gc == 4) {
+      hipLaunchKernelGGL((fwd_kernel<E, 4, HD>), grid, dim3(kThreads), 0, s, P, q, out, lse, lse_ld);
+      return;
+    }
+  }
+  if (gc == 2)
+    hipLaunchKernelGGL((fwd_kernel<E, 2, HD>), grid, dim3(kThreads), 0, s, P, q, out, lse, lse_ld);
+  else
+    hipLaunchKernelGGL((fwd_kernel<E, 1, HD>), grid, dim3(kThreads), 0, s, P, q, out, lse, lse_ld);
+}
+
 template <typename E>
 int launch_fwd_t(const ts_attn_problem& P, ts_attn_rows q, ts_attn_rows out, float* lse, int64_t lse_ld,
                hipStream_t s) {
   const int group = P.hq / P.hkv;
   const int gc = heads_per_block(group);
   const dim3 grid((unsigned)(P.n_q_work * P.hkv * (group / gc)));
-  if (gc == 4)
-    { ts::TimedLaunch timed_("attention.fwd_kernel", s); hipLaunchKernelGGL((fwd_wave_kernel<E, kFwdRowsPerWave / 16>), grid, dim3(64 * 128 / kFwdRowsPerWave), 0, s, P, q, out, lse, lse_ld); }
-  else if (gc == 2)
-    { ts::TimedLaunch timed_("attention.fwd_kernel", s); hipLaunchKernelGGL((fwd_kernel<E, 2>), grid, dim3(kThreads), 0, s, P, q, out, lse, lse_ld); }
-  else
-    { ts::TimedLaunch timed_("attention.fwd_kernel", s); hipLaunchKernelGGL((fwd_kernel<E, 1>), grid, dim3(kThreads), 0, s, P, q, out, lse, lse_ld); }
+  switch (P.head_dim) {
+    case 32: launch_fwd_generic<E, 32>(P, gc, grid, q, out, lse, lse_ld, s); break;
+    case 64: launch_fwd_generic<E, 64>(P, gc, grid, q, out, lse, lse_ld, s); break;
+    case 96: launch_fwd_generic<E, 96>(P, gc, grid, q, out, lse, lse_ld, s); break;
+    case 192: launch_fwd_generic<E, 192>(P, gc, grid, q, out, lse, lse_ld, s); break;
+    case 256: launch_fwd_generic<E, 256>(P, gc, grid, q, out, lse, lse_ld, s); break;
+    default:
+      if (gc == 4) {
+        ts::TimedLaunch timed_("attention.fwd_kernel", s);
+        hipLaunchKernelGGL((fwd_wave_kernel<E, kFwdRowsPerWave / 16>), grid, dim3(64 * 128 / kFwdRowsPerWave), 0, s,
+                           P, q, out, lse, lse_ld);
+      } else {
+        launch_fwd_generic<E, D>(P, gc, grid, q, out, lse, lse_ld, s);
+      }
+  }
   return ts::check_launch("ts_attn_fwd");
 }
 

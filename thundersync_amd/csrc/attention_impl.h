@@ -25,18 +25,33 @@ __device__ __forceinline__ float neg_inf() { return -__builtin_huge_valf(); }
 __device__ __forceinline__ u32x4 ld16(const bf16* p) { return *reinterpret_cast<const u32x4*>(p); }
 __device__ __forceinline__ void st16(bf16* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
 
-// A 64 x 128 tile of K or V rows moved global -> registers -> LDS by 256
-// threads; 16 consecutive threads read one 256-byte row.
+// Head dims the kernels take: a multiple of 32 up to 256.  128 runs the
+// tuned one-wave-per-head kernels (GQA groups that are a multiple of 4); every
+// other head dim, and groups that are not a multiple of 4, run the
+// register-staged kernels below, templated on the head dim HD.
+__host__ __device__ constexpr bool head_dim_supported(int hd) {
+  return hd == 32 || hd == 64 || hd == 96 || hd == 128 || hd == 192 || hd == 256;
+}
+
+// LDS row pitch (elements) of the register-staged kernels' tiles: 16 bytes of
+// padding per row
+template <int HD> constexpr int pitch_of() { return HD + 8; }
+
+// A 64 x HD tile of K or V rows moved global -> registers -> LDS by 256
+// threads; HD / 8 consecutive threads read one row.
+template <int HD>
 struct Tile {
-  u32x4 v[4];
+  u32x4 v[HD / 32];
 };
 
-__device__ __forceinline__ void tile_load(Tile& t, const bf16* base, int64_t row_stride, int nvalid,
+template <int HD>
+__device__ __forceinline__ void tile_load(Tile<HD>& t, const bf16* base, int64_t row_stride, int nvalid,
                                           int tid) {
+  constexpr int CH = HD / 8;
 #pragma unroll
-  for (int it = 0; it < 4; ++it) {
+  for (int it = 0; it < HD / 32; ++it) {
     const int idx = it * kThreads + tid;
-    const int row = idx >> 4, chunk = idx & 15;
+    const int row = idx / CH, chunk = idx % CH;
     if (row < nvalid)
       t.v[it] = ld16(base + (int64_t)row * row_stride + chunk * 8);
     else
@@ -44,37 +59,84 @@ __device__ __forceinline__ void tile_load(Tile& t, const bf16* base, int64_t row
   }
 }
 
-__device__ __forceinline__ void tile_store(const Tile& t, bf16* lds, int tid) {
+template <int HD>
+__device__ __forceinline__ void tile_store(const Tile<HD>& t, bf16* lds, int tid) {
+  constexpr int CH = HD / 8;
 #pragma unroll
-  for (int it = 0; it < 4; ++it) {
+  for (int it = 0; it < HD / 32; ++it) {
     const int idx = it * kThreads + tid;
-    st16(lds + (idx >> 4) * PITCH + (idx & 15) * 8, t.v[it]);
+    st16(lds + (idx / CH) * pitch_of<HD>() + (idx % CH) * 8, t.v[it]);
   }
 }
 
-// rows [0, 32) x 128 of a per-head query-row tensor -> LDS (256 threads, 2 loads each)
+// One 64-key K tile and V tile into LDS (all threads; the barriers order the
+// stores after every wave's reads of the previous tiles and the reads after
+// the stores).  Up to a head dim of 128 both tiles are in flight at once;
+// above it they go one after the other, halving the staging registers.
+template <int HD>
+__device__ __forceinline__ void stage_kv(bf16* sk, bf16* sv, const bf16* kp, int64_t k_stride, const bf16* vp,
+                                         int64_t v_stride, int nvalid, int tid) {
+  if constexpr (HD <= 128) {
+    Tile<HD> tk, tv;
+    tile_load(tk, kp, k_stride, nvalid, tid);
+    tile_load(tv, vp, v_stride, nvalid, tid);
+    __syncthreads();
+    tile_store(tk, sk, tid);
+    tile_store(tv, sv, tid);
+  } else {
+    Tile<HD> t;
+    tile_load(t, kp, k_stride, nvalid, tid);
+    __syncthreads();
+    tile_store(t, sk, tid);
+    tile_load(t, vp, v_stride, nvalid, tid);
+    tile_store(t, sv, tid);
+  }
+  __syncthreads();
+}
+
+// rows [0, 32) x HD of a per-head query-row tensor -> LDS (256 threads)
+template <int HD = D>
 __device__ __forceinline__ void rows32_to_lds(bf16* lds, const bf16* base, int64_t row_stride,
                                               int nvalid, int tid) {
+  constexpr int CH = HD / 8;
 #pragma unroll
-  for (int it = 0; it < 2; ++it) {
-    const int idx = it * kThreads + tid;
-    const int row = idx >> 4, chunk = idx & 15;
+  for (int idx = tid; idx < 32 * CH; idx += kThreads) {
+    const int row = idx / CH, chunk = idx % CH;
     u32x4 v = u32x4{0u, 0u, 0u, 0u};
     if (row < nvalid) v = ld16(base + (int64_t)row * row_stride + chunk * 8);
-    st16(lds + row * PITCH + chunk * 8, v);
+    st16(lds + row * pitch_of<HD>() + chunk * 8, v);
   }
 }
 
 // Eight LDS rows (row index given per slot j) at column c0, transposed: out[e]
 // holds column c0 + e of the eight rows, slot j from row rows[j].
+template <int HD = D>
 __device__ __forceinline__ void lds_rows_transposed(const bf16* lds, const int rows[8], int c0,
                                                     bf16x8 out[8]) {
   u32x4 in[8], tr[8];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) in[j] = ld16(lds + rows[j] * PITCH + c0);
+  for (int j = 0; j < 8; ++j) in[j] = ld16(lds + rows[j] * pitch_of<HD>() + c0);
   transpose8x8(in, tr);
 #pragma unroll
   for (int e = 0; e < 8; ++e) out[e] = as_bf16x8(tr[e]);
+}
+
+// Column block of the transposed operands (V^T, K^T, dO^T, Q^T) in the
+// register-staged kernels: the 16 rows of an MFMA tile are head-dim columns
+// 128 hh + 8 (lane & 15) + e (e = 0..7 over eight tiles), so a head dim takes
+// (HD + 127) / 128 blocks.  Lanes whose columns lie past HD read the last
+// eight columns instead; their output rows are never stored.
+template <int HD> constexpr int col_blocks() { return (HD + 127) / 128; }
+template <int HD>
+__device__ __forceinline__ int col_start(int hh, int lane) {
+  const int c0 = 128 * hh + 8 * (lane & 15);
+  return c0 < HD ? c0 : HD - 8;
+}
+// whether output rows 4 g4 + i of column block hh (head-dim columns
+// 128 hh + 32 g4 + 8 i .. + 7) lie inside the head dim
+template <int HD>
+__device__ __forceinline__ bool col_valid(int hh, int g4, int i) {
+  return 128 * hh + 32 * g4 + 8 * i < HD;
 }
 
 // the row of slot j for lane group g: 4g + (j & 3) + 16 (j >> 2)
@@ -91,16 +153,16 @@ template <typename T> __device__ __forceinline__ bf16x8 pack8(const float* x) {
   return as_bf16x8(r);
 }
 
-// Load a wave's 16 NQB query rows x 128 as B operands of S^T = K Q^T:
+// Load a wave's 16 NQB query rows x HD as B operands of S^T = K Q^T:
 // reg[qb][ks] = row (16 qb + (lane & 15)), columns 32 ks + 8 (lane >> 4) .. +7.
-template <int NQB>
-__device__ __forceinline__ void load_rows_b(bf16x8 (&reg)[NQB][4], const bf16* base, int64_t row_stride,
+template <int NQB, int HD = D>
+__device__ __forceinline__ void load_rows_b(bf16x8 (&reg)[NQB][HD / 32], const bf16* base, int64_t row_stride,
                                             int nvalid, int lane) {
 #pragma unroll
   for (int qb = 0; qb < NQB; ++qb) {
     const int row = 16 * qb + (lane & 15);
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
+    for (int ks = 0; ks < HD / 32; ++ks) {
       u32x4 v = u32x4{0u, 0u, 0u, 0u};
       if (row < nvalid) v = ld16(base + (int64_t)row * row_stride + 32 * ks + 8 * (lane >> 4));
       reg[qb][ks] = as_bf16x8(v);
@@ -110,16 +172,16 @@ __device__ __forceinline__ void load_rows_b(bf16x8 (&reg)[NQB][4], const bf16* b
 
 // S^T tile (64 keys x 32 rows) = K_lds Q^T: s[kb][qb] lane holds keys
 // 16 kb + 4 (lane >> 4) + i, row 16 qb + (lane & 15).
-template <typename E>
-__device__ __forceinline__ void tile_scores(f32x4 s[4][2], const bf16* sk, const bf16x8 qreg[2][4],
+template <typename E, int HD = D>
+__device__ __forceinline__ void tile_scores(f32x4 s[4][2], const bf16* sk, const bf16x8 qreg[2][HD / 32],
                                             int lane) {
 #pragma unroll
   for (int kb = 0; kb < 4; ++kb) {
     s[kb][0] = f32x4{0.f, 0.f, 0.f, 0.f};
     s[kb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const bf16x8 a = as_bf16x8(ld16(sk + (16 * kb + (lane & 15)) * PITCH + 32 * ks + 8 * (lane >> 4)));
+    for (int ks = 0; ks < HD / 32; ++ks) {
+      const bf16x8 a = as_bf16x8(ld16(sk + (16 * kb + (lane & 15)) * pitch_of<HD>() + 32 * ks + 8 * (lane >> 4)));
       s[kb][0] = mma16<E>(a, qreg[0][ks], s[kb][0]);
       s[kb][1] = mma16<E>(a, qreg[1][ks], s[kb][1]);
     }

@@ -97,7 +97,9 @@ def _available(like: torch.Tensor, kernel: str, key: int, trial) -> bool:
 
 def hip_attention_available(query: torch.Tensor) -> bool:
     """Whether this query (any layout with the head dim last) may take the HIP attention."""
-    if query.shape[-1] != 128:
+    from .attention import HEAD_DIMS
+
+    if query.shape[-1] not in HEAD_DIMS:
         return False
     return _available(query, "hip_attention", int(query.shape[-1]), attention_trial)
 
