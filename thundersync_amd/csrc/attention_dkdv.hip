@@ -508,6 +508,239 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_wave_kernel(ts_attn_problem 
   }
 }
 
+// ---------------------------------------------------------------------------
+// backward dK / dV with the keys split over the waves (head dims 128 and 256;
+// GQA groups of any size)
+//
+// A work-group owns P.kv_block keys (48 or 64) of one run and one KV head;
+// wave w owns keys 16 w .. 16 w + 15, their K^T and V^T in registers, and all
+// waves walk the same sequence of steps -- every query head of the group,
+// then every visible 32-row block -- reading one double-buffered LDS stage:
+// the step's Q and dO rows (HD-element rows, 16-byte chunk c of row r at slot
+// c ^ tile_swizzle(r & 15)) and the rows' 32 (lse * log2 e, delta) pairs,
+// filled by buffer_load ... lds with each wave issuing its share of the
+// instructions, one work-group barrier per step.  The buffer resource of a
+// tile covers exactly its valid rows, so rows past a segment's end arrive as
+// zeros and add nothing (S = dP = 0, statistics (0, 0), hence dS = 0 and a
+// zero dO row).  S = Q K^T and dP = dO V^T take the Q/dO rows as A operands;
+// dV^T += dO^T P and dK^T += Q^T dS take dO^T / Q^T from ds_read_b64_tr_b16
+// (the lane layout of the one-wave-per-head kernel).  A wave past the work
+// item's keys (kv_block 48) only issues its DMA share; only steps that cross
+// the diagonal are masked.
+// ---------------------------------------------------------------------------
+template <typename E, int HD>
+__global__ __launch_bounds__(kThreads, 1) void dkdv_split_kernel(ts_attn_problem P, ts_attn_rows Q,
+                                                                 ts_attn_rows dO,
+                                                                 const float* __restrict__ rowstats,
+                                                                 int64_t lse_ld) {
+  static_assert(HD == 128 || HD == 256, "the swizzle needs 16 or 32 chunks per row");
+  constexpr int CH = HD / 8;              // 16-byte chunks per row
+  constexpr int NKS = HD / 32;            // k-steps of S / dP over the head dim
+  constexpr int NMB = HD / 16;            // 16-column blocks of dK / dV
+  constexpr int TILE = 32 * HD;           // elements of a 32-row tile
+  constexpr int STAGE = 2 * TILE + 512;   // Q, dO, then 1 KB of statistics
+  constexpr int RPI = 64 / CH;            // rows one DMA instruction fills (4 or 2)
+  constexpr int NDMA = 32 / RPI;          // DMA instructions per tile (8 or 16)
+  constexpr int PER_WAVE = NDMA / 4;      // of them issued by each wave
+  __shared__ __attribute__((aligned(16))) bf16 s_b0[STAGE];
+  __shared__ __attribute__((aligned(16))) bf16 s_b1[STAGE];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g4 = lane >> 4, j16 = lane & 15;
+  int hk;
+  const int item = task_of(P.n_kv_work, P.n_kv_long, hk);
+  const int run_id = uniform_table(P.kv_work)[2 * item];
+  const int k0 = uniform_table(P.kv_work)[2 * item + 1];
+  const int group = P.hq / P.hkv;
+  const ts_attn_run run = load_uniform(P.runs, run_id);
+  const int wk0 = k0 + 16 * wave;  // the wave's first key (run-local)
+  const int mykey = wk0 + j16;      // the key column this lane holds
+  const bool in_block = 16 * wave < P.kv_block;
+  const bool wave_active = in_block && wk0 < run.len;  // wave-uniform
+  const bool key_valid = in_block && mykey < run.len;
+  const float c = P.scale * kLog2e;
+
+  int ro[4], to[8];
+  swizzled_offsets<HD>(lane, ro, to);
+  // DMA instruction t fills rows RPI t .. RPI t + RPI - 1: lane l the row
+  // RPI t + l / CH, slot l % CH with logical chunk (l % CH) ^ tile_swizzle(row);
+  // this wave issues t = wave + 4 u.  Byte offsets of the lane's row and chunk.
+  int qoff[PER_WAVE], doff[PER_WAVE];
+#pragma unroll
+  for (int u = 0; u < PER_WAVE; ++u) {
+    const int row = RPI * (wave + 4 * u) + lane / CH;
+    const int chunk = (lane % CH) ^ tile_swizzle(row & 15);
+    qoff[u] = (int)((row * Q.row_stride + chunk * 8) * 2);
+    doff[u] = (int)((row * dO.row_stride + chunk * 8) * 2);
+  }
+
+  // K^T and V^T operands: kreg[ks] = K[key mykey][32 ks + 8 g4 ..], vreg likewise
+  bf16x8 kreg[NKS], vreg[NKS];
+  {
+    const bf16* kp = (const bf16*)run.k + (int64_t)mykey * run.k_row_stride + (int64_t)hk * run.k_head_stride;
+    const bf16* vp = (const bf16*)run.v + (int64_t)mykey * run.v_row_stride + (int64_t)hk * run.v_head_stride;
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+      kreg[ks] = as_bf16x8(key_valid ? ld16(kp + 32 * ks + 8 * g4) : u32x4{0u, 0u, 0u, 0u});
+      vreg[ks] = as_bf16x8(key_valid ? ld16(vp + 32 * ks + 8 * g4) : u32x4{0u, 0u, 0u, 0u});
+    }
+  }
+  f32x4 dk[NMB], dv[NMB];
+#pragma unroll
+  for (int mb = 0; mb < NMB; ++mb) {
+    dk[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    dv[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  // step cursor: query head g of the group, then the visit / row block
+  struct Cursor {
+    int g;
+    VisitCursor v;
+  };
+  auto enter = [&](VisitCursor& cv) {
+    const ts_attn_ref ref = load_uniform(P.run_visits, run.visit0 + cv.vi);
+    const ts_attn_segment seg = load_uniform(P.segs, ref.index);
+    cv.q_len = seg.q_len;
+    cv.off = seg.kv_len - seg.q_len;
+    cv.kpos = ref.kpos;
+    cv.q_row0 = seg.q_row0;
+    const int rs = ref.kpos + k0 - cv.off;
+    cv.r0 = (rs < 0 ? 0 : rs) & ~31;
+  };
+  auto settle = [&](VisitCursor cv) -> VisitCursor {
+    while (cv.r0 >= cv.q_len) {
+      if (++cv.vi >= run.nvisit) break;
+      enter(cv);
+    }
+    return cv;
+  };
+  auto first_visit = [&]() -> VisitCursor {
+    VisitCursor cv{0, 0, 0, 0, 0, 0};
+    if (run.nvisit > 0) enter(cv);
+    return settle(cv);
+  };
+  // the step after `cu`; g == group at the end
+  auto advance = [&](Cursor cu) -> Cursor {
+    cu.v.r0 += 32;
+    if (cu.v.r0 >= cu.v.q_len) cu.v = settle(cu.v);
+    if (cu.v.vi >= run.nvisit) {
+      ++cu.g;
+      cu.v = first_visit();
+    }
+    return cu;
+  };
+  // DMA of step `cu`'s tiles into `buf` (zero-size resources when cu is past
+  // the end, so the instructions need no branch)
+  auto issue = [&](const Cursor& cu, bf16* buf) {
+    const bool live = cu.g < group && cu.v.vi < run.nvisit;
+    const int nrows = live ? max(0, min(32, cu.v.q_len - cu.v.r0)) : 0;
+    const int h = hk * group + (live ? cu.g : 0);
+    const int64_t row0 = live ? cu.v.q_row0 + cu.v.r0 : 0;
+    const bf16* qb = (const bf16*)Q.ptr + row0 * Q.row_stride + (int64_t)h * Q.head_stride;
+    const bf16* db = (const bf16*)dO.ptr + row0 * dO.row_stride + (int64_t)h * dO.head_stride;
+    const rsrc_t rq = make_rsrc(qb, (uint32_t)(nrows * Q.row_stride * 2));
+    const rsrc_t rd = make_rsrc(db, (uint32_t)(nrows * dO.row_stride * 2));
+#pragma unroll
+    for (int u = 0; u < PER_WAVE; ++u) {
+      buffer_dma16(rq, buf + (wave + 4 * u) * 512, qoff[u]);
+      buffer_dma16(rd, buf + TILE + (wave + 4 * u) * 512, doff[u]);
+    }
+    if (wave == 0) {
+      // 32 rows x 8 bytes of statistics: lanes 0..15, 16 bytes each (the
+      // other lanes read past the resource and write zeros after them)
+      const rsrc_t rs = make_rsrc(rowstats + 2 * ((int64_t)h * lse_ld + row0), (uint32_t)(nrows * 8));
+      buffer_dma16(rs, buf + 2 * TILE, lane < 16 ? lane * 16 : 0x7ffffff0);
+    }
+  };
+
+  // one step on the tiles in `cur_buf`; buffer roles fixed per call
+  auto step = [&](auto bsel, Cursor& cur, Cursor& nxt) {
+    bf16* cur_buf = bsel.value == 0 ? s_b0 : s_b1;
+    bf16* nxt_buf = bsel.value == 0 ? s_b1 : s_b0;
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's share of the step's tiles has landed
+    __syncthreads();                // every wave's share has, and nobody reads nxt_buf any more
+    issue(nxt, nxt_buf);
+    const int off = cur.v.off, r0 = cur.v.r0, kpos = cur.v.kpos;
+    const int nrows = min(32, cur.v.q_len - r0);
+    // the wave's keys are all invisible to this block when its first key is
+    // beyond the block's last row
+    if (wave_active && kpos + wk0 <= off + r0 + nrows - 1) {
+      const bf16* tq = cur_buf;
+      const bf16* td = cur_buf + TILE;
+      const float* sl = reinterpret_cast<const float*>(cur_buf + 2 * TILE);  // [32] (lse2, delta)
+      // S = Q K^T, dP = dO V^T: [qb] holds rows 16 qb + 4 g4 + i, key j16
+      f32x4 sc[2], dp[2];
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) {
+        sc[qb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        dp[qb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks)
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) {
+          const bf16x8 aq = as_bf16x8(ld16(tq + ro_of(ro, ks) + 16 * qb * HD));
+          const bf16x8 ad = as_bf16x8(ld16(td + ro_of(ro, ks) + 16 * qb * HD));
+          sc[qb] = mma16<E>(aq, kreg[ks], sc[qb]);
+          dp[qb] = mma16<E>(ad, vreg[ks], dp[qb]);
+        }
+      // P and dS as B operands: slot j = 4 qb + i  <->  row 16 qb + 4 g4 + i
+      float pv[8], dsv[8];
+      const int lim = off + r0 - kpos - mykey;  // row rl sees the key iff rl >= -lim
+      const bool diag = kpos + wk0 + 15 > off + r0;  // wave-uniform
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int rl = 16 * qb + 4 * g4 + i;
+          float p = fast_exp2(sc[qb][i] * c - sl[2 * rl]);
+          if (diag && rl + lim < 0) p = 0.f;
+          pv[4 * qb + i] = p;
+          dsv[4 * qb + i] = p * (dp[qb][i] - sl[2 * rl + 1]);
+        }
+      const bf16x8 pk = pack8<E>(pv);
+      const bf16x8 dsk = pack8<E>(dsv);
+      // dV^T += dO^T P, dK^T += Q^T dS: rows d = 16 mb + 4 g4 + i, column key j16
+#pragma unroll
+      for (int mb = 0; mb < NMB; ++mb) {
+        const int o = to_of(to, mb);
+        const u32x2 a0 = tr_read(td + o), a1 = tr_read(td + o + 16 * HD);
+        const u32x2 b0 = tr_read(tq + o), b1 = tr_read(tq + o + 16 * HD);
+        dv[mb] = mma16<E>(as_bf16x8(u32x4{a0[0], a0[1], a1[0], a1[1]}), pk, dv[mb]);
+        dk[mb] = mma16<E>(as_bf16x8(u32x4{b0[0], b0[1], b1[0], b1[1]}), dsk, dk[mb]);
+      }
+    }
+    cur = nxt;
+    nxt = advance(nxt);
+  };
+
+  Cursor cur{0, first_visit()};
+  if (cur.v.vi >= run.nvisit) cur.g = group;  // a run nobody reads
+  Cursor nxt = cur.g < group ? advance(cur) : cur;
+  issue(cur, s_b0);
+  while (cur.g < group) {
+    step(std::integral_constant<int, 0>{}, cur, nxt);
+    if (cur.g >= group) break;
+    step(std::integral_constant<int, 1>{}, cur, nxt);
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // the last (empty) DMA has landed before the waves exit
+  if (!key_valid) return;
+  // lane (g4, j16) holds d = 16 mb + 4 g4 .. + 3 of key mykey: 8-byte stores
+  if (run.dk) {
+    bf16* p = (bf16*)run.dk + (int64_t)mykey * run.dk_row_stride + (int64_t)hk * run.dk_head_stride + 4 * g4;
+#pragma unroll
+    for (int mb = 0; mb < NMB; ++mb)
+      *reinterpret_cast<u32x2*>(p + 16 * mb) =
+          u32x2{pack2<E>(dk[mb][0] * P.scale, dk[mb][1] * P.scale), pack2<E>(dk[mb][2] * P.scale, dk[mb][3] * P.scale)};
+  }
+  if (run.dv) {
+    bf16* p = (bf16*)run.dv + (int64_t)mykey * run.dv_row_stride + (int64_t)hk * run.dv_head_stride + 4 * g4;
+#pragma unroll
+    for (int mb = 0; mb < NMB; ++mb)
+      *reinterpret_cast<u32x2*>(p + 16 * mb) = u32x2{pack2<E>(dv[mb][0], dv[mb][1]), pack2<E>(dv[mb][2], dv[mb][3])};
+  }
+}
+
 template <typename E, int HD>
 void launch_dkdv_generic(dim3 grid, const ts_attn_problem& P, ts_attn_rows q, ts_attn_rows dout,
                          const float* rowstats, int64_t lse_ld, hipStream_t s) {
@@ -525,7 +758,11 @@ int launch_dkdv_t(const ts_attn_problem& P, ts_attn_rows q, ts_attn_rows dout, c
     case 64: launch_dkdv_generic<E, 64>(grid, P, q, dout, rowstats, lse_ld, s); break;
     case 96: launch_dkdv_generic<E, 96>(grid, P, q, dout, rowstats, lse_ld, s); break;
     case 192: launch_dkdv_generic<E, 192>(grid, P, q, dout, rowstats, lse_ld, s); break;
-    case 256: launch_dkdv_generic<E, 256>(grid, P, q, dout, rowstats, lse_ld, s); break;
+    case 256: {
+      ts::TimedLaunch timed_("attention.dkdv_kernel", s);
+      hipLaunchKernelGGL((dkdv_split_kernel<E, 256>), grid, dim3(kThreads), 0, s, P, q, dout, rowstats, lse_ld);
+      break;
+    }
     default:
       if (group % 4 == 0) {
         ts::TimedLaunch timed_("attention.dkdv_kernel", s);

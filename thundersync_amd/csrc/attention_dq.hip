@@ -1,5 +1,5 @@
 // Attention backward: row statistics and dQ (query-stationary).
-#include "attention_impl.h"
+#include "attention_dq_wave.h"
 
 namespace ts {
 namespace attn {
@@ -188,229 +188,6 @@ __global__ __launch_bounds__(kThreads, 1) void dq_kernel(ts_attn_problem P, ts_a
   }
 }
 
-// ---------------------------------------------------------------------------
-// backward dQ for GQA groups that are a multiple of 4 (query-stationary)
-//
-// A work-group owns 32 query rows of one segment for the 4 query heads of one
-// quarter of a GQA group; wave w takes head w & 3 and 16 NQB of the rows
-// (NQB = 1: eight waves, two per SIMD, so that one wave's LDS and MFMA waits
-// are covered by the other's work; NQB = 2: four waves of 32 rows, one per
-// SIMD).  Q and dO rows stay in registers as B operands, with the rows'
-// (lse * log2 e, delta) pairs.  The segment's key runs stream through 64-key
-// K/V tiles that all waves share: double-buffered LDS stages filled by
-// buffer_load ... lds (each wave issues its share of a tile's instructions;
-// rows past a run's end arrive as zeros and add nothing, because a zero K row
-// contributes zero to dQ), one work-group barrier per tile.  Tiles use the dK/dV kernel's 256-byte rows
-// with chunk c of row r at slot c ^ tile_swizzle(r & 15): K and V rows feed S^T = K Q^T
-// and dP^T = V dO^T as A operands, K^T for dQ^T += K^T dS^T comes from
-// ds_read_b64_tr_b16.  Only tiles that cross the diagonal are masked.
-// ---------------------------------------------------------------------------
-template <typename E, int NQB>
-__global__ __launch_bounds__(64 * 8 / NQB, 1) void dq_wave_kernel(ts_attn_problem P, ts_attn_rows Q, ts_attn_rows dO,
-                                                                 const float* __restrict__ rowstats,
-                                                                 int64_t lse_ld, ts_attn_rows dQ) {
-  constexpr int kWaves = 8 / NQB;
-  __shared__ __attribute__((aligned(16))) bf16 s_k0[kKV64];
-  __shared__ __attribute__((aligned(16))) bf16 s_v0[kKV64];
-  __shared__ __attribute__((aligned(16))) bf16 s_k1[kKV64];
-  __shared__ __attribute__((aligned(16))) bf16 s_v1[kKV64];
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int g4 = lane >> 4, j16 = lane & 15;
-  int yb;
-  const int item = task_of(P.n_q_work, P.n_q_long, yb);
-  const int seg_id = uniform_table(P.q_work)[2 * item];
-  const int q0 = uniform_table(P.q_work)[2 * item + 1];
-  const int group = P.hq / P.hkv;
-  const int chunks = group / 4;
-  const int hk = yb / chunks;
-  const int h = hk * group + (yb % chunks) * 4 + (wave & 3);
-  const int qw = q0 + 16 * NQB * (wave >> 2);  // this wave's first row
-  const ts_attn_segment seg = load_uniform(P.segs, seg_id);
-  const int T = seg.q_len;
-  const int off = seg.kv_len - seg.q_len;
-  const int last = min(q0 + 32, T) - 1;
-  const float c = P.scale * kLog2e;
-
-  // Q / dO rows as B operands: reg[qb][ks] = row qw + 16 qb + j16, columns 32 ks + 8 g4 ..
-  bf16x8 qreg[NQB][4], dreg[NQB][4];
-  const int64_t row0 = seg.q_row0 + qw;
-  load_rows_b(qreg, (const bf16*)Q.ptr + row0 * Q.row_stride + (int64_t)h * Q.head_stride, Q.row_stride,
-              T - qw, lane);
-  load_rows_b(dreg, (const bf16*)dO.ptr + row0 * dO.row_stride + (int64_t)h * dO.head_stride,
-              dO.row_stride, T - qw, lane);
-  // rows past the segment: zero Q and dO with statistics (0, 0) give dS = 0
-  float lse2[NQB], dlt[NQB];
-#pragma unroll
-  for (int qb = 0; qb < NQB; ++qb) {
-    const int row = qw + 16 * qb + j16;
-    lse2[qb] = 0.f;
-    dlt[qb] = 0.f;
-    if (row < T) {
-      const int64_t at = 2 * ((int64_t)h * lse_ld + seg.q_row0 + row);
-      lse2[qb] = rowstats[at];
-      dlt[qb] = rowstats[at + 1];
-    }
-  }
-  f32x4 ndlt[NQB];  // -delta of the lane's row, the starting value of the dP^T accumulators
-#pragma unroll
-  for (int qb = 0; qb < NQB; ++qb) ndlt[qb] = f32x4{-dlt[qb], -dlt[qb], -dlt[qb], -dlt[qb]};
-  f32x4 acc[8][NQB];
-#pragma unroll
-  for (int mb = 0; mb < 8; ++mb)
-#pragma unroll
-    for (int qb = 0; qb < NQB; ++qb) acc[mb][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  int ro[4], to[8];
-  swizzled_offsets(lane, ro, to);
-
-  // one 32-key half ss of a tile: S^T = K Q^T, dP^T = V dO^T for keys
-  // 32 ss .. 32 ss + 31 ([kb][qb] lane holds keys 32 ss + 16 kb + 4 g4 + i,
-  // row 16 qb + j16)
-  auto scores = [&](const bf16* tk, const bf16* tv, int ss, f32x4 (&sc)[2][NQB], f32x4 (&dp)[2][NQB])
-      __attribute__((always_inline)) {
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int qb = 0; qb < NQB; ++qb) {
-        sc[kb][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
-        dp[kb][qb] = ndlt[qb];  // the MFMAs accumulate dP^T - delta
-      }
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        const bf16x8 ak = as_bf16x8(ld16(tk + ro[ks] + (32 * ss + 16 * kb) * D));
-        const bf16x8 av = as_bf16x8(ld16(tv + ro[ks] + (32 * ss + 16 * kb) * D));
-#pragma unroll
-        for (int qb = 0; qb < NQB; ++qb) {
-          sc[kb][qb] = mma16<E>(ak, qreg[qb][ks], sc[kb][qb]);
-          dp[kb][qb] = mma16<E>(av, dreg[qb][ks], dp[kb][qb]);
-        }
-      }
-  };
-  // dS^T = P^T (dP^T - delta) (dp holds dP^T - delta), P^T = exp2(S^T c - lse2), packed as the B
-  // operand of dQ^T += K^T dS^T (slot j <-> key 32 ss + 16 (j >> 2) + 4 g4 +
-  // (j & 3)); DIAG masks keys past each row's diagonal
-  auto dscores = [&](auto diag, int kpos, int kt0, int ss, f32x4 (&sc)[2][NQB], const f32x4 (&dp)[2][NQB],
-                     bf16x8 (&dsk)[NQB]) __attribute__((always_inline)) {
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int qb = 0; qb < NQB; ++qb) {
-        // row qw + 16 qb + j16 sees key kt0 + 32 ss + 16 kb + 4 g4 + i iff i <= lim
-        const int lim = off + qw + 16 * qb + j16 - kpos - kt0 - 32 * ss - 16 * kb - 4 * g4;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          float p = fast_exp2(sc[kb][qb][i] * c - lse2[qb]);
-          if (decltype(diag)::value) p = i <= lim ? p : 0.f;
-          sc[kb][qb][i] = p * dp[kb][qb][i];
-        }
-      }
-#pragma unroll
-    for (int qb = 0; qb < NQB; ++qb) {
-      float tmp[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) tmp[j] = sc[j >> 2][qb][j & 3];
-      dsk[qb] = pack8<E>(tmp);
-    }
-  };
-  auto accumulate = [&](const bf16* tk, int ss, const bf16x8 (&dsk)[NQB]) __attribute__((always_inline)) {
-#pragma unroll
-    for (int mb = 0; mb < 8; ++mb) {
-      const u32x2 a0 = tr_read(tk + to[mb] + 32 * ss * D);
-      const u32x2 a1 = tr_read(tk + to[mb] + (32 * ss + 16) * D);
-      const bf16x8 a = as_bf16x8(u32x4{a0[0], a0[1], a1[0], a1[1]});
-#pragma unroll
-      for (int qb = 0; qb < NQB; ++qb) acc[mb][qb] = mma16<E>(a, dsk[qb], acc[mb][qb]);
-    }
-  };
-  // one tile, the halves software-pipelined: half 1's score MFMAs are issued
-  // beside half 0's exponentials, half 0's dQ MFMAs beside half 1's
-  auto tile_body = [&](auto diag, const bf16* tk, const bf16* tv, int kpos, int kt0) __attribute__((always_inline)) {
-    f32x4 sc0[2][NQB], dp0[2][NQB], sc1[2][NQB], dp1[2][NQB];
-    bf16x8 dsk0[NQB], dsk1[NQB];
-    scores(tk, tv, 0, sc0, dp0);
-    __builtin_amdgcn_sched_barrier(0);
-    scores(tk, tv, 1, sc1, dp1);
-    dscores(diag, kpos, kt0, 0, sc0, dp0, dsk0);
-    // 16 K/V reads and 16 NQB MFMAs of half 1 beside ~40 NQB VALU instructions
-    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // the first K/V reads of half 1
-#pragma unroll
-    for (int i = 0; i < 12; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, NQB, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, NQB == 2 ? 5 : 3, 0);
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, NQB, 0);
-      __builtin_amdgcn_sched_group_barrier(0x002, NQB == 2 ? 4 : 3, 0);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    dscores(diag, kpos, kt0, 1, sc1, dp1, dsk1);
-    accumulate(tk, 0, dsk0);
-    __builtin_amdgcn_sched_group_barrier(0x100, 8, 1);  // K^T reads for dQ of half 0
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
-#pragma unroll
-      for (int qb = 0; qb < NQB; ++qb) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 1);
-        __builtin_amdgcn_sched_group_barrier(0x002, NQB == 2 ? 4 : 5, 1);
-      }
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    accumulate(tk, 1, dsk1);
-    // K^T fragment reads of half 1 kept four blocks ahead of their MFMAs
-    __builtin_amdgcn_sched_group_barrier(0x100, 8, 2);
-#pragma unroll
-    for (int mb = 0; mb < 8; ++mb) {
-      __builtin_amdgcn_sched_group_barrier(0x008, NQB, 2);
-      if (mb + 4 < 8) __builtin_amdgcn_sched_group_barrier(0x100, 2, 2);
-    }
-  };
-
-  auto step = [&](auto bsel, TileCursor& cur) {
-    const int kpos = cur.kpos;
-    const int kt0 = cur.kt0;
-    const TileCursor nxt = next_kv_tile(P, seg, last, cur);
-    __builtin_amdgcn_s_waitcnt(0);  // this wave's part of the tile has landed
-    __syncthreads();                // every part has, and the other stage is free
-    const bf16* tk = bsel.value == 0 ? s_k0 : s_k1;
-    const bf16* tv = bsel.value == 0 ? s_v0 : s_v1;
-    if (nxt.sp < seg.nspan)
-      issue_kv_tile<kWaves>(hk, wave, lane, nxt, bsel.value == 0 ? s_k1 : s_k0, bsel.value == 0 ? s_v1 : s_v0);
-
-    if (kpos + kt0 + BK - 1 > off + qw)
-      tile_body(std::true_type{}, tk, tv, kpos, kt0);
-    else
-      tile_body(std::false_type{}, tk, tv, kpos, kt0);
-    cur = nxt;
-  };
-
-  TileCursor cur = first_kv_tile(P, seg, last);
-  if (cur.sp < seg.nspan) issue_kv_tile<kWaves>(hk, wave, lane, cur, s_k0, s_v0);
-  while (cur.sp < seg.nspan) {
-    step(std::integral_constant<int, 0>{}, cur);
-    if (cur.sp >= seg.nspan) break;
-    step(std::integral_constant<int, 1>{}, cur);
-  }
-
-  // dQ^T: acc[mb][qb] lane holds d = 16 mb + 4 g4 + i of row qw + 16 qb + j16
-#pragma unroll
-  for (int qb = 0; qb < NQB; ++qb) {
-    const int row = qw + 16 * qb + j16;
-    if (row >= T) continue;
-    bf16* drow = (bf16*)dQ.ptr + (seg.q_row0 + row) * dQ.row_stride + (int64_t)h * dQ.head_stride + 4 * g4;
-#pragma unroll
-    for (int mb = 0; mb < 8; ++mb) {
-      const f32x4 v = acc[mb][qb] * P.scale;
-      *reinterpret_cast<u32x2*>(drow + 16 * mb) = u32x2{pack2<E>(v[0], v[1]), pack2<E>(v[2], v[3])};
-    }
-  }
-}
-
 template <typename E, int HD>
 void launch_delta_hd(const ts_attn_problem& P, ts_attn_rows out, ts_attn_rows dout, const float* lse, float* rowstats,
                      int64_t lse_ld, int64_t pairs, hipStream_t s) {
@@ -465,7 +242,7 @@ int launch_dq_t(const ts_attn_problem& P, ts_attn_rows q, ts_attn_rows dout, con
     case 64: launch_dq_generic<E, 64>(P, gc, grid, q, dout, rowstats, lse_ld, dq, s); break;
     case 96: launch_dq_generic<E, 96>(P, gc, grid, q, dout, rowstats, lse_ld, dq, s); break;
     case 192: launch_dq_generic<E, 192>(P, gc, grid, q, dout, rowstats, lse_ld, dq, s); break;
-    case 256: launch_dq_generic<E, 256>(P, gc, grid, q, dout, rowstats, lse_ld, dq, s); break;
+    case 256: launch_dq_wave256(P, gc, grid, q, dout, rowstats, lse_ld, dq, s); break;
     default:
       if (gc == 4) {
         ts::TimedLaunch timed_("attention.dq_kernel", s);

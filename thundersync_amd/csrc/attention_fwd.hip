@@ -159,13 +159,16 @@ __global__ __launch_bounds__(kThreads, HD > 128 ? 1 : 2) void fwd_kernel(ts_attn
 }
 
 // ---------------------------------------------------------------------------
-// forward for GQA groups that are a multiple of 4
+// forward with the waves sharing K/V tiles (head dim 128 with GQA groups that
+// are a multiple of 4 (GC = 4); head dim 256 with any group, GC heads per
+// work-group)
 //
-// A work-group owns 32 query rows of one segment for the 4 query heads of one
-// quarter of a GQA group; wave w takes head w & 3 and 16 NQB of the rows
-// (NQB = 2: four waves, two work-groups and two waves per SIMD; NQB = 1:
-// eight waves of 16 rows, four waves per SIMD, measured no faster on C2 at
-// 1.32 ms).  The heads share 64-key K/V
+// A work-group owns 128 / GC query rows of one segment for GC query heads of
+// one GQA group; wave w takes head w % GC and 16 NQB rows (at head dim 128
+// with GC = 4: NQB = 2, four waves, two work-groups and two waves per SIMD;
+// NQB = 1, eight waves of 16 rows, four waves per SIMD, measured no faster on
+// C2 at 1.32 ms; at head dim 256 NQB = 1, eight waves, two per SIMD, one
+// work-group per CU for its 128 KB of tiles).  The heads share 64-key K/V
 // tiles, streamed by buffer DMA into double-buffered swizzled LDS stages (one
 // work-group barrier per tile).  Q rows stay in registers as B operands of
 // S^T = K Q^T; V^T for O^T += V^T P^T comes from ds_read_b64_tr_b16.  Each
@@ -181,16 +184,17 @@ __global__ __launch_bounds__(kThreads, HD > 128 ? 1 : 2) void fwd_kernel(ts_attn
 constexpr float kRescaleSlack = 8.f;    // log2 units
 constexpr float kRescaleBound = 256.f;  // 2^kRescaleSlack
 
-template <typename E, int NQB>
-__global__ __launch_bounds__(64 * 8 / NQB, NQB == 1 ? 4 : 2) void fwd_wave_kernel(ts_attn_problem P, ts_attn_rows Q,
+template <typename E, int NQB, int HD = D, int GC = 4>
+__global__ __launch_bounds__(64 * 8 / NQB, HD > 128 ? (NQB == 1 ? 2 : 1) : (NQB == 1 ? 4 : 2)) void fwd_wave_kernel(ts_attn_problem P, ts_attn_rows Q,
                                                                                   ts_attn_rows O,
                                                                                   float* __restrict__ lse,
                                                                                   int64_t lse_ld) {
   constexpr int kWaves = 8 / NQB;
-  __shared__ __attribute__((aligned(16))) bf16 s_k0[kKV64];
-  __shared__ __attribute__((aligned(16))) bf16 s_v0[kKV64];
-  __shared__ __attribute__((aligned(16))) bf16 s_k1[kKV64];
-  __shared__ __attribute__((aligned(16))) bf16 s_v1[kKV64];
+  constexpr int NKS = HD / 32, NMB = HD / 16;  // k-steps of S; 16-column blocks of O
+  __shared__ __attribute__((aligned(16))) bf16 s_k0[BK * HD];
+  __shared__ __attribute__((aligned(16))) bf16 s_v0[BK * HD];
+  __shared__ __attribute__((aligned(16))) bf16 s_k1[BK * HD];
+  __shared__ __attribute__((aligned(16))) bf16 s_v1[BK * HD];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g4 = lane >> 4, j16 = lane & 15;
@@ -199,32 +203,32 @@ __global__ __launch_bounds__(64 * 8 / NQB, NQB == 1 ? 4 : 2) void fwd_wave_kerne
   const int seg_id = uniform_table(P.q_work)[2 * item];
   const int q0 = uniform_table(P.q_work)[2 * item + 1];
   const int group = P.hq / P.hkv;
-  const int chunks = group / 4;
+  const int chunks = group / GC;
   const int hk = yb / chunks;
-  const int h = hk * group + (yb % chunks) * 4 + (wave & 3);
-  const int qw = q0 + 16 * NQB * (wave >> 2);  // this wave's first row
+  const int h = hk * group + (yb % chunks) * GC + (wave % GC);
+  const int qw = q0 + 16 * NQB * (wave / GC);  // this wave's first row
   const ts_attn_segment seg = load_uniform(P.segs, seg_id);
   const int T = seg.q_len;
   const int off = seg.kv_len - seg.q_len;
-  const int last = min(q0 + 32, T) - 1;
+  const int last = min(q0 + 16 * NQB * kWaves / GC, T) - 1;
   const float c = P.scale * kLog2e;
 
   // Q rows as B operands: qreg[qb][ks] = row qw + 16 qb + j16, columns 32 ks + 8 g4 ..
-  bf16x8 qreg[NQB][4];
-  load_rows_b(qreg, (const bf16*)Q.ptr + (seg.q_row0 + qw) * Q.row_stride + (int64_t)h * Q.head_stride,
+  bf16x8 qreg[NQB][NKS];
+  load_rows_b<NQB, HD>(qreg, (const bf16*)Q.ptr + (seg.q_row0 + qw) * Q.row_stride + (int64_t)h * Q.head_stride,
               Q.row_stride, T - qw, lane);
-  f32x4 acc[8][NQB];
+  f32x4 acc[NMB][NQB];
   float m[NQB], l[NQB];  // reference point (log2 units) of this lane's column; its part of the
                          // column's sum of exp2(s c - m)
 #pragma unroll
   for (int qb = 0; qb < NQB; ++qb) {
 #pragma unroll
-    for (int mb = 0; mb < 8; ++mb) acc[mb][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int mb = 0; mb < NMB; ++mb) acc[mb][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
     m[qb] = neg_inf();
     l[qb] = 0.f;
   }
   int ro[4], to[8];
-  swizzled_offsets(lane, ro, to);
+  swizzled_offsets<HD>(lane, ro, to);
 
   auto step = [&](auto bsel, TileCursor& cur) {
     const int kpos = cur.kpos, run_len = cur.len;
@@ -235,7 +239,7 @@ __global__ __launch_bounds__(64 * 8 / NQB, NQB == 1 ? 4 : 2) void fwd_wave_kerne
     const bf16* tk = bsel.value == 0 ? s_k0 : s_k1;
     const bf16* tv = bsel.value == 0 ? s_v0 : s_v1;
     if (nxt.sp < seg.nspan)
-      issue_kv_tile<kWaves>(hk, wave, lane, nxt, bsel.value == 0 ? s_k1 : s_k0, bsel.value == 0 ? s_v1 : s_v0);
+      issue_kv_tile<kWaves, HD>(hk, wave, lane, nxt, bsel.value == 0 ? s_k1 : s_k0, bsel.value == 0 ? s_v1 : s_v0);
 
     const bool masked = (kpos + kt0 + BK - 1 > off + qw) | (kt0 + BK > run_len);
     // two halves of 32 keys, each one online-softmax update:
@@ -252,8 +256,8 @@ __global__ __launch_bounds__(64 * 8 / NQB, NQB == 1 ? 4 : 2) void fwd_wave_kerne
 #pragma unroll
         for (int qb = 0; qb < NQB; ++qb) sc[kb][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-          const bf16x8 ak = as_bf16x8(ld16(tk + ro[ks] + (32 * ss + 16 * kb) * D));
+        for (int ks = 0; ks < NKS; ++ks) {
+          const bf16x8 ak = as_bf16x8(ld16(tk + ro_of(ro, ks) + (32 * ss + 16 * kb) * HD));
 #pragma unroll
           for (int qb = 0; qb < NQB; ++qb) sc[kb][qb] = mma16<E>(ak, qreg[qb][ks], sc[kb][qb]);
         }
@@ -261,9 +265,9 @@ __global__ __launch_bounds__(64 * 8 / NQB, NQB == 1 ? 4 : 2) void fwd_wave_kerne
       // K fragment reads three (kb, ks) steps ahead of their MFMAs
       __builtin_amdgcn_sched_group_barrier(0x100, 3, 1);
 #pragma unroll
-      for (int st = 0; st < 8; ++st) {
+      for (int st = 0; st < 2 * NKS; ++st) {
         __builtin_amdgcn_sched_group_barrier(0x008, NQB, 1);
-        if (st + 3 < 8) __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
+        if (st + 3 < 2 * NKS) __builtin_amdgcn_sched_group_barrier(0x100, 1, 1);
       }
       __builtin_amdgcn_s_setprio(0);
       if (masked) {
@@ -312,7 +316,7 @@ __global__ __launch_bounds__(64 * 8 / NQB, NQB == 1 ? 4 : 2) void fwd_wave_kerne
             const float alpha = fast_exp2(m[qb] - mnew);  // 0 on the first visible keys (m = -inf)
             l[qb] *= alpha;
 #pragma unroll
-            for (int mb = 0; mb < 8; ++mb) acc[mb][qb] *= alpha;
+            for (int mb = 0; mb < NMB; ++mb) acc[mb][qb] *= alpha;
             m[qb] = mnew;
           }
           const float mref = m[qb] == neg_inf() ? 0.f : m[qb];
@@ -338,9 +342,9 @@ __global__ __launch_bounds__(64 * 8 / NQB, NQB == 1 ? 4 : 2) void fwd_wave_kerne
       }
       __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-      for (int mb = 0; mb < 8; ++mb) {
-        const u32x2 a0 = tr_read(tv + to[mb] + 32 * ss * D);
-        const u32x2 a1 = tr_read(tv + to[mb] + (32 * ss + 16) * D);
+      for (int mb = 0; mb < NMB; ++mb) {
+        const u32x2 a0 = tr_read(tv + to_of(to, mb) + 32 * ss * HD);
+        const u32x2 a1 = tr_read(tv + to_of(to, mb) + (32 * ss + 16) * HD);
         const bf16x8 a = as_bf16x8(u32x4{a0[0], a0[1], a1[0], a1[1]});
 #pragma unroll
         for (int qb = 0; qb < NQB; ++qb) acc[mb][qb] = mma16<E>(a, pk[qb], acc[mb][qb]);
@@ -348,9 +352,9 @@ __global__ __launch_bounds__(64 * 8 / NQB, NQB == 1 ? 4 : 2) void fwd_wave_kerne
       // V^T fragment reads kept four blocks ahead of their MFMAs
       __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
 #pragma unroll
-      for (int mb = 0; mb < 8; ++mb) {
+      for (int mb = 0; mb < NMB; ++mb) {
         __builtin_amdgcn_sched_group_barrier(0x008, NQB, 0);
-        if (mb + 4 < 8) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        if (mb + 4 < NMB) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
       }
       __builtin_amdgcn_sched_barrier(0);
       __builtin_amdgcn_s_setprio(0);
@@ -359,7 +363,7 @@ __global__ __launch_bounds__(64 * 8 / NQB, NQB == 1 ? 4 : 2) void fwd_wave_kerne
   };
 
   TileCursor cur = first_kv_tile(P, seg, last);
-  if (cur.sp < seg.nspan) issue_kv_tile<kWaves>(hk, wave, lane, cur, s_k0, s_v0);
+  if (cur.sp < seg.nspan) issue_kv_tile<kWaves, HD>(hk, wave, lane, cur, s_k0, s_v0);
   while (cur.sp < seg.nspan) {
     step(std::integral_constant<int, 0>{}, cur);
     if (cur.sp >= seg.nspan) break;
@@ -375,7 +379,7 @@ __global__ __launch_bounds__(64 * 8 / NQB, NQB == 1 ? 4 : 2) void fwd_wave_kerne
     const float inv = ls > 0.f ? 1.f / ls : 0.f;
     bf16* orow = (bf16*)O.ptr + (seg.q_row0 + row) * O.row_stride + (int64_t)h * O.head_stride + 4 * g4;
 #pragma unroll
-    for (int mb = 0; mb < 8; ++mb) {
+    for (int mb = 0; mb < NMB; ++mb) {
       const f32x4 v = acc[mb][qb] * inv;
       *reinterpret_cast<u32x2*>(orow + 16 * mb) = u32x2{pack2<E>(v[0], v[1]), pack2<E>(v[2], v[3])};
     }
@@ -414,7 +418,16 @@ int launch_fwd_t(const ts_attn_problem& P, ts_attn_rows q, ts_attn_rows out, flo
     case 64: launch_fwd_generic<E, 64>(P, gc, grid, q, out, lse, lse_ld, s); break;
     case 96: launch_fwd_generic<E, 96>(P, gc, grid, q, out, lse, lse_ld, s); break;
     case 192: launch_fwd_generic<E, 192>(P, gc, grid, q, out, lse, lse_ld, s); break;
-    case 256: launch_fwd_generic<E, 256>(P, gc, grid, q, out, lse, lse_ld, s); break;
+    case 256: {
+      ts::TimedLaunch timed_("attention.fwd_kernel", s);
+      if (gc == 4)
+        hipLaunchKernelGGL((fwd_wave_kernel<E, 1, 256, 4>), grid, dim3(512), 0, s, P, q, out, lse, lse_ld);
+      else if (gc == 2)
+        hipLaunchKernelGGL((fwd_wave_kernel<E, 1, 256, 2>), grid, dim3(512), 0, s, P, q, out, lse, lse_ld);
+      else
+        hipLaunchKernelGGL((fwd_wave_kernel<E, 1, 256, 1>), grid, dim3(512), 0, s, P, q, out, lse, lse_ld);
+      break;
+    }
     default:
       if (gc == 4) {
         ts::TimedLaunch timed_("attention.fwd_kernel", s);

@@ -314,49 +314,72 @@ __device__ __forceinline__ TileCursor first_kv_tile(const ts_attn_problem& P, co
 // 2.2 clk per transposed read per CU, against 4.2 and 4.1 for s(r) = r).
 __device__ __forceinline__ int tile_swizzle(int r) { return r ^ ((r & 1) ? 12 : 0); }
 
-// DMA of one 64-key K/V tile of KV head hk into swizzled LDS tiles (256-byte
-// rows, chunk c of row r at slot c ^ tile_swizzle(r & 15)).  The WAVES waves
-// of a work-group (4 or 8) each issue instructions t = wave + WAVES u (rows
-// 4 t .. 4 t + 3); lane (g4, j16) fills row 4 t + g4, slot j16 with logical
-// chunk j16 ^ tile_swizzle((4 wave + g4) & 15).  Rows past the run arrive as
+// DMA of one 64-key K/V tile of KV head hk into swizzled LDS tiles (rows of
+// HD elements, chunk c of row r at slot c ^ tile_swizzle(r & 15)).  The WAVES
+// waves of a work-group (4 or 8) each issue instructions t = wave + WAVES u;
+// instruction t fills rows RPI t .. RPI t + RPI - 1 (RPI = 4 at HD 128, 2 at
+// 256): lane l the row RPI t + l / (HD / 8), slot l % (HD / 8) with logical
+// chunk (l % (HD / 8)) ^ tile_swizzle(row).  Rows past the run arrive as
 // zeros.
-template <int WAVES = 4>
+template <int WAVES = 4, int HD = D>
 __device__ __forceinline__ void issue_kv_tile(int hk, int wave, int lane, const TileCursor& tc, bf16* sk,
                                               bf16* sv) {
-  static_assert(WAVES == 4 || WAVES == 8, "a tile is 16 instructions of 4 rows");
-  const int g4 = lane >> 4, j16 = lane & 15;
-  const int dma_row = 4 * wave + g4;
-  const int dma_chunk = (j16 ^ tile_swizzle((4 * wave + g4) & 15)) << 3;
+  static_assert(WAVES == 4 || WAVES == 8, "a tile is 16 or 32 instructions");
+  static_assert(HD == 128 || HD == 256, "the swizzle needs 16 or 32 chunks per row");
+  constexpr int CH = HD / 8, RPI = 64 / CH, NI = BK / RPI;
   const int nvalid = min(BK, tc.len - tc.kt0);
   const bf16* kb = (const bf16*)tc.k + (int64_t)tc.kt0 * tc.k_row_stride + (int64_t)hk * tc.k_head_stride;
   const bf16* vb = (const bf16*)tc.v + (int64_t)tc.kt0 * tc.v_row_stride + (int64_t)hk * tc.v_head_stride;
   const rsrc_t rk = make_rsrc(kb, (uint32_t)(nvalid * tc.k_row_stride * 2));
   const rsrc_t rv = make_rsrc(vb, (uint32_t)(nvalid * tc.v_row_stride * 2));
-  const int ko = (int)((dma_row * tc.k_row_stride + dma_chunk) * 2);
-  const int vo = (int)((dma_row * tc.v_row_stride + dma_chunk) * 2);
-  const int kstep = (int)(4 * WAVES * tc.k_row_stride * 2), vstep = (int)(4 * WAVES * tc.v_row_stride * 2);
+  if constexpr (HD == 128) {
+    // rows 4 t + g4: the swizzle of row 4 (t + WAVES u) + g4 is that of row 4 t + g4
+    const int g4 = lane >> 4, j16 = lane & 15;
+    const int dma_row = 4 * wave + g4;
+    const int dma_chunk = (j16 ^ tile_swizzle((4 * wave + g4) & 15)) << 3;
+    const int ko = (int)((dma_row * tc.k_row_stride + dma_chunk) * 2);
+    const int vo = (int)((dma_row * tc.v_row_stride + dma_chunk) * 2);
+    const int kstep = (int)(4 * WAVES * tc.k_row_stride * 2), vstep = (int)(4 * WAVES * tc.v_row_stride * 2);
 #pragma unroll
-  for (int u = 0; u < 16 / WAVES; ++u) {
-    buffer_dma16(rk, sk + (wave + WAVES * u) * 512, ko + u * kstep);
-    buffer_dma16(rv, sv + (wave + WAVES * u) * 512, vo + u * vstep);
+    for (int u = 0; u < 16 / WAVES; ++u) {
+      buffer_dma16(rk, sk + (wave + WAVES * u) * 512, ko + u * kstep);
+      buffer_dma16(rv, sv + (wave + WAVES * u) * 512, vo + u * vstep);
+    }
+  } else {
+#pragma unroll
+    for (int u = 0; u < NI / WAVES; ++u) {
+      const int t = wave + WAVES * u;
+      const int row = RPI * t + lane / CH;
+      const int chunk = ((lane % CH) ^ tile_swizzle(row & 15)) << 3;
+      buffer_dma16(rk, sk + t * 512, (int)((row * tc.k_row_stride + chunk) * 2));
+      buffer_dma16(rv, sv + t * 512, (int)((row * tc.v_row_stride + chunk) * 2));
+    }
   }
 }
 
-// per-lane LDS offsets (elements) into a 256-byte-row swizzled tile:
+// per-lane LDS offsets (elements) into a swizzled tile of HD-element rows:
 // ro[ks]: row j16, logical chunk 4 ks + g4 (A-operand row reads of 16 rows);
 // to[mb]: row 4 g4 + j16 / 4, columns 16 mb + 4 (j16 & 3) .. + 3 (the
-// addresses of a ds_read_b64_tr_b16 that yields X[4 g4 + t][16 mb + j16])
+// addresses of a ds_read_b64_tr_b16 that yields X[4 g4 + t][16 mb + j16]).
+// The swizzle permutes chunks within aligned groups of 16, so at head dim 256
+// the offsets of k-step ks + 4 and column block mb + 8 are those of ks and mb
+// plus 128 elements: only the first four and eight are kept (the rest fold
+// into the reads' immediate offsets).
+template <int HD = D>
 __device__ __forceinline__ void swizzled_offsets(int lane, int ro[4], int to[8]) {
   const int g4 = lane >> 4, j16 = lane & 15;
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks) ro[ks] = j16 * D + (((4 * ks + g4) ^ tile_swizzle(j16)) << 3);
+  for (int ks = 0; ks < 4; ++ks) ro[ks] = j16 * HD + (((4 * ks + g4) ^ tile_swizzle(j16)) << 3);
 #pragma unroll
   for (int mb = 0; mb < 8; ++mb) {
     const int r = 4 * g4 + (j16 >> 2);
     const int col = 16 * mb + 4 * (j16 & 3);
-    to[mb] = r * D + ((((col >> 3) ^ tile_swizzle(r)) & 15) << 3) + (col & 7);
+    to[mb] = r * HD + (((col >> 3) ^ tile_swizzle(r)) << 3) + (col & 7);
   }
 }
+// the offsets of k-step ks and column block mb
+__device__ __forceinline__ int ro_of(const int ro[4], int ks) { return ro[ks & 3] + 128 * (ks >> 2); }
+__device__ __forceinline__ int to_of(const int to[8], int mb) { return to[mb & 7] + 128 * (mb >> 3); }
 
 
 // ---------------------------------------------------------------------------
