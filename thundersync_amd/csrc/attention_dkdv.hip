@@ -684,6 +684,14 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_split_kernel(ts_attn_problem
           sc[qb] = mma16<E>(aq, kreg[ks], sc[qb]);
           dp[qb] = mma16<E>(ad, vreg[ks], dp[qb]);
         }
+      // Q/dO row reads two k-steps ahead of their MFMAs
+      __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+        if (ks + 2 < NKS) __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+      }
+      __builtin_amdgcn_sched_barrier(0);
       // P and dS as B operands: slot j = 4 qb + i  <->  row 16 qb + 4 g4 + i
       float pv[8], dsv[8];
       const int lim = off + r0 - kpos - mykey;  // row rl sees the key iff rl >= -lim
@@ -700,6 +708,7 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_split_kernel(ts_attn_problem
         }
       const bf16x8 pk = pack8<E>(pv);
       const bf16x8 dsk = pack8<E>(dsv);
+      __builtin_amdgcn_sched_barrier(0);
       // dV^T += dO^T P, dK^T += Q^T dS: rows d = 16 mb + 4 g4 + i, column key j16
 #pragma unroll
       for (int mb = 0; mb < NMB; ++mb) {
@@ -708,6 +717,13 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_split_kernel(ts_attn_problem
         const u32x2 b0 = tr_read(tq + o), b1 = tr_read(tq + o + 16 * HD);
         dv[mb] = mma16<E>(as_bf16x8(u32x4{a0[0], a0[1], a1[0], a1[1]}), pk, dv[mb]);
         dk[mb] = mma16<E>(as_bf16x8(u32x4{b0[0], b0[1], b1[0], b1[1]}), dsk, dk[mb]);
+      }
+      // dO^T / Q^T reads four blocks ahead of their MFMAs
+      __builtin_amdgcn_sched_group_barrier(0x100, 16, 1);
+#pragma unroll
+      for (int mb = 0; mb < NMB; ++mb) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 1);
+        if (mb + 4 < NMB) __builtin_amdgcn_sched_group_barrier(0x100, 4, 1);
       }
     }
     cur = nxt;

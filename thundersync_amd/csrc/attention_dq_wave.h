@@ -161,10 +161,10 @@ __global__ __launch_bounds__(64 * 8 / (NQB * NP), 1) void dq_wave_kernel(ts_attn
   // one tile, the halves software-pipelined: half 1's score MFMAs are issued
   // beside half 0's exponentials, half 0's dQ MFMAs beside half 1's
   auto tile_body = [&](auto diag, const bf16* tk, const bf16* tv, int kpos, int kt0) __attribute__((always_inline)) {
-    if constexpr (HD > 128) {
-      // at head dim 256 the halves run one after the other: the pipelined
-      // form's two halves of S and dP do not fit the registers beside the
-      // dQ accumulators and the Q/dO rows
+    if constexpr (HD > 128 && kWaves == 8) {
+      // at head dim 256 with two waves per SIMD the halves run one after the
+      // other: the pipelined form's two halves of S and dP do not fit the
+      // registers beside the dQ accumulators and the Q/dO rows
 #pragma unroll
       for (int ss = 0; ss < 2; ++ss) {
         f32x4 sc[2][NQB], dp[2][NQB];
