@@ -780,12 +780,11 @@ int launch_dkdv_t(const ts_attn_problem& P, ts_attn_rows q, ts_attn_rows dout, c
       break;
     }
     default:
-      if (group % 4 == 0) {
-        ts::TimedLaunch timed_("attention.dkdv_kernel", s);
+      ts::TimedLaunch timed_("attention.dkdv_kernel", s);
+      if (group % 4 == 0)
         hipLaunchKernelGGL((dkdv_wave_kernel<E, 3>), grid, dim3(kThreads), 0, s, P, q, dout, rowstats, lse_ld);
-      } else {
-        launch_dkdv_generic<E, D>(grid, P, q, dout, rowstats, lse_ld, s);
-      }
+      else
+        hipLaunchKernelGGL((dkdv_split_kernel<E, D>), grid, dim3(kThreads), 0, s, P, q, dout, rowstats, lse_ld);
   }
   return ts::check_launch("ts_attn_bwd (dkdv)");
 }

@@ -243,14 +243,16 @@ int launch_dq_t(const ts_attn_problem& P, ts_attn_rows q, ts_attn_rows dout, con
     case 96: launch_dq_generic<E, 96>(P, gc, grid, q, dout, rowstats, lse_ld, dq, s); break;
     case 192: launch_dq_generic<E, 192>(P, gc, grid, q, dout, rowstats, lse_ld, dq, s); break;
     case 256: launch_dq_wave256(P, gc, grid, q, dout, rowstats, lse_ld, dq, s); break;
-    default:
-      if (gc == 4) {
-        ts::TimedLaunch timed_("attention.dq_kernel", s);
+    default: {
+      ts::TimedLaunch timed_("attention.dq_kernel", s);
+      if (gc == 4)
         hipLaunchKernelGGL((dq_wave_kernel<E, kDqRowsPerWave / 16>), grid, dim3(64 * 128 / kDqRowsPerWave), 0, s, P, q,
                            dout, rowstats, lse_ld, dq);
-      } else {
-        launch_dq_generic<E, D>(P, gc, grid, q, dout, rowstats, lse_ld, dq, s);
-      }
+      else if (gc == 2)
+        hipLaunchKernelGGL((dq_wave_kernel<E, 1, D, 2>), grid, dim3(512), 0, s, P, q, dout, rowstats, lse_ld, dq);
+      else
+        hipLaunchKernelGGL((dq_wave_kernel<E, 1, D, 1>), grid, dim3(512), 0, s, P, q, dout, rowstats, lse_ld, dq);
+    }
   }
   return ts::check_launch("ts_attn_bwd (dq)");
 }

@@ -428,14 +428,16 @@ int launch_fwd_t(const ts_attn_problem& P, ts_attn_rows q, ts_attn_rows out, flo
         hipLaunchKernelGGL((fwd_wave_kernel<E, 1, 256, 1>), grid, dim3(512), 0, s, P, q, out, lse, lse_ld);
       break;
     }
-    default:
-      if (gc == 4) {
-        ts::TimedLaunch timed_("attention.fwd_kernel", s);
+    default: {
+      ts::TimedLaunch timed_("attention.fwd_kernel", s);
+      if (gc == 4)
         hipLaunchKernelGGL((fwd_wave_kernel<E, kFwdRowsPerWave / 16>), grid, dim3(64 * 128 / kFwdRowsPerWave), 0, s,
                            P, q, out, lse, lse_ld);
-      } else {
-        launch_fwd_generic<E, D>(P, gc, grid, q, out, lse, lse_ld, s);
-      }
+      else if (gc == 2)
+        hipLaunchKernelGGL((fwd_wave_kernel<E, 2, D, 2>), grid, dim3(256), 0, s, P, q, out, lse, lse_ld);
+      else
+        hipLaunchKernelGGL((fwd_wave_kernel<E, 2, D, 1>), grid, dim3(256), 0, s, P, q, out, lse, lse_ld);
+    }
   }
   return ts::check_launch("ts_attn_fwd");
 }
