@@ -13,12 +13,12 @@ namespace attn {
 // w keys 16 w .. 16 w + 15 (a wave past the block only helps stage the
 // tiles), and loops over every query head of the group and every visible
 // 32-row block; Q and dO rows pass through registers into padded LDS rows,
-// dO^T and Q^T come from register transposes of 8 x 8 blocks.
+// dO^T and Q^T come from ds_read_b64_tr_b16 (tr_frag).
 template <typename E, int HD>
 __global__ __launch_bounds__(kThreads, HD > 128 ? 1 : 2) void dkdv_kernel(ts_attn_problem P, ts_attn_rows Q,
                                                            ts_attn_rows dO, const float* __restrict__ rowstats,
                                                            int64_t lse_ld) {
-  constexpr int NH = col_blocks<HD>();
+  constexpr int NMB = HD / 16;  // 16-column blocks of dK / dV
   __shared__ __attribute__((aligned(16))) bf16 sq[32 * pitch_of<HD>()];
   __shared__ __attribute__((aligned(16))) bf16 sd[32 * pitch_of<HD>()];
   __shared__ float s_lse2[32];
@@ -53,14 +53,12 @@ __global__ __launch_bounds__(kThreads, HD > 128 ? 1 : 2) void dkdv_kernel(ts_att
       vreg[ks] = as_bf16x8(b);
     }
   }
-  f32x4 dk[NH][8], dv[NH][8];
+  f32x4 dk[NMB], dv[NMB];
 #pragma unroll
-  for (int hh = 0; hh < NH; ++hh)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      dk[hh][e] = f32x4{0.f, 0.f, 0.f, 0.f};
-      dv[hh][e] = f32x4{0.f, 0.f, 0.f, 0.f};
-    }
+  for (int mb = 0; mb < NMB; ++mb) {
+    dk[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    dv[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
 
   for (int vi = 0; vi < run.nvisit; ++vi) {
     const ts_attn_ref ref = load_uniform(P.run_visits, run.visit0 + vi);
@@ -125,50 +123,29 @@ __global__ __launch_bounds__(kThreads, HD > 128 ? 1 : 2) void dkdv_kernel(ts_att
           }
         const bf16x8 pk = pack8<E>(pv);
         const bf16x8 dsk = pack8<E>(dsv);
-        int rows[8];
-        slot_rows(lane >> 4, 0, rows);
 #pragma unroll
-        for (int hh = 0; hh < NH; ++hh) {
-          const int c0 = col_start<HD>(hh, lane);
-          bf16x8 at[8];
-          lds_rows_transposed<HD>(sd, rows, c0, at);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) dv[hh][e] = mma16<E>(at[e], pk, dv[hh][e]);
-          lds_rows_transposed<HD>(sq, rows, c0, at);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) dk[hh][e] = mma16<E>(at[e], dsk, dk[hh][e]);
+        for (int mb = 0; mb < NMB; ++mb) {
+          dv[mb] = mma16<E>(tr_frag<HD>(sd, 0, mb, lane), pk, dv[mb]);
+          dk[mb] = mma16<E>(tr_frag<HD>(sq, 0, mb, lane), dsk, dk[mb]);
         }
       }
     }
   }
   if (!key_valid) return;
+  // dk[mb] / dv[mb] lane (g4, j16) holds d = 16 mb + 4 g4 + i of key mykey: 8-byte stores
   if (run.dk) {
-    bf16* p = (bf16*)run.dk + (int64_t)mykey * run.dk_row_stride + (int64_t)hk * run.dk_head_stride +
-              32 * (lane >> 4);
+    bf16* p = (bf16*)run.dk + (int64_t)mykey * run.dk_row_stride + (int64_t)hk * run.dk_head_stride + 4 * (lane >> 4);
 #pragma unroll
-    for (int hh = 0; hh < NH; ++hh)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        if (!col_valid<HD>(hh, lane >> 4, i)) continue;
-        float tmp[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) tmp[e] = dk[hh][e][i] * P.scale;
-        st16(p + 128 * hh + 8 * i, as_u32x4(pack8<E>(tmp)));
-      }
+    for (int mb = 0; mb < NMB; ++mb) {
+      const f32x4 v = dk[mb] * P.scale;
+      *reinterpret_cast<u32x2*>(p + 16 * mb) = u32x2{pack2<E>(v[0], v[1]), pack2<E>(v[2], v[3])};
+    }
   }
   if (run.dv) {
-    bf16* p = (bf16*)run.dv + (int64_t)mykey * run.dv_row_stride + (int64_t)hk * run.dv_head_stride +
-              32 * (lane >> 4);
+    bf16* p = (bf16*)run.dv + (int64_t)mykey * run.dv_row_stride + (int64_t)hk * run.dv_head_stride + 4 * (lane >> 4);
 #pragma unroll
-    for (int hh = 0; hh < NH; ++hh)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        if (!col_valid<HD>(hh, lane >> 4, i)) continue;
-        float tmp[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) tmp[e] = dv[hh][e][i];
-        st16(p + 128 * hh + 8 * i, as_u32x4(pack8<E>(tmp)));
-      }
+    for (int mb = 0; mb < NMB; ++mb)
+      *reinterpret_cast<u32x2*>(p + 16 * mb) = u32x2{pack2<E>(dv[mb][0], dv[mb][1]), pack2<E>(dv[mb][2], dv[mb][3])};
   }
 }
 

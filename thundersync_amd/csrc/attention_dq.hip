@@ -60,12 +60,12 @@ __global__ __launch_bounds__(kThreads) void delta_kernel(ts_attn_rows O, ts_attn
 // ---------------------------------------------------------------------------
 // Register-staged dQ for any supported head dim HD (the forward's work split:
 // wave w takes head w % GC and rows 32 (w / GC) ..); K^T for dQ^T += K^T dS^T
-// from register transposes of 8 x 8 blocks.
+// from ds_read_b64_tr_b16 (tr_frag).
 template <typename E, int GC, int HD>
 __global__ __launch_bounds__(kThreads, 1) void dq_kernel(ts_attn_problem P, ts_attn_rows Q,
                                                          ts_attn_rows dO, const float* __restrict__ rowstats,
                                                          int64_t lse_ld, ts_attn_rows dQ) {
-  constexpr int NH = col_blocks<HD>();
+  constexpr int NMB = HD / 16;  // 16-column blocks of dQ
   __shared__ __attribute__((aligned(16))) bf16 sk[BK * pitch_of<HD>()];
   __shared__ __attribute__((aligned(16))) bf16 sv[BK * pitch_of<HD>()];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -104,13 +104,11 @@ __global__ __launch_bounds__(kThreads, 1) void dq_kernel(ts_attn_problem P, ts_a
       dlt[qb] = rowstats[at + 1];
     }
   }
-  f32x4 acc[2][NH][8];
+  f32x4 acc[2][NMB];
 #pragma unroll
   for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
-    for (int hh = 0; hh < NH; ++hh)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc[qb][hh][e] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int mb = 0; mb < NMB; ++mb) acc[qb][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   for (int sp = 0; sp < seg.nspan; ++sp) {
     const ts_attn_ref ref = load_uniform(P.seg_spans, seg.span0 + sp);
@@ -153,17 +151,11 @@ __global__ __launch_bounds__(kThreads, 1) void dq_kernel(ts_attn_problem P, ts_a
           for (int j = 0; j < 8; ++j) tmp[j] = s[2 * ss + (j >> 2)][qb][j & 3];
           dsk[qb] = pack8<E>(tmp);
         }
-        int rows[8];
-        slot_rows(lane >> 4, 32 * ss, rows);
 #pragma unroll
-        for (int hh = 0; hh < NH; ++hh) {
-          bf16x8 kt[8];
-          lds_rows_transposed<HD>(sk, rows, col_start<HD>(hh, lane), kt);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            acc[0][hh][e] = mma16<E>(kt[e], dsk[0], acc[0][hh][e]);
-            acc[1][hh][e] = mma16<E>(kt[e], dsk[1], acc[1][hh][e]);
-          }
+        for (int mb = 0; mb < NMB; ++mb) {
+          const bf16x8 kt = tr_frag<HD>(sk, 32 * ss, mb, lane);
+          acc[0][mb] = mma16<E>(kt, dsk[0], acc[0][mb]);
+          acc[1][mb] = mma16<E>(kt, dsk[1], acc[1][mb]);
         }
       }
     }
@@ -173,18 +165,13 @@ __global__ __launch_bounds__(kThreads, 1) void dq_kernel(ts_attn_problem P, ts_a
   for (int qb = 0; qb < 2; ++qb) {
     const int row = wq0 + 16 * qb + (lane & 15);
     if (row >= T) continue;
-    bf16* drow = (bf16*)dQ.ptr + (seg.q_row0 + row) * dQ.row_stride + (int64_t)h * dQ.head_stride +
-                 32 * (lane >> 4);
+    // acc[qb][mb] lane holds d = 16 mb + 4 g4 + i of this row: 8-byte stores
+    bf16* drow = (bf16*)dQ.ptr + (seg.q_row0 + row) * dQ.row_stride + (int64_t)h * dQ.head_stride + 4 * (lane >> 4);
 #pragma unroll
-    for (int hh = 0; hh < NH; ++hh)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        if (!col_valid<HD>(hh, lane >> 4, i)) continue;
-        float tmp[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) tmp[e] = acc[qb][hh][e][i] * P.scale;
-        st16(drow + 128 * hh + 8 * i, as_u32x4(pack8<E>(tmp)));
-      }
+    for (int mb = 0; mb < NMB; ++mb) {
+      const f32x4 v = acc[qb][mb] * P.scale;
+      *reinterpret_cast<u32x2*>(drow + 16 * mb) = u32x2{pack2<E>(v[0], v[1]), pack2<E>(v[2], v[3])};
+    }
   }
 }
 

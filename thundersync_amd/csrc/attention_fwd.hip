@@ -11,12 +11,12 @@ namespace attn {
 // are not a multiple of 4 (and, at head dims other than 128, those that are):
 // a work-group owns 32 4 / GC query rows of GC query heads (wave w: head
 // w % GC, rows 32 (w / GC) ..); K/V tiles of 64 keys pass through registers
-// into padded LDS rows; V^T comes from register transposes of 8 x 8 blocks.
+// into padded LDS rows; V^T comes from ds_read_b64_tr_b16 (tr_frag).
 template <typename E, int GC, int HD>
 __global__ __launch_bounds__(kThreads, HD > 128 ? 1 : 2) void fwd_kernel(ts_attn_problem P, ts_attn_rows Q,
                                                           ts_attn_rows O, float* __restrict__ lse,
                                                           int64_t lse_ld) {
-  constexpr int NH = col_blocks<HD>();
+  constexpr int NMB = HD / 16;  // 16-column blocks of O
   __shared__ __attribute__((aligned(16))) bf16 sk[BK * pitch_of<HD>()];
   __shared__ __attribute__((aligned(16))) bf16 sv[BK * pitch_of<HD>()];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -41,13 +41,11 @@ __global__ __launch_bounds__(kThreads, HD > 128 ? 1 : 2) void fwd_kernel(ts_attn
   const bf16* qbase = (const bf16*)Q.ptr + (seg.q_row0 + wq0) * Q.row_stride + (int64_t)h * Q.head_stride;
   load_rows_b<2, HD>(qreg, qbase, Q.row_stride, active ? T - wq0 : 0, lane);
 
-  f32x4 o[2][NH][8];
+  f32x4 o[2][NMB];
 #pragma unroll
   for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
-    for (int hh = 0; hh < NH; ++hh)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) o[qb][hh][e] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int mb = 0; mb < NMB; ++mb) o[qb][mb] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m[2] = {neg_inf(), neg_inf()};
   float lsum[2] = {0.f, 0.f};
 
@@ -104,9 +102,7 @@ __global__ __launch_bounds__(kThreads, HD > 128 ? 1 : 2) void fwd_kernel(ts_attn
           }
         lsum[qb] = lsum[qb] * alpha + ps;
 #pragma unroll
-        for (int hh = 0; hh < NH; ++hh)
-#pragma unroll
-          for (int e = 0; e < 8; ++e) o[qb][hh][e] *= alpha;
+        for (int mb = 0; mb < NMB; ++mb) o[qb][mb] *= alpha;
       }
       // O^T += V^T P^T, 32 keys per k-step
 #pragma unroll
@@ -119,17 +115,11 @@ __global__ __launch_bounds__(kThreads, HD > 128 ? 1 : 2) void fwd_kernel(ts_attn
           for (int j = 0; j < 8; ++j) tmp[j] = s[2 * ss + (j >> 2)][qb][j & 3];
           pk[qb] = pack8<E>(tmp);
         }
-        int rows[8];
-        slot_rows(lane >> 4, 32 * ss, rows);
 #pragma unroll
-        for (int hh = 0; hh < NH; ++hh) {
-          bf16x8 vt[8];
-          lds_rows_transposed<HD>(sv, rows, col_start<HD>(hh, lane), vt);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            o[0][hh][e] = mma16<E>(vt[e], pk[0], o[0][hh][e]);
-            o[1][hh][e] = mma16<E>(vt[e], pk[1], o[1][hh][e]);
-          }
+        for (int mb = 0; mb < NMB; ++mb) {
+          const bf16x8 vt = tr_frag<HD>(sv, 32 * ss, mb, lane);
+          o[0][mb] = mma16<E>(vt, pk[0], o[0][mb]);
+          o[1][mb] = mma16<E>(vt, pk[1], o[1][mb]);
         }
       }
     }
@@ -141,18 +131,13 @@ __global__ __launch_bounds__(kThreads, HD > 128 ? 1 : 2) void fwd_kernel(ts_attn
     const int row = wq0 + 16 * qb + (lane & 15);
     if (row >= T) continue;
     const float inv = l > 0.f ? 1.f / l : 0.f;
-    bf16* orow = (bf16*)O.ptr + (seg.q_row0 + row) * O.row_stride + (int64_t)h * O.head_stride +
-                 32 * (lane >> 4);
+    // o[qb][mb] lane holds d = 16 mb + 4 g4 + i of this row: 8-byte stores
+    bf16* orow = (bf16*)O.ptr + (seg.q_row0 + row) * O.row_stride + (int64_t)h * O.head_stride + 4 * (lane >> 4);
 #pragma unroll
-    for (int hh = 0; hh < NH; ++hh)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        if (!col_valid<HD>(hh, lane >> 4, i)) continue;
-        float tmp[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) tmp[e] = o[qb][hh][e][i] * inv;
-        st16(orow + 128 * hh + 8 * i, as_u32x4(pack8<E>(tmp)));
-      }
+    for (int mb = 0; mb < NMB; ++mb) {
+      const f32x4 v = o[qb][mb] * inv;
+      *reinterpret_cast<u32x2*>(orow + 16 * mb) = u32x2{pack2<E>(v[0], v[1]), pack2<E>(v[2], v[3])};
+    }
     if ((lane >> 4) == 0)
       lse[(int64_t)h * lse_ld + seg.q_row0 + row] = l > 0.f ? (m[qb] + fast_log2(l)) * kLn2 : neg_inf();
   }

@@ -108,37 +108,6 @@ __device__ __forceinline__ void rows32_to_lds(bf16* lds, const bf16* base, int64
   }
 }
 
-// Eight LDS rows (row index given per slot j) at column c0, transposed: out[e]
-// holds column c0 + e of the eight rows, slot j from row rows[j].
-template <int HD = D>
-__device__ __forceinline__ void lds_rows_transposed(const bf16* lds, const int rows[8], int c0,
-                                                    bf16x8 out[8]) {
-  u32x4 in[8], tr[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) in[j] = ld16(lds + rows[j] * pitch_of<HD>() + c0);
-  transpose8x8(in, tr);
-#pragma unroll
-  for (int e = 0; e < 8; ++e) out[e] = as_bf16x8(tr[e]);
-}
-
-// Column block of the transposed operands (V^T, K^T, dO^T, Q^T) in the
-// register-staged kernels: the 16 rows of an MFMA tile are head-dim columns
-// 128 hh + 8 (lane & 15) + e (e = 0..7 over eight tiles), so a head dim takes
-// (HD + 127) / 128 blocks.  Lanes whose columns lie past HD read the last
-// eight columns instead; their output rows are never stored.
-template <int HD> constexpr int col_blocks() { return (HD + 127) / 128; }
-template <int HD>
-__device__ __forceinline__ int col_start(int hh, int lane) {
-  const int c0 = 128 * hh + 8 * (lane & 15);
-  return c0 < HD ? c0 : HD - 8;
-}
-// whether output rows 4 g4 + i of column block hh (head-dim columns
-// 128 hh + 32 g4 + 8 i .. + 7) lie inside the head dim
-template <int HD>
-__device__ __forceinline__ bool col_valid(int hh, int g4, int i) {
-  return 128 * hh + 32 * g4 + 8 * i < HD;
-}
-
 // the row of slot j for lane group g: 4g + (j & 3) + 16 (j >> 2)
 __device__ __forceinline__ void slot_rows(int g, int base, int rows[8]) {
 #pragma unroll
@@ -234,6 +203,21 @@ __device__ __forceinline__ u32x2 tr_read(const bf16* p) {
   u32x2 r;
   __builtin_memcpy(&r, &v, 8);
   return r;
+}
+
+// A transposed operand of the register-staged kernels from a padded LDS tile
+// (row pitch HD + 8 elements) by two ds_read_b64_tr_b16: the 16 x 32 A
+// operand X^T[16 mb .. 16 mb + 15][row0 + slot rows], slot j <-> row
+// row0 + 16 (j >> 2) + 4 g4 + (j & 3) (the slot order of slot_rows).  Lane
+// (g4, j16) addresses row row0 + 4 g4 + j16 / 4 and columns
+// 16 mb + 4 (j16 & 3) .. + 3, and receives X[row0 + 4 g4 + t][16 mb + j16],
+// t = 0..3, then the same from 16 rows further.
+template <int HD>
+__device__ __forceinline__ bf16x8 tr_frag(const bf16* lds, int row0, int mb, int lane) {
+  const int g4 = lane >> 4, j16 = lane & 15;
+  const bf16* p = lds + (row0 + 4 * g4 + (j16 >> 2)) * pitch_of<HD>() + 16 * mb + 4 * (j16 & 3);
+  const u32x2 a = tr_read(p), b = tr_read(p + 16 * pitch_of<HD>());
+  return as_bf16x8(u32x4{a[0], a[1], b[0], b[1]});
 }
 
 // A key run's position in its visit list with the visited segment's fields
