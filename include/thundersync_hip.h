@@ -240,6 +240,43 @@ int ts_attn_bwd(const ts_attn_problem* problem, ts_attn_rows q, ts_attn_rows out
                 ts_attn_rows dout, const float* lse, int64_t lse_ld, float* rowstats,
                 ts_attn_rows dq, void* stream);
 
+/* dS route of the backward.  ts_attn_bwd's dQ kernel recomputes S = Q K^T
+ * and dP = dO V^T, which its dK/dV kernels also compute; on this route the
+ * dK/dV kernels store dS = P (dP - delta) (in the element type, as rounded
+ * for their own dK product) into a caller-provided workspace and the dQ
+ * kernel forms dQ = scale dS K from it: the MFMA work of the backward drops
+ * from 14 to 10 D flops per (row, key, head) for one write and one read of
+ * 2 bytes per pair and head.  Same results contract as ts_attn_bwd
+ * (deterministic, no atomics).
+ *
+ * ts_attn_ds_route(head_dim, group): 1 where the route exists (head dim
+ * 256; head dim 128 with GQA groups hq / hkv that are not a multiple of 4);
+ * elsewhere ts_attn_bwd_ds runs ts_attn_bwd's kernels and leaves the
+ * workspace untouched.
+ *
+ * ts_attn_ds_layout: the workspace layout of a set of tables (host copies;
+ * run_len, visit0 and nvisit are the runs' len / visit0 / nvisit fields):
+ * per span and per visit the element offset of that (segment, run) pair's
+ * dS blocks within one head's part, and the elements of one head's part
+ * (*ds_head).  Each pair takes 512 elements (32 rows x 16 keys) per block of
+ * the keys its rows see, 2 bytes each: about 2 bytes per visible pair and
+ * head.  TS_OK or TS_ERR_INVALID.
+ *
+ * ts_attn_bwd_ds: as ts_attn_bwd, with span_ds / visit_ds the device copies
+ * of the layout's offsets and `ds` a 16-byte aligned device workspace of at
+ * least hq * ds_head * 2 bytes (its contents on entry do not matter).
+ * No counterpart in the reference, whose flash/FA4 backward kernels own
+ * their scratch; it replaces the same calls as ts_attn_bwd. */
+int ts_attn_ds_route(int head_dim, int group);
+int ts_attn_ds_layout(const ts_attn_segment* segs, int32_t n_segs, const ts_attn_ref* seg_spans,
+                      int64_t n_spans, const int32_t* run_len, int32_t n_runs,
+                      const ts_attn_ref* run_visits, const int32_t* visit0, const int32_t* nvisit,
+                      int64_t n_visits, int64_t* span_ds, int64_t* visit_ds, int64_t* ds_head);
+int ts_attn_bwd_ds(const ts_attn_problem* problem, ts_attn_rows q, ts_attn_rows out,
+                   ts_attn_rows dout, const float* lse, int64_t lse_ld, float* rowstats,
+                   ts_attn_rows dq, const int64_t* span_ds, const int64_t* visit_ds,
+                   int64_t ds_head, void* ds, int64_t ds_bytes, void* stream);
+
 /* ------------------------------------------------------------------------
  * Fused chunked-vocab logprob / entropy (bf16 or fp16 operands, fp32 results)
  *

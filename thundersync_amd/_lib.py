@@ -79,6 +79,16 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _INT,
         [ctypes.POINTER(AttnProblem), AttnRows, AttnRows, AttnRows, _P, _I64, _P, AttnRows, _P],
     ),
+    "ts_attn_ds_route": (_INT, [_INT, _INT]),
+    "ts_attn_ds_layout": (
+        _INT,
+        [_P, ctypes.c_int32, _P, _I64, _P, ctypes.c_int32, _P, _P, _P, _I64, _P, _P, ctypes.POINTER(_I64)],
+    ),
+    "ts_attn_bwd_ds": (
+        _INT,
+        [ctypes.POINTER(AttnProblem), AttnRows, AttnRows, AttnRows, _P, _I64, _P, AttnRows, _P, _P, _I64, _P,
+         _I64, _P],
+    ),
 }
 
 TS_OK = 0

@@ -46,6 +46,7 @@ from __future__ import annotations
 
 import ctypes
 import math
+import os
 import threading
 from collections.abc import Sequence
 from dataclasses import dataclass, field
@@ -250,6 +251,50 @@ class AttnLayout:
                 self._tables[key] = hit
         return hit
 
+    def ds_tables(self, device: torch.device) -> dict:
+        """The dS route's workspace layout (``ts_attn_ds_layout``): elements per
+        head and the per-span / per-visit offsets, uploaded once per device."""
+        key = ("ds", device.type, device.index)
+        hit = self._tables.get(key)
+        if hit is not None:
+            return hit
+        tabs = self.device_tables(device)
+        with self._lock:
+            hit = self._tables.get(key)
+            if hit is None:
+                segs, spans, visits, _, _ = tabs["arrays"]
+                run_len = np.array([r.length for r in self.runs], np.int32)
+                visit0 = np.array(tabs["visit0"], np.int32)
+                nvisit = np.array(tabs["nvisit"], np.int32)
+                span_ds = np.zeros(max(spans.shape[0], 1), np.int64)
+                visit_ds = np.zeros(max(visits.shape[0], 1), np.int64)
+                head = ctypes.c_int64(0)
+
+                def ptr(a):
+                    return a.ctypes.data if a.size else None
+
+                lib = _lib.require_library()
+                _lib.check(
+                    lib.ts_attn_ds_layout(ptr(segs), len(segs), ptr(spans), spans.shape[0], ptr(run_len),
+                                          len(run_len), ptr(visits), ptr(visit0), ptr(nvisit), visits.shape[0],
+                                          span_ds.ctypes.data, visit_ds.ctypes.data, ctypes.byref(head)),
+                    "ts_attn_ds_layout",
+                )
+                blob = np.concatenate([span_ds, visit_ds])
+                host = torch.from_numpy(blob).pin_memory() if device.type == "cuda" else torch.from_numpy(blob)
+                dev = host.to(device, non_blocking=True)
+                hit = {
+                    "blob": dev,
+                    "host": host,
+                    "head": int(head.value),
+                    "span": dev.data_ptr(),
+                    "visit": dev.data_ptr() + 8 * span_ds.shape[0],
+                    "span_ds": span_ds[: spans.shape[0]],
+                    "visit_ds": visit_ds[: visits.shape[0]],
+                }
+                self._tables[key] = hit
+        return hit
+
     def problem(self, device, runs_ptr: int, scale: float, dtype: torch.dtype = torch.bfloat16,
                 head_dim: int = HEAD_DIM) -> AttnProblem:
         t = self.device_tables(device)
@@ -381,6 +426,27 @@ def _validate_call(layout: AttnLayout, query: torch.Tensor, keys, values) -> Non
                 raise ValueError(f"{name} source {i} has {t.shape[0]} rows, layout {layout.source_rows[i]}")
 
 
+# Largest dS workspace (bytes) the backward allocates for the dS route (dK/dV
+# kernels store dS, dQ = dS K from it; about 2 bytes per visible pair and
+# head); a problem above it, or with THUNDERSYNC_ATTN_DS=off, runs the route
+# that recomputes S and dP in the dQ kernel.
+DS_MAX_BYTES = 16 << 30
+DS_ENV = "THUNDERSYNC_ATTN_DS"
+
+
+def _ds_route(layout: AttnLayout, query: torch.Tensor, lib):
+    """(workspace tables, bytes) when this backward takes the dS route, else None."""
+    if os.environ.get(DS_ENV, "auto").strip().lower() == "off" or DS_MAX_BYTES <= 0:
+        return None
+    if not lib.ts_attn_ds_route(query.shape[2], layout.hq // layout.hkv):
+        return None
+    tabs = layout.ds_tables(query.device)
+    nbytes = layout.hq * tabs["head"] * 2
+    if nbytes > DS_MAX_BYTES:
+        return None
+    return tabs, nbytes
+
+
 class _Attention(torch.autograd.Function):
     """out, lse = attention over `layout`; grads to query and every key source."""
 
@@ -435,13 +501,27 @@ class _Attention(torch.autograd.Function):
         rowstats = torch.empty(layout.hq, max(layout.q_rows, 1), 2, dtype=torch.float32, device=query.device)
         problem = layout.problem(query.device, runs.data_ptr(), ctx.scale, query.dtype, query.shape[2])
         check_tables(layout, problem, host, query.device)
-        with operator_range("hip_attention_backward", rows=layout.q_rows, segments=len(layout.seg_q)):
-            _lib.check(
-                lib.ts_attn_bwd(ctypes.byref(problem), _rows(query), _rows(out), _rows(dout),
-                                lse.data_ptr(), lse.shape[1], rowstats.data_ptr(), _rows(dq),
-                                _lib.stream_of(query)),
-                f"ts_attn_bwd(rows={layout.q_rows}, hq={layout.hq}, hkv={layout.hkv})",
-            )
+        ds = _ds_route(layout, query, lib)
+        with operator_range("hip_attention_backward", rows=layout.q_rows, segments=len(layout.seg_q),
+                            ds_route=ds is not None):
+            if ds is None:
+                _lib.check(
+                    lib.ts_attn_bwd(ctypes.byref(problem), _rows(query), _rows(out), _rows(dout),
+                                    lse.data_ptr(), lse.shape[1], rowstats.data_ptr(), _rows(dq),
+                                    _lib.stream_of(query)),
+                    f"ts_attn_bwd(rows={layout.q_rows}, hq={layout.hq}, hkv={layout.hkv})",
+                )
+            else:
+                tabs, nbytes = ds
+                work = torch.empty(max(nbytes // 2, 8), dtype=query.dtype, device=query.device)
+                _lib.check(
+                    lib.ts_attn_bwd_ds(ctypes.byref(problem), _rows(query), _rows(out), _rows(dout),
+                                       lse.data_ptr(), lse.shape[1], rowstats.data_ptr(), _rows(dq),
+                                       tabs["span"], tabs["visit"], tabs["head"], work.data_ptr(),
+                                       work.numel() * 2, _lib.stream_of(query)),
+                    f"ts_attn_bwd_ds(rows={layout.q_rows}, hq={layout.hq}, hkv={layout.hkv})",
+                )
+                del work
         count_attention_path(HIP_BACKWARD_PATH)
         ctx.keep_bwd = (runs, host)
         return (dq, None, None, None, *dkeys, *dvalues)

@@ -66,6 +66,41 @@ int validate(const ts_attn_problem* p, const char* what) {
   return TS_OK;
 }
 
+// delta, then dQ and dK/dV: recomputing S and dP in the dQ kernel (`ds`
+// null), or storing dS in the dK/dV kernels and forming dQ = dS K from it
+int backward(const ts_attn_problem* problem, ts_attn_rows q, ts_attn_rows out, ts_attn_rows dout,
+             const float* lse, int64_t lse_ld, float* rowstats, ts_attn_rows dq, const DsArgs* ds,
+             const char* what, void* stream) {
+  int st = validate(problem, what);
+  if (st != TS_OK) return st;
+  const ts_attn_problem& P = *problem;
+  if (P.n_q_work == 0 && P.n_kv_work == 0) return TS_OK;
+  TS_CHECK_ARG(aligned_rows(q) && aligned_rows(out) && aligned_rows(dout) && aligned_rows(dq),
+               "%s: q/out/dout/dq must be 16-byte aligned with strides that are "
+               "multiples of 8 elements", what);
+  TS_CHECK_ARG(q.row_stride < (1ll << 25) && dout.row_stride < (1ll << 25),
+               "%s: q/dout row strides must be below 2^25 elements", what);
+  TS_CHECK_ARG(lse && rowstats && lse_ld >= P.q_rows, "%s: lse/rowstats null or lse_ld too small", what);
+  TS_CHECK_ARG(P.n_kv_work == 0 || (P.kv_work && P.run_visits), "%s: null kv tables", what);
+  // every row block reads dS that the dK/dV items store: with no dK/dV items
+  // (no visited run) there is nothing to read and the recompute runs
+  if (P.n_kv_work == 0) ds = nullptr;
+  hipStream_t s = (hipStream_t)stream;
+  st = launch_delta(P, out, dout, lse, rowstats, lse_ld, s);
+  if (st != TS_OK) return st;
+  if (ds) {
+    st = launch_dkdv(P, q, dout, rowstats, lse_ld, ds, s);
+    if (st == TS_OK && P.n_q_work > 0) st = launch_dq_ds(P, *ds, dq, s);
+    return st;
+  }
+  if (P.n_q_work > 0) {
+    st = launch_dq(P, q, dout, rowstats, lse_ld, dq, s);
+    if (st != TS_OK) return st;
+  }
+  if (P.n_kv_work > 0) st = launch_dkdv(P, q, dout, rowstats, lse_ld, nullptr, s);
+  return st;
+}
+
 }  // namespace attn
 }  // namespace ts
 
@@ -92,27 +127,69 @@ int ts_attn_fwd(const ts_attn_problem* problem, ts_attn_rows q, ts_attn_rows out
 
 int ts_attn_bwd(const ts_attn_problem* problem, ts_attn_rows q, ts_attn_rows out, ts_attn_rows dout,
                 const float* lse, int64_t lse_ld, float* rowstats, ts_attn_rows dq, void* stream) {
+  return ts::attn::backward(problem, q, out, dout, lse, lse_ld, rowstats, dq, nullptr, "ts_attn_bwd", stream);
+}
+
+int ts_attn_ds_route(int head_dim, int group) { return group > 0 && ts::attn::ds_route(head_dim, group) ? 1 : 0; }
+
+int ts_attn_ds_layout(const ts_attn_segment* segs, int32_t n_segs, const ts_attn_ref* seg_spans, int64_t n_spans,
+                      const int32_t* run_len, int32_t n_runs, const ts_attn_ref* run_visits,
+                      const int32_t* visit0, const int32_t* nvisit, int64_t n_visits, int64_t* span_ds,
+                      int64_t* visit_ds, int64_t* ds_head) {
   using namespace ts::attn;
-  int st = validate(problem, "ts_attn_bwd");
-  if (st != TS_OK) return st;
-  const ts_attn_problem& P = *problem;
-  if (P.n_q_work == 0 && P.n_kv_work == 0) return TS_OK;
-  TS_CHECK_ARG(aligned_rows(q) && aligned_rows(out) && aligned_rows(dout) && aligned_rows(dq),
-               "ts_attn_bwd: q/out/dout/dq must be 16-byte aligned with strides that are "
-               "multiples of 8 elements");
-  TS_CHECK_ARG(q.row_stride < (1ll << 25) && dout.row_stride < (1ll << 25),
-               "ts_attn_bwd: q/dout row strides must be below 2^25 elements");
-  TS_CHECK_ARG(lse && rowstats && lse_ld >= P.q_rows, "ts_attn_bwd: lse/rowstats null or lse_ld too small");
-  TS_CHECK_ARG(P.n_kv_work == 0 || (P.kv_work && P.run_visits), "ts_attn_bwd: null kv tables");
-  hipStream_t s = (hipStream_t)stream;
-  st = launch_delta(P, out, dout, lse, rowstats, lse_ld, s);
-  if (st != TS_OK) return st;
-  if (P.n_q_work > 0) {
-    st = launch_dq(P, q, dout, rowstats, lse_ld, dq, s);
-    if (st != TS_OK) return st;
+  const char* what = "ts_attn_ds_layout";
+  TS_CHECK_ARG(n_segs >= 0 && n_spans >= 0 && n_runs >= 0 && n_visits >= 0 && ds_head, "%s: bad sizes", what);
+  TS_CHECK_ARG((n_segs == 0 || segs) && (n_spans == 0 || (seg_spans && span_ds)) &&
+                   (n_runs == 0 || (run_len && visit0 && nvisit)) && (n_visits == 0 || (run_visits && visit_ds)),
+               "%s: null table", what);
+  int64_t total = 0;
+  for (int32_t s = 0; s < n_segs; ++s) {
+    const ts_attn_segment& g = segs[s];
+    TS_CHECK_ARG(g.q_len >= 0 && g.span0 >= 0 && g.nspan >= 0 && (int64_t)g.span0 + g.nspan <= n_spans,
+                 "%s: segment %d spans [%d, %d) outside the %lld spans", what, s, g.span0, g.span0 + g.nspan,
+                 (long long)n_spans);
+    for (int32_t i = 0; i < g.nspan; ++i) {
+      const ts_attn_ref& r = seg_spans[g.span0 + i];
+      TS_CHECK_ARG(r.index >= 0 && r.index < n_runs && run_len[r.index] > 0, "%s: segment %d span %d names run %d",
+                   what, s, i, r.index);
+      span_ds[g.span0 + i] = total;
+      const DsRect R{g.kv_len - g.q_len - r.kpos, (run_len[r.index] + 15) >> 4, g.q_len};
+      total += ds_rect_blocks(R) * kDsBlock;
+    }
   }
-  if (P.n_kv_work > 0) st = launch_dkdv(P, q, dout, rowstats, lse_ld, s);
-  return st;
+  for (int32_t r = 0; r < n_runs; ++r) {
+    TS_CHECK_ARG(visit0[r] >= 0 && nvisit[r] >= 0 && (int64_t)visit0[r] + nvisit[r] <= n_visits,
+                 "%s: run %d visits outside the %lld visits", what, r, (long long)n_visits);
+    for (int32_t i = 0; i < nvisit[r]; ++i) {
+      const ts_attn_ref& v = run_visits[visit0[r] + i];
+      TS_CHECK_ARG(v.index >= 0 && v.index < n_segs, "%s: run %d visit %d names segment %d", what, r, i, v.index);
+      const ts_attn_segment& g = segs[v.index];
+      int32_t j = 0;
+      while (j < g.nspan && !(seg_spans[g.span0 + j].index == r && seg_spans[g.span0 + j].kpos == v.kpos)) ++j;
+      TS_CHECK_ARG(j < g.nspan, "%s: run %d visit %d is not a span of segment %d", what, r, i, v.index);
+      visit_ds[visit0[r] + i] = span_ds[g.span0 + j];
+    }
+  }
+  *ds_head = total;
+  return TS_OK;
+}
+
+int ts_attn_bwd_ds(const ts_attn_problem* problem, ts_attn_rows q, ts_attn_rows out, ts_attn_rows dout,
+                   const float* lse, int64_t lse_ld, float* rowstats, ts_attn_rows dq, const int64_t* span_ds,
+                   const int64_t* visit_ds, int64_t ds_head, void* ds, int64_t ds_bytes, void* stream) {
+  using namespace ts::attn;
+  const char* what = "ts_attn_bwd_ds";
+  TS_CHECK_ARG(problem != nullptr, "%s: null problem", what);
+  if (problem->hkv <= 0 || problem->hq % problem->hkv || !ds_route(problem->head_dim, problem->hq / problem->hkv))
+    return backward(problem, q, out, dout, lse, lse_ld, rowstats, dq, nullptr, what, stream);
+  TS_CHECK_ARG(ds_head >= 0 && problem->hq > 0 && ds_bytes / 2 / problem->hq >= ds_head,
+               "%s: workspace of %lld bytes below %d heads x %lld elements", what, (long long)ds_bytes, problem->hq,
+               (long long)ds_head);
+  TS_CHECK_ARG((problem->n_q_work == 0 && problem->n_kv_work == 0) ||
+                   (ds && (uint64_t)ds % 16 == 0 && span_ds && visit_ds),
+               "%s: null or unaligned workspace or tables", what);
+  const DsArgs args{span_ds, visit_ds, ds_head, (uint64_t)ds};
+  return backward(problem, q, out, dout, lse, lse_ld, rowstats, dq, &args, what, stream);
 }
 
 int ts_attn_check_tables(const ts_attn_problem* problem, const ts_attn_segment* segs,

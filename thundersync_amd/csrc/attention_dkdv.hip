@@ -505,11 +505,11 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_wave_kernel(ts_attn_problem 
 // item's keys (kv_block 48) only issues its DMA share; only steps that cross
 // the diagonal are masked.
 // ---------------------------------------------------------------------------
-template <typename E, int HD>
+template <typename E, int HD, bool DS = false>
 __global__ __launch_bounds__(kThreads, 1) void dkdv_split_kernel(ts_attn_problem P, ts_attn_rows Q,
                                                                  ts_attn_rows dO,
                                                                  const float* __restrict__ rowstats,
-                                                                 int64_t lse_ld) {
+                                                                 int64_t lse_ld, DsArgs S) {
   static_assert(HD == 128 || HD == 256, "the swizzle needs 16 or 32 chunks per row");
   constexpr int CH = HD / 8;              // 16-byte chunks per row
   constexpr int NKS = HD / 32;            // k-steps of S / dP over the head dim
@@ -536,6 +536,7 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_split_kernel(ts_attn_problem
   const bool wave_active = in_block && wk0 < run.len;  // wave-uniform
   const bool key_valid = in_block && mykey < run.len;
   const float c = P.scale * kLog2e;
+  const int nkb = (run.len + 15) >> 4;  // 16-key blocks of the run
 
   int ro[4], to[8];
   swizzled_offsets<HD>(lane, ro, to);
@@ -569,6 +570,19 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_split_kernel(ts_attn_problem
     dv[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
+  // the dS block computed by the last step and not stored yet (when
+  // pend_live), to pend_at (this lane's element of it).  The bookkeeping
+  // (this, the workspace pointer and head size, the cursors' visit offsets)
+  // is kept in VGPRs, derived from an opaque zero: the kernel's scalar
+  // registers are all taken, and scalar spills or reloads of kernel
+  // arguments inside the loop would serialize its LDS reads.
+  int vzero;
+  asm volatile("v_mov_b32 %0, 0" : "=v"(vzero));
+  bf16* const ds_lane = DS ? (bf16*)S.ptr + (vzero + ds_store_offset(lane) / 2) : nullptr;
+  const int64_t ds_head = DS ? S.head + vzero : 0;
+  bf16* pend_at = ds_lane;
+  bool pend_live = false;
+  bf16x8 pend = as_bf16x8(u32x4{0u, 0u, 0u, 0u});
   // step cursor: query head g of the group, then the visit / row block
   struct Cursor {
     int g;
@@ -583,6 +597,14 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_split_kernel(ts_attn_problem
     cv.q_row0 = seg.q_row0;
     const int rs = ref.kpos + k0 - cv.off;
     cv.r0 = (rs < 0 ? 0 : rs) & ~31;
+    if constexpr (DS) {
+      // consumed here, so that no scalar load is outstanding when the next
+      // step's LDS reads count their completions
+      const int vb = (int)(load_uniform(S.visit, run.visit0 + cv.vi) / kDsBlock +
+                           ds_blocks_before(DsRect{cv.off - cv.kpos, nkb, cv.q_len}, cv.r0 >> 5));
+      asm volatile("" ::"s"(vb));
+      cv.dsb = vzero + vb;
+    }
   };
   auto settle = [&](VisitCursor cv) -> VisitCursor {
     while (cv.r0 >= cv.q_len) {
@@ -592,12 +614,13 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_split_kernel(ts_attn_problem
     return cv;
   };
   auto first_visit = [&]() -> VisitCursor {
-    VisitCursor cv{0, 0, 0, 0, 0, 0};
+    VisitCursor cv{0, 0, 0, 0, 0, 0, 0};
     if (run.nvisit > 0) enter(cv);
     return settle(cv);
   };
   // the step after `cu`; g == group at the end
   auto advance = [&](Cursor cu) -> Cursor {
+    if constexpr (DS) cu.v.dsb += ds_blocks_in(DsRect{cu.v.off - cu.v.kpos, nkb, cu.v.q_len}, cu.v.r0 >> 5);
     cu.v.r0 += 32;
     if (cu.v.r0 >= cu.v.q_len) cu.v = settle(cu.v);
     if (cu.v.vi >= run.nvisit) {
@@ -641,7 +664,18 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_split_kernel(ts_attn_problem
     const int nrows = min(32, cur.v.q_len - r0);
     // the wave's keys are all invisible to this block when its first key is
     // beyond the block's last row
-    if (wave_active && kpos + wk0 <= off + r0 + nrows - 1) {
+    const bool live = wave_active && kpos + wk0 <= off + r0 + nrows - 1;
+    if constexpr (DS) {
+      // the previous step's dS block, stored a step before the next wait for
+      // all of this wave's memory operations; then this step's destination
+      // (block wk0 / 16 of row block r0 / 32, inside the rectangle when the
+      // wave computes it).  Address arithmetic stays out of the MFMA phases,
+      // whose interleaving it would disturb.
+      if (pend_live) global_st16(pend_at, as_u32x4(pend));
+      pend_live = live;
+      pend_at = ds_lane + (int64_t)(hk * group + cur.g) * ds_head + (int64_t)(cur.v.dsb + (wk0 >> 4)) * kDsBlock;
+    }
+    if (live) {
       const bf16* tq = cur_buf;
       const bf16* td = cur_buf + TILE;
       const float* sl = reinterpret_cast<const float*>(cur_buf + 2 * TILE);  // [32] (lse2, delta)
@@ -672,19 +706,22 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_split_kernel(ts_attn_problem
       // P and dS as B operands: slot j = 4 qb + i  <->  row 16 qb + 4 g4 + i
       float pv[8], dsv[8];
       const int lim = off + r0 - kpos - mykey;  // row rl sees the key iff rl >= -lim
-      const bool diag = kpos + wk0 + 15 > off + r0;  // wave-uniform
+      // wave-uniform: the keys cross the diagonal (or, when dS is stored, the
+      // run's end: P of a key past it, whose K row is zero, is exp2(-lse2))
+      const bool diag = (kpos + wk0 + 15 > off + r0) | (DS && wk0 + 16 > run.len);
 #pragma unroll
       for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int rl = 16 * qb + 4 * g4 + i;
           float p = fast_exp2(sc[qb][i] * c - sl[2 * rl]);
-          if (diag && rl + lim < 0) p = 0.f;
+          if (diag && ((rl + lim < 0) | (DS && !key_valid))) p = 0.f;
           pv[4 * qb + i] = p;
           dsv[4 * qb + i] = p * (dp[qb][i] - sl[2 * rl + 1]);
         }
       const bf16x8 pk = pack8<E>(pv);
       const bf16x8 dsk = pack8<E>(dsv);
+      if constexpr (DS) pend = dsk;
       __builtin_amdgcn_sched_barrier(0);
       // dV^T += dO^T P, dK^T += Q^T dS: rows d = 16 mb + 4 g4 + i, column key j16
 #pragma unroll
@@ -716,6 +753,8 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_split_kernel(ts_attn_problem
     if (cur.g >= group) break;
     step(std::integral_constant<int, 1>{}, cur, nxt);
   }
+  if constexpr (DS)
+    if (pend_live) global_st16(pend_at, as_u32x4(pend));
   __builtin_amdgcn_s_waitcnt(0);  // the last (empty) DMA has landed before the waves exit
   if (!key_valid) return;
   // lane (g4, j16) holds d = 16 mb + 4 g4 .. + 3 of key mykey: 8-byte stores
@@ -741,35 +780,41 @@ void launch_dkdv_generic(dim3 grid, const ts_attn_problem& P, ts_attn_rows q, ts
   hipLaunchKernelGGL((dkdv_kernel<E, HD>), grid, dim3(kThreads), 0, s, P, q, dout, rowstats, lse_ld);
 }
 
+template <typename E, bool DS>
+void launch_dkdv_tuned(dim3 grid, const ts_attn_problem& P, ts_attn_rows q, ts_attn_rows dout,
+                       const float* rowstats, int64_t lse_ld, const DsArgs& S, hipStream_t s) {
+  const int group = P.hq / P.hkv;
+  ts::TimedLaunch timed_("attention.dkdv_kernel", s);
+  if (P.head_dim == 256)
+    hipLaunchKernelGGL((dkdv_split_kernel<E, 256, DS>), grid, dim3(kThreads), 0, s, P, q, dout, rowstats, lse_ld, S);
+  else if (group % 4 == 0)
+    hipLaunchKernelGGL((dkdv_wave_kernel<E, 3>), grid, dim3(kThreads), 0, s, P, q, dout, rowstats, lse_ld);
+  else
+    hipLaunchKernelGGL((dkdv_split_kernel<E, D, DS>), grid, dim3(kThreads), 0, s, P, q, dout, rowstats, lse_ld, S);
+}
+
 template <typename E>
 int launch_dkdv_t(const ts_attn_problem& P, ts_attn_rows q, ts_attn_rows dout, const float* rowstats,
-                int64_t lse_ld, hipStream_t s) {
-  const int group = P.hq / P.hkv;
+                  int64_t lse_ld, const DsArgs* ds, hipStream_t s) {
   const dim3 grid((unsigned)(P.n_kv_work * P.hkv));
   switch (P.head_dim) {
     case 32: launch_dkdv_generic<E, 32>(grid, P, q, dout, rowstats, lse_ld, s); break;
     case 64: launch_dkdv_generic<E, 64>(grid, P, q, dout, rowstats, lse_ld, s); break;
     case 96: launch_dkdv_generic<E, 96>(grid, P, q, dout, rowstats, lse_ld, s); break;
     case 192: launch_dkdv_generic<E, 192>(grid, P, q, dout, rowstats, lse_ld, s); break;
-    case 256: {
-      ts::TimedLaunch timed_("attention.dkdv_kernel", s);
-      hipLaunchKernelGGL((dkdv_split_kernel<E, 256>), grid, dim3(kThreads), 0, s, P, q, dout, rowstats, lse_ld);
-      break;
-    }
-    default:
-      ts::TimedLaunch timed_("attention.dkdv_kernel", s);
-      if (group % 4 == 0)
-        hipLaunchKernelGGL((dkdv_wave_kernel<E, 3>), grid, dim3(kThreads), 0, s, P, q, dout, rowstats, lse_ld);
+    default:  // 128 and 256
+      if (ds)
+        launch_dkdv_tuned<E, true>(grid, P, q, dout, rowstats, lse_ld, *ds, s);
       else
-        hipLaunchKernelGGL((dkdv_split_kernel<E, D>), grid, dim3(kThreads), 0, s, P, q, dout, rowstats, lse_ld);
+        launch_dkdv_tuned<E, false>(grid, P, q, dout, rowstats, lse_ld, DsArgs{}, s);
   }
   return ts::check_launch("ts_attn_bwd (dkdv)");
 }
 
 int launch_dkdv(const ts_attn_problem& P, ts_attn_rows q, ts_attn_rows dout, const float* rowstats,
-                int64_t lse_ld, hipStream_t s) {
-  return P.dtype == kF16 ? launch_dkdv_t<f16>(P, q, dout, rowstats, lse_ld, s)
-                         : launch_dkdv_t<bf16>(P, q, dout, rowstats, lse_ld, s);
+                int64_t lse_ld, const DsArgs* ds, hipStream_t s) {
+  return P.dtype == kF16 ? launch_dkdv_t<f16>(P, q, dout, rowstats, lse_ld, ds, s)
+                         : launch_dkdv_t<bf16>(P, q, dout, rowstats, lse_ld, ds, s);
 }
 
 }  // namespace attn

@@ -230,7 +230,92 @@ struct VisitCursor {
   int off;         // its kv_len - q_len
   int kpos;        // position of the run's first key in the segment's key order
   int64_t q_row0;  // its first row in the packed Q / dO / statistics
+  int dsb;         // dS route: index, within a head, of row block r0 / 32's first dS block
 };
+
+// ---------------------------------------------------------------------------
+// dS workspace: the backward route that stores dS once and forms dQ = dS K
+// from it instead of recomputing S and dP in the dQ kernel.
+//
+// The dK/dV kernels compute dS = P (dP - delta) for every visible (row, key)
+// pair, rounded to the element type for their dK product; on this route they
+// also store it.  Unit of storage: a block of 32 query rows x 16 keys (512
+// elements) of one (segment, span) pair of one query head.  The blocks of a
+// pair form its rectangle: row block rb (segment rows 32 rb .. 32 rb + 31)
+// holds the run's 16-key blocks 0 .. n(rb) - 1, the prefix that some row of
+// it below q_len sees, row block after row block (invisible blocks take no
+// space).  A head's rectangles sit at the offsets of the span and visit
+// tables; heads follow one another.
+//
+// Inside a block, row r and key k: slot s = 8 ((r >> 2) & 3) + 4 (r >> 4) +
+// (r & 3) (so lane (g4, j16) of a dK/dV wave, which holds rows 16 qb + 4 g4 + i
+// of key j16, owns slots 8 g4 .. 8 g4 + 7), element 32 k + 8 (c ^ ((k >> 1) &
+// 2)) + (s & 7) with c = s >> 3: 64-byte key rows of four 16-byte chunks,
+// the chunks of keys 4..7 and 12..15 swapped in pairs so that the dQ
+// kernel's transposed LDS reads of keys 4 g4 + t (lanes g4 = 0, 1 in one
+// pass) touch distinct banks.
+// ---------------------------------------------------------------------------
+constexpr int kDsBlock = 512;  // elements of a 32-row x 16-key block
+
+struct DsArgs {
+  const int64_t* span;   // per seg_spans entry: element offset of its rectangle within a head
+  const int64_t* visit;  // per run_visits entry: that of the span it visits
+  int64_t head;          // elements per head
+  uint64_t ptr;          // device address of the workspace (hq * head elements)
+};
+
+// One (segment, span) rectangle: row r of the segment sees run key j iff
+// j <= d + r (d = kv_len - q_len - kpos); nkb 16-key blocks; q_len rows.
+struct DsRect {
+  int d;
+  int nkb;
+  int q_len;
+};
+
+__host__ __device__ inline int64_t floor_div(int64_t a, int64_t b) { return a >= 0 ? a / b : -((-a + b - 1) / b); }
+__host__ __device__ inline int64_t imin64(int64_t a, int64_t b) { return a < b ? a : b; }
+__host__ __device__ inline int64_t imax64(int64_t a, int64_t b) { return a > b ? a : b; }
+
+// key blocks stored for row block rb: those holding a key that one of its
+// rows below q_len sees
+__host__ __device__ inline int ds_blocks_in(const DsRect& R, int rb) {
+  const int64_t maxrow = imin64(32 * (int64_t)rb + 31, R.q_len - 1);
+  const int64_t last = R.d + maxrow;  // the last run key that row sees
+  return last < 0 ? 0 : (int)imin64(R.nkb, last / 16 + 1);
+}
+
+// blocks stored before row block rb (rb below the last row block + 1): the
+// earlier row blocks are whole (32 rows below q_len), row block t holding
+// clamp(2 t + c, 0, nkb) blocks with c = floor((d + 31) / 16) + 1; summed in
+// closed form over the zero, linear and saturated stretches of t
+__host__ __device__ inline int64_t ds_blocks_before(const DsRect& R, int rb) {
+  const int64_t c = floor_div((int64_t)R.d + 31, 16) + 1, n = R.nkb;
+  const int64_t t0 = imax64(0, floor_div(-c, 2) + 1);  // first t with 2 t + c > 0
+  const int64_t t1 = imax64(0, -floor_div(c - n, 2));  // first t with 2 t + c >= n
+  const int64_t b = imin64(rb, t1), a = imin64(t0, b);
+  return (b - a) * (a + b - 1 + c) + n * imax64(0, rb - t1);
+}
+
+// blocks of the whole rectangle
+__host__ __device__ inline int64_t ds_rect_blocks(const DsRect& R) {
+  const int nrb = (R.q_len + 31) >> 5;
+  return nrb == 0 ? 0 : ds_blocks_before(R, nrb - 1) + ds_blocks_in(R, nrb - 1);
+}
+
+// 16 bytes to global memory through a global-address-space pointer: a
+// global store (a generic pointer makes it a FLAT store, which also counts
+// on the LDS counter and so turns every later LDS wait into a full drain)
+__device__ __forceinline__ void global_st16(bf16* p, u32x4 v) {
+  *(__attribute__((address_space(1))) u32x4*)(p) = v;
+}
+
+// byte offset of lane (g4, j16)'s 16-byte store of its dS slots in a block
+__device__ __forceinline__ int ds_store_offset(int lane) {
+  const int g4 = lane >> 4, j16 = lane & 15;
+  return 64 * j16 + 16 * (g4 ^ ((j16 >> 1) & 2));
+}
+
+
 
 
 constexpr int kKV64 = BK * D;  // elements of one 64-key tile
@@ -389,8 +474,19 @@ int launch_delta(const ts_attn_problem& P, ts_attn_rows out, ts_attn_rows dout, 
                  float* rowstats, int64_t lse_ld, hipStream_t s);
 int launch_dq(const ts_attn_problem& P, ts_attn_rows q, ts_attn_rows dout, const float* rowstats,
               int64_t lse_ld, ts_attn_rows dq, hipStream_t s);
+// `ds` null: dK/dV only; else the kernels also store dS into the workspace
+// (only where ds_route holds)
 int launch_dkdv(const ts_attn_problem& P, ts_attn_rows q, ts_attn_rows dout, const float* rowstats,
-                int64_t lse_ld, hipStream_t s);
+                int64_t lse_ld, const DsArgs* ds, hipStream_t s);
+// dQ = scale dS K from the workspace the dK/dV launch filled
+int launch_dq_ds(const ts_attn_problem& P, const DsArgs& ds, ts_attn_rows dq, hipStream_t s);
+
+// the dS route exists where the key-split dK/dV kernel runs: head dim 256,
+// and head dim 128 with GQA groups that are not a multiple of 4 (the
+// one-wave-per-head kernel has no registers left for the stores)
+inline bool ds_route(int head_dim, int group) {
+  return head_dim == 256 || (head_dim == 128 && group % 4 != 0);
+}
 
 }  // namespace attn
 }  // namespace ts
