@@ -1,8 +1,7 @@
 """The attention backward's two routes against the CPU oracle.
 
-Where the key-split dK/dV kernel runs (head dim 256; head dim 128 with GQA
-groups that are not a multiple of 4) the backward takes the dS route by
-default: the dK/dV kernel stores dS and the dQ kernel forms dQ = dS K from it.
+At head dim 256 the backward takes the dS route by default: the dK/dV kernel
+stores dS and the dQ kernel forms dQ = dS K from it.
 ``THUNDERSYNC_ATTN_DS=off`` (or a problem whose workspace exceeds
 ``attention.DS_MAX_BYTES``) selects the route whose dQ kernel recomputes S and
 dP.  Both are checked against the fp32 oracle at the attention tests' bar
@@ -59,15 +58,18 @@ def run_both(monkeypatch, cuda, q, ks, vs, dout, layout, scale):
 
 CHAINS = [
     # head dim, query rows, chunk lengths, hq, hkv
-    (128, 130, [7, 64, 130], 32, 8),     # group 4: one-wave-per-head dK/dV, recompute route only
+    (128, 130, [7, 64, 130], 32, 8),     # group 4
     (128, 200, [300, 17, 200], 40, 8),   # group 5: key-split dK/dV, dQ 1 head x 4 row blocks
     (128, 77, [120, 77], 16, 8),         # group 2
     (128, 33, [80, 33], 4, 4),           # group 1
     (128, 1, [9], 4, 1),                 # one row
-    (128, 40, [100, 23, 45], 6, 2),      # runs shorter than the rows, a run past row 0's keys
+    (128, 40, [100, 23, 45], 6, 2),
     (256, 150, [300, 150], 24, 4),       # the reference's FA4 test heads
     (256, 64, [64], 8, 2),
     (256, 45, [33, 61], 6, 6),
+    (256, 40, [100, 23, 45], 6, 2),      # runs shorter than the rows, a run past row 0's keys
+    (256, 1, [9], 4, 1),                 # one row
+    (256, 200, [300, 17, 200], 40, 8),   # group 5
 ]
 
 
@@ -93,15 +95,15 @@ def test_routes_agree_with_the_oracle(monkeypatch, cuda, d, t, chunks, hq, hkv):
 
 
 def test_fp16_route(monkeypatch, cuda):
-    print("routes fp16 d=128 t=96 chunks=[50, 96] hq=6 hkv=2", flush=True)
+    print("routes fp16 d=256 t=96 chunks=[50, 96] hq=6 hkv=2", flush=True)
     g = torch.Generator().manual_seed(4)
-    q = torch.randn(96, 6, 128, generator=g).half()
-    ks = [torch.randn(n, 2, 128, generator=g).half() for n in (50, 96)]
-    vs = [torch.randn(n, 2, 128, generator=g).half() for n in (50, 96)]
-    dout = torch.randn(96, 6, 128, generator=g).half()
-    want, wq, wks, wvs = ref.attention_with_grads(q, ks, vs, dout, 128 ** -0.5)
+    q = torch.randn(96, 6, 256, generator=g).half()
+    ks = [torch.randn(n, 2, 256, generator=g).half() for n in (50, 96)]
+    vs = [torch.randn(n, 2, 256, generator=g).half() for n in (50, 96)]
+    dout = torch.randn(96, 6, 256, generator=g).half()
+    want, wq, wks, wvs = ref.attention_with_grads(q, ks, vs, dout, 256 ** -0.5)
     (_, dq1, dk1, dv1), (_, dq2, _, _) = run_both(monkeypatch, cuda, q, ks, vs, dout,
-                                                  hip.chain_layout(96, [50, 96], 6, 2), 128 ** -0.5)
+                                                  hip.chain_layout(96, [50, 96], 6, 2), 256 ** -0.5)
     assert dq1.dtype == torch.float16
     close(dq1, wq, "dq (dS route)")
     close(dq2, wq, "dq (recompute route)")
@@ -111,7 +113,7 @@ def test_fp16_route(monkeypatch, cuda):
 
 
 def test_forest_route(monkeypatch, cuda):
-    """A random three-level forest (40/8 heads, d128) through the dS route
+    """A random three-level forest (24/4 heads, d256) through the dS route
     against the dense-mask oracle."""
     rng = random.Random(21)
     prompt = [rng.randrange(50000) for _ in range(90)]
@@ -128,7 +130,7 @@ def test_forest_route(monkeypatch, cuda):
          for g, i, segs in spec]))
     oplan = ofo.compile_plan(ofo.build_forest(
         [ofo.Trajectory([ofo.Segment(tuple(t), k, s) for k, t, s in segs], g, i) for g, i, segs in spec]))
-    p, hq, hkv, d = plan.n_physical, 40, 8, 128
+    p, hq, hkv, d = plan.n_physical, 24, 4, 256
     print(f"forest route: {p} tokens, {plan.n_nodes} nodes", flush=True)
     mask = torch.tensor(ofo.visibility_mask(oplan))
     g = torch.Generator().manual_seed(2)
@@ -150,14 +152,12 @@ def test_forest_route(monkeypatch, cuda):
 
 def test_workspace_cap_selects_the_recompute_route(monkeypatch, cuda):
     lay = hip.chain_layout(64, [64], 6, 2)
-    q = torch.randn(64, 6, 128, device=cuda, dtype=torch.bfloat16)
+    q = torch.randn(64, 6, 256, device=cuda, dtype=torch.bfloat16)
     lib = _lib.require_library()
     monkeypatch.setenv(hip.DS_ENV, "auto")
     assert hip._ds_route(lay, q, lib) is not None
     monkeypatch.setattr(hip, "DS_MAX_BYTES", 1024)
     assert hip._ds_route(lay, q, lib) is None
     monkeypatch.setattr(hip, "DS_MAX_BYTES", 16 << 30)
+    assert hip._ds_route(lay, q[..., :128].contiguous(), lib) is None  # head dim 128: recompute route
     assert hip._ds_route(lay, q[..., :64].contiguous(), lib) is None  # head dim 64: no dS kernels
-    lay4 = hip.chain_layout(64, [64], 8, 2)
-    q4 = torch.randn(64, 8, 128, device=cuda, dtype=torch.bfloat16)
-    assert hip._ds_route(lay4, q4, lib) is None  # group 4 at head dim 128: the one-wave-per-head kernel

@@ -37,8 +37,9 @@ Reference entry points mirrored here (same argument meaning):
   (engine/streaming.py:1314-1423).
 
 Element types: bf16 and fp16 (Q, K, V of one call share one).  Head dims D:
-32, 64, 96, 128, 192 and 256 (128 with GQA groups that are a multiple of 4 runs
-the one-wave-per-head kernels, every other case the register-staged ones).
+32, 64, 96, 128, 192 and 256 (128 and 256 run the DMA-staged kernels, the
+others the register-staged ones).  At head dim 256 the backward stores dS
+once in a workspace and forms dQ = dS K from it (see ``DS_MAX_BYTES``).
 There is no host path: CPU tensors, other dtypes or head dims raise.
 """
 

@@ -1,5 +1,5 @@
 // Attention backward, dS route: dQ = scale * dS K from the dS blocks the
-// dK/dV kernels stored (head dims 128 and 256).
+// dK/dV kernel stored (head dim 256; the kernel is written for 128 too).
 //
 // A work-group owns the work item's 128 / GC query rows of one segment for GC
 // query heads of one GQA group: wave w takes head w % GC and the 32-row block
@@ -201,10 +201,7 @@ void launch_dq_ds_t(const ts_attn_problem& P, const DsArgs& S, ts_attn_rows dq, 
   const int group = P.hq / P.hkv;
   const int gc = heads_per_block(group);
   const dim3 grid((unsigned)(P.n_q_work * P.hkv * (group / gc)));
-  if (P.head_dim == 256)
-    launch_dq_ds_hd<E, 256>(P, gc, grid, S, dq, s);
-  else
-    launch_dq_ds_hd<E, 128>(P, gc, grid, S, dq, s);
+  launch_dq_ds_hd<E, 256>(P, gc, grid, S, dq, s);  // the dS route is head dim 256 only
 }
 
 int launch_dq_ds(const ts_attn_problem& P, const DsArgs& S, ts_attn_rows dq, hipStream_t s) {

@@ -481,12 +481,12 @@ int launch_dkdv(const ts_attn_problem& P, ts_attn_rows q, ts_attn_rows dout, con
 // dQ = scale dS K from the workspace the dK/dV launch filled
 int launch_dq_ds(const ts_attn_problem& P, const DsArgs& ds, ts_attn_rows dq, hipStream_t s);
 
-// the dS route exists where the key-split dK/dV kernel runs: head dim 256,
-// and head dim 128 with GQA groups that are not a multiple of 4 (the
-// one-wave-per-head kernel has no registers left for the stores)
-inline bool ds_route(int head_dim, int group) {
-  return head_dim == 256 || (head_dim == 128 && group % 4 != 0);
-}
+// the dS route: head dim 256.  At head dim 128 the one-wave-per-head dK/dV
+// kernel (groups that are a multiple of 4) has no registers left for the
+// stores, and in the key-split kernel the stores' bookkeeping costs its step
+// more than the dQ kernel saves (a dK/dV step is half as long as at 256 for
+// the same dS bytes).
+inline bool ds_route(int head_dim, int /*group*/) { return head_dim == 256; }
 
 }  // namespace attn
 }  // namespace ts
