@@ -263,7 +263,9 @@ int ts_attn_bwd(const ts_attn_problem* problem, ts_attn_rows q, ts_attn_rows out
  *
  * ts_attn_bwd_ds: as ts_attn_bwd, with span_ds / visit_ds the device copies
  * of the layout's offsets and `ds` a 16-byte aligned device workspace of at
- * least hq * ds_head * 2 bytes (its contents on entry do not matter).
+ * least (hq * ds_head + 512) * 2 bytes: every head's part, then one block
+ * that takes the stores of steps that compute no dS (its contents on entry
+ * do not matter).
  * No counterpart in the reference, whose flash/FA4 backward kernels own
  * their scratch; it replaces the same calls as ts_attn_bwd. */
 int ts_attn_ds_route(int head_dim, int group);

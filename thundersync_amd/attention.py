@@ -442,7 +442,7 @@ def _ds_route(layout: AttnLayout, query: torch.Tensor, lib):
     if not lib.ts_attn_ds_route(query.shape[2], layout.hq // layout.hkv):
         return None
     tabs = layout.ds_tables(query.device)
-    nbytes = layout.hq * tabs["head"] * 2
+    nbytes = (layout.hq * tabs["head"] + 512) * 2  # every head's part, then the sink block
     if nbytes > DS_MAX_BYTES:
         return None
     return tabs, nbytes
@@ -514,7 +514,7 @@ class _Attention(torch.autograd.Function):
                 )
             else:
                 tabs, nbytes = ds
-                work = torch.empty(max(nbytes // 2, 8), dtype=query.dtype, device=query.device)
+                work = torch.empty(nbytes // 2, dtype=query.dtype, device=query.device)
                 _lib.check(
                     lib.ts_attn_bwd_ds(ctypes.byref(problem), _rows(query), _rows(out), _rows(dout),
                                        lse.data_ptr(), lse.shape[1], rowstats.data_ptr(), _rows(dq),

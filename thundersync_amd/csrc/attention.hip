@@ -182,9 +182,10 @@ int ts_attn_bwd_ds(const ts_attn_problem* problem, ts_attn_rows q, ts_attn_rows 
   TS_CHECK_ARG(problem != nullptr, "%s: null problem", what);
   if (problem->hkv <= 0 || problem->hq % problem->hkv || !ds_route(problem->head_dim, problem->hq / problem->hkv))
     return backward(problem, q, out, dout, lse, lse_ld, rowstats, dq, nullptr, what, stream);
-  TS_CHECK_ARG(ds_head >= 0 && problem->hq > 0 && ds_bytes / 2 / problem->hq >= ds_head,
-               "%s: workspace of %lld bytes below %d heads x %lld elements", what, (long long)ds_bytes, problem->hq,
-               (long long)ds_head);
+  TS_CHECK_ARG(ds_head >= 0 && problem->hq > 0 && ds_bytes / 2 >= kDsBlock &&
+                   (ds_bytes / 2 - kDsBlock) / problem->hq >= ds_head,
+               "%s: workspace of %lld bytes below (%d heads x %lld + 512) elements", what, (long long)ds_bytes,
+               problem->hq, (long long)ds_head);
   TS_CHECK_ARG((problem->n_q_work == 0 && problem->n_kv_work == 0) ||
                    (ds && (uint64_t)ds % 16 == 0 && span_ds && visit_ds),
                "%s: null or unaligned workspace or tables", what);

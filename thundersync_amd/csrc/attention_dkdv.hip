@@ -537,6 +537,9 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_split_kernel(ts_attn_problem
   const bool key_valid = in_block && mykey < run.len;
   const float c = P.scale * kLog2e;
   const int nkb = (run.len + 15) >> 4;  // 16-key blocks of the run
+  // the key position the causal mask compares against; dS route: a key past
+  // the run is put past every row (2^24 rows), so the mask zeroes its P too
+  const int mask_key = mykey + (DS && !key_valid ? (1 << 24) : 0);
 
   int ro[4], to[8];
   swizzled_offsets<HD>(lane, ro, to);
@@ -570,23 +573,29 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_split_kernel(ts_attn_problem
     dv[mb] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
-  // the dS block computed by the last step and not stored yet (when
-  // pend_live), to pend_at (this lane's element of it).  The bookkeeping
-  // (this, the workspace pointer and head size, the cursors' visit offsets)
-  // is kept in VGPRs, derived from an opaque zero: the kernel's scalar
-  // registers are all taken, and scalar spills or reloads of kernel
-  // arguments inside the loop would serialize its LDS reads.
+  // dS route.  The dS block computed by a step is stored by the next one
+  // (a step before the next wait for all of this wave's memory operations),
+  // to pend_at: this lane's element of the block, or of the workspace's sink
+  // block (after every head's part) when the step computed none, so the
+  // store needs no branch.  The cursor carries `at`, this lane's element of
+  // its step's block, advanced by the row block's block count each step and
+  // located afresh only on entering a visit or head.  The bookkeeping is kept
+  // in VGPRs, derived from an opaque zero: the kernel's scalar registers are
+  // all taken, and scalar spills or reloads of kernel arguments inside the
+  // loop would serialize its LDS reads.
   int vzero;
   asm volatile("v_mov_b32 %0, 0" : "=v"(vzero));
-  bf16* const ds_lane = DS ? (bf16*)S.ptr + (vzero + ds_store_offset(lane) / 2) : nullptr;
   const int64_t ds_head = DS ? S.head + vzero : 0;
-  bf16* pend_at = ds_lane;
-  bool pend_live = false;
+  bf16* const ds_base = DS ? (bf16*)S.ptr + (vzero + ds_store_offset(lane) / 2) : nullptr;
+  bf16* const ds_sink = ds_base + P.hq * ds_head;
+  bf16* const ds_lane = ds_base + (int64_t)(wk0 >> 4) * kDsBlock;  // key block wk0 / 16
+  bf16* pend_at = ds_sink;
   bf16x8 pend = as_bf16x8(u32x4{0u, 0u, 0u, 0u});
   // step cursor: query head g of the group, then the visit / row block
   struct Cursor {
     int g;
     VisitCursor v;
+    bf16* at;  // dS route: this lane's element of the step's dS block
   };
   auto enter = [&](VisitCursor& cv) {
     const ts_attn_ref ref = load_uniform(P.run_visits, run.visit0 + cv.vi);
@@ -597,14 +606,6 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_split_kernel(ts_attn_problem
     cv.q_row0 = seg.q_row0;
     const int rs = ref.kpos + k0 - cv.off;
     cv.r0 = (rs < 0 ? 0 : rs) & ~31;
-    if constexpr (DS) {
-      // consumed here, so that no scalar load is outstanding when the next
-      // step's LDS reads count their completions
-      const int vb = (int)(load_uniform(S.visit, run.visit0 + cv.vi) / kDsBlock +
-                           ds_blocks_before(DsRect{cv.off - cv.kpos, nkb, cv.q_len}, cv.r0 >> 5));
-      asm volatile("" ::"s"(vb));
-      cv.dsb = vzero + vb;
-    }
   };
   auto settle = [&](VisitCursor cv) -> VisitCursor {
     while (cv.r0 >= cv.q_len) {
@@ -614,18 +615,44 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_split_kernel(ts_attn_problem
     return cv;
   };
   auto first_visit = [&]() -> VisitCursor {
-    VisitCursor cv{0, 0, 0, 0, 0, 0, 0};
+    VisitCursor cv{0, 0, 0, 0, 0, 0};
     if (run.nvisit > 0) enter(cv);
     return settle(cv);
   };
+  // `at` of a cursor on a visit (its rectangle's offset, the blocks of the
+  // row blocks before r0 / 32)
+  auto locate = [&](const Cursor& cu) -> bf16* {
+    // consumed here, so that no scalar load is outstanding when the next
+    // step's LDS reads count their completions
+    const int64_t blk = load_uniform(S.visit, run.visit0 + cu.v.vi) / kDsBlock +
+                        ds_blocks_before(DsRect{cu.v.off - cu.v.kpos, nkb, cu.v.q_len}, cu.v.r0 >> 5);
+    asm volatile("" ::"s"(blk));
+    return ds_lane + (int64_t)(hk * group + cu.g) * ds_head + blk * kDsBlock;
+  };
   // the step after `cu`; g == group at the end
   auto advance = [&](Cursor cu) -> Cursor {
-    if constexpr (DS) cu.v.dsb += ds_blocks_in(DsRect{cu.v.off - cu.v.kpos, nkb, cu.v.q_len}, cu.v.r0 >> 5);
+    // blocks of the row block being left (32-bit: d + row < kv_len)
+    int inc = 0;
+    if constexpr (DS) {
+      const int last = cu.v.off - cu.v.kpos + min(cu.v.r0 + 31, cu.v.q_len - 1);
+      inc = last < 0 ? 0 : min(nkb, (last >> 4) + 1);
+    }
+    bool next_row_block = true;  // same visit and head
     cu.v.r0 += 32;
-    if (cu.v.r0 >= cu.v.q_len) cu.v = settle(cu.v);
+    if (cu.v.r0 >= cu.v.q_len) {
+      cu.v = settle(cu.v);
+      next_row_block = false;
+    }
     if (cu.v.vi >= run.nvisit) {
       ++cu.g;
       cu.v = first_visit();
+      next_row_block = false;
+    }
+    if constexpr (DS) {
+      if (next_row_block)
+        cu.at += (int64_t)inc * kDsBlock;
+      else if (cu.g < group && cu.v.vi < run.nvisit)
+        cu.at = locate(cu);
     }
     return cu;
   };
@@ -660,21 +687,20 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_split_kernel(ts_attn_problem
     __builtin_amdgcn_s_waitcnt(0);  // this wave's share of the step's tiles has landed
     __syncthreads();                // every wave's share has, and nobody reads nxt_buf any more
     issue(nxt, nxt_buf);
+    // dS route: the previous step's dS block, stored a step before the next
+    // wait for all of this wave's memory operations (after the DMA, which
+    // it would otherwise hold up in the memory queue)
+    if constexpr (DS) global_st16(pend_at, as_u32x4(pend));
     const int off = cur.v.off, r0 = cur.v.r0, kpos = cur.v.kpos;
     const int nrows = min(32, cur.v.q_len - r0);
     // the wave's keys are all invisible to this block when its first key is
     // beyond the block's last row
     const bool live = wave_active && kpos + wk0 <= off + r0 + nrows - 1;
-    if constexpr (DS) {
-      // the previous step's dS block, stored a step before the next wait for
-      // all of this wave's memory operations; then this step's destination
-      // (block wk0 / 16 of row block r0 / 32, inside the rectangle when the
-      // wave computes it).  Address arithmetic stays out of the MFMA phases,
-      // whose interleaving it would disturb.
-      if (pend_live) global_st16(pend_at, as_u32x4(pend));
-      pend_live = live;
-      pend_at = ds_lane + (int64_t)(hk * group + cur.g) * ds_head + (int64_t)(cur.v.dsb + (wk0 >> 4)) * kDsBlock;
-    }
+    // dS route: this step's destination (block wk0 / 16 of row block r0 / 32,
+    // inside the rectangle when the wave computes it; its address was formed
+    // at the previous step's tail, off the path from the barrier to the first
+    // MFMA)
+    if constexpr (DS) pend_at = live ? cur.at : ds_sink;
     if (live) {
       const bf16* tq = cur_buf;
       const bf16* td = cur_buf + TILE;
@@ -705,7 +731,7 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_split_kernel(ts_attn_problem
       __builtin_amdgcn_sched_barrier(0);
       // P and dS as B operands: slot j = 4 qb + i  <->  row 16 qb + 4 g4 + i
       float pv[8], dsv[8];
-      const int lim = off + r0 - kpos - mykey;  // row rl sees the key iff rl >= -lim
+      const int lim = off + r0 - kpos - mask_key;  // row rl sees the key iff rl >= -lim
       // wave-uniform: the keys cross the diagonal (or, when dS is stored, the
       // run's end: P of a key past it, whose K row is zero, is exp2(-lse2))
       const bool diag = (kpos + wk0 + 15 > off + r0) | (DS && wk0 + 16 > run.len);
@@ -715,7 +741,7 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_split_kernel(ts_attn_problem
         for (int i = 0; i < 4; ++i) {
           const int rl = 16 * qb + 4 * g4 + i;
           float p = fast_exp2(sc[qb][i] * c - sl[2 * rl]);
-          if (diag && ((rl + lim < 0) | (DS && !key_valid))) p = 0.f;
+          if (diag && rl + lim < 0) p = 0.f;
           pv[4 * qb + i] = p;
           dsv[4 * qb + i] = p * (dp[qb][i] - sl[2 * rl + 1]);
         }
@@ -744,8 +770,10 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_split_kernel(ts_attn_problem
     nxt = advance(nxt);
   };
 
-  Cursor cur{0, first_visit()};
+  Cursor cur{0, first_visit(), ds_sink};
   if (cur.v.vi >= run.nvisit) cur.g = group;  // a run nobody reads
+  if constexpr (DS)
+    if (cur.g < group) cur.at = locate(cur);
   Cursor nxt = cur.g < group ? advance(cur) : cur;
   issue(cur, s_b0);
   while (cur.g < group) {
@@ -754,7 +782,7 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_split_kernel(ts_attn_problem
     step(std::integral_constant<int, 1>{}, cur, nxt);
   }
   if constexpr (DS)
-    if (pend_live) global_st16(pend_at, as_u32x4(pend));
+    global_st16(pend_at, as_u32x4(pend));
   __builtin_amdgcn_s_waitcnt(0);  // the last (empty) DMA has landed before the waves exit
   if (!key_valid) return;
   // lane (g4, j16) holds d = 16 mb + 4 g4 .. + 3 of key mykey: 8-byte stores

@@ -230,7 +230,6 @@ struct VisitCursor {
   int off;         // its kv_len - q_len
   int kpos;        // position of the run's first key in the segment's key order
   int64_t q_row0;  // its first row in the packed Q / dO / statistics
-  int dsb;         // dS route: index, within a head, of row block r0 / 32's first dS block
 };
 
 // ---------------------------------------------------------------------------
@@ -272,7 +271,6 @@ struct DsRect {
   int q_len;
 };
 
-__host__ __device__ inline int64_t floor_div(int64_t a, int64_t b) { return a >= 0 ? a / b : -((-a + b - 1) / b); }
 __host__ __device__ inline int64_t imin64(int64_t a, int64_t b) { return a < b ? a : b; }
 __host__ __device__ inline int64_t imax64(int64_t a, int64_t b) { return a > b ? a : b; }
 
@@ -287,11 +285,12 @@ __host__ __device__ inline int ds_blocks_in(const DsRect& R, int rb) {
 // blocks stored before row block rb (rb below the last row block + 1): the
 // earlier row blocks are whole (32 rows below q_len), row block t holding
 // clamp(2 t + c, 0, nkb) blocks with c = floor((d + 31) / 16) + 1; summed in
-// closed form over the zero, linear and saturated stretches of t
+// closed form over the zero, linear and saturated stretches of t.  Floor
+// divisions by powers of two are arithmetic shifts (no branches).
 __host__ __device__ inline int64_t ds_blocks_before(const DsRect& R, int rb) {
-  const int64_t c = floor_div((int64_t)R.d + 31, 16) + 1, n = R.nkb;
-  const int64_t t0 = imax64(0, floor_div(-c, 2) + 1);  // first t with 2 t + c > 0
-  const int64_t t1 = imax64(0, -floor_div(c - n, 2));  // first t with 2 t + c >= n
+  const int64_t c = (((int64_t)R.d + 31) >> 4) + 1, n = R.nkb;
+  const int64_t t0 = imax64(0, ((-c) >> 1) + 1);  // first t with 2 t + c > 0
+  const int64_t t1 = imax64(0, -((c - n) >> 1));  // first t with 2 t + c >= n
   const int64_t b = imin64(rb, t1), a = imin64(t0, b);
   return (b - a) * (a + b - 1 + c) + n * imax64(0, rb - t1);
 }
