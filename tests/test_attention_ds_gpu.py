@@ -1,7 +1,8 @@
 """The attention backward's two routes against the CPU oracle.
 
-At head dim 256 the backward takes the dS route by default: the dK/dV kernel
-stores dS and the dQ kernel forms dQ = dS K from it.
+At head dim 256, and at head dim 128 with GQA groups that are a multiple of
+4, the backward takes the dS route by default: the dK/dV kernel stores dS and
+the dQ kernel forms dQ = dS K from it.
 ``THUNDERSYNC_ATTN_DS=off`` (or a problem whose workspace exceeds
 ``attention.DS_MAX_BYTES``) selects the route whose dQ kernel recomputes S and
 dP.  Both are checked against the fp32 oracle at the attention tests' bar
@@ -58,11 +59,12 @@ def run_both(monkeypatch, cuda, q, ks, vs, dout, layout, scale):
 
 CHAINS = [
     # head dim, query rows, chunk lengths, hq, hkv
-    (128, 130, [7, 64, 130], 32, 8),     # group 4
+    (128, 130, [7, 64, 130], 32, 8),     # group 4: one-wave-per-head dK/dV storing dS
     (128, 200, [300, 17, 200], 40, 8),   # group 5: key-split dK/dV, dQ 1 head x 4 row blocks
     (128, 77, [120, 77], 16, 8),         # group 2
     (128, 33, [80, 33], 4, 4),           # group 1
     (128, 1, [9], 4, 1),                 # one row
+    (128, 64, [300, 17, 64], 8, 2),      # group 4, a run past row 0's keys
     (128, 40, [100, 23, 45], 6, 2),
     (256, 150, [300, 150], 24, 4),       # the reference's FA4 test heads
     (256, 64, [64], 8, 2),

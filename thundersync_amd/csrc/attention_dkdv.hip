@@ -176,11 +176,11 @@ __global__ __launch_bounds__(kThreads, HD > 128 ? 1 : 2) void dkdv_kernel(ts_att
 // enters the next visit.  The per-head partials are summed across waves
 // through LDS in wave order.
 // ---------------------------------------------------------------------------
-template <typename E, int KB>
+template <typename E, int KB, bool DS = false>
 __global__ __launch_bounds__(kThreads, 1) void dkdv_wave_kernel(ts_attn_problem P, ts_attn_rows Q,
                                                                 ts_attn_rows dO,
                                                                 const float* __restrict__ rowstats,
-                                                                int64_t lse_ld) {
+                                                                int64_t lse_ld, DsArgs S) {
   // per wave and stage: Q tile, dO tile, then 32 (lse2, delta) pairs
   __shared__ __attribute__((aligned(16))) bf16 s_b0[4][kStage32];
   __shared__ __attribute__((aligned(16))) bf16 s_b1[4][kStage32];
@@ -196,6 +196,15 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_wave_kernel(ts_attn_problem 
   constexpr int NK = 16 * KB;  // keys per work-group
   const int nkeys = min(NK, run.len - k0);
   const float c = P.scale * kLog2e;
+  const int nkb = (run.len + 15) >> 4;  // 16-key blocks of the run
+  // dS route: this lane's element of key block k0 / 16 in head 0's part, and
+  // the sink block; kept in VGPRs (derived from an opaque zero), like the
+  // key-split kernel's
+  int vzero;
+  asm volatile("v_mov_b32 %0, 0" : "=v"(vzero));
+  const int64_t ds_head = DS ? S.head + vzero : 0;
+  bf16* const ds_base = DS ? (bf16*)S.ptr + (vzero + ds_store_offset(lane) / 2) : nullptr;
+  bf16* const ds_lane = ds_base + (int64_t)(k0 >> 4) * kDsBlock;
 
   // per-lane LDS offsets (elements)
   int ro[4], to[8], dchunk[4];
@@ -269,6 +278,36 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_wave_kernel(ts_attn_problem 
     if (run.nvisit > 0) enter(c);
     return settle(c);
   };
+  // dS route: this lane's element of block k0 / 16 of c's row block in head
+  // h's part (c on a visit)
+  auto locate = [&](const VisitCursor& c, int h) -> bf16* {
+    // consumed here, so that no scalar load is outstanding when the next
+    // step's LDS reads count their completions
+    const int64_t blk = load_uniform(S.visit, run.visit0 + c.vi) / kDsBlock +
+                        ds_blocks_before(DsRect{c.off - c.kpos, nkb, c.q_len}, c.r0 >> 5);
+    asm volatile("" ::"s"(blk));
+    return ds_lane + (int64_t)h * ds_head + blk * kDsBlock;
+  };
+  // the block after c (settled: past its visit's rows, the next visit's
+  // first); dS route: `at` follows it, advanced by c's row block's block
+  // count within a visit, located afresh on entering the next
+  auto next_block = [&](VisitCursor c, bf16*& at, int h) -> VisitCursor {
+    int inc = 0;
+    if constexpr (DS) {
+      const int last = c.off - c.kpos + min(c.r0 + 31, c.q_len - 1);
+      inc = last < 0 ? 0 : min(nkb, (last >> 4) + 1);
+    }
+    const int vi0 = c.vi;
+    c.r0 += 32;
+    if (c.r0 >= c.q_len) c = settle(c);  // tables are read only here
+    if constexpr (DS) {
+      if (c.vi == vi0)
+        at += (int64_t)inc * kDsBlock;
+      else if (c.vi < run.nvisit)
+        at = locate(c, h);
+    }
+    return c;
+  };
   // DMA of block `cur` (nothing, as zero-size buffer resources, when it is
   // past the run's last visit)
   auto issue = [&](const VisitCursor& cur, int h, bf16* buf) {
@@ -298,7 +337,7 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_wave_kernel(ts_attn_problem 
   // `nxt` is the block after `cur`, already settled: the step's body up to the
   // cursor update is branch-free, so the next block's DMA set-up interleaves
   // with the MFMAs
-  auto step = [&](auto bsel, VisitCursor& cur, VisitCursor& nxt, int h) {
+  auto step = [&](auto bsel, VisitCursor& cur, VisitCursor& nxt, int h, bf16*& cur_at, bf16*& nxt_at) {
       const int off = cur.off, r0 = cur.r0, kpos = cur.kpos;
       __builtin_amdgcn_s_waitcnt(0);  // this block's tiles have landed
       // static buffer roles: the LDS reads below and the prefetch into the other
@@ -355,10 +394,14 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_wave_kernel(ts_attn_problem 
         }
       // P and dS as B operands: slot j = 4 qb + i  <->  row 16 qb + 4 g4 + i
       bf16x8 pk[KB], dsk[KB];
-      if (kpos + k0 + NK - 1 > off + r0) {  // the block crosses the diagonal
+      // the block crosses the diagonal (or, when dS is stored, the run's end:
+      // P of a key past it, whose K row is zero, is exp2(-lse2), not 0)
+      if ((kpos + k0 + NK - 1 > off + r0) | (DS && nkeys < NK)) {
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) {
-          const int lim = off + r0 - kpos - (k0 + 16 * kb + j16);  // row rl sees the key iff rl >= -lim
+          // row rl sees the key iff rl >= -lim; dS route: a key past the run
+          // is put past every row (2^24 rows)
+          const int lim = off + r0 - kpos - (k0 + 16 * kb + j16) - (DS && 16 * kb + j16 >= nkeys ? (1 << 24) : 0);
           float pv[8], dsv[8];
 #pragma unroll
           for (int qb = 0; qb < 2; ++qb)
@@ -387,6 +430,15 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_wave_kernel(ts_attn_problem 
           pk[kb] = pack8<E>(pv);
           dsk[kb] = pack8<E>(dsv);
         }
+      }
+      if constexpr (DS) {
+        // this step's dS blocks (key blocks k0 / 16 + kb of row block r0 / 32)
+        // that the rectangle holds
+        const int last = off - kpos + min(r0 + 31, cur.q_len - 1);
+        const int nb = (last < 0 ? 0 : min(nkb, (last >> 4) + 1)) - (k0 >> 4);
+#pragma unroll
+        for (int kb = 0; kb < KB; ++kb)
+          if (kb < nb) global_st16(cur_at + kb * kDsBlock, as_u32x4(dsk[kb]));
       }
       // dV^T += dO^T P, dK^T += Q^T dS: rows d = 16 mb + 4 g4 + i, column key;
       // the dO^T / Q^T fragments of block mb + 2 are read while block mb's
@@ -418,22 +470,24 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_wave_kernel(ts_attn_problem 
         if (mb + 2 < 8) __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
       }
       cur = nxt;
-      nxt.r0 += 32;
-      if (nxt.r0 >= nxt.q_len) nxt = settle(nxt);  // tables are read only here
+      if constexpr (DS) cur_at = nxt_at;
+      nxt = next_block(nxt, nxt_at, h);
   };
 
   for (int g = wave; g < group; g += 4) {
     const int h = hk * group + g;
     VisitCursor cur = first();
-    VisitCursor nxt = cur;
-    nxt.r0 += 32;
-    nxt = settle(nxt);
+    bf16* cur_at = ds_lane;
+    if constexpr (DS)
+      if (cur.vi < run.nvisit) cur_at = locate(cur, h);
+    bf16* nxt_at = cur_at;
+    VisitCursor nxt = next_block(cur, nxt_at, h);
     __builtin_amdgcn_s_waitcnt(0);  // the previous head's last (empty) DMA has landed
     if (cur.vi < run.nvisit) issue(cur, h, s_b0[wave]);
     while (cur.vi < run.nvisit) {
-      step(std::integral_constant<int, 0>{}, cur, nxt, h);
+      step(std::integral_constant<int, 0>{}, cur, nxt, h, cur_at, nxt_at);
       if (cur.vi >= run.nvisit) break;
-      step(std::integral_constant<int, 1>{}, cur, nxt, h);
+      step(std::integral_constant<int, 1>{}, cur, nxt, h, cur_at, nxt_at);
     }
   }
 
@@ -816,7 +870,7 @@ void launch_dkdv_tuned(dim3 grid, const ts_attn_problem& P, ts_attn_rows q, ts_a
   if (P.head_dim == 256)
     hipLaunchKernelGGL((dkdv_split_kernel<E, 256, DS>), grid, dim3(kThreads), 0, s, P, q, dout, rowstats, lse_ld, S);
   else if (group % 4 == 0)
-    hipLaunchKernelGGL((dkdv_wave_kernel<E, 3>), grid, dim3(kThreads), 0, s, P, q, dout, rowstats, lse_ld);
+    hipLaunchKernelGGL((dkdv_wave_kernel<E, 3, DS>), grid, dim3(kThreads), 0, s, P, q, dout, rowstats, lse_ld, S);
   else  // the dS route is head dim 256 only
     hipLaunchKernelGGL((dkdv_split_kernel<E, D>), grid, dim3(kThreads), 0, s, P, q, dout, rowstats, lse_ld, S);
 }

@@ -1,5 +1,5 @@
 // Attention backward, dS route: dQ = scale * dS K from the dS blocks the
-// dK/dV kernel stored (head dim 256; the kernel is written for 128 too).
+// dK/dV kernel stored (head dims 256, and 128 with groups of 4).
 //
 // A work-group owns the work item's 128 / GC query rows of one segment for GC
 // query heads of one GQA group: wave w takes head w % GC and the 32-row block
@@ -102,7 +102,7 @@ __global__ __launch_bounds__(kThreads, HD > 128 ? 1 : 2) void dq_ds_kernel(ts_at
     const u32x4 rd = raw_descriptor((const E*)S.ptr + ds_at + (int64_t)kb0 * kDsBlock, (uint32_t)(nb * kDsBlock * 2));
     bf16* dbuf = buf + KTILE + wave * DTILE;
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) buffer_dma16_untracked(rd, dbuf + kk * kDsBlock, kk * kDsBlock * 2 + lane * 16);
+    for (int kk = 0; kk < 4; ++kk) buffer_dma16_untracked_nt(rd, dbuf + kk * kDsBlock, kk * kDsBlock * 2 + lane * 16);
   };
 
   f32x4 acc[NMB][2];
@@ -201,7 +201,10 @@ void launch_dq_ds_t(const ts_attn_problem& P, const DsArgs& S, ts_attn_rows dq, 
   const int group = P.hq / P.hkv;
   const int gc = heads_per_block(group);
   const dim3 grid((unsigned)(P.n_q_work * P.hkv * (group / gc)));
-  launch_dq_ds_hd<E, 256>(P, gc, grid, S, dq, s);  // the dS route is head dim 256 only
+  if (P.head_dim == 256)
+    launch_dq_ds_hd<E, 256>(P, gc, grid, S, dq, s);
+  else
+    launch_dq_ds_hd<E, 128>(P, gc, grid, S, dq, s);
 }
 
 int launch_dq_ds(const ts_attn_problem& P, const DsArgs& S, ts_attn_rows dq, hipStream_t s) {

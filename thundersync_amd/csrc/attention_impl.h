@@ -303,9 +303,11 @@ __host__ __device__ inline int64_t ds_rect_blocks(const DsRect& R) {
 
 // 16 bytes to global memory through a global-address-space pointer: a
 // global store (a generic pointer makes it a FLAT store, which also counts
-// on the LDS counter and so turns every later LDS wait into a full drain)
+// on the LDS counter and so turns every later LDS wait into a full drain),
+// non-temporal (the dS stream is read back once, by another kernel: its
+// lines should not displace the Q/dO and K/V lines the kernels reuse)
 __device__ __forceinline__ void global_st16(bf16* p, u32x4 v) {
-  *(__attribute__((address_space(1))) u32x4*)(p) = v;
+  __builtin_nontemporal_store(v, (__attribute__((address_space(1))) u32x4*)(p));
 }
 
 // byte offset of lane (g4, j16)'s 16-byte store of its dS slots in a block
@@ -480,12 +482,14 @@ int launch_dkdv(const ts_attn_problem& P, ts_attn_rows q, ts_attn_rows dout, con
 // dQ = scale dS K from the workspace the dK/dV launch filled
 int launch_dq_ds(const ts_attn_problem& P, const DsArgs& ds, ts_attn_rows dq, hipStream_t s);
 
-// the dS route: head dim 256.  At head dim 128 the one-wave-per-head dK/dV
-// kernel (groups that are a multiple of 4) has no registers left for the
-// stores, and in the key-split kernel the stores' bookkeeping costs its step
-// more than the dQ kernel saves (a dK/dV step is half as long as at 256 for
-// the same dS bytes).
-inline bool ds_route(int head_dim, int /*group*/) { return head_dim == 256; }
+// the dS route: head dim 256, and head dim 128 with groups that are a
+// multiple of 4 (the one-wave-per-head dK/dV kernel).  Not in the key-split
+// kernel at head dim 128 (other groups): a step there is half as long as at
+// 256 for the same dS bytes, and the stores cost it more than the dQ kernel
+// saves.
+inline bool ds_route(int head_dim, int group) {
+  return head_dim == 256 || (head_dim == 128 && group % 4 == 0);
+}
 
 }  // namespace attn
 }  // namespace ts

@@ -226,6 +226,15 @@ __device__ __forceinline__ void buffer_dma16_untracked(u32x4 desc, void* lds, in
                : "memory", "m0");
 }
 
+// buffer_dma16_untracked with the non-temporal hint: for a stream read once
+__device__ __forceinline__ void buffer_dma16_untracked_nt(u32x4 desc, void* lds, int voffset) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void*)lds);
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, 0 offen nt lds"
+               :
+               : "s"(m0), "v"(voffset), "s"(desc)
+               : "memory", "m0");
+}
+
 // ---------------------------------------------------------------------------
 // wave reductions over lanes that differ in the given xor masks
 // ---------------------------------------------------------------------------
