@@ -3,9 +3,10 @@
 At head dim 256, and at head dim 128 with GQA groups that are a multiple of
 4, the backward takes the dS route by default: the dK/dV kernel stores dS and
 the dQ kernel forms dQ = dS K from it.
-``THUNDERSYNC_ATTN_DS=off`` (or a problem whose workspace exceeds
-``attention.DS_MAX_BYTES``) selects the route whose dQ kernel recomputes S and
-dP.  Both are checked against the fp32 oracle at the attention tests' bar
+``THUNDERSYNC_ATTN_DS=off`` (or a problem whose single KV head's workspace
+exceeds ``attention.DS_MAX_BYTES``) selects the route whose dQ kernel
+recomputes S and dP; a problem whose whole workspace exceeds the cap runs the
+dS route over groups of KV heads.  Both are checked against the fp32 oracle at the attention tests' bar
 (2e-2 max-abs, scaled by max|ref| above 1) over GQA groups of 4, 5, 2, 1 and 6,
 ragged lengths (query rows not a multiple of 32, runs not a multiple of 16,
 runs before, across and after the diagonal), fp16 and a forest; dK/dV are
@@ -158,8 +159,44 @@ def test_workspace_cap_selects_the_recompute_route(monkeypatch, cuda):
     lib = _lib.require_library()
     monkeypatch.setenv(hip.DS_ENV, "auto")
     assert hip._ds_route(lay, q, lib) is not None
-    monkeypatch.setattr(hip, "DS_MAX_BYTES", 1024)
+    monkeypatch.setattr(hip, "DS_MAX_BYTES", 1024)  # not even one KV head's dS
     assert hip._ds_route(lay, q, lib) is None
+    monkeypatch.setenv(hip.DS_ENV, "off")
+    monkeypatch.setattr(hip, "DS_MAX_BYTES", 16 << 30)
+    assert hip._ds_route(lay, q, lib) is None
+    monkeypatch.setenv(hip.DS_ENV, "auto")
     monkeypatch.setattr(hip, "DS_MAX_BYTES", 16 << 30)
     assert hip._ds_route(lay, q[..., :128].contiguous(), lib) is None  # head dim 128: recompute route
     assert hip._ds_route(lay, q[..., :64].contiguous(), lib) is None  # head dim 64: no dS kernels
+
+
+@pytest.mark.parametrize("d,t,chunks,hq,hkv", [(128, 200, [300, 17, 200], 32, 8), (256, 150, [300, 150], 24, 4)])
+def test_kv_head_groups_match_one_call(monkeypatch, cuda, d, t, chunks, hq, hkv):
+    """A workspace cap that holds two KV heads' dS runs the route in calls over
+    two KV heads at a time; every gradient equals the one-call route's bit for
+    bit (the heads are independent and each sees the same kernels)."""
+    print(f"kv-head groups d={d} t={t} chunks={chunks} hq={hq} hkv={hkv}", flush=True)
+    g = torch.Generator().manual_seed(31 + d)
+    q = torch.randn(t, hq, d, generator=g).bfloat16()
+    ks = [torch.randn(n, hkv, d, generator=g).bfloat16() for n in chunks]
+    vs = [torch.randn(n, hkv, d, generator=g).bfloat16() for n in chunks]
+    dout = torch.randn(t, hq, d, generator=g).bfloat16()
+    layout = hip.chain_layout(t, chunks, hq, hkv)
+    lib = _lib.require_library()
+    monkeypatch.setenv(hip.DS_ENV, "auto")
+    results = []
+    for cap in (None, (2 * (hq // hkv) * layout.ds_tables(cuda)["head"] + 512) * 2):
+        if cap is not None:
+            monkeypatch.setattr(hip, "DS_MAX_BYTES", cap)
+        qc = q.to(cuda).requires_grad_()
+        kc = [k.to(cuda).requires_grad_() for k in ks]
+        vc = [v.to(cuda).requires_grad_() for v in vs]
+        assert hip._ds_route(layout, qc, lib)[1] == (hkv if cap is None else 2)
+        out, _ = hip.attention(qc, layout, kc, vc, d ** -0.5)
+        out.backward(dout.to(cuda))
+        torch.cuda.synchronize()
+        results.append((qc.grad, [k.grad for k in kc], [v.grad for v in vc]))
+    (dq1, dk1, dv1), (dq2, dk2, dv2) = results
+    assert torch.equal(dq1, dq2)
+    for i in range(len(chunks)):
+        assert torch.equal(dk1[i], dk2[i]) and torch.equal(dv1[i], dv2[i])

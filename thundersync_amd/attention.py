@@ -429,23 +429,47 @@ def _validate_call(layout: AttnLayout, query: torch.Tensor, keys, values) -> Non
 
 # Largest dS workspace (bytes) the backward allocates for the dS route (dK/dV
 # kernels store dS, dQ = dS K from it; about 2 bytes per visible pair and
-# head); a problem above it, or with THUNDERSYNC_ATTN_DS=off, runs the route
-# that recomputes S and dP in the dQ kernel.
+# head).  A problem above it runs the route over groups of KV heads, as many
+# per call as fit (KV heads are independent: their query heads, dS and
+# gradients do not mix); one whose single KV head does not fit, or any under
+# THUNDERSYNC_ATTN_DS=off, runs the route that recomputes S and dP in the dQ
+# kernel.
 DS_MAX_BYTES = 16 << 30
 DS_ENV = "THUNDERSYNC_ATTN_DS"
 
 
 def _ds_route(layout: AttnLayout, query: torch.Tensor, lib):
-    """(workspace tables, bytes) when this backward takes the dS route, else None."""
+    """(workspace tables, KV heads per call) when this backward takes the dS
+    route, else None."""
     if os.environ.get(DS_ENV, "auto").strip().lower() == "off" or DS_MAX_BYTES <= 0:
         return None
-    if not lib.ts_attn_ds_route(query.shape[2], layout.hq // layout.hkv):
+    group = layout.hq // layout.hkv
+    if not lib.ts_attn_ds_route(query.shape[2], group):
         return None
     tabs = layout.ds_tables(query.device)
-    nbytes = (layout.hq * tabs["head"] + 512) * 2  # every head's part, then the sink block
-    if nbytes > DS_MAX_BYTES:
+    # a call over n KV heads needs (n * group * head + 512) elements: every
+    # query head's part, then the sink block
+    per_kv_head = group * max(tabs["head"], 1)
+    kv_heads = min(layout.hkv, (DS_MAX_BYTES // 2 - 512) // per_kv_head)
+    if kv_heads < 1:
         return None
-    return tabs, nbytes
+    return tabs, kv_heads
+
+
+def _head_rows(rows: AttnRows, first_head: int) -> AttnRows:
+    """A rows view that starts at head `first_head` (2-byte elements)."""
+    return AttnRows(rows.ptr + first_head * rows.head_stride * 2, rows.row_stride, rows.head_stride)
+
+
+def _head_runs(host: torch.Tensor, first_kv_head: int, device) -> tuple[torch.Tensor, torch.Tensor]:
+    """A copy of a run table whose K/V/dK/dV addresses start at KV head `first_kv_head`."""
+    table = host.numpy().view(RUN_DTYPE).copy()
+    for name in ("k", "v", "dk", "dv"):
+        live = table[name] != 0
+        table[name][live] += (first_kv_head * table[f"{name}_head_stride"][live] * 2).astype(np.uint64)
+    sub = torch.from_numpy(table.view(np.uint8)).pin_memory() if device.type == "cuda" else torch.from_numpy(
+        table.view(np.uint8))
+    return sub.to(device, non_blocking=True), sub
 
 
 class _Attention(torch.autograd.Function):
@@ -513,15 +537,29 @@ class _Attention(torch.autograd.Function):
                     f"ts_attn_bwd(rows={layout.q_rows}, hq={layout.hq}, hkv={layout.hkv})",
                 )
             else:
-                tabs, nbytes = ds
-                work = torch.empty(nbytes // 2, dtype=query.dtype, device=query.device)
-                _lib.check(
-                    lib.ts_attn_bwd_ds(ctypes.byref(problem), _rows(query), _rows(out), _rows(dout),
-                                       lse.data_ptr(), lse.shape[1], rowstats.data_ptr(), _rows(dq),
-                                       tabs["span"], tabs["visit"], tabs["head"], work.data_ptr(),
-                                       work.numel() * 2, _lib.stream_of(query)),
-                    f"ts_attn_bwd_ds(rows={layout.q_rows}, hq={layout.hq}, hkv={layout.hkv})",
-                )
+                tabs, kv_heads = ds
+                group = layout.hq // layout.hkv
+                work = torch.empty(kv_heads * group * tabs["head"] + 512, dtype=query.dtype, device=query.device)
+                rows = [_rows(t) for t in (query, out, dout, dq)]
+                keep = []
+                for hk0 in range(0, layout.hkv, kv_heads):
+                    n, h0 = min(kv_heads, layout.hkv - hk0), hk0 * group
+                    sub = problem
+                    if n != layout.hkv:  # KV heads hk0 .. hk0 + n - 1 and their query heads
+                        sub_runs, sub_host = _head_runs(host, hk0, query.device)
+                        keep.append((sub_runs, sub_host))
+                        sub = AttnProblem.from_buffer_copy(problem)
+                        sub.hq, sub.hkv, sub.runs = n * group, n, sub_runs.data_ptr()
+                        check_tables(layout, sub, sub_host, query.device)
+                    q_r, o_r, do_r, dq_r = (_head_rows(r, h0) for r in rows)
+                    _lib.check(
+                        lib.ts_attn_bwd_ds(ctypes.byref(sub), q_r, o_r, do_r, lse.data_ptr() + h0 * lse.shape[1] * 4,
+                                           lse.shape[1], rowstats.data_ptr() + h0 * lse.shape[1] * 8, dq_r,
+                                           tabs["span"], tabs["visit"], tabs["head"], work.data_ptr(),
+                                           work.numel() * 2, _lib.stream_of(query)),
+                        f"ts_attn_bwd_ds(rows={layout.q_rows}, hq={layout.hq}, hkv={layout.hkv}, heads from {h0})",
+                    )
+                ctx.keep_bwd_heads = keep
                 del work
         count_attention_path(HIP_BACKWARD_PATH)
         ctx.keep_bwd = (runs, host)
