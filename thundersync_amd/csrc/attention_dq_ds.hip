@@ -41,6 +41,13 @@ __device__ __forceinline__ void issue_k_tile(int hk, int wave, int lane, const T
   }
 }
 
+// wait until at most N vector-memory instructions of this wave are outstanding
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  __builtin_amdgcn_s_waitcnt(0x0f70 | (N & 15) | ((N >> 4) << 14));
+}
+
 template <typename E, int HD, int GC>
 __global__ __launch_bounds__(kThreads, HD > 128 ? 1 : 2) void dq_ds_kernel(ts_attn_problem P, DsArgs S,
                                                                            ts_attn_rows dQ) {
@@ -155,8 +162,13 @@ __global__ __launch_bounds__(kThreads, HD > 128 ? 1 : 2) void dq_ds_kernel(ts_at
     }
   }
   for (int i = 0; i < issued; ++i) {
-    if (NST > 2 && issued - i > 1)
-      __builtin_amdgcn_s_waitcnt(0x0f70 | ((PER_TILE * (NST - 2)) & 15) | (((PER_TILE * (NST - 2)) >> 4) << 14));
+    // tile i has landed once at most the instructions of the tiles issued
+    // after it are outstanding (they complete in issue order)
+    const int ahead = issued - 1 - i;
+    if (NST > 3 && ahead >= 2)
+      wait_vmcnt<2 * PER_TILE>();
+    else if (NST > 2 && ahead >= 1)
+      wait_vmcnt<PER_TILE>();
     else
       __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();  // tile i is in every stage; stage (i - 1) % NST is free
