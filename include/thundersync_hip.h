@@ -249,10 +249,9 @@ int ts_attn_bwd(const ts_attn_problem* problem, ts_attn_rows q, ts_attn_rows out
  * 2 bytes per pair and head.  Same results contract as ts_attn_bwd
  * (deterministic, no atomics).
  *
- * ts_attn_ds_route(head_dim, group): 1 where the route exists (head dim
- * 256 with every GQA group size hq / hkv; head dim 128 with groups that are
- * a multiple of 4); elsewhere ts_attn_bwd_ds runs ts_attn_bwd's kernels and
- * leaves the workspace untouched.
+ * ts_attn_ds_route(head_dim, group): 1 where the route exists (head dims
+ * 128 and 256, every GQA group size hq / hkv); elsewhere ts_attn_bwd_ds runs
+ * ts_attn_bwd's kernels and leaves the workspace untouched.
  *
  * ts_attn_ds_layout: the workspace layout of a set of tables (host copies;
  * run_len, visit0 and nvisit are the runs' len / visit0 / nvisit fields):

@@ -1,8 +1,7 @@
 """The attention backward's two routes against the CPU oracle.
 
-At head dim 256, and at head dim 128 with GQA groups that are a multiple of
-4, the backward takes the dS route by default: the dK/dV kernel stores dS and
-the dQ kernel forms dQ = dS K from it.
+At head dims 128 and 256 the backward takes the dS route by default: the
+dK/dV kernel stores dS and the dQ kernel forms dQ = dS K from it.
 ``THUNDERSYNC_ATTN_DS=off`` (or a problem whose single KV head's workspace
 exceeds ``attention.DS_MAX_BYTES``) selects the route whose dQ kernel
 recomputes S and dP; a problem whose whole workspace exceeds the cap runs the
@@ -166,7 +165,7 @@ def test_workspace_cap_selects_the_recompute_route(monkeypatch, cuda):
     assert hip._ds_route(lay, q, lib) is None
     monkeypatch.setenv(hip.DS_ENV, "auto")
     monkeypatch.setattr(hip, "DS_MAX_BYTES", 16 << 30)
-    assert hip._ds_route(lay, q[..., :128].contiguous(), lib) is None  # head dim 128: recompute route
+    assert hip._ds_route(lay, q[..., :128].contiguous(), lib) is not None  # head dim 128, group 3
     assert hip._ds_route(lay, q[..., :64].contiguous(), lib) is None  # head dim 64: no dS kernels
 
 

@@ -871,8 +871,8 @@ void launch_dkdv_tuned(dim3 grid, const ts_attn_problem& P, ts_attn_rows q, ts_a
     hipLaunchKernelGGL((dkdv_split_kernel<E, 256, DS>), grid, dim3(kThreads), 0, s, P, q, dout, rowstats, lse_ld, S);
   else if (group % 4 == 0)
     hipLaunchKernelGGL((dkdv_wave_kernel<E, 3, DS>), grid, dim3(kThreads), 0, s, P, q, dout, rowstats, lse_ld, S);
-  else  // the dS route is head dim 256 only
-    hipLaunchKernelGGL((dkdv_split_kernel<E, D>), grid, dim3(kThreads), 0, s, P, q, dout, rowstats, lse_ld, S);
+  else
+    hipLaunchKernelGGL((dkdv_split_kernel<E, D, DS>), grid, dim3(kThreads), 0, s, P, q, dout, rowstats, lse_ld, S);
 }
 
 template <typename E>

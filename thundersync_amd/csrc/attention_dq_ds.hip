@@ -1,5 +1,5 @@
 // Attention backward, dS route: dQ = scale * dS K from the dS blocks the
-// dK/dV kernel stored (head dims 256, and 128 with groups of 4).
+// dK/dV kernel stored (head dims 128 and 256).
 //
 // A work-group owns the work item's 128 / GC query rows of one segment for GC
 // query heads of one GQA group: wave w takes head w % GC and the 32-row block

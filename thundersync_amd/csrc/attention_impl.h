@@ -482,14 +482,9 @@ int launch_dkdv(const ts_attn_problem& P, ts_attn_rows q, ts_attn_rows dout, con
 // dQ = scale dS K from the workspace the dK/dV launch filled
 int launch_dq_ds(const ts_attn_problem& P, const DsArgs& ds, ts_attn_rows dq, hipStream_t s);
 
-// the dS route: head dim 256, and head dim 128 with groups that are a
-// multiple of 4 (the one-wave-per-head dK/dV kernel).  Not in the key-split
-// kernel at head dim 128 (other groups): a step there is half as long as at
-// 256 for the same dS bytes, and the stores cost it more than the dQ kernel
-// saves.
-inline bool ds_route(int head_dim, int group) {
-  return head_dim == 256 || (head_dim == 128 && group % 4 == 0);
-}
+// the dS route: head dims 128 and 256 (the DMA-staged dK/dV kernels), every
+// GQA group size
+inline bool ds_route(int head_dim, int /*group*/) { return head_dim == 128 || head_dim == 256; }
 
 }  // namespace attn
 }  // namespace ts
