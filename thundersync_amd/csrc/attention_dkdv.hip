@@ -174,7 +174,9 @@ __global__ __launch_bounds__(kThreads, HD > 128 ? 1 : 2) void dkdv_kernel(ts_att
 // score MFMAs, so its scalar set-up interleaves with them, and the visit
 // cursor caches its segment's fields, so a step reads no table unless it
 // enters the next visit.  The per-head partials are summed across waves
-// through LDS in wave order.
+// through LDS in wave order.  On the dS route (DS) a step stores its dS
+// blocks right after computing them (the kernel has no registers for a
+// deferred copy), through a per-lane pointer that follows the visit cursor.
 // ---------------------------------------------------------------------------
 template <typename E, int KB, bool DS = false>
 __global__ __launch_bounds__(kThreads, 1) void dkdv_wave_kernel(ts_attn_problem P, ts_attn_rows Q,
@@ -197,8 +199,8 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_wave_kernel(ts_attn_problem 
   const int nkeys = min(NK, run.len - k0);
   const float c = P.scale * kLog2e;
   const int nkb = (run.len + 15) >> 4;  // 16-key blocks of the run
-  // dS route: this lane's element of key block k0 / 16 in head 0's part, and
-  // the sink block; kept in VGPRs (derived from an opaque zero), like the
+  // dS route: this lane's element of key block k0 / 16 in head 0's part;
+  // the bookkeeping is kept in VGPRs (derived from an opaque zero), like the
   // key-split kernel's
   int vzero;
   asm volatile("v_mov_b32 %0, 0" : "=v"(vzero));
