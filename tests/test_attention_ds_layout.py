@@ -142,3 +142,28 @@ def test_refuses_a_visit_that_is_no_span():
     visits[0]["kpos"] = 3
     st, *_ = ds_layout(segs, spans, run_len, visits, visit0, nvisit)
     assert st != _lib.TS_OK and "not a span" in _lib.require_library().ts_hip_last_error().decode()
+
+
+def test_route_groups_kv_heads_under_the_cap(monkeypatch):
+    """The backward's route choice (host side): every KV head per call when
+    the whole workspace fits the cap, else as many as fit, else the
+    recompute route; head dims without dS kernels and the off switch take
+    the recompute route."""
+    lib = _lib.require_library()
+    lay = att.chain_layout(150, [300, 150], 24, 4)
+    head = lay.ds_tables(CPU)["head"]
+    q = torch.zeros(150, 24, 256, dtype=torch.bfloat16)
+    monkeypatch.setenv(att.DS_ENV, "auto")
+    monkeypatch.setattr(att, "DS_MAX_BYTES", (24 * head + 512) * 2)
+    assert att._ds_route(lay, q, lib)[1] == 4
+    monkeypatch.setattr(att, "DS_MAX_BYTES", (24 * head + 512) * 2 - 2)
+    assert att._ds_route(lay, q, lib)[1] == 3
+    monkeypatch.setattr(att, "DS_MAX_BYTES", (6 * head + 512) * 2)
+    assert att._ds_route(lay, q, lib)[1] == 1
+    monkeypatch.setattr(att, "DS_MAX_BYTES", (6 * head + 512) * 2 - 2)
+    assert att._ds_route(lay, q, lib) is None
+    monkeypatch.setattr(att, "DS_MAX_BYTES", 16 << 30)
+    assert att._ds_route(lay, q[..., :128], lib)[1] == 4
+    assert att._ds_route(lay, q[..., :64], lib) is None
+    monkeypatch.setenv(att.DS_ENV, "off")
+    assert att._ds_route(lay, q, lib) is None
