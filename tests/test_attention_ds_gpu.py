@@ -157,6 +157,7 @@ def test_workspace_cap_selects_the_recompute_route(monkeypatch, cuda):
     q = torch.randn(64, 6, 256, device=cuda, dtype=torch.bfloat16)
     lib = _lib.require_library()
     monkeypatch.setenv(hip.DS_ENV, "auto")
+    monkeypatch.setattr(hip, "DS_FREE_FRACTION", 0.0)  # the cap alone decides
     assert hip._ds_route(lay, q, lib) is not None
     monkeypatch.setattr(hip, "DS_MAX_BYTES", 1024)  # not even one KV head's dS
     assert hip._ds_route(lay, q, lib) is None
@@ -183,6 +184,7 @@ def test_kv_head_groups_match_one_call(monkeypatch, cuda, d, t, chunks, hq, hkv)
     layout = hip.chain_layout(t, chunks, hq, hkv)
     lib = _lib.require_library()
     monkeypatch.setenv(hip.DS_ENV, "auto")
+    monkeypatch.setattr(hip, "DS_FREE_FRACTION", 0.0)  # the cap alone decides
     results = []
     for cap in (None, (2 * (hq // hkv) * layout.ds_tables(cuda)["head"] + 512) * 2):
         if cap is not None:

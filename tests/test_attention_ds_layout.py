@@ -154,6 +154,7 @@ def test_route_groups_kv_heads_under_the_cap(monkeypatch):
     head = lay.ds_tables(CPU)["head"]
     q = torch.zeros(150, 24, 256, dtype=torch.bfloat16)
     monkeypatch.setenv(att.DS_ENV, "auto")
+    monkeypatch.setattr(att, "DS_FREE_FRACTION", 0.0)  # the cap alone decides
     monkeypatch.setattr(att, "DS_MAX_BYTES", (24 * head + 512) * 2)
     assert att._ds_route(lay, q, lib)[1] == 4
     monkeypatch.setattr(att, "DS_MAX_BYTES", (24 * head + 512) * 2 - 2)
@@ -167,3 +168,31 @@ def test_route_groups_kv_heads_under_the_cap(monkeypatch):
     assert att._ds_route(lay, q[..., :64], lib) is None
     monkeypatch.setenv(att.DS_ENV, "off")
     assert att._ds_route(lay, q, lib) is None
+
+
+def test_route_takes_free_device_memory_above_the_cap(monkeypatch):
+    """A workspace above DS_MAX_BYTES still runs in one call when it fits in
+    DS_FREE_FRACTION of the device's free memory; with less free memory the
+    route falls back to KV-head groups, and a workspace within the cap never
+    asks the device."""
+    lib = _lib.require_library()
+    lay = att.chain_layout(150, [300, 150], 24, 4)
+    head = lay.ds_tables(CPU)["head"]
+    need = (24 * head + 512) * 2  # bytes of the one-call workspace
+    q = torch.zeros(150, 24, 256, dtype=torch.bfloat16)
+    monkeypatch.setenv(att.DS_ENV, "auto")
+    monkeypatch.setattr(att, "DS_MAX_BYTES", (6 * head + 512) * 2)  # one KV head
+    monkeypatch.setattr(att, "DS_FREE_FRACTION", 0.25)
+    monkeypatch.setattr(att, "_device_free_bytes", lambda device: 4 * need)
+    assert att._ds_route(lay, q, lib)[1] == 4
+    monkeypatch.setattr(att, "_device_free_bytes", lambda device: 4 * need - 8)
+    assert att._ds_route(lay, q, lib)[1] == 3
+    monkeypatch.setattr(att, "_device_free_bytes", lambda device: 0)
+    assert att._ds_route(lay, q, lib)[1] == 1
+
+    def refuse(device):
+        raise AssertionError("a workspace within the cap must not query the device")
+
+    monkeypatch.setattr(att, "DS_MAX_BYTES", need)
+    monkeypatch.setattr(att, "_device_free_bytes", refuse)
+    assert att._ds_route(lay, q, lib)[1] == 4

@@ -427,15 +427,27 @@ def _validate_call(layout: AttnLayout, query: torch.Tensor, keys, values) -> Non
                 raise ValueError(f"{name} source {i} has {t.shape[0]} rows, layout {layout.source_rows[i]}")
 
 
-# Largest dS workspace (bytes) the backward allocates for the dS route (dK/dV
+# dS workspace (bytes) the backward may allocate for the dS route (dK/dV
 # kernels store dS, dQ = dS K from it; about 2 bytes per visible pair and
-# head).  A problem above it runs the route over groups of KV heads, as many
-# per call as fit (KV heads are independent: their query heads, dS and
-# gradients do not mix); one whose single KV head does not fit, or any under
-# THUNDERSYNC_ATTN_DS=off, runs the route that recomputes S and dP in the dQ
-# kernel.
+# head): DS_MAX_BYTES always, and a workspace above it when it fits in
+# DS_FREE_FRACTION of the device's free memory (an MI355X holds 288 GB; the
+# reference's 16-trajectory retained-chunk pack needs ~52 GB).  A problem
+# above the cap runs the route over groups of KV heads, as many per call as
+# fit (KV heads are independent: their query heads, dS and gradients do not
+# mix, and the grouped calls give the one-call gradients bit for bit); one
+# whose single KV head does not fit, or any under THUNDERSYNC_ATTN_DS=off,
+# runs the route that recomputes S and dP in the dQ kernel.
 DS_MAX_BYTES = 16 << 30
+DS_FREE_FRACTION = 0.25
 DS_ENV = "THUNDERSYNC_ATTN_DS"
+
+
+def _device_free_bytes(device: torch.device) -> int:
+    """Free memory of `device` in bytes (0 for a host device)."""
+    if device.type != "cuda":
+        return 0
+    free, _total = torch.cuda.mem_get_info(device)
+    return int(free)
 
 
 def _ds_route(layout: AttnLayout, query: torch.Tensor, lib):
@@ -450,7 +462,10 @@ def _ds_route(layout: AttnLayout, query: torch.Tensor, lib):
     # a call over n KV heads needs (n * group * head + 512) elements: every
     # query head's part, then the sink block
     per_kv_head = group * max(tabs["head"], 1)
-    kv_heads = min(layout.hkv, (DS_MAX_BYTES // 2 - 512) // per_kv_head)
+    cap = DS_MAX_BYTES
+    if (layout.hkv * per_kv_head + 512) * 2 > cap and DS_FREE_FRACTION > 0:
+        cap = max(cap, int(_device_free_bytes(query.device) * DS_FREE_FRACTION))
+    kv_heads = min(layout.hkv, (cap // 2 - 512) // per_kv_head)
     if kv_heads < 1:
         return None
     return tabs, kv_heads
