@@ -133,7 +133,12 @@ def repeat_for(fn, seconds=CPU_BASELINE_SECONDS, max_reps=20000):
 
 
 def timed(step, steps, warmup, kernels):
-    """(ms per step, {kernel: (avg ms per launch, launches per step)})."""
+    """(ms per step, {kernel: (avg ms per launch, launches per step)}).
+
+    The wall clock times `steps` steps with the library's per-kernel HIP-event
+    brackets off (two event records per launch are instrumentation, not the
+    job); a second pass of the same steps with the brackets on gives the
+    per-kernel device times."""
     import torch
 
     from thundersync_amd._lib import KernelTimer
@@ -141,18 +146,27 @@ def timed(step, steps, warmup, kernels):
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
     with KernelTimer():
-        t0 = time.perf_counter()
         for _ in range(steps):
             step()
         torch.cuda.synchronize()
-        t1 = time.perf_counter()
         per = {}
         for k in kernels:
             total, n = KernelTimer.read(k)
             if n:
                 per[k] = (total / n, n / steps)
     return (t1 - t0) * 1e3 / steps, per
+
+
+# Sub-millisecond secondaries (RMSNorm, boundary adjoints) repeat their step
+# at least this many times, so that the timed region is tens of
+# milliseconds rather than a few launch latencies; their JSON records the count.
+SHORT_STEPS, SHORT_WARMUP = 200, 20
 
 
 def measured_traffic(workload, kernel):
@@ -668,7 +682,8 @@ def bench_rmsnorm(args, device):
 
     kernels = ["rmsnorm.rmsnorm_fwd_lanes", "rmsnorm.rmsnorm_fwd_rowwave", "rmsnorm.rmsnorm_bwd_vec",
                "rmsnorm.rmsnorm_dw_reduce"]
-    ms, per = timed(step, args.steps, args.warmup, kernels)
+    steps, warmup = max(args.steps, SHORT_STEPS), max(args.warmup, SHORT_WARMUP)
+    ms, per = timed(step, steps, warmup, kernels)
     fwd_bytes = 4 * r * w_ + 4 * r + 2 * w_
     bwd_bytes = 6 * r * w_ + 4 * r + 2 * w_ + 4 * w_
     work = {"rmsnorm.rmsnorm_fwd_lanes": fwd_bytes, "rmsnorm.rmsnorm_fwd_rowwave": fwd_bytes,
@@ -680,6 +695,8 @@ def bench_rmsnorm(args, device):
         "ms_per_step": round(ms, 4),
         "roofline": roofline_of({k: x for k, x in per.items() if work[k]}, work, "GB/s", PEAKS["hbm_gbs"], "rmsnorm"),
         "kernels": {k: {"avg_ms": round(x, 4), "launches_per_step": m} for k, (x, m) in per.items()},
+        "steps": steps,
+        "warmup": warmup,
         "config": {"workload": "RMSNorm fwd+bwd [16384, 4096] bf16, FP32 VJP with dW", "seed": args.seed},
     }
     if not args.no_cpu_baseline:
@@ -735,7 +752,8 @@ def bench_adjoint(args, device):
         boundary_adjoint.reduce_boundary_adjoints(adj, existing=existing)
 
     kernels = ["adjoint.reduce_kernel"]
-    ms, per = timed(step, args.steps, args.warmup, kernels)
+    steps, warmup = max(args.steps, SHORT_STEPS), max(args.warmup, SHORT_WARMUP)
+    ms, per = timed(step, steps, warmup, kernels)
     n = ADJOINT_SHAPE[0] * ADJOINT_SHAPE[1]
     nbytes = (ADJOINT_DEGREE + 1) * n * 2 + n * 2  # every input read once, the output written once
     result = {
@@ -745,6 +763,8 @@ def bench_adjoint(args, device):
         "ms_per_step": round(ms, 4),
         "roofline": roofline_of(per, {"adjoint.reduce_kernel": nbytes}, "GB/s", PEAKS["hbm_gbs"], "adjoint"),
         "kernels": {k: {"avg_ms": round(x, 4), "launches_per_step": m} for k, (x, m) in per.items()},
+        "steps": steps,
+        "warmup": warmup,
         "config": {"workload": f"boundary adjoint: existing + {ADJOINT_DEGREE} consumer adjoints "
                                f"[{ADJOINT_SHAPE[0]}, {ADJOINT_SHAPE[1]}] bf16, fp32 accumulation",
                    "seed": args.seed},

@@ -176,27 +176,40 @@ def require_library() -> ctypes.CDLL:
     return lib
 
 
-def check(status: int, what: str) -> None:
-    """Raise RuntimeError naming the kernel call when a status is not TS_OK."""
+def check(status: int, what) -> None:
+    """Raise RuntimeError naming the kernel call when a status is not TS_OK;
+    ``what`` is the call's description, or a function that builds it (so a
+    hot call site formats nothing when the call succeeds)."""
     if status != TS_OK:
         lib = require_library()
         message = lib.ts_hip_last_error().decode()
+        if callable(what):
+            what = what()
         raise RuntimeError(f"{what} failed (status {status}): {message}")
 
 
-def dtype_code(dtype) -> int:
-    import torch
+_DTYPE_CODES: dict | None = None
 
-    codes = {torch.float32: TS_F32, torch.float16: TS_F16, torch.bfloat16: TS_BF16}
-    if dtype not in codes:
+
+def dtype_code(dtype) -> int:
+    global _DTYPE_CODES
+    if _DTYPE_CODES is None:
+        import torch
+
+        _DTYPE_CODES = {torch.float32: TS_F32, torch.float16: TS_F16, torch.bfloat16: TS_BF16}
+    code = _DTYPE_CODES.get(dtype)
+    if code is None:
         raise TypeError(f"unsupported dtype {dtype}")
-    return codes[dtype]
+    return code
 
 
 def stream_of(tensor) -> int:
     """The current HIP stream of ``tensor``'s device, as an integer handle."""
     import torch
 
+    raw = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+    if raw is not None and tensor.device.index is not None:
+        return raw(tensor.device.index)
     return torch.cuda.current_stream(tensor.device).cuda_stream
 
 

@@ -59,9 +59,23 @@ def rms_norm_forward(hidden: torch.Tensor, weight: torch.Tensor, eps: float):
             x.data_ptr(), w.data_ptr(), y.data_ptr(), rstd.data_ptr(), rows, width,
             float(eps), _lib.dtype_code(x.dtype), _lib.stream_of(x),
         ),
-        f"ts_rmsnorm_fwd(rows={rows}, width={width}, dtype={x.dtype})",
+        lambda: f"ts_rmsnorm_fwd(rows={rows}, width={width}, dtype={x.dtype})",
     )
     return y, rstd
+
+
+_WORKSPACE_BYTES: dict[tuple[int, int], int] = {}
+
+
+def _workspace_bytes(lib, rows: int, width: int) -> int:
+    """ts_rmsnorm_bwd_workspace(rows, width), asked once per shape."""
+    key = (rows, width)
+    nbytes = _WORKSPACE_BYTES.get(key)
+    if nbytes is None:
+        if len(_WORKSPACE_BYTES) > 4096:
+            _WORKSPACE_BYTES.clear()
+        nbytes = _WORKSPACE_BYTES[key] = int(lib.ts_rmsnorm_bwd_workspace(rows, width))
+    return nbytes
 
 
 def rms_norm_backward(gradient, hidden, weight, rstd, needs=(True, True)):
@@ -78,7 +92,7 @@ def rms_norm_backward(gradient, hidden, weight, rstd, needs=(True, True)):
     dw = torch.empty_like(w) if needs[1] else None
     if dx is None and dw is None:
         return None, None
-    ws_bytes = int(lib.ts_rmsnorm_bwd_workspace(rows, width)) if dw is not None else 0
+    ws_bytes = _workspace_bytes(lib, rows, width) if dw is not None else 0
     workspace = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=x.device)
     _lib.check(
         lib.ts_rmsnorm_bwd(
@@ -86,7 +100,7 @@ def rms_norm_backward(gradient, hidden, weight, rstd, needs=(True, True)):
             _lib.ptr(dx), _lib.ptr(dw), workspace.data_ptr(), ws_bytes, rows, width,
             _lib.dtype_code(x.dtype), _lib.stream_of(x),
         ),
-        f"ts_rmsnorm_bwd(rows={rows}, width={width}, dtype={x.dtype})",
+        lambda: f"ts_rmsnorm_bwd(rows={rows}, width={width}, dtype={x.dtype})",
     )
     return dx, dw
 
