@@ -3,19 +3,23 @@
 //
 // A work-group owns the work item's 128 / GC query rows of one segment for GC
 // query heads of one GQA group: wave w takes head w % GC and the 32-row block
-// w / GC, so the four waves share the 64-key K tiles of their KV head.  Each
-// tile step streams, by buffer DMA into an LDS stage, the K tile (rows of HD
-// elements, 16-byte chunk c of row r at slot c ^ tile_swizzle(r & 15)) and
-// every wave's four dS blocks for its row block and the tile's four 16-key
-// blocks (the rectangle's prefix its rows see: blocks past it arrive as
-// zeros, as do K rows past the run).  Per 32-key half of the tile,
+// w / GC, so the four waves share the K tiles of their KV head (KT keys: 32 at
+// head dim 128, 64 at 256).  Each tile step streams, by buffer DMA into an
+// LDS stage, the K tile (rows of HD elements, 16-byte chunk c of row r at slot
+// c ^ tile_swizzle(r & 15)) and every wave's KT / 16 dS blocks for its row
+// block and the tile's 16-key blocks (the rectangle's prefix its rows see:
+// blocks past it arrive as zeros, as do K rows past the run).  Per 32 keys of
+// the tile,
 //     dQ^T[d][slot] += K^T[d][key] dS^T[key][slot]
 // with K^T from ds_read_b64_tr_b16 over the K tile (lane (g4, j16): keys
 // 4 g4 + t and 16 + 4 g4 + t of column d = 16 mb + j16) and dS^T from the same
 // transposed read over the blocks (keys 4 g4 + t of slot 16 mb' + j16): the two
 // operands order the 32 keys alike, and the output columns are the blocks'
 // row slots.  dS is zero wherever a row does not see a key, so no masking.
-// Memory-bound on the dS stream: NST stages keep NST - 1 tiles in flight.
+// Memory-bound on the dS stream: NST stages keep NST - 1 tiles in flight.  At
+// head dim 128 a stage of 32-key tiles is 16 KB, so four work-groups share a
+// CU (against two with 64-key tiles: C2 dQ 1.04 -> 0.99 ms); more independent
+// work-groups hide each other's waits better than deeper stages do.
 // The DMA is issued untracked by the compiler (its waits would otherwise
 // cover the stage being filled as well as the one being read): each step
 // waits for its own tile with an explicit vmcnt and a work-group barrier.
@@ -26,10 +30,10 @@ namespace attn {
 
 // the K half of issue_kv_tile: a 64-key K tile, every wave its share of the
 // HD / 2 DMA instructions (rows past the run arrive as zeros)
-template <int HD>
+template <int HD, int KT>
 __device__ __forceinline__ void issue_k_tile(int hk, int wave, int lane, const TileCursor& tc, bf16* sk) {
-  constexpr int CH = HD / 8, RPI = 64 / CH, NI = BK / RPI;
-  const int nvalid = min(BK, tc.len - tc.kt0);
+  constexpr int CH = HD / 8, RPI = 64 / CH, NI = KT / RPI;
+  const int nvalid = min(KT, tc.len - tc.kt0);
   const bf16* kb = (const bf16*)tc.k + (int64_t)tc.kt0 * tc.k_row_stride + (int64_t)hk * tc.k_head_stride;
   const u32x4 rk = raw_descriptor(kb, (uint32_t)(nvalid * tc.k_row_stride * 2));
 #pragma unroll
@@ -48,16 +52,26 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt(0x0f70 | (N & 15) | ((N >> 4) << 14));
 }
 
+#ifndef TS_DQDS_KT128
+#define TS_DQDS_KT128 32
+#endif
+// keys per K tile: 64 at head dim 256, TS_DQDS_KT128 (32) at 128
+template <int HD> constexpr int dq_ds_tile_keys() { return HD > 128 ? BK : TS_DQDS_KT128; }
+// work-groups per CU the LDS stages allow
+template <int HD> constexpr int dq_ds_occupancy() { return HD > 128 ? 1 : (dq_ds_tile_keys<HD>() == 64 ? 2 : 4); }
+
 template <typename E, int HD, int GC>
-__global__ __launch_bounds__(kThreads, HD > 128 ? 1 : 2) void dq_ds_kernel(ts_attn_problem P, DsArgs S,
-                                                                           ts_attn_rows dQ) {
+__global__ __launch_bounds__(kThreads, dq_ds_occupancy<HD>()) void dq_ds_kernel(ts_attn_problem P, DsArgs S,
+                                                                                ts_attn_rows dQ) {
   static_assert(HD == 128 || HD == 256, "the K tile swizzle needs 16 or 32 chunks per row");
+  constexpr int KT = dq_ds_tile_keys<HD>();      // keys per tile (64 or 32)
+  constexpr int NKB = KT / 16;                   // 16-key dS blocks per tile
   constexpr int NMB = HD / 16;                   // 16-column blocks of dQ
   constexpr int NST = HD > 128 ? 3 : 2;          // LDS stages
-  constexpr int KTILE = BK * HD;                 // elements of a K tile
-  constexpr int DTILE = 4 * kDsBlock;            // a wave's four dS blocks
+  constexpr int KTILE = KT * HD;                 // elements of a K tile
+  constexpr int DTILE = NKB * kDsBlock;          // a wave's dS blocks of the tile
   constexpr int STAGE = KTILE + 4 * DTILE;
-  constexpr int PER_TILE = HD / 32 + 4;          // DMA instructions per wave and tile
+  constexpr int PER_TILE = KT * HD / 2048 + NKB;  // DMA instructions per wave and tile
   __shared__ __attribute__((aligned(16))) bf16 s_buf[NST * STAGE];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -102,14 +116,14 @@ __global__ __launch_bounds__(kThreads, HD > 128 ? 1 : 2) void dq_ds_kernel(ts_at
   };
   auto issue = [&](const TileCursor& tc, int st) {
     bf16* buf = s_buf + st * STAGE;
-    issue_k_tile<HD>(hk, wave, lane, tc, buf);
+    issue_k_tile<HD, KT>(hk, wave, lane, tc, buf);
     if (tc.sp != ds_sp) ds_enter(tc);
     const int kb0 = tc.kt0 >> 4;
-    const int nb = max(0, min(4, ds_n - kb0));
+    const int nb = max(0, min(NKB, ds_n - kb0));
     const u32x4 rd = raw_descriptor((const E*)S.ptr + ds_at + (int64_t)kb0 * kDsBlock, (uint32_t)(nb * kDsBlock * 2));
     bf16* dbuf = buf + KTILE + wave * DTILE;
 #pragma unroll
-    for (int kk = 0; kk < 4; ++kk) buffer_dma16_untracked_nt(rd, dbuf + kk * kDsBlock, kk * kDsBlock * 2 + lane * 16);
+    for (int kk = 0; kk < NKB; ++kk) buffer_dma16_untracked_nt(rd, dbuf + kk * kDsBlock, kk * kDsBlock * 2 + lane * 16);
   };
 
   f32x4 acc[NMB][2];
@@ -123,7 +137,7 @@ __global__ __launch_bounds__(kThreads, HD > 128 ? 1 : 2) void dq_ds_kernel(ts_at
     const bf16* tk = s_buf + st * STAGE;
     const bf16* td = tk + KTILE + wave * DTILE;
 #pragma unroll
-    for (int ss = 0; ss < 2; ++ss) {
+    for (int ss = 0; ss < KT / 32; ++ss) {
       bf16x8 b[2];
 #pragma unroll
       for (int mbp = 0; mbp < 2; ++mbp) {
@@ -151,13 +165,13 @@ __global__ __launch_bounds__(kThreads, HD > 128 ? 1 : 2) void dq_ds_kernel(ts_at
   };
 
   // tiles i .. i + NST - 2 are in flight at the top of step i
-  TileCursor nx = first_kv_tile(P, seg, last);
+  TileCursor nx = first_kv_tile<KT>(P, seg, last);
   int issued = 0;
 #pragma unroll
   for (int p = 0; p < NST - 1; ++p) {
     if (nx.sp < seg.nspan) {
       issue(nx, p);
-      nx = next_kv_tile(P, seg, last, nx);
+      nx = next_kv_tile<KT>(P, seg, last, nx);
       ++issued;
     }
   }
@@ -174,7 +188,7 @@ __global__ __launch_bounds__(kThreads, HD > 128 ? 1 : 2) void dq_ds_kernel(ts_at
     __syncthreads();  // tile i is in every stage; stage (i - 1) % NST is free
     if (nx.sp < seg.nspan) {
       issue(nx, (i + NST - 1) % NST);
-      nx = next_kv_tile(P, seg, last, nx);
+      nx = next_kv_tile<KT>(P, seg, last, nx);
       ++issued;
     }
     compute(i % NST);

@@ -348,10 +348,11 @@ __device__ __forceinline__ void enter_span(const ts_attn_problem& P, const ts_at
 // `last` (segment-local) can see; sp == nspan when none is left.  Spans are in
 // key order, so once a tile starts past the last visible key so do all later
 // ones.  Tables are read only on entering a span.
+template <int KT = BK>
 __device__ __forceinline__ TileCursor next_kv_tile(const ts_attn_problem& P, const ts_attn_segment& seg,
                                                    int last, TileCursor tc) {
   const int off = seg.kv_len - seg.q_len;
-  tc.kt0 += BK;
+  tc.kt0 += KT;
   while (tc.sp < seg.nspan) {
     if (tc.kt0 >= tc.len) {
       if (++tc.sp < seg.nspan) enter_span(P, seg, tc);
@@ -365,11 +366,12 @@ __device__ __forceinline__ TileCursor next_kv_tile(const ts_attn_problem& P, con
 }
 
 // the first visible tile of a segment
+template <int KT = BK>
 __device__ __forceinline__ TileCursor first_kv_tile(const ts_attn_problem& P, const ts_attn_segment& seg,
                                                     int last) {
-  TileCursor tc{0, -BK, 0, 0, 0, 0, 0, 0, 0, 0};
+  TileCursor tc{0, -KT, 0, 0, 0, 0, 0, 0, 0, 0};
   if (seg.nspan > 0) enter_span(P, seg, tc);
-  return next_kv_tile(P, seg, last, tc);
+  return next_kv_tile<KT>(P, seg, last, tc);
 }
 
 // Row swizzle of the 256-byte-row LDS tiles: 16-byte chunk c of row r sits at
