@@ -150,15 +150,17 @@ __global__ __launch_bounds__(kThreads, HD > 128 ? 1 : 2) void fwd_kernel(ts_attn
 //
 // A work-group owns 128 / GC query rows of one segment for GC query heads of
 // one GQA group; wave w takes head w % GC and 16 NQB rows (at head dim 128
-// with GC = 4: NQB = 2, four waves, two work-groups and two waves per SIMD;
-// NQB = 1, eight waves of 16 rows, four waves per SIMD, measured no faster on
-// C2 at 1.32 ms; at head dim 256 NQB = 1, eight waves, two per SIMD, one
-// work-group per CU for its 128 KB of tiles).  The heads share 64-key K/V
-// tiles, streamed by buffer DMA into double-buffered swizzled LDS stages (one
+// with GC = 4: NQB = 2, four waves; NQB = 1, eight waves of 16 rows, four
+// waves per SIMD, measured no faster on C2 at 1.32 ms; at head dim 256
+// NQB = 1, eight waves, two per SIMD, one work-group per CU for its 128 KB of
+// tiles).  The heads share K/V tiles of KT keys (32 at head dim 128: 32 KB
+// of stages per work-group, three work-groups and three waves per SIMD at 168
+// VGPRs, against two with 64-key tiles: C2 forward 1.20 -> 1.09 ms; 64 at
+// 256), streamed by buffer DMA into double-buffered swizzled LDS stages (one
 // work-group barrier per tile).  Q rows stay in registers as B operands of
-// S^T = K Q^T; V^T for O^T += V^T P^T comes from ds_read_b64_tr_b16.  Each
-// lane owns one query column (16 qb + j16) and 16 of the tile's 64 keys; the
-// other 48 sit in the lanes j16 + 16, + 32, + 48.  The softmax runs in the
+// S^T = K Q^T; V^T for O^T += V^T P^T comes from ds_read_b64_tr_b16.  Per 32
+// keys of a tile each lane owns one query column (16 qb + j16) and 8 of the
+// keys, the others sitting in the lanes j16 + 16, + 32, + 48.  The softmax runs in the
 // log2 domain with the scale folded into one FMA per score, and the
 // reference point m of a row moves only when the row maximum exceeds it by
 // more than 8 (a factor of 256): the accumulators are rescaled in the rare
@@ -169,17 +171,25 @@ __global__ __launch_bounds__(kThreads, HD > 128 ? 1 : 2) void fwd_kernel(ts_attn
 constexpr float kRescaleSlack = 8.f;    // log2 units
 constexpr float kRescaleBound = 256.f;  // 2^kRescaleSlack
 
-template <typename E, int NQB, int HD = D, int GC = 4>
-__global__ __launch_bounds__(64 * 8 / NQB, HD > 128 ? (NQB == 1 ? 2 : 1) : (NQB == 1 ? 4 : 2)) void fwd_wave_kernel(ts_attn_problem P, ts_attn_rows Q,
+#ifndef TS_FWD_KT128
+#define TS_FWD_KT128 32
+#endif
+// work-groups per CU: their LDS stages (two K/V stages of KT keys) and registers
+template <int NQB, int HD, int KT>
+constexpr int fwd_occupancy() { return HD > 128 ? (NQB == 1 ? 2 : 1) : (NQB == 1 ? 4 : (KT == 32 ? 3 : 2)); }
+
+template <typename E, int NQB, int HD = D, int GC = 4, int KT = BK>
+__global__ __launch_bounds__(64 * 8 / NQB, (fwd_occupancy<NQB, HD, KT>())) void fwd_wave_kernel(ts_attn_problem P, ts_attn_rows Q,
                                                                                   ts_attn_rows O,
                                                                                   float* __restrict__ lse,
                                                                                   int64_t lse_ld) {
   constexpr int kWaves = 8 / NQB;
   constexpr int NKS = HD / 32, NMB = HD / 16;  // k-steps of S; 16-column blocks of O
-  __shared__ __attribute__((aligned(16))) bf16 s_k0[BK * HD];
-  __shared__ __attribute__((aligned(16))) bf16 s_v0[BK * HD];
-  __shared__ __attribute__((aligned(16))) bf16 s_k1[BK * HD];
-  __shared__ __attribute__((aligned(16))) bf16 s_v1[BK * HD];
+  static_assert(KT == 64 || KT == 32, "tiles of 64 or 32 keys");
+  __shared__ __attribute__((aligned(16))) bf16 s_k0[KT * HD];
+  __shared__ __attribute__((aligned(16))) bf16 s_v0[KT * HD];
+  __shared__ __attribute__((aligned(16))) bf16 s_k1[KT * HD];
+  __shared__ __attribute__((aligned(16))) bf16 s_v1[KT * HD];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g4 = lane >> 4, j16 = lane & 15;
@@ -218,20 +228,20 @@ __global__ __launch_bounds__(64 * 8 / NQB, HD > 128 ? (NQB == 1 ? 2 : 1) : (NQB 
   auto step = [&](auto bsel, TileCursor& cur) {
     const int kpos = cur.kpos, run_len = cur.len;
     const int kt0 = cur.kt0;
-    const TileCursor nxt = next_kv_tile(P, seg, last, cur);
+    const TileCursor nxt = next_kv_tile<KT>(P, seg, last, cur);
     __builtin_amdgcn_s_waitcnt(0);  // this wave's part of the tile has landed
     __syncthreads();                // every part has, and the other stage is free
     const bf16* tk = bsel.value == 0 ? s_k0 : s_k1;
     const bf16* tv = bsel.value == 0 ? s_v0 : s_v1;
     if (nxt.sp < seg.nspan)
-      issue_kv_tile<kWaves, HD>(hk, wave, lane, nxt, bsel.value == 0 ? s_k1 : s_k0, bsel.value == 0 ? s_v1 : s_v0);
+      issue_kv_tile<kWaves, HD, KT>(hk, wave, lane, nxt, bsel.value == 0 ? s_k1 : s_k0, bsel.value == 0 ? s_v1 : s_v0);
 
-    const bool masked = (kpos + kt0 + BK - 1 > off + qw) | (kt0 + BK > run_len);
+    const bool masked = (kpos + kt0 + KT - 1 > off + qw) | (kt0 + KT > run_len);
     // two halves of 32 keys, each one online-softmax update:
     // S^T = K Q^T with sc[kb][qb] holding keys 32 ss + 16 kb + 4 g4 + i of column
     // 16 qb + j16, then O^T += V^T P^T with slot j <-> key 32 ss + 16 (j >> 2) + 4 g4 + (j & 3)
 #pragma unroll
-    for (int ss = 0; ss < 2; ++ss) {
+    for (int ss = 0; ss < KT / 32; ++ss) {
       f32x4 sc[2][NQB];
       // wave priority 1 over the MFMA phases, 0 over the softmax: of the two
       // waves on a SIMD, the one with MFMAs to issue goes first (fwd -1.4 %)
@@ -347,8 +357,8 @@ __global__ __launch_bounds__(64 * 8 / NQB, HD > 128 ? (NQB == 1 ? 2 : 1) : (NQB 
     cur = nxt;
   };
 
-  TileCursor cur = first_kv_tile(P, seg, last);
-  if (cur.sp < seg.nspan) issue_kv_tile<kWaves, HD>(hk, wave, lane, cur, s_k0, s_v0);
+  TileCursor cur = first_kv_tile<KT>(P, seg, last);
+  if (cur.sp < seg.nspan) issue_kv_tile<kWaves, HD, KT>(hk, wave, lane, cur, s_k0, s_v0);
   while (cur.sp < seg.nspan) {
     step(std::integral_constant<int, 0>{}, cur);
     if (cur.sp >= seg.nspan) break;
@@ -416,8 +426,8 @@ int launch_fwd_t(const ts_attn_problem& P, ts_attn_rows q, ts_attn_rows out, flo
     default: {
       ts::TimedLaunch timed_("attention.fwd_kernel", s);
       if (gc == 4)
-        hipLaunchKernelGGL((fwd_wave_kernel<E, kFwdRowsPerWave / 16>), grid, dim3(64 * 128 / kFwdRowsPerWave), 0, s,
-                           P, q, out, lse, lse_ld);
+        hipLaunchKernelGGL((fwd_wave_kernel<E, kFwdRowsPerWave / 16, D, 4, TS_FWD_KT128>), grid,
+                           dim3(64 * 128 / kFwdRowsPerWave), 0, s, P, q, out, lse, lse_ld);
       else if (gc == 2)
         hipLaunchKernelGGL((fwd_wave_kernel<E, 2, D, 2>), grid, dim3(256), 0, s, P, q, out, lse, lse_ld);
       else

@@ -393,13 +393,14 @@ __device__ __forceinline__ int tile_swizzle(int r) { return r ^ ((r & 1) ? 12 : 
 // 256): lane l the row RPI t + l / (HD / 8), slot l % (HD / 8) with logical
 // chunk (l % (HD / 8)) ^ tile_swizzle(row).  Rows past the run arrive as
 // zeros.
-template <int WAVES = 4, int HD = D>
+template <int WAVES = 4, int HD = D, int KT = BK>
 __device__ __forceinline__ void issue_kv_tile(int hk, int wave, int lane, const TileCursor& tc, bf16* sk,
                                               bf16* sv) {
   static_assert(WAVES == 4 || WAVES == 8, "a tile is 16 or 32 instructions");
   static_assert(HD == 128 || HD == 256, "the swizzle needs 16 or 32 chunks per row");
-  constexpr int CH = HD / 8, RPI = 64 / CH, NI = BK / RPI;
-  const int nvalid = min(BK, tc.len - tc.kt0);
+  constexpr int CH = HD / 8, RPI = 64 / CH, NI = KT / RPI;
+  static_assert(NI % WAVES == 0, "every wave issues the same number of instructions");
+  const int nvalid = min(KT, tc.len - tc.kt0);
   const bf16* kb = (const bf16*)tc.k + (int64_t)tc.kt0 * tc.k_row_stride + (int64_t)hk * tc.k_head_stride;
   const bf16* vb = (const bf16*)tc.v + (int64_t)tc.kt0 * tc.v_row_stride + (int64_t)hk * tc.v_head_stride;
   const rsrc_t rk = make_rsrc(kb, (uint32_t)(nvalid * tc.k_row_stride * 2));
@@ -413,7 +414,7 @@ __device__ __forceinline__ void issue_kv_tile(int hk, int wave, int lane, const 
     const int vo = (int)((dma_row * tc.v_row_stride + dma_chunk) * 2);
     const int kstep = (int)(4 * WAVES * tc.k_row_stride * 2), vstep = (int)(4 * WAVES * tc.v_row_stride * 2);
 #pragma unroll
-    for (int u = 0; u < 16 / WAVES; ++u) {
+    for (int u = 0; u < NI / WAVES; ++u) {
       buffer_dma16(rk, sk + (wave + WAVES * u) * 512, ko + u * kstep);
       buffer_dma16(rv, sv + (wave + WAVES * u) * 512, vo + u * vstep);
     }
