@@ -55,10 +55,17 @@ __device__ __forceinline__ void wait_vmcnt() {
 #ifndef TS_DQDS_KT128
 #define TS_DQDS_KT128 32
 #endif
-// keys per K tile: 64 at head dim 256, TS_DQDS_KT128 (32) at 128
-template <int HD> constexpr int dq_ds_tile_keys() { return HD > 128 ? BK : TS_DQDS_KT128; }
+#ifndef TS_DQDS_KT256
+#define TS_DQDS_KT256 64
+#endif
+// keys per K tile: TS_DQDS_KT256 (64) at head dim 256, TS_DQDS_KT128 (32) at 128
+template <int HD> constexpr int dq_ds_tile_keys() { return HD > 128 ? TS_DQDS_KT256 : TS_DQDS_KT128; }
+// LDS stages: three of 48 KB at head dim 256 with 64-key tiles, else two
+template <int HD> constexpr int dq_ds_stages() { return HD > 128 && dq_ds_tile_keys<HD>() == 64 ? 3 : 2; }
 // work-groups per CU the LDS stages allow
-template <int HD> constexpr int dq_ds_occupancy() { return HD > 128 ? 1 : (dq_ds_tile_keys<HD>() == 64 ? 2 : 4); }
+template <int HD> constexpr int dq_ds_occupancy() {
+  return HD > 128 ? (dq_ds_tile_keys<HD>() == 64 ? 1 : 3) : (dq_ds_tile_keys<HD>() == 64 ? 2 : 4);
+}
 
 template <typename E, int HD, int GC>
 __global__ __launch_bounds__(kThreads, dq_ds_occupancy<HD>()) void dq_ds_kernel(ts_attn_problem P, DsArgs S,
@@ -67,7 +74,7 @@ __global__ __launch_bounds__(kThreads, dq_ds_occupancy<HD>()) void dq_ds_kernel(
   constexpr int KT = dq_ds_tile_keys<HD>();      // keys per tile (64 or 32)
   constexpr int NKB = KT / 16;                   // 16-key dS blocks per tile
   constexpr int NMB = HD / 16;                   // 16-column blocks of dQ
-  constexpr int NST = HD > 128 ? 3 : 2;          // LDS stages
+  constexpr int NST = dq_ds_stages<HD>();        // LDS stages
   constexpr int KTILE = KT * HD;                 // elements of a K tile
   constexpr int DTILE = NKB * kDsBlock;          // a wave's dS blocks of the tile
   constexpr int STAGE = KTILE + 4 * DTILE;
