@@ -174,6 +174,10 @@ constexpr float kRescaleBound = 256.f;  // 2^kRescaleSlack
 #ifndef TS_FWD_KT128
 #define TS_FWD_KT128 32
 #endif
+// keys per K/V tile at head dim 128 for GQA groups that are not a multiple of 4
+#ifndef TS_FWD_KT128_GC
+#define TS_FWD_KT128_GC 32
+#endif
 // work-groups per CU: their LDS stages (two K/V stages of KT keys) and registers
 template <int NQB, int HD, int KT>
 constexpr int fwd_occupancy() { return HD > 128 ? (NQB == 1 ? 2 : 1) : (NQB == 1 ? 4 : (KT == 32 ? 3 : 2)); }
@@ -429,9 +433,11 @@ int launch_fwd_t(const ts_attn_problem& P, ts_attn_rows q, ts_attn_rows out, flo
         hipLaunchKernelGGL((fwd_wave_kernel<E, kFwdRowsPerWave / 16, D, 4, TS_FWD_KT128>), grid,
                            dim3(64 * 128 / kFwdRowsPerWave), 0, s, P, q, out, lse, lse_ld);
       else if (gc == 2)
-        hipLaunchKernelGGL((fwd_wave_kernel<E, 2, D, 2>), grid, dim3(256), 0, s, P, q, out, lse, lse_ld);
+        hipLaunchKernelGGL((fwd_wave_kernel<E, 2, D, 2, TS_FWD_KT128_GC>), grid, dim3(256), 0, s, P, q, out, lse,
+                           lse_ld);
       else
-        hipLaunchKernelGGL((fwd_wave_kernel<E, 2, D, 1>), grid, dim3(256), 0, s, P, q, out, lse, lse_ld);
+        hipLaunchKernelGGL((fwd_wave_kernel<E, 2, D, 1, TS_FWD_KT128_GC>), grid, dim3(256), 0, s, P, q, out, lse,
+                           lse_ld);
     }
   }
   return ts::check_launch("ts_attn_fwd");
