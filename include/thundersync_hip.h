@@ -62,6 +62,15 @@ int ts_rmsnorm_fwd(const void* x, const void* w, void* y, float* rstd,
                    int64_t rows, int64_t width, float eps, int dtype,
                    void* stream);
 
+/* 1 when ts_rmsnorm_fwd and ts_rmsnorm_bwd both take a contiguous
+ * [rows, width] problem on the device `stream` belongs to, else 0 (a single
+ * row that torch sums across work-groups; a width the backward has no kernel
+ * for).  No launch, no allocation.  The module swap's eligibility test: the
+ * reference's StableQwen3RMSNorm keeps the stock forward outside its own
+ * path (accel/rms_norm.py:49-52), and the swap here does the same for the
+ * shapes this returns 0 for. */
+int ts_rmsnorm_supported(int64_t rows, int64_t width, void* stream);
+
 /* Workspace bytes ts_rmsnorm_bwd needs for `rows` x `width`. */
 int64_t ts_rmsnorm_bwd_workspace(int64_t rows, int64_t width);
 
@@ -90,8 +99,10 @@ int ts_rmsnorm_bwd(const void* dy, const void* x, const void* w,
  * callers that cannot allocate device memory (code under HIP graph capture,
  * tight serving loops, harnesses that forbid hipMalloc).  TS_ERR_INVALID when
  * ts_rmsnorm_bwd_workspace(rows, width) exceeds the array (every row count
- * fits for width <= 8192).  All calls on one GPU share its array: calls that
- * overlap on one GPU race.  Results are bit-identical to ts_rmsnorm_bwd's. */
+ * fits for width <= 8192).  All calls on one GPU share its array, so only one
+ * caller per GPU may have a call in flight at a time: calls that overlap on
+ * one GPU (two streams, two threads) race on the partials.  Results are
+ * bit-identical to ts_rmsnorm_bwd's. */
 int ts_rmsnorm_bwd_noalloc(const void* dy, const void* x, const void* w,
                            const float* rstd, void* dx, void* dw, int64_t rows,
                            int64_t width, int dtype, void* stream);
@@ -459,35 +470,6 @@ int ts_timing_read(const char* kernel, double* total_ms, int64_t* launches);
  * reference. */
 int ts_device_clocks(int device, int* cus, int* clock_khz, int* mem_clock_khz, int* mem_bus_bits);
 
-/* Runs one v_mfma_f32_16x16x32_bf16 and one v_mfma_f32_32x32x16_bf16 on
- * operands the caller lays out per lane (a, b: 64 lanes x 8 bf16 each), and
- * the 8x8 16-bit register transpose on `t_in` (64 lanes x 8 x 8 bf16).
- * Writes d16: 64 x 4 fp32, d32: 64 x 16 fp32, t_out: 64 x 8 x 8 bf16.
- * Used by the test suite to pin the lane layouts the kernels assume. */
-int ts_probe_layouts(const void* a, const void* b, float* d16, float* d32,
-                     const void* t_in, void* t_out, void* stream);
-
-/* Runs, in one wave, a global_load_lds_dwordx4 in which lane i loads the
- * 16 bytes src[perm[i]] (src: 64 x 16 bytes, perm: 64 ints in [0, 64)) and
- * copies the resulting 1 KB LDS block to dma_out, then a ds_read_b64_tr_b16
- * in which lane i addresses element 4 i of an LDS array holding the 16-bit
- * values 0..511, writing each lane's four values to tr_out (64 x 8 bytes),
- * then a buffer_load_dwordx4 ... lds through a raw buffer resource over the
- * first valid_bytes (0..1024) of src, lane i at byte offset 16 perm[i], into
- * an LDS block prefilled with 0xdeadbeef, copied to buf_out (1 KB): lanes
- * whose offset is at or past valid_bytes are out of range and must leave
- * zeros.  Used by the test suite to pin gfx950's LDS DMA, transpose-read and
- * buffer range-check behaviour. */
-int ts_probe_lds(const void* src, const int* perm, void* dma_out, void* tr_out, void* buf_out,
-                 int valid_bytes, void* stream);
-
-/* Runs, in one wave over in[0..63], the cross-row reductions the kernels use
- * (maximum and sum over lanes l, l ^ 16, l ^ 32, l ^ 48 by v_permlane16_swap
- * and v_permlane32_swap) and the raw swaps.  Writes out[0..383]: the maximum,
- * the sum, the two results of v_permlane16_swap(in, in) and the two of
- * v_permlane32_swap(in, in), 64 floats each.  Used by the test suite to pin
- * the lane semantics (no counterpart in the reference). */
-int ts_probe_lanes(const float* in, float* out, void* stream);
 
 #ifdef __cplusplus
 }

@@ -155,6 +155,7 @@ def test_route_groups_kv_heads_under_the_cap(monkeypatch):
     q = torch.zeros(150, 24, 256, dtype=torch.bfloat16)
     monkeypatch.setenv(att.DS_ENV, "auto")
     monkeypatch.setattr(att, "DS_FREE_FRACTION", 0.0)  # the cap alone decides
+    monkeypatch.setattr(att, "_device_free_bytes", lambda device: 1 << 50)
     monkeypatch.setattr(att, "DS_MAX_BYTES", (24 * head + 512) * 2)
     assert att._ds_route(lay, q, lib)[1] == 4
     monkeypatch.setattr(att, "DS_MAX_BYTES", (24 * head + 512) * 2 - 2)
@@ -172,9 +173,9 @@ def test_route_groups_kv_heads_under_the_cap(monkeypatch):
 
 def test_route_takes_free_device_memory_above_the_cap(monkeypatch):
     """A workspace above DS_MAX_BYTES still runs in one call when it fits in
-    DS_FREE_FRACTION of the device's free memory; with less free memory the
-    route falls back to KV-head groups, and a workspace within the cap never
-    asks the device."""
+    DS_FREE_FRACTION of the memory the device can supply; with less the route
+    falls back to KV-head groups, and with nothing left to the recompute
+    route."""
     lib = _lib.require_library()
     lay = att.chain_layout(150, [300, 150], 24, 4)
     head = lay.ds_tables(CPU)["head"]
@@ -188,11 +189,26 @@ def test_route_takes_free_device_memory_above_the_cap(monkeypatch):
     monkeypatch.setattr(att, "_device_free_bytes", lambda device: 4 * need - 8)
     assert att._ds_route(lay, q, lib)[1] == 3
     monkeypatch.setattr(att, "_device_free_bytes", lambda device: 0)
-    assert att._ds_route(lay, q, lib)[1] == 1
+    assert att._ds_route(lay, q, lib) is None
 
-    def refuse(device):
-        raise AssertionError("a workspace within the cap must not query the device")
 
-    monkeypatch.setattr(att, "DS_MAX_BYTES", need)
-    monkeypatch.setattr(att, "_device_free_bytes", refuse)
+def test_route_never_takes_more_than_half_the_available_memory(monkeypatch):
+    """Within DS_MAX_BYTES the workspace is still bounded by
+    DS_AVAILABLE_FRACTION of what the device can supply: a nearly full device
+    runs fewer KV heads per call, or the recompute route."""
+    lib = _lib.require_library()
+    lay = att.chain_layout(150, [300, 150], 24, 4)
+    head = lay.ds_tables(CPU)["head"]
+    need = (24 * head + 512) * 2
+    q = torch.zeros(150, 24, 256, dtype=torch.bfloat16)
+    monkeypatch.setenv(att.DS_ENV, "auto")
+    monkeypatch.setattr(att, "DS_MAX_BYTES", 16 << 30)
+    assert need < att.DS_MAX_BYTES and att.DS_AVAILABLE_FRACTION == 0.5
+    monkeypatch.setattr(att, "_device_free_bytes", lambda device: 2 * need)
     assert att._ds_route(lay, q, lib)[1] == 4
+    monkeypatch.setattr(att, "_device_free_bytes", lambda device: 2 * need - 8)
+    assert att._ds_route(lay, q, lib)[1] == 3
+    monkeypatch.setattr(att, "_device_free_bytes", lambda device: 2 * (6 * head + 512) * 2)
+    assert att._ds_route(lay, q, lib)[1] == 1
+    monkeypatch.setattr(att, "_device_free_bytes", lambda device: 2 * (6 * head + 512) * 2 - 8)
+    assert att._ds_route(lay, q, lib) is None

@@ -130,7 +130,10 @@ def test_forest_shapes_of_the_benchmark_configs():
     assert all(kr[0] == (0, 2048) for kr in plan.key_ranges[1:])
 
 
-def test_pack_layout_cumulative_lengths_and_input_order():
+PACK_GOLDEN = json.loads((Path(__file__).parent / "golden" / "pack_layout.json").read_text())
+
+
+def test_pack_layout_cumulative_lengths():
     lengths = [157, 157, 42, 157]
     ancestors = [
         ([torch.zeros(n, 1, 1) for n in chunks], [torch.zeros(n, 1, 1) for n in chunks])
@@ -142,15 +145,43 @@ def test_pack_layout_cumulative_lengths_and_input_order():
     assert layout.cu_lengths.dtype == torch.int32 and layout.cu_lengths.tolist() == cu_l
     assert layout.cu_prefixes.dtype == torch.int32 and layout.cu_prefixes.tolist() == cu_p
     assert layout.prefixes == prefixes and layout.counts == [3, 4, 1, 2]
-    order = ref.pack_input_order(layout.counts)
+    assert cu_l == [0, 157, 314, 356, 513] and cu_p == [0, 806, 1565, 2057, 2706]
+
+
+def _tagged_ancestors(counts):
+    """One distinct tensor per (half, segment, chunk); identity says which."""
+    return [([torch.zeros(c + 1, 1, 1) for c in range(n)], [torch.zeros(c + 1, 1, 1) for c in range(n)])
+            for n in counts]
+
+
+@pytest.mark.parametrize("name", sorted(PACK_GOLDEN))
+def test_pack_layout_input_order_matches_reference(name):
+    """PackLayout.inputs / by_segment against the order the reference's own
+    _PackLayout produced (engine/streaming.py:1636-1650; fixture written by
+    tests/golden/make_pack_golden.py)."""
+    case = PACK_GOLDEN[name]
+    counts = case["counts"]
+    ancestors = _tagged_ancestors(counts)
+    layout = pack_layout([1] * len(counts), ancestors)
+    assert layout.counts == counts
     inputs = layout.inputs(ancestors)
-    assert len(inputs) == 2 * len(order)
-    for pos, (s, c) in enumerate(order):
-        assert inputs[pos] is ancestors[s][0][c]
-        assert inputs[len(order) + pos] is ancestors[s][1][c]
-    regrouped = layout.by_segment(tuple(inputs[: len(order)]))
-    for s, ks in enumerate(regrouped):
-        assert all(a is b for a, b in zip(ks, ancestors[s][0]))
+    assert len(inputs) == len(case["inputs"])
+    for got, (half, s, c) in zip(inputs, case["inputs"]):
+        assert got is ancestors[s][half][c]
+    total = sum(counts)
+    regrouped = layout.by_segment(tuple(inputs[:total]))
+    assert [len(seg) for seg in regrouped] == [len(seg) for seg in case["by_segment"]]
+    for seg, positions in zip(regrouped, case["by_segment"]):
+        assert all(a is inputs[p] for a, p in zip(seg, positions))
+
+
+@pytest.mark.parametrize("name", sorted(PACK_GOLDEN))
+def test_oracle_pack_input_order_matches_reference(name):
+    case = PACK_GOLDEN[name]
+    order = ref.pack_input_order(case["counts"])
+    total = sum(case["counts"])
+    assert [[0, s, c] for s, c in order] == case["inputs"][:total]
+    assert [[1, s, c] for s, c in order] == case["inputs"][total:]
 
 
 @pytest.mark.parametrize("name", sorted(GOLDEN))

@@ -61,3 +61,16 @@ def test_argument_errors_are_reported_without_a_device(monkeypatch):
             raise AssertionError("check() did not raise")
     finally:
         _lib.reset()
+
+
+def test_the_operator_library_exports_no_test_probes():
+    """The hardware probes live in the test-only tests/probe/libts_probe.so."""
+    from tests.probe.build_probe import LIB_PATH as PROBE_LIB
+
+    lib = ctypes.CDLL(str(_lib.LIB_PATH))
+    for name in ("ts_probe_layouts", "ts_probe_lds", "ts_probe_lanes"):
+        assert not hasattr(lib, name), name
+    assert PROBE_LIB.exists(), "build the probe library first (__graft_entry__.build())"
+    probe = ctypes.CDLL(str(PROBE_LIB))
+    for name in ("ts_probe_layouts", "ts_probe_lds", "ts_probe_lanes", "ts_probe_last_error"):
+        assert hasattr(probe, name), name

@@ -8,13 +8,40 @@ thundersync_amd/csrc/common.h, computed here with numpy.
 
 from __future__ import annotations
 
+import ctypes
+
 import numpy as np
 import pytest
 import torch
 
+from tests.probe.build_probe import LIB_PATH as PROBE_LIB
 from thundersync_amd import _lib
 
 pytestmark = pytest.mark.gpu
+
+_P, _INT = ctypes.c_void_p, ctypes.c_int
+PROBE_SIGNATURES = {
+    "ts_probe_last_error": (ctypes.c_char_p, []),
+    "ts_probe_layouts": (_INT, [_P] * 7),
+    "ts_probe_lds": (_INT, [_P] * 5 + [_INT, _P]),
+    "ts_probe_lanes": (_INT, [_P] * 3),
+}
+
+
+def probe_library() -> ctypes.CDLL:
+    """The test-only probe library (tests/probe/libts_probe.so)."""
+    if not PROBE_LIB.exists():
+        pytest.fail(f"{PROBE_LIB} is not built (run __graft_entry__.build())")
+    lib = ctypes.CDLL(str(PROBE_LIB))
+    for name, (restype, argtypes) in PROBE_SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype, fn.argtypes = restype, argtypes
+    return lib
+
+
+def probe_check(lib, status: int, what: str) -> None:
+    if status != 0:
+        raise RuntimeError(f"{what} failed (status {status}): {lib.ts_probe_last_error().decode()}")
 
 
 def expected_16(a, b):
@@ -49,7 +76,7 @@ def expected_32(a, b):
 
 
 def test_mfma_and_transpose_layouts(cuda):
-    lib = _lib.require_library()
+    lib = probe_library()
     rng = np.random.default_rng(0)
     a = rng.integers(-4, 5, size=(64, 8)).astype(np.float32)
     b = rng.integers(-4, 5, size=(64, 8)).astype(np.float32)
@@ -61,7 +88,8 @@ def test_mfma_and_transpose_layouts(cuda):
     d32 = torch.empty(64, 16, dtype=torch.float32, device=cuda)
     t_out = torch.empty(64, 8, 8, dtype=torch.bfloat16, device=cuda)
     print("probe: ts_probe_layouts", flush=True)
-    _lib.check(
+    probe_check(
+        lib,
         lib.ts_probe_layouts(da.data_ptr(), db.data_ptr(), d16.data_ptr(), d32.data_ptr(),
                              dt.data_ptr(), t_out.data_ptr(), _lib.stream_of(da)),
         "ts_probe_layouts",
@@ -77,7 +105,7 @@ def test_mfma_and_transpose_layouts(cuda):
 def test_lds_dma_and_transpose_read_layouts(cuda):
     """Record where global_load_lds_dwordx4 puts each lane's 16 bytes, and the
     lane mapping of ds_read_b64_tr_b16 over contiguous 8-byte rows."""
-    lib = _lib.require_library()
+    lib = probe_library()
     src = torch.arange(64 * 4, dtype=torch.int32, device=cuda)  # 16 bytes per lane: 4l..4l+3
     perm = torch.tensor(np.random.default_rng(1).permutation(64), dtype=torch.int32, device=cuda)
     dma = torch.empty(64 * 4, dtype=torch.int32, device=cuda)
@@ -85,7 +113,7 @@ def test_lds_dma_and_transpose_read_layouts(cuda):
     buf = torch.empty(64 * 4, dtype=torch.int32, device=cuda)
     valid = 16 * 37 + 8  # rows 0..36 in range; row 37 straddles the end; 38.. out of range
     print("probe: ts_probe_lds", flush=True)
-    _lib.check(lib.ts_probe_lds(src.data_ptr(), perm.data_ptr(), dma.data_ptr(), tr.data_ptr(),
+    probe_check(lib, lib.ts_probe_lds(src.data_ptr(), perm.data_ptr(), dma.data_ptr(), tr.data_ptr(),
                                 buf.data_ptr(), valid, _lib.stream_of(src)), "ts_probe_lds")
     torch.cuda.synchronize()
     got = dma.view(64, 4).cpu().numpy()
@@ -113,12 +141,12 @@ def test_lds_dma_and_transpose_read_layouts(cuda):
 def test_cross_row_lane_reductions(cuda):
     """rows_max4 / rows_sum4 combine lanes l, l^16, l^32, l^48 (the attention
     softmax's column reductions), pinned against numpy on distinct values."""
-    lib = _lib.require_library()
+    lib = probe_library()
     x = np.random.default_rng(5).permutation(64).astype(np.float32) - 20.0
     src = torch.tensor(x, device=cuda)
     out = torch.empty(6 * 64, dtype=torch.float32, device=cuda)
     print("probe: ts_probe_lanes", flush=True)
-    _lib.check(lib.ts_probe_lanes(src.data_ptr(), out.data_ptr(), _lib.stream_of(src)), "ts_probe_lanes")
+    probe_check(lib, lib.ts_probe_lanes(src.data_ptr(), out.data_ptr(), _lib.stream_of(src)), "ts_probe_lanes")
     torch.cuda.synchronize()
     got = out.view(6, 64).cpu().numpy()
     rows = x.reshape(4, 16)

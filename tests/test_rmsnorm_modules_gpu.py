@@ -142,3 +142,40 @@ def test_source_swap_skips_fp32(cuda):
     model = tiny_model(cuda, torch.float32)
     use_stable_qwen3_rms_norm(model)
     assert use_compiled_source_rms_norm(model) == 0
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_byte_guard_passes_on_the_device(cuda, dtype):
+    """The byte-identity guard's comparison on the device: every row class of
+    a 4096-wide and a 128-wide norm reproduces torch's bytes, so the module
+    keeps the HIP forward."""
+    from thundersync_amd import rms_norm
+
+    print(f"rms norm byte guard {dtype}", flush=True)
+    rms_norm.reset_primal_checks()
+    g = torch.Generator(device=cuda).manual_seed(9)
+    for width in (4096, 128):
+        w = torch.linspace(0.4, 3.0, width, device=cuda).to(dtype)
+        for rows in (1, 2, 3, 5, 12, 31, 100, 300, 513, 2049):
+            x = torch.randn(rows, width, device=cuda, dtype=dtype, generator=g)
+            assert rms_norm.hip_takes(x, w)
+            assert rms_norm.primal_matches_stock(x, w, 1e-6), (width, rows)
+            y, _ = rms_norm.primal_forward(x, w, 1e-6)
+            assert torch.equal(y, rms_norm.stock_forward(x, w, 1e-6)[0])
+    assert all(rms_norm._MATCHES.values())
+
+
+def test_swapped_module_takes_stock_forward_for_refused_shapes(cuda):
+    """A single row that torch sums across work-groups is refused by the
+    kernel; the swapped module then runs the stock forward."""
+    from transformers.models.qwen3.modeling_qwen3 import Qwen3RMSNorm
+
+    from thundersync_amd import rms_norm
+
+    width = 1 << 18
+    model = torch.nn.Sequential(Qwen3RMSNorm(width, eps=1e-6)).to(cuda, torch.bfloat16)
+    x = torch.randn(1, width, device=cuda, dtype=torch.bfloat16)
+    want = model(x).detach()
+    rms_norm.use_stable_qwen3_rms_norm(model)
+    assert not rms_norm.hip_takes(x, model[0].weight)
+    assert torch.equal(model(x).detach(), want)

@@ -87,3 +87,33 @@ def test_forest_logprobs_stats_without_a_device(monkeypatch):
     assert stats.physical_tokens == plan.n_physical and stats.logical_tokens == 3 * 3 + 3 + 4 + 1
     assert stats.padded_tokens == 3 * 7 and stats.projected_positions == plan.score_src.numel()
     assert calls[0] == plan.score_src.numel() and calls[1] == plan.n_physical
+
+
+def test_step_stats_ratios_and_text():
+    """engine/step.py:170-194: both ratios are against the padded rectangle."""
+    from thundersync_amd.step import StepStats
+
+    stats = StepStats(physical_tokens=10, logical_tokens=16, padded_tokens=21, projected_positions=7,
+                      logical_scored=8)
+    assert stats.token_compression == 21 / 10
+    assert stats.projection_reduction == 21 / 7
+    assert str(stats) == "tokens 21 -> 10 (2.10x)   projected 21 -> 7 (3.00x)"
+    assert StepStats(0, 0, 0, 0, 0).token_compression == 0.0
+
+
+def test_split_by_trajectory_concatenates_a_repeated_id():
+    """Trajectory ids default to 0 and need not be unique: every token of an
+    id is returned, in logical order, as the reference's mask selection does
+    (engine/step.py:483-486)."""
+    trajs = [forest.Trajectory([forest.Segment.prompt([1, 2, 3]), forest.Segment.action(body)], group_id=0,
+                               traj_id=t)
+             for t, body in zip((0, 1, 0), ([4, 5, 6], [4, 5, 7, 8], [9]))]
+    plan = forest.compile_plan(forest.build_forest(trajs))
+    logical = torch.arange(plan.logical_to_slot.numel(), dtype=torch.float32)
+    per = split_by_trajectory(plan, logical)
+    traj = plan.logical_traj
+    # id 0 comes back after id 1: two separate runs of it in logical order
+    assert torch.unique_consecutive(traj).tolist() == [0, 1, 0]
+    assert sorted(per) == [0, 1]
+    for tid in (0, 1):
+        assert torch.equal(per[tid], logical[traj == tid])

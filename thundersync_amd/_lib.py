@@ -39,12 +39,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "ts_hip_version": (ctypes.c_char_p, []),
     "ts_hip_last_error": (ctypes.c_char_p, []),
     "ts_rmsnorm_fwd": (_INT, [_P, _P, _P, _P, _I64, _I64, _F, _INT, _P]),
+    "ts_rmsnorm_supported": (_INT, [_I64, _I64, _P]),
     "ts_rmsnorm_bwd_workspace": (_I64, [_I64, _I64]),
     "ts_rmsnorm_bwd": (_INT, [_P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _INT, _P]),
     "ts_rmsnorm_bwd_noalloc": (_INT, [_P, _P, _P, _P, _P, _P, _I64, _I64, _INT, _P]),
-    "ts_probe_layouts": (_INT, [_P, _P, _P, _P, _P, _P, _P]),
-    "ts_probe_lds": (_INT, [_P, _P, _P, _P, _P, _INT, _P]),
-    "ts_probe_lanes": (_INT, [_P, _P, _P]),
     "ts_device_clocks": (_INT, [_INT, ctypes.POINTER(_INT), ctypes.POINTER(_INT), ctypes.POINTER(_INT),
                                 ctypes.POINTER(_INT)]),
     "ts_timing_enable": (_INT, [_INT]),

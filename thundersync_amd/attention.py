@@ -429,25 +429,33 @@ def _validate_call(layout: AttnLayout, query: torch.Tensor, keys, values) -> Non
 
 # dS workspace (bytes) the backward may allocate for the dS route (dK/dV
 # kernels store dS, dQ = dS K from it; about 2 bytes per visible pair and
-# head): DS_MAX_BYTES always, and a workspace above it when it fits in
-# DS_FREE_FRACTION of the device's free memory (an MI355X holds 288 GB; the
-# reference's 16-trajectory retained-chunk pack needs ~52 GB).  A problem
-# above the cap runs the route over groups of KV heads, as many per call as
-# fit (KV heads are independent: their query heads, dS and gradients do not
-# mix, and the grouped calls give the one-call gradients bit for bit); one
-# whose single KV head does not fit, or any under THUNDERSYNC_ATTN_DS=off,
-# runs the route that recomputes S and dP in the dQ kernel.
+# head): up to DS_MAX_BYTES, and a workspace above it when it fits in
+# DS_FREE_FRACTION of the memory the device can still supply (an MI355X holds
+# 288 GB; the reference's 16-trajectory retained-chunk pack needs ~52 GB);
+# never more than DS_AVAILABLE_FRACTION of that memory, so a device that is
+# nearly full takes the route over fewer KV heads, or not at all, instead of
+# failing inside the backward.  The memory the device can supply is its free
+# memory plus what torch's allocator holds unused.  A problem above the cap
+# runs the route over groups of KV heads, as many per call as fit (KV heads
+# are independent: their query heads, dS and gradients do not mix, and the
+# grouped calls give the one-call gradients bit for bit); one whose single KV
+# head does not fit, one whose workspace allocation fails all the same, or
+# any under THUNDERSYNC_ATTN_DS=off, runs the route that recomputes S and dP
+# in the dQ kernel.
 DS_MAX_BYTES = 16 << 30
 DS_FREE_FRACTION = 0.25
+DS_AVAILABLE_FRACTION = 0.5
 DS_ENV = "THUNDERSYNC_ATTN_DS"
 
 
 def _device_free_bytes(device: torch.device) -> int:
-    """Free memory of `device` in bytes (0 for a host device)."""
+    """Memory `device` can still supply in bytes: free device memory plus the
+    allocator's reserved but unallocated bytes (0 for a host device)."""
     if device.type != "cuda":
         return 0
     free, _total = torch.cuda.mem_get_info(device)
-    return int(free)
+    cached = torch.cuda.memory_reserved(device) - torch.cuda.memory_allocated(device)
+    return int(free) + max(int(cached), 0)
 
 
 def _ds_route(layout: AttnLayout, query: torch.Tensor, lib):
@@ -462,9 +470,11 @@ def _ds_route(layout: AttnLayout, query: torch.Tensor, lib):
     # a call over n KV heads needs (n * group * head + 512) elements: every
     # query head's part, then the sink block
     per_kv_head = group * max(tabs["head"], 1)
+    available = _device_free_bytes(query.device)
     cap = DS_MAX_BYTES
     if (layout.hkv * per_kv_head + 512) * 2 > cap and DS_FREE_FRACTION > 0:
-        cap = max(cap, int(_device_free_bytes(query.device) * DS_FREE_FRACTION))
+        cap = max(cap, int(available * DS_FREE_FRACTION))
+    cap = min(cap, int(available * DS_AVAILABLE_FRACTION))
     kv_heads = min(layout.hkv, (cap // 2 - 512) // per_kv_head)
     if kv_heads < 1:
         return None
@@ -542,6 +552,14 @@ class _Attention(torch.autograd.Function):
         problem = layout.problem(query.device, runs.data_ptr(), ctx.scale, query.dtype, query.shape[2])
         check_tables(layout, problem, host, query.device)
         ds = _ds_route(layout, query, lib)
+        if ds is not None:
+            tabs, kv_heads = ds
+            group = layout.hq // layout.hkv
+            try:
+                work = torch.empty(kv_heads * group * tabs["head"] + 512, dtype=query.dtype,
+                                   device=query.device)
+            except torch.cuda.OutOfMemoryError:
+                ds = None
         with operator_range("hip_attention_backward", rows=layout.q_rows, segments=len(layout.seg_q),
                             ds_route=ds is not None):
             if ds is None:
@@ -552,9 +570,6 @@ class _Attention(torch.autograd.Function):
                     f"ts_attn_bwd(rows={layout.q_rows}, hq={layout.hq}, hkv={layout.hkv})",
                 )
             else:
-                tabs, kv_heads = ds
-                group = layout.hq // layout.hkv
-                work = torch.empty(kv_heads * group * tabs["head"] + 512, dtype=query.dtype, device=query.device)
                 rows = [_rows(t) for t in (query, out, dout, dq)]
                 keep = []
                 for hk0 in range(0, layout.hkv, kv_heads):

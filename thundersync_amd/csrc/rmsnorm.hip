@@ -776,6 +776,19 @@ int ts_rmsnorm_fwd(const void* x, const void* w, void* y, float* rstd, int64_t r
   return TS_ERR_INVALID;
 }
 
+int ts_rmsnorm_supported(int64_t rows, int64_t width, void* stream) {
+  if (rows < 0 || width <= 0 || width > (1 << 24)) return 0;
+  if (rows > 0) {
+    ts::RowReduce c;
+    if (!ts::torch_row_reduce(rows, width, ts::stream_cus((hipStream_t)stream), c)) return 0;
+    const bool lanes = c.bh == 1 && c.bw <= ts::kWave && (!c.vec || width % 4 == 0);
+    if (!lanes && rows > 0x7fffffff) return 0;
+  }
+  const ts::Geometry g = ts::pick(width, 0);
+  if (g.lpr == 0 && (width + 4) * (int64_t)sizeof(float) > 160 * 1024) return 0;
+  return 1;
+}
+
 int64_t ts_rmsnorm_bwd_workspace(int64_t rows, int64_t width) {
   if (rows <= 0 || width <= 0) return 0;
   return ts::bwd_parts(rows, width) * width * (int64_t)sizeof(float);

@@ -21,7 +21,8 @@ is the ``[chunk, V]`` bf16 dlogits block plus a workspace of vocabulary-range
 partial sums for grad_hidden when one block's row tiles do not fill the GPU,
 and the fp32 ``[V, D]`` accumulator when the weight gradient is needed.
 
-bf16 only, GPU only: other dtypes and CPU tensors raise.
+bf16 or fp16 (one element type per call), GPU only: other dtypes and CPU
+tensors raise.
 """
 
 from __future__ import annotations

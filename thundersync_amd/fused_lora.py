@@ -16,7 +16,8 @@ are cast to the activation dtype before the products, as the reference does.
 
 Activations must be bf16 or fp16 CUDA tensors (the weight of the same dtype)
 with ``in`` and ``out`` multiples of 8;
-anything else raises -- there is no host fallback.  The caller merges before
+anything else raises -- there is no host fallback.  ``fuse_merged_lora_forward``
+converts only the layers that meet this (and leaves the rest as they were).  The caller merges before
 and unmerges after (the optimizer step moves A and B and leaves the merged
 weight stale), which the two module-level functions do through the layer's
 own ``merge`` / ``unmerge`` (PEFT's ``LoraLayer`` API).
@@ -155,10 +156,34 @@ def _adapter_of(layer: torch.nn.Module, adapter: str):
     return a_dict[adapter].weight, b_dict[adapter].weight, scale
 
 
+# largest adapter rank the backward's rank products take (ts_lora_bwd)
+MAX_RANK = 256
+
+
+def fusable(base: torch.nn.Linear, a_weight: torch.Tensor, b_weight: torch.Tensor) -> bool:
+    """Whether the kernels can run a layer: a bf16 or fp16 GPU base weight
+    with ``in`` and ``out`` multiples of 8, adapters on its device that fit
+    it, a rank of at most :data:`MAX_RANK`, and a loaded library.  A layer
+    that fails stays unmerged and keeps its own forward."""
+    w = base.weight
+    if not w.is_cuda or w.dtype not in (torch.bfloat16, torch.float16) or w.dim() != 2:
+        return False
+    out_f, in_f = w.shape
+    rank = a_weight.shape[0] if a_weight.dim() == 2 else -1
+    if in_f % 8 or out_f % 8 or not 0 < rank <= MAX_RANK:
+        return False
+    if tuple(a_weight.shape) != (rank, in_f) or tuple(b_weight.shape) != (out_f, rank):
+        return False
+    if a_weight.device != w.device or b_weight.device != w.device:
+        return False
+    return _lib.library() is not None
+
+
 def fuse_merged_lora_forward(peft_model: torch.nn.Module) -> int:
     """Merge each LoRA layer's active adapter into its base weight in place and
     route the layer through :class:`FusedLoRALinear`; returns how many layers
-    were converted (accel/fused_lora.py:70-108).  Call
+    were converted (accel/fused_lora.py:70-108).  Layers the kernels cannot
+    run (:func:`fusable`) are left unmerged and unconverted.  Call
     :func:`unfuse_merged_lora_forward` before the optimizer step."""
     adapter = _active_adapter(peft_model, strict=True)
     converted = 0
@@ -168,6 +193,8 @@ def fuse_merged_lora_forward(peft_model: torch.nn.Module) -> int:
         base = getattr(layer, "base_layer", None)
         parts = _adapter_of(layer, adapter)
         if parts is None or not isinstance(base, torch.nn.Linear):
+            continue
+        if not fusable(base, parts[0], parts[1]):
             continue
         layer.merge(adapter_names=[adapter])
         a_weight, b_weight, scale = parts

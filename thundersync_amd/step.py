@@ -104,11 +104,18 @@ class StepStats:
 
     @property
     def token_compression(self) -> float:
-        return self.logical_tokens / max(self.physical_tokens, 1)
+        """Forward tokens saved by padding removal and prefix sharing together."""
+        return self.padded_tokens / max(self.physical_tokens, 1)
 
     @property
     def projection_reduction(self) -> float:
+        """Unembedding rows saved by projecting only the scored positions."""
         return self.padded_tokens / max(self.projected_positions, 1)
+
+    def __str__(self) -> str:
+        return (f"tokens {self.padded_tokens:,} -> {self.physical_tokens:,} ({self.token_compression:.2f}x)   "
+                f"projected {self.padded_tokens:,} -> {self.projected_positions:,} "
+                f"({self.projection_reduction:.2f}x)")
 
 
 def _project(hidden, weight, rows, targets, chunk):
@@ -165,8 +172,14 @@ def split_by_trajectory(plan, logical: torch.Tensor) -> dict[int, torch.Tensor]:
     """``[L]`` logprobs as ``{trajectory id: its logprobs}`` (engine/step.py:475-490).
 
     The logical order keeps each trajectory's tokens together, so the pieces
-    are the runs of equal ids in ``plan.logical_traj``.
+    are normally the runs of equal ids in ``plan.logical_traj``.  Trajectory
+    ids need not be unique (``Trajectory.traj_id`` defaults to 0): when an id
+    comes back after another, its runs are concatenated in logical order, as
+    the reference's mask selection does.
     """
     ids, counts = torch.unique_consecutive(plan.logical_traj, return_counts=True)
-    pieces = dict(zip((int(i) for i in ids.tolist()), logical.split(counts.tolist())))
-    return {tid: pieces[tid] for tid in sorted(pieces)}
+    runs = logical.split(counts.tolist())
+    pieces: dict[int, list[torch.Tensor]] = {}
+    for tid, run in zip((int(i) for i in ids.tolist()), runs):
+        pieces.setdefault(tid, []).append(run)
+    return {tid: (p[0] if len(p) == 1 else torch.cat(p)) for tid, p in sorted(pieces.items())}
