@@ -1,5 +1,5 @@
 #!/usr/bin/env python3
-"""Benchmark of the hot path on one MI355X; prints ONE JSON line.
+"""Benchmark of the hot path on one MI355X; its last line is ONE JSON summary.
 
 Workloads (synthetic data drawn from fixed seeds):
 
@@ -7,25 +7,34 @@ Workloads (synthetic data drawn from fixed seeds):
   2048-token prompt and 8 sibling completions of lengths U[256, 4096],
   32 query / 8 KV heads, head dim 128, bf16; TFLOP/s counted as
   14 * D * Hq * (exactly visible query/key pairs).
-* ``secondary[0]``: C4 chunked retained-KV attention, forward + backward --
-  4 groups of a 1024-token prompt and 4 completions U[1024, 16384], every
-  512-token query chunk over the group's prompt chunks, its trajectory's
-  earlier chunks and itself, K/V held as one tensor per chunk.
-* ``secondary[1]``: C3 fused logprob + entropy, forward + gradient wrt
-  hidden -- hidden [16384, 4096], head [151936, 4096], 70% of rows scored
-  and gated before the projection (the reference's production schedule),
-  frozen head; scored tokens/s, 6 * N * V * D FLOP.
-* ``secondary[2]``: C3 ungated -- the same operator over all 16,384 rows;
-  projected tokens/s.
-* ``secondary[3]``: RMSNorm forward + backward on [16384, 4096] bf16; GB/s.
-* ``secondary[4]``: boundary-adjoint reduction -- an existing parent
-  adjoint plus 16 consumer adjoints of [4096, 4096] bf16 summed in fp32 into
-  a new tensor; GB/s of inputs read plus output written.
-* ``secondary[5]``: merged-weight LoRA linear, forward + backward (dx, dA,
-  dB) at a C5 q_proj slice: 16384 tokens, 4096 -> 4096, rank 16.
-* ``--only c5`` (not in the default run): one GRPO-shaped update of the
-  Qwen3-8B-shaped C5 decoder through every operator of the build, wall time
-  and per-kernel breakdown.
+* ``secondary`` rows, by name:
+  - ``C4``: chunked retained-KV attention, forward + backward -- 4 groups of
+    a 1024-token prompt and 4 completions U[1024, 16384], every 512-token
+    query chunk over the group's prompt chunks, its trajectory's earlier
+    chunks and itself, K/V held as one tensor per chunk;
+  - ``branch_d256``: the reference's own bottom-right branch shape at head
+    dim 256 (9288 query rows over 3000 + 9288 keys, 24/4 heads), with
+    ``vs_baseline`` against the reference's published FA4 time;
+  - ``C3_gated``: fused logprob + entropy, forward + gradient wrt hidden --
+    hidden [16384, 4096], head [151936, 4096], 70% of rows scored and gated
+    before the projection (the reference's production schedule), frozen
+    head; scored tokens/s, 6 * N * V * D FLOP;
+  - ``C3_ungated``: the same operator over all 16,384 rows; projected
+    tokens/s;
+  - ``rmsnorm``: RMSNorm forward + backward on [16384, 4096] bf16; GB/s;
+  - ``adjoint``: boundary-adjoint reduction -- an existing parent adjoint
+    plus 16 consumer adjoints of [4096, 4096] bf16 summed in fp32 into a new
+    tensor; GB/s of inputs read plus output written;
+  - ``lora``: merged-weight LoRA linear, forward + backward (dx, dA, dB) at
+    a C5 q_proj slice: 16384 tokens, 4096 -> 4096, rank 16;
+  - ``C5``: one GRPO-shaped update of the Qwen3-8B-shaped decoder through
+    every operator of the build; seconds per update and per-kernel
+    breakdown.
+
+Output: one ``bench_detail`` line with every workload's full record
+(per-kernel times, configs, device memory), then the summary line the
+driver reads, which carries the contract's keys for the headline workload
+and one short row per secondary.
 
 The MFMA peak is derived from the device's CU count and peak engine clock
 (4096 dense bf16 FLOP per CU per clock), the HBM peak is the published
@@ -133,12 +142,16 @@ def repeat_for(fn, seconds=CPU_BASELINE_SECONDS, max_reps=20000):
 
 
 def timed(step, steps, warmup, kernels):
-    """(ms per step, {kernel: (avg ms per launch, launches per step)}).
+    """(ms per step, {kernel: (avg ms per launch, launches per step)}, memory).
 
     The wall clock times `steps` steps with the library's per-kernel HIP-event
     brackets off (two event records per launch are instrumentation, not the
     job); a second pass of the same steps with the brackets on gives the
-    per-kernel device times."""
+    per-kernel device times.  ``memory``: the device memory allocated when
+    the timed steps start (inputs, resident state) and the peak allocated
+    while they run (``torch.cuda.max_memory_allocated``), in bytes; the
+    difference is what a step takes on top (workspaces, activations,
+    gradients)."""
     import torch
 
     from thundersync_amd._lib import KernelTimer
@@ -146,11 +159,15 @@ def timed(step, steps, warmup, kernels):
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
+    resident = torch.cuda.memory_allocated()
+    torch.cuda.reset_peak_memory_stats()
     t0 = time.perf_counter()
     for _ in range(steps):
         step()
     torch.cuda.synchronize()
     t1 = time.perf_counter()
+    peak = torch.cuda.max_memory_allocated()
+    mem = {"resident_bytes": int(resident), "peak_bytes": int(peak), "step_bytes": int(peak - resident)}
     with KernelTimer():
         for _ in range(steps):
             step()
@@ -160,7 +177,7 @@ def timed(step, steps, warmup, kernels):
             total, n = KernelTimer.read(k)
             if n:
                 per[k] = (total / n, n / steps)
-    return (t1 - t0) * 1e3 / steps, per
+    return (t1 - t0) * 1e3 / steps, per, mem
 
 
 # Sub-millisecond secondaries (RMSNorm, boundary adjoints) repeat their step
@@ -169,19 +186,18 @@ def timed(step, steps, warmup, kernels):
 SHORT_STEPS, SHORT_WARMUP = 200, 20
 
 
-def measured_traffic(workload, kernel):
-    """HBM bytes per launch of `kernel` in `workload` from profiles/traffic.json:
-    rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs of this script with
-    ``--only <workload>``, each scaled by what the counter reads for a plain
-    device copy of known size.  None when the table has no entry."""
+def measured_entry(workload, kernel) -> dict:
+    """The profiles/traffic.json entry of `kernel` in `workload` ({} when none):
+    HBM bytes per launch from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE runs
+    of this script with ``--only <workload>``, each scaled by what the counter
+    reads for a plain device copy of known size, and, where measured, the
+    engine clock the kernel ran at (GRBM_GUI_ACTIVE cycles per XCD over the
+    dispatch's duration)."""
     path = ROOT / "profiles" / "traffic.json"
     if not path.exists():
-        return None, None
+        return {}
     table = json.loads(path.read_text())
-    entry = table.get("workloads", {}).get(workload, {}).get(kernel)
-    if entry is None:
-        return None, None
-    return entry["traffic_bytes"], entry["measured_at_commit"]
+    return table.get("workloads", {}).get(workload, {}).get(kernel) or {}
 
 
 def roofline_of(per, work_per_step, unit, peak, workload):
@@ -195,8 +211,9 @@ def roofline_of(per, work_per_step, unit, peak, workload):
     avg_ms, launches = per[name]
     per_launch = work_per_step[name] / launches
     achieved = per_launch / (avg_ms * 1e-3) / (1e12 if unit == "TFLOP/s" else 1e9)
-    traffic, commit = measured_traffic(workload, name)
-    return {
+    entry = measured_entry(workload, name)
+    traffic = entry.get("traffic_bytes")
+    out = {
         "kernel": name,
         "bound": "mfma" if unit == "TFLOP/s" else "hbm",
         "achieved": round(achieved, 2),
@@ -204,11 +221,19 @@ def roofline_of(per, work_per_step, unit, peak, workload):
         "unit": unit,
         "frac": round(achieved / peak, 4),
         "traffic": traffic,
-        "traffic_source": f"profiles/traffic.json, measured at commit {commit}" if traffic is not None else None,
+        "traffic_source": (f"profiles/traffic.json, measured at commit {entry.get('measured_at_commit')}"
+                           if traffic is not None else None),
         "avg_launch_ms": round(avg_ms, 4),
         "launches_per_step": launches,
         "work_per_launch": per_launch,
     }
+    clock = entry.get("clock_mhz")
+    if clock and unit == "TFLOP/s":
+        # context, not the roofline: the MFMA peak at the clock the chip held
+        # while this kernel ran, and the kernel's fraction of that
+        out["sustained_clock_mhz"] = round(clock)
+        out["frac_at_sustained_clock"] = round(achieved / (peak * clock / PEAKS["clock_mhz"]), 4)
+    return out
 
 
 # ---------------------------------------------------------------------------
@@ -253,7 +278,7 @@ def bench_attention(args, device):
         out.backward(dout)
 
     kernels = ["attention.fwd_kernel", "attention.delta_kernel", "attention.dq_kernel", "attention.dkdv_kernel"]
-    ms, per = timed(step, args.steps, args.warmup, kernels)
+    ms, per, mem = timed(step, args.steps, args.warmup, kernels)
     flop = 14 * d * hq * pairs
     work = {
         "attention.fwd_kernel": 4 * d * hq * pairs,
@@ -265,6 +290,7 @@ def bench_attention(args, device):
         "value": round(flop / (ms * 1e-3) / 1e12, 2),
         "unit": "TFLOP/s",
         "ms_per_step": round(ms, 4),
+        "memory": mem,
         "roofline": roofline_of(per, work, "TFLOP/s", PEAKS["bf16_tflops"], "attention"),
         "kernels": {k: {"avg_ms": round(a, 4), "launches_per_step": n} for k, (a, n) in per.items()},
         "config": {
@@ -354,7 +380,7 @@ def bench_fa4_branch(args, device):
         out.backward(dout)
 
     kernels = ["attention.fwd_kernel", "attention.delta_kernel", "attention.dq_kernel", "attention.dkdv_kernel"]
-    ms, per = timed(step, args.steps, args.warmup, kernels)
+    ms, per, mem = timed(step, args.steps, args.warmup, kernels)
     flop = 14 * d * hq * pairs
     work = {
         "attention.fwd_kernel": 4 * d * hq * pairs,
@@ -369,6 +395,7 @@ def bench_fa4_branch(args, device):
         "value": round(tflops, 2),
         "unit": "TFLOP/s",
         "ms_per_step": round(ms, 4),
+        "memory": mem,
         "vs_baseline": round(tflops / reference_tflops, 4),
         "baseline": {"ms": FA4_BRANCH_REFERENCE_MS, "tflops": round(reference_tflops, 1),
                      "what": "the reference's FA4 fwd+bwd at this shape on unstated NVIDIA hardware "
@@ -490,7 +517,7 @@ def bench_chunked(args, device):
         out.backward(dout)
 
     kernels = ["attention.fwd_kernel", "attention.delta_kernel", "attention.dq_kernel", "attention.dkdv_kernel"]
-    ms, per = timed(step, args.steps, args.warmup, kernels)
+    ms, per, mem = timed(step, args.steps, args.warmup, kernels)
     flop = 14 * d * hq * pairs
     work = {
         "attention.fwd_kernel": 4 * d * hq * pairs,
@@ -503,6 +530,7 @@ def bench_chunked(args, device):
         "value": round(flop / (ms * 1e-3) / 1e12, 2),
         "unit": "TFLOP/s",
         "ms_per_step": round(ms, 4),
+        "memory": mem,
         "roofline": roofline_of(per, work, "TFLOP/s", PEAKS["bf16_tflops"], "chunked"),
         "kernels": {k: {"avg_ms": round(a, 4), "launches_per_step": n} for k, (a, n) in per.items()},
         "config": {
@@ -597,7 +625,7 @@ def bench_logprob(args, device, gate: bool = True):
 
     kernels = ["logprob.fwd_stats_kernel", "logprob.target_logit_kernel", "logprob.combine_kernel",
                "logprob.dlogits_kernel", "logprob.grad_hidden_kernel", "logprob.grad_hidden_reduce_kernel"]
-    ms, per = timed(step, args.steps, args.warmup, kernels)
+    ms, per, mem = timed(step, args.steps, args.warmup, kernels)
     gemm = 2 * rows * v * d
     work = {
         "logprob.fwd_stats_kernel": gemm,
@@ -616,6 +644,7 @@ def bench_logprob(args, device, gate: bool = True):
         "tflops": round(flop / (ms * 1e-3) / 1e12, 2),
         "mfma_frac": round(flop / (ms * 1e-3) / 1e12 / PEAKS["bf16_tflops"], 4),
         "ms_per_step": round(ms, 4),
+        "memory": mem,
         "roofline": roofline_of({k: x for k, x in per.items() if work[k]}, work, "TFLOP/s", PEAKS["bf16_tflops"],
                                 "logprob" if gate else "logprob_ungated"),
         "kernels": {k: {"avg_ms": round(x, 4), "launches_per_step": m} for k, (x, m) in per.items()},
@@ -683,7 +712,7 @@ def bench_rmsnorm(args, device):
     kernels = ["rmsnorm.rmsnorm_fwd_lanes", "rmsnorm.rmsnorm_fwd_rowwave", "rmsnorm.rmsnorm_bwd_vec",
                "rmsnorm.rmsnorm_dw_reduce"]
     steps, warmup = max(args.steps, SHORT_STEPS), max(args.warmup, SHORT_WARMUP)
-    ms, per = timed(step, steps, warmup, kernels)
+    ms, per, mem = timed(step, steps, warmup, kernels)
     fwd_bytes = 4 * r * w_ + 4 * r + 2 * w_
     bwd_bytes = 6 * r * w_ + 4 * r + 2 * w_ + 4 * w_
     work = {"rmsnorm.rmsnorm_fwd_lanes": fwd_bytes, "rmsnorm.rmsnorm_fwd_rowwave": fwd_bytes,
@@ -693,6 +722,7 @@ def bench_rmsnorm(args, device):
         "value": round((fwd_bytes + bwd_bytes) / (ms * 1e-3) / 1e9, 1),
         "unit": "GB/s",
         "ms_per_step": round(ms, 4),
+        "memory": mem,
         "roofline": roofline_of({k: x for k, x in per.items() if work[k]}, work, "GB/s", PEAKS["hbm_gbs"], "rmsnorm"),
         "kernels": {k: {"avg_ms": round(x, 4), "launches_per_step": m} for k, (x, m) in per.items()},
         "steps": steps,
@@ -753,7 +783,7 @@ def bench_adjoint(args, device):
 
     kernels = ["adjoint.reduce_kernel"]
     steps, warmup = max(args.steps, SHORT_STEPS), max(args.warmup, SHORT_WARMUP)
-    ms, per = timed(step, steps, warmup, kernels)
+    ms, per, mem = timed(step, steps, warmup, kernels)
     n = ADJOINT_SHAPE[0] * ADJOINT_SHAPE[1]
     nbytes = (ADJOINT_DEGREE + 1) * n * 2 + n * 2  # every input read once, the output written once
     result = {
@@ -761,6 +791,7 @@ def bench_adjoint(args, device):
         "value": round(nbytes / (ms * 1e-3) / 1e9, 1),
         "unit": "GB/s",
         "ms_per_step": round(ms, 4),
+        "memory": mem,
         "roofline": roofline_of(per, {"adjoint.reduce_kernel": nbytes}, "GB/s", PEAKS["hbm_gbs"], "adjoint"),
         "kernels": {k: {"avg_ms": round(x, 4), "launches_per_step": m} for k, (x, m) in per.items()},
         "steps": steps,
@@ -823,7 +854,7 @@ def bench_lora(args, device):
 
     kernels = ["lora.fwd_kernel", "lora.grad_x_kernel", "lora.grad_x_reduce_kernel", "lora.rank_kernel",
                "lora.grad_a_kernel", "lora.grad_b_kernel", "lora.reduce_kernel"]
-    ms, per = timed(step, args.steps, args.warmup, kernels)
+    ms, per, mem = timed(step, args.steps, args.warmup, kernels)
     gemm = 2 * t * fin * fout
     adapter = 2 * t * r * (fin + fout)  # g B and x A^T, then u^T x and g^T t: the same count again
     work = {"lora.fwd_kernel": gemm, "lora.grad_x_kernel": gemm, "lora.rank_kernel": adapter,
@@ -839,6 +870,7 @@ def bench_lora(args, device):
         "value": round(flop / (ms * 1e-3) / 1e12, 2),
         "unit": "TFLOP/s",
         "ms_per_step": round(ms, 4),
+        "memory": mem,
         "roofline": roofline_of({k: v for k, v in per.items() if work[k]}, work, "TFLOP/s", PEAKS["bf16_tflops"],
                                 "lora"),
         "adapter_gradients": {"ms": round(adapter_ms, 4), "bytes": adapter_bytes,
@@ -961,7 +993,7 @@ def bench_c5(args, device):
                "lora.fwd_kernel", "lora.grad_x_kernel", "lora.grad_x_reduce_kernel", "lora.rank_kernel",
                "lora.grad_a_kernel", "lora.grad_b_kernel", "lora.reduce_kernel"]
     steps, warmup = max(1, min(args.steps, 3)), max(1, min(args.warmup, 1))
-    ms, per = timed(update, steps, warmup, kernels)
+    ms, per, mem = timed(update, steps, warmup, kernels)
     p, layers, d, hq = plan.n_physical, 36, 128, 32
     pairs = att.forest_layout(plan, 32, 8).visible_pairs()
     proj = 2 * p * (4096 * 4096 * 2 + 4096 * 1024 * 2)  # q, k, v, o of one layer
@@ -991,6 +1023,7 @@ def bench_c5(args, device):
         "unit": "s",
         "higher_is_better": False,
         "ms_per_step": round(ms, 1),
+        "memory": mem,
         "library_kernel_ms": round(ours, 1),
         "other_ms": round(ms - ours, 1),
         "kernels": kern,
@@ -1054,30 +1087,66 @@ def main():
         out["ms_per_step"] = att.pop("ms_per_step")
         out["config"] = att.pop("config")
         out["roofline"] = att.pop("roofline")
+        out["memory"] = att.pop("memory")
         out["kernels"] = att.pop("kernels")
         if "cpu_baseline" in att:
             out["cpu_baseline"] = att.pop("cpu_baseline")
-    if args.only in ("all", "chunked"):
-        out["secondary"].append(bench_chunked(args, device))
-    if args.only in ("all", "fa4_branch"):
-        out["secondary"].append(bench_fa4_branch(args, device))
-    if args.only in ("all", "logprob"):
-        out["secondary"].append(bench_logprob(args, device))
-    if args.only in ("all", "logprob_ungated"):
-        out["secondary"].append(bench_logprob(args, device, gate=False))
-    if args.only in ("all", "rmsnorm"):
-        out["secondary"].append(bench_rmsnorm(args, device))
-    if args.only in ("all", "adjoint"):
-        out["secondary"].append(bench_adjoint(args, device))
-    if args.only in ("all", "lora"):
-        out["secondary"].append(bench_lora(args, device))
-    if args.only == "c5":
-        out["secondary"].append(bench_c5(args, device))
+    runs = (("C4", "chunked", lambda: bench_chunked(args, device)),
+            ("branch_d256", "fa4_branch", lambda: bench_fa4_branch(args, device)),
+            ("C3_gated", "logprob", lambda: bench_logprob(args, device)),
+            ("C3_ungated", "logprob_ungated", lambda: bench_logprob(args, device, gate=False)),
+            ("rmsnorm", "rmsnorm", lambda: bench_rmsnorm(args, device)),
+            ("adjoint", "adjoint", lambda: bench_adjoint(args, device)),
+            ("lora", "lora", lambda: bench_lora(args, device)),
+            ("C5", "c5", lambda: bench_c5(args, device)))
+    for name, only, run in runs:
+        if args.only in ("all", only):
+            torch.cuda.empty_cache()
+            result = run()
+            result["name"] = name
+            out["secondary"].append(result)
     props = torch.cuda.get_device_properties(device)
     out["device"] = {"name": props.name, "arch": getattr(props, "gcnArchName", ""),
                      "cus": props.multi_processor_count}
     out["peaks"] = dict(PEAKS)
-    print(json.dumps(out), flush=True)
+    # the full record first, then the one-line summary the driver reads last
+    print(json.dumps({"bench_detail": out}), flush=True)
+    print(json.dumps(summary(out), separators=(",", ":")), flush=True)
+
+
+SECONDARY_FIELDS = ["value", "unit", "ms_per_step", "dominant_kernel", "dominant_frac", "peak_mem_GB",
+                    "cpu_baseline"]
+
+
+def summary(out: dict) -> dict:
+    """The headline line: the contract's keys, the roofline and CPU baseline of
+    the headline workload, and one short row per secondary workload (fields
+    in ``secondary.fields``), short enough that a log tail keeps it whole.
+    Everything else (per-kernel tables, configs) is in the preceding
+    ``bench_detail`` line."""
+    keys = ("metric", "value", "unit", "n_gpus", "steps", "warmup", "ms_per_step", "higher_is_better", "scaling",
+            "vs_baseline", "dtype", "data")
+    line = {k: out[k] for k in keys}
+    cfg = out.get("config", {})
+    line["config"] = {k: cfg[k] for k in ("workload", "visible_pairs", "flop_per_step", "seed") if k in cfg}
+    if "roofline" in out:
+        line["roofline"] = {k: v for k, v in out["roofline"].items() if k not in ("traffic_source", "work_per_launch")}
+    if "cpu_baseline" in out:
+        line["cpu_baseline"] = {k: v for k, v in out["cpu_baseline"].items() if k not in ("seconds", "cpu_model")}
+    if "memory" in out:
+        line["peak_mem_bytes"] = out["memory"]["peak_bytes"]
+        line["step_mem_bytes"] = out["memory"]["step_bytes"]
+    rows = {"fields": SECONDARY_FIELDS}
+    for r in out["secondary"]:
+        roof = r.get("roofline") or {}
+        cpu = r.get("cpu_baseline") or {}
+        mem = r.get("memory") or {}
+        kernel = (roof.get("kernel") or "").split(".")[-1].removesuffix("_kernel") or None
+        rows[r["name"]] = [r["value"], r["unit"], round(r["ms_per_step"], 3), kernel, roof.get("frac"),
+                           round(mem["peak_bytes"] / 1e9, 2) if mem else None, cpu.get("value")]
+    line["secondary"] = rows
+    line["peaks"] = {k: out["peaks"][k] for k in ("bf16_tflops", "hbm_gbs") if k in out.get("peaks", {})}
+    return line
 
 
 if __name__ == "__main__":

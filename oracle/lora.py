@@ -37,7 +37,8 @@ def unfused_forward(x, weight, lora_a, lora_b, scaling):
 
 def fused_backward(grad_out, x, weight_eff, lora_a, lora_b, scaling, *, round_rank: bool = False):
     """accel/fused_lora.py:35-48 in fp64: (dx, dA, dB).  With ``round_rank`` the
-    rank-sized products ``g B`` and ``x A^T`` are rounded to bf16 before use."""
+    rank-sized products ``g B`` and ``x A^T`` are rounded to bf16 before use.
+    ``weight_eff`` None skips dx (returned as None)."""
     g, xx = grad_out.double(), x.double()
     a, b = lora_a.double(), lora_b.double()
     u = g @ b
@@ -45,7 +46,7 @@ def fused_backward(grad_out, x, weight_eff, lora_a, lora_b, scaling, *, round_ra
     if round_rank:
         u = u.to(torch.bfloat16).double()
         t = t.to(torch.bfloat16).double()
-    dx = g @ weight_eff.double()
+    dx = None if weight_eff is None else g @ weight_eff.double()
     da = scaling * (u.t() @ xx)
     db = scaling * (g.t() @ t)
     return dx, da, db
