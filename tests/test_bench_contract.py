@@ -38,9 +38,46 @@ def test_traffic_table_entries_name_their_commit():
     table = json.loads((ROOT / "profiles" / "traffic.json").read_text())
     for workload, kernels in table["workloads"].items():
         for kernel, entry in kernels.items():
-            traffic, commit = bench.measured_traffic(workload, kernel)
-            assert abs(traffic - (entry["fetch_bytes"] + entry["write_bytes"])) <= 1  # rounding
-            assert commit and len(commit) >= 7
+            got = bench.measured_entry(workload, kernel)
+            assert abs(got["traffic_bytes"] - (entry["fetch_bytes"] + entry["write_bytes"])) <= 1  # rounding
+            assert got["measured_at_commit"] and len(got["measured_at_commit"]) >= 7
+
+
+def test_summary_line_keeps_every_secondary_in_a_short_line(monkeypatch):
+    """The summary line (the driver reads the last 2000 characters of the
+    output) carries the contract's keys, the roofline and CPU baseline, and
+    one row per secondary workload."""
+    out = {k: 1 for k in ("value", "n_gpus", "steps", "warmup", "ms_per_step")}
+    out.update(metric=bench.METRIC, unit="TFLOP/s", higher_is_better=True, scaling="weak", vs_baseline=None,
+               dtype="bf16", data="synthetic",
+               config={"workload": "C2 forest attention fwd+bwd: 2048-token shared prompt + 8 completions "
+                                   "U[256,4096], 32/8 heads, head_dim 128, bf16", "visible_pairs": 71374048,
+                       "flop_per_step": 4092873408512, "seed": 0, "completion_lengths": list(range(8))},
+               roofline={"kernel": "attention.dkdv_kernel", "bound": "mfma", "achieved": 844.39, "peak": 2516.6,
+                         "unit": "TFLOP/s", "frac": 0.3355, "traffic": 12655191624, "avg_launch_ms": 2.7698,
+                         "launches_per_step": 1.0, "traffic_source": "x" * 80, "work_per_launch": 2.3e12,
+                         "sustained_clock_mhz": 2100, "frac_at_sustained_clock": 0.3834},
+               cpu_baseline={"value": 1.0852, "unit": "TFLOP/s", "cores": 16, "cpu_model": "AMD EPYC 9575F",
+                             "kind": "port", "seconds": 10.5,
+                             "sample": "prompt node (2048 rows) + first completion node (2943 rows) of the "
+                                       "same C2 forest, 12457536 visible pairs, fp32 masked S"},
+               memory={"resident_bytes": 10 ** 9, "peak_bytes": 6123456789, "step_bytes": 5123456789},
+               peaks={"bf16_tflops": 2516.6, "hbm_gbs": 8000.0, "clock_mhz": 2400.0},
+               kernels={"k%d" % i: {"avg_ms": 1.0} for i in range(40)})
+    names = ["C4", "branch_d256", "C3_gated", "C3_ungated", "rmsnorm", "adjoint", "lora", "C5"]
+    out["secondary"] = [{"name": n, "value": 123456.78, "unit": "tokens/s", "ms_per_step": 57.59123,
+                         "roofline": {"kernel": "logprob.grad_hidden_reduce_kernel", "frac": 0.3123},
+                         "memory": {"peak_bytes": 60123456789}, "cpu_baseline": {"value": 1.1412},
+                         "kernels": {"k%d" % i: {"avg_ms": 1.0} for i in range(20)}} for n in names]
+    line = json.dumps(bench.summary(out), separators=(",", ":"))
+    assert len(line) < 1900, len(line)
+    back = json.loads(line)
+    for key in ("metric", "value", "unit", "n_gpus", "steps", "warmup", "ms_per_step", "higher_is_better",
+                "scaling", "vs_baseline", "dtype", "data", "config", "roofline", "cpu_baseline"):
+        assert key in back, key
+    assert set(back["secondary"]) == {"fields", *names}
+    assert len(back["secondary"]["C4"]) == len(back["secondary"]["fields"])
+    assert back["peak_mem_bytes"] == 6123456789
 
 
 def test_repeat_for_runs_at_least_once_and_stops():
