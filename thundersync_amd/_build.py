@@ -45,11 +45,13 @@ def device_flags() -> list[str]:
 
 # Extra code-generation flags per translation unit.  attention_dq.hip: the dQ
 # kernel's S/dP tiles and dQ accumulators fit the VGPRs, and MFMA results
-# written to VGPRs spare it per-tile copies out of the accumulation registers
-# (the dK/dV kernel, which needs the accumulation registers for its 48-key
-# accumulators, keeps the default).
+# written to VGPRs spare it per-tile copies out of the accumulation registers.
 FILE_FLAGS = {
     "attention_dq.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+    # the one-wave-per-head dK/dV kernel: S and dP in VGPRs (MFMA results in
+    # VGPRs), its dK/dV accumulators in the accumulation registers through
+    # inline assembly
+    "attention_dkdv_wave.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
 }
 
 

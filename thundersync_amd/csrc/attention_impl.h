@@ -482,6 +482,11 @@ int launch_dq(const ts_attn_problem& P, ts_attn_rows q, ts_attn_rows dout, const
 // (only where ds_route holds)
 int launch_dkdv(const ts_attn_problem& P, ts_attn_rows q, ts_attn_rows dout, const float* rowstats,
                 int64_t lse_ld, const DsArgs* ds, hipStream_t s);
+// the one-wave-per-head dK/dV kernel (groups that are a multiple of 4, head
+// dim 128; attention_dkdv_wave.hip), storing dS when DS
+template <typename E, bool DS>
+void launch_dkdv_wave(dim3 grid, const ts_attn_problem& P, ts_attn_rows q, ts_attn_rows dout,
+                      const float* rowstats, int64_t lse_ld, const DsArgs& S, hipStream_t s);
 // dQ = scale dS K from the workspace the dK/dV launch filled
 int launch_dq_ds(const ts_attn_problem& P, const DsArgs& ds, ts_attn_rows dq, hipStream_t s);
 
