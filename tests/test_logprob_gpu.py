@@ -215,9 +215,10 @@ def test_weight_gradient_c3_head(cuda):
 
 
 def test_backward_memory_is_one_chunk(cuda):
-    """Peak extra device memory of the backward is the [chunk, V] bf16 dlogits
-    block plus the grad_hidden workspace (the reference's O(chunk * V),
-    fused_logprob.py:20-24), not O(N * V)."""
+    """Peak extra device memory of the backward is one bf16 dlogits block of
+    two chunks of rows -- the bytes of the reference's own fp32 [chunk, V]
+    logit block (fused_logprob.py:137-175) -- plus the grad_hidden workspace:
+    the reference's O(chunk * V) (fused_logprob.py:20-24), not O(N * V)."""
     from thundersync_amd import _lib
 
     n, d, v, chunk = 4096, 4096, 151936, 1024
@@ -242,7 +243,7 @@ def test_backward_memory_is_one_chunk(cuda):
     print(f"backward extra {extra / 2**20:.1f} MiB: dlogits {dl_bytes / 2**20:.1f} + workspace "
           f"{ws_bytes / 2**20:.1f} + grad_hidden {grad_hidden / 2**20:.1f} MiB", flush=True)
     assert extra <= dl_bytes + ws_bytes + grad_hidden + small
-    assert dl_bytes <= chunk * v * 2 + chunk * 16
+    assert dl_bytes <= chunk * v * 4 + chunk * 32  # an fp32 [chunk, V] block
 
 
 def test_repeated_runs_are_bit_identical(cuda):
@@ -304,3 +305,24 @@ def test_predictor_logprobs_match_the_streaming_gather(cuda, first_scored):
     assert empty.shape == (0,) and empty.device == w.to(cuda).device
     with pytest.raises(ValueError, match="one entry per position"):
         hip.predictor_logprobs(bc, hc, tokens[:-1], scored, w.to(cuda))
+
+
+def test_short_last_block_gets_a_large_enough_workspace(cuda):
+    """A last dlogits block with fewer row tiles splits the vocabulary into
+    more ranges than a full block and needs a larger grad-hidden workspace
+    (3205 rows in blocks of 2048: 1157 rows, 4 ranges against 2); the
+    backward sizes the workspace for both.  Rows are independent, so the
+    oracle on sampled rows of both blocks is an exact check of them."""
+    n, d, v, chunk = 3205, 4096, 16384, 1024
+    assert hip.backward_block_rows(n, chunk) == 2048
+    print(f"logprob short last block n={n} d={d} v={v}", flush=True)
+    h, w, t, g_lp, g_ent = _inputs(n, d, v, seed=17)
+    hc = h.to(cuda).requires_grad_()
+    lp, ent = hip.fused_logprob_entropy(hc, w.to(cuda), t.to(cuda), chunk=chunk)
+    (lp * g_lp.to(cuda) + ent * g_ent.to(cuda)).sum().backward()
+    torch.cuda.synchronize()
+    rows = torch.tensor([0, 1, 2047, 2048, 2049, 2600, 3203, 3204])
+    want_lp, want_ent = ref.logprob_entropy_forward(h[rows], w, t[rows], 1024)
+    want_gh, _ = ref.logprob_entropy_backward(h[rows], w, t[rows], want_ent, g_lp[rows], g_ent[rows], 1024)
+    torch.testing.assert_close(lp.cpu()[rows], want_lp, rtol=0, atol=1e-3)
+    rel_close(hc.grad.cpu()[rows], want_gh, 1e-2, "grad hidden")

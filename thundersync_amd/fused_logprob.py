@@ -10,8 +10,9 @@ them in the GEMM epilogue; no ``[N, V]`` or ``[chunk, V]`` logit block is
 ever stored.  It returns logprob, entropy and the per-row log-sum-exp, which
 the backward reuses instead of recomputing the row statistics.
 
-Backward, per block of ``chunk`` rows (the reference's chunk loop,
-FL:143-193, with its O(chunk * V) memory): ``ts_logprob_dlogits`` recomputes
+Backward, per block of two chunks of rows (the reference's chunk loop,
+FL:143-193, with its O(chunk * V) memory: a bf16 block of two chunks is the
+size of the reference's fp32 logit block of one): ``ts_logprob_dlogits`` recomputes
 the logits and writes the block's bf16 dlogits (rounded to bf16 as the
 reference rounds its dlogits to the hidden dtype, FL:165 and :295);
 ``ts_logprob_grad_hidden`` multiplies them by the weight, read in place;
@@ -107,11 +108,18 @@ def _forward(hidden, weight, target, with_entropy):
     return lp, ent, lse
 
 
+# Rows of a dlogits block, in chunks: the reference's chunk loop holds an fp32
+# [chunk, V] logit block at a time (FL:137-175); a bf16 dlogits block of
+# BLOCK_CHUNKS = 2 chunks takes the same bytes, and its launches end in a
+# partial round of work-groups half as often as one-chunk blocks would.
+BLOCK_CHUNKS = 2
+
+
 def backward_block_rows(n: int, chunk: int) -> int:
-    """Rows per dlogits block: ``chunk`` (at least one row), rounded down to a
-    multiple of 256 (whole GEMM tiles) when that stays positive, and never more
-    than the rows there are."""
-    block = max(1, int(chunk))
+    """Rows per dlogits block: ``BLOCK_CHUNKS * chunk`` (at least one row),
+    rounded down to a multiple of 256 (whole GEMM tiles) when that stays
+    positive, and never more than the rows there are."""
+    block = max(1, BLOCK_CHUNKS * int(chunk))
     if block >= 256:
         block -= block % 256
     return min(block, max(n, 1))
@@ -133,7 +141,10 @@ def _backward(hidden, weight, target, lse, ent, grad_lp, grad_ent, chunk, needs_
     code = _lib.dtype_code(h.dtype)
     block = backward_block_rows(n, chunk)
     dl = torch.empty(block, vp, dtype=w.dtype, device=w.device)
-    ws_bytes = int(lib.ts_logprob_grad_hidden_workspace(block, d, v))
+    # the last block may be shorter, and fewer row tiles take more vocabulary
+    # ranges: size the workspace for whichever of the two block sizes needs more
+    tail = n % block
+    ws_bytes = max(int(lib.ts_logprob_grad_hidden_workspace(rows, d, v)) for rows in {block, tail or block})
     ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=h.device)
     g_lp = grad_lp.to(torch.float32).contiguous()
     g_ent = grad_ent.to(torch.float32).contiguous() if grad_ent is not None else None
