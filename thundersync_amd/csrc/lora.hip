@@ -21,9 +21,11 @@
 //                 contraction (rows), one launch each, C = u^T . x^T-tile
 //                 (x K-strided) and C = g^T-tile . t (g K-strided);
 //   reduce        sums the row ranges in range order and scales by s.
-// The rank-sized side of a rank/adapter tile holds `rank` valid rows of 256:
-// those products are bound by reading g and x (twice each over the backward),
-// not by the MFMA work the tile leaves idle.
+// Ranks above 64 run the rank and adapter products on that core too (the
+// rank side of a tile holding `rank` valid rows of 256); ranks up to 64 run
+// them on narrow 16-column MFMA tiles (lora_rank_narrow_kernel,
+// lora_adapter_narrow_kernel), which are bound by reading g and x (twice
+// each over the backward) rather than by MFMA work the tile leaves idle.
 #include <algorithm>
 
 #include "common.h"
@@ -214,12 +216,199 @@ __global__ __launch_bounds__(kGemmThreads, 1) void lora_grad_b_kernel(AdapterArg
   }
 }
 
+// ---------------------------------------------------------------------------
+// narrow ranks (at most kNarrowRank): the rank projections and adapter
+// gradients on 16 x 16 x 32 MFMA tiles whose rank side is the rank rounded up
+// to 16 (RB blocks of 16), instead of 256-wide tiles that hold `rank` valid
+// rows.  These products read g and x once each and do 2 rank FLOP per
+// element read: they are bound by HBM, and the narrow tiles leave the MFMA
+// work at what they need and spread them over enough work-groups to keep
+// loads in flight on every CU.
+// ---------------------------------------------------------------------------
+constexpr int kNarrowRank = 64;
+
+// rank projections: out^T[r][m] = sum_k src[m][k] proj[r][k].  A work-group
+// of 4 waves takes 64 rows (wave w rows 16 w ..) of one job over the whole of
+// K (measured against 4 waves sharing the K of 16 rows, whose partial sums
+// meet in LDS: 67 against 74 us on the C5 layer shape -- every work-group
+// also reads all of proj, from L2, so fewer rows per work-group read more).
+// A K block is 4 k-steps of 32: lane (g4, j16) loads k = k_blk + 32 s +
+// 8 g4 .. + 7 of row j16 for step s (each load instruction reads 64
+// contiguous bytes of each of the 16 rows); the B operands are proj rows
+// 16 rb + j16 at the same k.  Rows past `rows` and chunks past K load as
+// zeros, so the padding columns of out^T come out as exact zeros.
+template <typename E, int RB>
+__global__ __launch_bounds__(256) void lora_rank_narrow_kernel(RankArgs p) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int g4 = lane >> 4, j16 = lane & 15;
+  const int n_mt = (p.rows + 63) / 64;
+  const int jb = (int)blockIdx.x / n_mt;
+  const RankJob job = p.job[jb];
+  const int m0 = ((int)blockIdx.x - jb * n_mt) * 64 + 16 * wave;
+  const int row = m0 + j16;
+  const bool row_ok = row < p.rows;
+  const bf16* src = job.src + (int64_t)(row_ok ? row : 0) * job.ld_src + 8 * g4;
+  const bf16* proj[RB];
+  bool r_ok[RB];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    const int r = 16 * rb + j16;
+    r_ok[rb] = r < p.rank;
+    proj[rb] = job.proj + (int64_t)(r_ok[rb] ? r : 0) * job.ld_proj + 8 * g4;
+  }
+  f32x4 acc[RB];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) acc[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const u32x4 zero = u32x4{0u, 0u, 0u, 0u};
+#pragma unroll 2
+  for (int k = 0; k < job.k; k += 128) {
+    u32x4 a[4], b[RB][4];
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      const bool k_ok = k + 32 * st + 8 * g4 < job.k;
+      a[st] = row_ok && k_ok ? ld16(src + k + 32 * st) : zero;
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) b[rb][st] = r_ok[rb] && k_ok ? ld16(proj[rb] + k + 32 * st) : zero;
+    }
+#pragma unroll
+    for (int st = 0; st < 4; ++st)
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) acc[rb] = mma16<E>(as_bf16x8(a[st]), as_bf16x8(b[rb][st]), acc[rb]);
+  }
+  // acc[rb] lane (g4, j16): rows m0 + 4 g4 + i of rank 16 rb + j16
+  const int m = m0 + 4 * g4;
+  if (m >= p.ld_out) return;
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    if (!r_ok[rb]) continue;
+    *reinterpret_cast<u32x2*>(job.out + (int64_t)(16 * rb + j16) * p.ld_out + m) =
+        u32x2{pack2<E>(acc[rb][0], acc[rb][1]), pack2<E>(acc[rb][2], acc[rb][3])};
+  }
+}
+
+// adapter gradients over the row range [kb, kb + kper) of split s, for the
+// 128 columns of tile t:
+//   A side: part[s][r][k] = sum_m uT[r][m] x[m][k]
+//   B side: part[s][k][r] = sum_m tT[r][m] g[m][k]
+// The 4 waves split the range into 32-row steps (wave w steps w, w + 4, ...)
+// and their partial sums are added through LDS in wave order.  In a step
+// lane (g4, j16) loads rows 8 g4 .. 8 g4 + 7 at columns c0 + 8 j16 .. + 7
+// (for each row the 16 lanes of a group read 256 contiguous bytes) and
+// transposes the 8 x 8 block in registers, giving the B operands of 8 MFMAs,
+// MFMA c taking column c0 + 8 j16 + c on lane j16; the A operands are the
+// rank-side rows 16 rb + j16 at the step's rows 8 g4 .. + 7 (contiguous in
+// uT / tT).
+template <typename E, int RB, bool B_SIDE>
+__global__ __launch_bounds__(256) void lora_adapter_narrow_kernel(AdapterArgs p) {
+  __shared__ f32x4 red[3][8][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int g4 = lane >> 4, j16 = lane & 15;
+  const int s = (int)blockIdx.x / p.n_tiles, t = (int)blockIdx.x - s * p.n_tiles;
+  const int col = 128 * t + 8 * j16;
+  const bool col_ok = col < p.width;
+  const int kb = s * p.kper, ke = min(p.rows, kb + p.kper);
+  const bf16* big = p.big + (col_ok ? col : 0);
+  const bf16* small[RB];
+  bool r_ok[RB];
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    const int r = 16 * rb + j16;
+    r_ok[rb] = r < p.rank;
+    small[rb] = p.uT + (int64_t)(r_ok[rb] ? r : 0) * p.ld_rt;
+  }
+  f32x4 acc[8][RB];
+#pragma unroll
+  for (int c = 0; c < 8; ++c)
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb) acc[c][rb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const u32x4 zero = u32x4{0u, 0u, 0u, 0u};
+#pragma unroll 2
+  for (int m = kb + 32 * wave; m < ke; m += 128) {
+    const int mr = m + 8 * g4;  // this lane's first row of the step
+    u32x4 rows8[8], cols8[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      rows8[i] = col_ok && mr + i < ke ? ld16(big + (int64_t)(mr + i) * p.ld_big) : zero;
+    bf16x8 a[RB];
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+      a[rb] = as_bf16x8(r_ok[rb] && mr < p.ld_rt ? ld16(small[rb] + mr) : zero);
+    transpose8x8(rows8, cols8);  // cols8[c]: column col + c of rows mr .. mr + 7
+#pragma unroll
+    for (int c = 0; c < 8; ++c)
+#pragma unroll
+      for (int rb = 0; rb < RB; ++rb) acc[c][rb] = mma16<E>(a[rb], as_bf16x8(cols8[c]), acc[c][rb]);
+  }
+  // waves 1..3 hand their sums to wave 0, one 16-rank block at a time
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    if (wave > 0) {
+#pragma unroll
+      for (int c = 0; c < 8; ++c) red[wave - 1][c][lane] = acc[c][rb];
+    }
+    __syncthreads();
+    if (wave == 0) {
+#pragma unroll
+      for (int c = 0; c < 8; ++c)
+#pragma unroll
+        for (int w = 0; w < 3; ++w) acc[c][rb] += red[w][c][lane];
+    }
+    __syncthreads();
+  }
+  // acc[c][rb] lane (g4, j16): ranks 16 rb + 4 g4 + i, column col + c
+  if (wave > 0 || !col_ok) return;
+  float* part = p.part + (int64_t)s * p.rank * p.width;
+#pragma unroll
+  for (int rb = 0; rb < RB; ++rb) {
+    const int r0 = 16 * rb + 4 * g4;
+    if (r0 >= p.rank) continue;
+    if constexpr (B_SIDE) {
+      // part[s][k][r]: the lane's four ranks are consecutive
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        float* o = part + (int64_t)(col + c) * p.rank + r0;
+        if (r0 + 3 < p.rank && (p.rank & 3) == 0) {
+          *reinterpret_cast<f32x4*>(o) = acc[c][rb];
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (r0 + i < p.rank) o[i] = acc[c][rb][i];
+        }
+      }
+    } else {
+      // part[s][r][k]: the lane's eight columns are consecutive
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (r0 + i >= p.rank) continue;
+        float* o = part + (int64_t)(r0 + i) * p.width + col;
+        *reinterpret_cast<f32x4*>(o) = f32x4{acc[0][rb][i], acc[1][rb][i], acc[2][rb][i], acc[3][rb][i]};
+        *reinterpret_cast<f32x4*>(o + 4) = f32x4{acc[4][rb][i], acc[5][rb][i], acc[6][rb][i], acc[7][rb][i]};
+      }
+    }
+  }
+}
+
+// row ranges of the contraction for the narrow adapter products: about 1024
+// work-groups of 128 columns, ranges a whole number of 32-row steps and at
+// least 512 rows
+inline void narrow_split(int64_t rows, int64_t width, int& msplit, int& kper, int& tiles) {
+  tiles = (int)((width + 127) / 128);
+  int64_t k = (1024 + tiles - 1) / tiles;
+  k = std::min<int64_t>(k, std::max<int64_t>(1, rows / 512));
+  k = std::max<int64_t>(1, std::min<int64_t>(k, 256));
+  int64_t per = (rows + k - 1) / k;
+  per = (per + 31) / 32 * 32;
+  msplit = (int)((rows + per - 1) / per);
+  kper = (int)per;
+}
+
 // out[e] = scale * sum_s part[s][e], splits added in order
 __global__ __launch_bounds__(kThreads) void lora_reduce_kernel(const float* __restrict__ part, int msplit,
                                                                int64_t n, float scale, float* __restrict__ out) {
   const int64_t e = (int64_t)blockIdx.x * kThreads + threadIdx.x;
   if (e >= n) return;
   float acc = part[e];
+#pragma unroll 8
   for (int s = 1; s < msplit; ++s) acc += part[(int64_t)s * n + e];
   out[e] = acc * scale;
 }
@@ -248,15 +437,22 @@ bool ok16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 struct BwdLayout {
   int64_t ld_rt, rank_bytes, part_a, part_b, dx;
-  int msplit_a, kper_a, msplit_b, kper_b;
+  int msplit_a, kper_a, msplit_b, kper_b, tiles_a, tiles_b;
 };
 
 inline BwdLayout bwd_layout(int64_t rows, int64_t in, int64_t out, int64_t rank) {
   BwdLayout L;
   L.ld_rt = round8(rows);
   L.rank_bytes = align256(rank * L.ld_rt * 2);
-  adapter_split(rows, (in + TN - 1) / TN, L.msplit_a, L.kper_a);
-  adapter_split(rows, (out + TM - 1) / TM, L.msplit_b, L.kper_b);
+  if (rank <= kNarrowRank) {
+    narrow_split(rows, in, L.msplit_a, L.kper_a, L.tiles_a);
+    narrow_split(rows, out, L.msplit_b, L.kper_b, L.tiles_b);
+  } else {
+    adapter_split(rows, (in + TN - 1) / TN, L.msplit_a, L.kper_a);
+    adapter_split(rows, (out + TM - 1) / TM, L.msplit_b, L.kper_b);
+    L.tiles_a = (int)((in + TN - 1) / TN);
+    L.tiles_b = (int)((out + TM - 1) / TM);
+  }
   L.part_a = align256((int64_t)L.msplit_a * rank * in * 4);
   L.part_b = align256((int64_t)L.msplit_b * out * rank * 4);
   L.dx = align256(ts_logprob_grad_hidden_workspace(rows, in, out));
@@ -364,18 +560,35 @@ int ts_lora_bwd(const void* grad_out, int64_t ld_grad_out, const void* x, int64_
                                             static_cast<const bf16*>(lora_b_t), out_features, (int)out_features, uT};
   if (want_b) rk.job[rk.n_jobs++] = RankJob{static_cast<const bf16*>(x), ld_x, static_cast<const bf16*>(lora_a),
                                             in_features, (int)in_features, tT};
+  const int rb = (int)((rank + 15) / 16);  // 16-rank blocks of the narrow kernels
   {
     ts::TimedLaunch timed_("lora.rank_kernel", s);
-    TS_LAUNCH_E(dtype, lora_rank_kernel, dim3((unsigned)(rk.n_mtiles * rk.n_jobs)), dim3(kGemmThreads), 0, s, rk);
+    if (rank <= kNarrowRank) {
+      const dim3 grid((unsigned)(((rows + 63) / 64) * rk.n_jobs));
+#define TS_RANK_NARROW(RB)                                                                   \
+  if (rb == RB) TS_LAUNCH_E_T(dtype, lora_rank_narrow_kernel, RB, grid, dim3(256), 0, s, rk);
+      TS_RANK_NARROW(1) TS_RANK_NARROW(2) TS_RANK_NARROW(3) TS_RANK_NARROW(4)
+#undef TS_RANK_NARROW
+    } else {
+      TS_LAUNCH_E(dtype, lora_rank_kernel, dim3((unsigned)(rk.n_mtiles * rk.n_jobs)), dim3(kGemmThreads), 0, s, rk);
+    }
   }
   int st = ts::check_launch("ts_lora_bwd rank");
   if (st != TS_OK) return st;
   if (want_a) {
     AdapterArgs a{uT, L.ld_rt, static_cast<const bf16*>(x), ld_x, (int)rows, (int)rank, (int)in_features,
-                  (int)((in_features + TN - 1) / TN), L.msplit_a, L.kper_a, part_a};
+                  L.tiles_a, L.msplit_a, L.kper_a, part_a};
     {
       ts::TimedLaunch timed_("lora.grad_a_kernel", s);
-      TS_LAUNCH_E(dtype, lora_grad_a_kernel, dim3((unsigned)(a.n_tiles * a.msplit)), dim3(kGemmThreads), 0, s, a);
+      const dim3 grid((unsigned)(a.n_tiles * a.msplit));
+      if (rank <= kNarrowRank) {
+#define TS_ADAPTER_NARROW(RB)                                                                      \
+  if (rb == RB) TS_LAUNCH_E_T2(dtype, lora_adapter_narrow_kernel, RB, false, grid, dim3(256), 0, s, a);
+        TS_ADAPTER_NARROW(1) TS_ADAPTER_NARROW(2) TS_ADAPTER_NARROW(3) TS_ADAPTER_NARROW(4)
+#undef TS_ADAPTER_NARROW
+      } else {
+        TS_LAUNCH_E(dtype, lora_grad_a_kernel, grid, dim3(kGemmThreads), 0, s, a);
+      }
     }
     const int64_t n = rank * in_features;
     {
@@ -388,10 +601,18 @@ int ts_lora_bwd(const void* grad_out, int64_t ld_grad_out, const void* x, int64_
   }
   if (want_b) {
     AdapterArgs b{tT, L.ld_rt, static_cast<const bf16*>(grad_out), ld_grad_out, (int)rows, (int)rank,
-                  (int)out_features, (int)((out_features + TM - 1) / TM), L.msplit_b, L.kper_b, part_b};
+                  (int)out_features, L.tiles_b, L.msplit_b, L.kper_b, part_b};
     {
       ts::TimedLaunch timed_("lora.grad_b_kernel", s);
-      TS_LAUNCH_E(dtype, lora_grad_b_kernel, dim3((unsigned)(b.n_tiles * b.msplit)), dim3(kGemmThreads), 0, s, b);
+      const dim3 grid((unsigned)(b.n_tiles * b.msplit));
+      if (rank <= kNarrowRank) {
+#define TS_ADAPTER_NARROW(RB)                                                                     \
+  if (rb == RB) TS_LAUNCH_E_T2(dtype, lora_adapter_narrow_kernel, RB, true, grid, dim3(256), 0, s, b);
+        TS_ADAPTER_NARROW(1) TS_ADAPTER_NARROW(2) TS_ADAPTER_NARROW(3) TS_ADAPTER_NARROW(4)
+#undef TS_ADAPTER_NARROW
+      } else {
+        TS_LAUNCH_E(dtype, lora_grad_b_kernel, grid, dim3(kGemmThreads), 0, s, b);
+      }
     }
     const int64_t n = out_features * rank;
     {
