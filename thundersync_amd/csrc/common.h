@@ -345,11 +345,6 @@ int check_launch(const char* what);
     if ((dtype) == ::ts::kF16) hipLaunchKernelGGL((kernel<::ts::f16, A1>), __VA_ARGS__);     \
     else hipLaunchKernelGGL((kernel<::ts::bf16, A1>), __VA_ARGS__);                          \
   } while (0)
-#define TS_LAUNCH_E_T2(dtype, kernel, A1, A2, ...)                                           \
-  do {                                                                                       \
-    if ((dtype) == ::ts::kF16) hipLaunchKernelGGL((kernel<::ts::f16, A1, A2>), __VA_ARGS__); \
-    else hipLaunchKernelGGL((kernel<::ts::bf16, A1, A2>), __VA_ARGS__);                      \
-  } while (0)
 
 // out [rows, dim] (bf16) = lhs [rows, vocab] . W [vocab, dim] on the MFMA core
 // (the logprob grad-hidden GEMM), launches timed under `label` and, for the

@@ -24,7 +24,7 @@
 // Ranks above 64 run the rank and adapter products on that core too (the
 // rank side of a tile holding `rank` valid rows of 256); ranks up to 64 run
 // them on narrow 16-column MFMA tiles (lora_rank_narrow_kernel,
-// lora_adapter_narrow_kernel), which are bound by reading g and x (twice
+// lora_grad_{a,b}_narrow_kernel), which are bound by reading g and x (twice
 // each over the backward) rather than by MFMA work the tile leaves idle.
 #include <algorithm>
 
@@ -299,7 +299,7 @@ __global__ __launch_bounds__(256) void lora_rank_narrow_kernel(RankArgs p) {
 // rank-side rows 16 rb + j16 at the step's rows 8 g4 .. + 7 (contiguous in
 // uT / tT).
 template <typename E, int RB, bool B_SIDE>
-__global__ __launch_bounds__(256) void lora_adapter_narrow_kernel(AdapterArgs p) {
+__device__ __forceinline__ void adapter_narrow(const AdapterArgs& p) {
   __shared__ f32x4 red[3][8][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int g4 = lane >> 4, j16 = lane & 15;
@@ -386,6 +386,16 @@ __global__ __launch_bounds__(256) void lora_adapter_narrow_kernel(AdapterArgs p)
       }
     }
   }
+}
+
+// the two sides as kernels of their own (distinct names in profiles)
+template <typename E, int RB>
+__global__ __launch_bounds__(256) void lora_grad_a_narrow_kernel(AdapterArgs p) {
+  adapter_narrow<E, RB, false>(p);
+}
+template <typename E, int RB>
+__global__ __launch_bounds__(256) void lora_grad_b_narrow_kernel(AdapterArgs p) {
+  adapter_narrow<E, RB, true>(p);
 }
 
 // row ranges of the contraction for the narrow adapter products: about 1024
@@ -583,7 +593,7 @@ int ts_lora_bwd(const void* grad_out, int64_t ld_grad_out, const void* x, int64_
       const dim3 grid((unsigned)(a.n_tiles * a.msplit));
       if (rank <= kNarrowRank) {
 #define TS_ADAPTER_NARROW(RB)                                                                      \
-  if (rb == RB) TS_LAUNCH_E_T2(dtype, lora_adapter_narrow_kernel, RB, false, grid, dim3(256), 0, s, a);
+  if (rb == RB) TS_LAUNCH_E_T(dtype, lora_grad_a_narrow_kernel, RB, grid, dim3(256), 0, s, a);
         TS_ADAPTER_NARROW(1) TS_ADAPTER_NARROW(2) TS_ADAPTER_NARROW(3) TS_ADAPTER_NARROW(4)
 #undef TS_ADAPTER_NARROW
       } else {
@@ -607,7 +617,7 @@ int ts_lora_bwd(const void* grad_out, int64_t ld_grad_out, const void* x, int64_
       const dim3 grid((unsigned)(b.n_tiles * b.msplit));
       if (rank <= kNarrowRank) {
 #define TS_ADAPTER_NARROW(RB)                                                                     \
-  if (rb == RB) TS_LAUNCH_E_T2(dtype, lora_adapter_narrow_kernel, RB, true, grid, dim3(256), 0, s, b);
+  if (rb == RB) TS_LAUNCH_E_T(dtype, lora_grad_b_narrow_kernel, RB, grid, dim3(256), 0, s, b);
         TS_ADAPTER_NARROW(1) TS_ADAPTER_NARROW(2) TS_ADAPTER_NARROW(3) TS_ADAPTER_NARROW(4)
 #undef TS_ADAPTER_NARROW
       } else {
