@@ -67,6 +67,27 @@ __global__ __launch_bounds__(64) void probe_lds_kernel(const u32x4* __restrict__
   tr_out[l] = o;
 }
 
+// One wave: a buffer_load_dwordx4 ... lds with instruction offset 1024 (the
+// builtin's immediate offset), lane i at voffset 16 i, into a 2 KB LDS block
+// prefilled with 0xdeadbeef, copied to out (2 KB).  The resource covers all
+// of src (128 x 16 bytes); every global byte read lies inside it (1024 +
+// 16 i + 16 <= 2048) and every LDS byte written inside the block whether
+// the offset moves the LDS address too or not.
+__global__ __launch_bounds__(64) void probe_dma_offset_kernel(const u32x4* __restrict__ src,
+                                                              u32x4* __restrict__ out) {
+  __shared__ __attribute__((aligned(16))) u32x4 block[128];
+  const int l = threadIdx.x;
+  block[l] = u32x4{0xdeadbeefu, 0xdeadbeefu, 0xdeadbeefu, 0xdeadbeefu};
+  block[64 + l] = u32x4{0xdeadbeefu, 0xdeadbeefu, 0xdeadbeefu, 0xdeadbeefu};
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(make_rsrc(src, 128 * 16), (lds_void*)block, 16, 16 * l, 0, 1024, 0);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  out[l] = block[l];
+  out[64 + l] = block[64 + l];
+}
+
 // out[0:64] rows_max4, out[64:128] rows_sum4 of in[lane]; out[128:192] and
 // out[192:256] the two results of v_permlane16_swap(in, in), out[256:320]
 // and out[320:384] those of v_permlane32_swap(in, in)
@@ -136,6 +157,14 @@ const char* ts_probe_last_error(void) { return g_probe_error; }
 // v_permlane32_swap(in, in), 64 floats each.  Used by the test suite to pin
 // the lane semantics.
 // int ts_probe_lanes(const float* in, float* out, void* stream);
+//
+// Runs, in one wave, a buffer_load_dwordx4 ... lds with immediate
+// instruction offset 1024, lane i at voffset 16 i, through a raw buffer
+// resource over src (128 x 16 bytes) into a 2 KB LDS block prefilled with
+// 0xdeadbeef, and copies the block to out (2 KB).  Used by the test suite to
+// pin whether the instruction offset moves the LDS address as well as the
+// global one.
+// int ts_probe_dma_offset(const void* src, void* out, void* stream);
 
 int ts_probe_layouts(const void* a, const void* b, float* d16, float* d32,
                      const void* t_in, void* t_out, void* stream) {
@@ -160,6 +189,13 @@ int ts_probe_lds(const void* src, const int* perm, void* dma_out, void* tr_out, 
                      (const ts::u32x4*)src, perm, (ts::u32x4*)dma_out, (ts::u32x2*)tr_out,
                      (ts::u32x4*)buf_out, valid_bytes);
   return launched("ts_probe_lds");
+}
+
+int ts_probe_dma_offset(const void* src, void* out, void* stream) {
+  if (!(src && out)) return refuse("ts_probe_dma_offset: null pointer");
+  hipLaunchKernelGGL(ts::probe_dma_offset_kernel, dim3(1), dim3(64), 0, (hipStream_t)stream,
+                     (const ts::u32x4*)src, (ts::u32x4*)out);
+  return launched("ts_probe_dma_offset");
 }
 
 }  // extern "C"

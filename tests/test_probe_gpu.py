@@ -25,6 +25,7 @@ PROBE_SIGNATURES = {
     "ts_probe_layouts": (_INT, [_P] * 7),
     "ts_probe_lds": (_INT, [_P] * 5 + [_INT, _P]),
     "ts_probe_lanes": (_INT, [_P] * 3),
+    "ts_probe_dma_offset": (_INT, [_P] * 3),
 }
 
 
@@ -159,3 +160,23 @@ def test_cross_row_lane_reductions(cuda):
         want = np.sort(np.stack([x, x[np.arange(64) ^ partner]]), axis=0)
         np.testing.assert_array_equal(pair, want)
     print("permlane16_swap:", got[2][:20].tolist(), got[3][:20].tolist(), flush=True)
+
+
+def test_buffer_dma_instruction_offset_moves_both_addresses(cuda):
+    """buffer_load_dwordx4 ... lds with an immediate instruction offset: the
+    offset is added to the LDS destination as well as to the global address,
+    so one M0 value serves DMA instructions whose LDS and global offsets
+    advance together (lane i's 16 bytes from byte 1024 + 16 i land at LDS
+    byte 1024 + 16 i; the first 1 KB of the block is left alone)."""
+    lib = probe_library()
+    src = torch.arange(128 * 4, dtype=torch.int32, device=cuda)
+    out = torch.empty(128 * 4, dtype=torch.int32, device=cuda)
+    print("probe: ts_probe_dma_offset", flush=True)
+    probe_check(lib, lib.ts_probe_dma_offset(src.data_ptr(), out.data_ptr(), _lib.stream_of(src)),
+                "ts_probe_dma_offset")
+    torch.cuda.synchronize()
+    got = out.view(128, 4).cpu().numpy()
+    print("dma offset: LDS rows 0, 64:", got[0].tolist(), got[64].tolist(), flush=True)
+    untouched = np.full((64, 4), np.int32(np.uint32(0xDEADBEEF).view(np.int32)))
+    np.testing.assert_array_equal(got[:64], untouched)
+    np.testing.assert_array_equal(got[64:], np.arange(256, 512).reshape(64, 4))

@@ -30,6 +30,19 @@ __device__ __forceinline__ void mma16_acc(f32x4& acc, bf16x8 a, bf16x8 b) {
   }
 }
 
+// a 32-row block of one visit of the work-group's run, with the DMA sources
+// of its Q, dO and statistics rows for the wave's current head
+struct WaveCursor {
+  int vi;           // visit index; >= nvisit at the end
+  int r0;           // first row of the block (segment-local)
+  int q_len;        // rows of the visited segment
+  int off;          // its kv_len - q_len
+  int kpos;         // position of the run's first key in the segment's key order
+  const bf16* q;    // Q row r0 of the segment, current head
+  const bf16* d;    // dO row r0 likewise
+  const float* st;  // the row's (lse2, delta) pair
+};
+
 // ---------------------------------------------------------------------------
 // backward dK / dV, one wave per query head (GQA groups that are a multiple of 4)
 //
@@ -103,13 +116,19 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_wave_kernel(ts_attn_problem 
   // chunk slot j16 with logical chunk j16 ^ tile_swizzle(4 (t & 3) + g4)
 #pragma unroll
   for (int t = 0; t < 4; ++t) dchunk[t] = (j16 ^ tile_swizzle(4 * t + g4)) << 3;
-  // byte offsets of this lane's row and chunk within a 16-row half tile
+  // byte offsets of this lane's row and chunk within a 16-row half tile, less
+  // the 1024 t that DMA instruction t adds to both addresses as its
+  // instruction offset (a row stride is at least 128 elements, so they stay
+  // non-negative)
   int qoff[4], doff[4];
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
-    qoff[t] = (int)(((4 * t + g4) * Q.row_stride + dchunk[t]) * 2);
-    doff[t] = (int)(((4 * t + g4) * dO.row_stride + dchunk[t]) * 2);
+    qoff[t] = (int)(((4 * t + g4) * Q.row_stride + dchunk[t]) * 2) - 1024 * t;
+    doff[t] = (int)(((4 * t + g4) * dO.row_stride + dchunk[t]) * 2) - 1024 * t;
   }
+  const int64_t q32 = 32 * Q.row_stride, d32 = 32 * dO.row_stride;  // one block of rows
+  const int64_t q16 = 16 * Q.row_stride, d16 = 16 * dO.row_stride;  // its upper half
+  const uint32_t qrow_bytes = (uint32_t)(Q.row_stride * 2), drow_bytes = (uint32_t)(dO.row_stride * 2);
 
   // K^T and V^T operands: kreg[kb][ks] = K[k0 + 16 kb + j16][32 ks + 8 g4 ..], vreg likewise
   bf16x8 kreg[KB][4], vreg[KB][4];
@@ -136,45 +155,51 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_wave_kernel(ts_attn_problem 
       dv[mb][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
 
+  int hh = 0;  // the wave's current head
   // enter visit c.vi (< nvisit): cache its segment's fields and start at the
-  // first 32-row block whose rows can see key k0
-  auto enter = [&](VisitCursor& c) {
+  // first 32-row block whose rows can see key k0, with that block's Q, dO and
+  // statistics rows of head hh
+  auto enter = [&](WaveCursor& c) {
     const ts_attn_ref ref = load_uniform(P.run_visits, run.visit0 + c.vi);
     const ts_attn_segment seg = load_uniform(P.segs, ref.index);
     c.q_len = seg.q_len;
     c.off = seg.kv_len - seg.q_len;
     c.kpos = ref.kpos;
-    c.q_row0 = seg.q_row0;
     const int rs = ref.kpos + k0 - c.off;
     c.r0 = (rs < 0 ? 0 : rs) & ~31;
+    const int64_t row0 = seg.q_row0 + c.r0;
+    c.q = (const bf16*)Q.ptr + row0 * Q.row_stride + (int64_t)hh * Q.head_stride;
+    c.d = (const bf16*)dO.ptr + row0 * dO.row_stride + (int64_t)hh * dO.head_stride;
+    c.st = rowstats + 2 * ((int64_t)hh * lse_ld + row0);
   };
   // first block at or after c; skips visits with no visible rows
-  auto settle = [&](VisitCursor c) -> VisitCursor {
+  auto settle = [&](WaveCursor c) -> WaveCursor {
     while (c.r0 >= c.q_len) {
       if (++c.vi >= run.nvisit) break;
       enter(c);
     }
     return c;
   };
-  auto first = [&]() -> VisitCursor {
-    VisitCursor c{0, 0, 0, 0, 0, 0};
+  auto first = [&]() -> WaveCursor {
+    WaveCursor c{0, 0, 0, 0, 0, nullptr, nullptr, nullptr};
     if (run.nvisit > 0) enter(c);
     return settle(c);
   };
   // dS route: this lane's element of block k0 / 16 of c's row block in head
-  // h's part (c on a visit)
-  auto locate = [&](const VisitCursor& c, int h) -> bf16* {
+  // hh's part (c on a visit)
+  auto locate = [&](const WaveCursor& c) -> bf16* {
     // consumed here, so that no scalar load is outstanding when the next
     // step's LDS reads count their completions
     const int64_t blk = load_uniform(S.visit, run.visit0 + c.vi) / kDsBlock +
                         ds_blocks_before(DsRect{c.off - c.kpos, nkb, c.q_len}, c.r0 >> 5);
     asm volatile("" ::"s"(blk));
-    return ds_lane + (int64_t)h * ds_head + blk * kDsBlock;
+    return ds_lane + (int64_t)hh * ds_head + blk * kDsBlock;
   };
   // the block after c (settled: past its visit's rows, the next visit's
-  // first); dS route: `at` follows it, advanced by c's row block's block
-  // count within a visit, located afresh on entering the next
-  auto next_block = [&](VisitCursor c, bf16*& at, int h) -> VisitCursor {
+  // first): within a visit the DMA sources advance by 32 rows; dS route:
+  // `at` follows it, advanced by c's row block's block count within a visit,
+  // located afresh on entering the next
+  auto next_block = [&](WaveCursor c, bf16*& at) -> WaveCursor {
     int inc = 0;
     if constexpr (DS) {
       const int last = c.off - c.kpos + min(c.r0 + 31, c.q_len - 1);
@@ -182,37 +207,42 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_wave_kernel(ts_attn_problem 
     }
     const int vi0 = c.vi;
     c.r0 += 32;
+    c.q += q32;
+    c.d += d32;
+    c.st += 64;
     if (c.r0 >= c.q_len) c = settle(c);  // tables are read only here
     if constexpr (DS) {
       if (c.vi == vi0)
         at += (int64_t)inc * kDsBlock;
       else if (c.vi < run.nvisit)
-        at = locate(c, h);
+        at = locate(c);
     }
     return c;
   };
   // DMA of block `cur` (nothing, as zero-size buffer resources, when it is
-  // past the run's last visit)
-  auto issue = [&](const VisitCursor& cur, int h, bf16* buf) {
+  // past the run's last visit): each of the four 4 KB quarters of the Q and
+  // dO tiles is four instructions under one M0, instruction t at instruction
+  // offset 1024 t
+  auto issue = [&](const WaveCursor& cur, bf16* buf) {
     const int nrows = max(0, min(32, cur.q_len - cur.r0));
     const int n_lo = min(16, nrows), n_hi = nrows - n_lo;
-    const int64_t row0 = cur.q_row0 + cur.r0;
-    const bf16* qb = (const bf16*)Q.ptr + row0 * Q.row_stride + (int64_t)h * Q.head_stride;
-    const bf16* db = (const bf16*)dO.ptr + row0 * dO.row_stride + (int64_t)h * dO.head_stride;
-    const rsrc_t q_lo = make_rsrc(qb, (uint32_t)(n_lo * Q.row_stride * 2));
-    const rsrc_t q_hi = make_rsrc(qb + 16 * Q.row_stride, (uint32_t)(n_hi * Q.row_stride * 2));
-    const rsrc_t d_lo = make_rsrc(db, (uint32_t)(n_lo * dO.row_stride * 2));
-    const rsrc_t d_hi = make_rsrc(db + 16 * dO.row_stride, (uint32_t)(n_hi * dO.row_stride * 2));
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      buffer_dma16(q_lo, buf + t * 512, qoff[t]);
-      buffer_dma16(q_hi, buf + (4 + t) * 512, qoff[t]);
-      buffer_dma16(d_lo, buf + kTile32 + t * 512, doff[t]);
-      buffer_dma16(d_hi, buf + kTile32 + (4 + t) * 512, doff[t]);
-    }
+    const rsrc_t q_lo = make_rsrc(cur.q, n_lo * qrow_bytes);
+    const rsrc_t q_hi = make_rsrc(cur.q + q16, n_hi * qrow_bytes);
+    const rsrc_t d_lo = make_rsrc(cur.d, n_lo * drow_bytes);
+    const rsrc_t d_hi = make_rsrc(cur.d + d16, n_hi * drow_bytes);
+    auto quarter = [&](const rsrc_t& r, bf16* lds, const int (&voff)[4]) __attribute__((always_inline)) {
+      buffer_dma16_at<0>(r, lds, voff[0]);
+      buffer_dma16_at<1024>(r, lds, voff[1]);
+      buffer_dma16_at<2048>(r, lds, voff[2]);
+      buffer_dma16_at<3072>(r, lds, voff[3]);
+    };
+    quarter(q_lo, buf, qoff);
+    quarter(q_hi, buf + 4 * 512, qoff);
+    quarter(d_lo, buf + kTile32, doff);
+    quarter(d_hi, buf + kTile32 + 4 * 512, doff);
     // 32 rows x 8 bytes of statistics: lanes 0..15, 16 bytes each (the other
     // lanes read past the resource and write zeros after them)
-    const rsrc_t rs = make_rsrc(rowstats + 2 * ((int64_t)h * lse_ld + row0), (uint32_t)(nrows * 8));
+    const rsrc_t rs = make_rsrc(cur.st, (uint32_t)(nrows * 8));
     buffer_dma16(rs, buf + 2 * kTile32, lane < 16 ? lane * 16 : 0x7ffffff0);
   };
 
@@ -220,14 +250,14 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_wave_kernel(ts_attn_problem 
   // `nxt` is the block after `cur`, already settled: the step's body up to the
   // cursor update is branch-free, so the next block's DMA set-up interleaves
   // with the MFMAs
-  auto step = [&](auto bsel, VisitCursor& cur, VisitCursor& nxt, int h, bf16*& cur_at, bf16*& nxt_at) {
+  auto step = [&](auto bsel, WaveCursor& cur, WaveCursor& nxt, bf16*& cur_at, bf16*& nxt_at) {
       const int off = cur.off, r0 = cur.r0, kpos = cur.kpos;
       __builtin_amdgcn_s_waitcnt(0);  // this block's tiles have landed
       // static buffer roles: the LDS reads below and the prefetch into the other
       // buffer touch different arrays, so no wait for the prefetch is needed
       bf16* cur_buf = bsel.value == 0 ? s_b0[wave] : s_b1[wave];
       bf16* nxt_buf = bsel.value == 0 ? s_b1[wave] : s_b0[wave];
-      issue(nxt, h, nxt_buf);
+      issue(nxt, nxt_buf);
       const bf16* tq = cur_buf;
       const bf16* td = cur_buf + kTile32;
       const float* sl = reinterpret_cast<const float*>(cur_buf + 2 * kTile32);  // [32] (lse2, delta)
@@ -362,23 +392,23 @@ __global__ __launch_bounds__(kThreads, 1) void dkdv_wave_kernel(ts_attn_problem 
       }
       cur = nxt;
       if constexpr (DS) cur_at = nxt_at;
-      nxt = next_block(nxt, nxt_at, h);
+      nxt = next_block(nxt, nxt_at);
   };
 
   for (int g = wave; g < group; g += 4) {
-    const int h = hk * group + g;
-    VisitCursor cur = first();
+    hh = hk * group + g;
+    WaveCursor cur = first();
     bf16* cur_at = ds_lane;
     if constexpr (DS)
-      if (cur.vi < run.nvisit) cur_at = locate(cur, h);
+      if (cur.vi < run.nvisit) cur_at = locate(cur);
     bf16* nxt_at = cur_at;
-    VisitCursor nxt = next_block(cur, nxt_at, h);
+    WaveCursor nxt = next_block(cur, nxt_at);
     __builtin_amdgcn_s_waitcnt(0);  // the previous head's last (empty) DMA has landed
-    if (cur.vi < run.nvisit) issue(cur, h, s_b0[wave]);
+    if (cur.vi < run.nvisit) issue(cur, s_b0[wave]);
     while (cur.vi < run.nvisit) {
-      step(std::integral_constant<int, 0>{}, cur, nxt, h, cur_at, nxt_at);
+      step(std::integral_constant<int, 0>{}, cur, nxt, cur_at, nxt_at);
       if (cur.vi >= run.nvisit) break;
-      step(std::integral_constant<int, 1>{}, cur, nxt, h, cur_at, nxt_at);
+      step(std::integral_constant<int, 1>{}, cur, nxt, cur_at, nxt_at);
     }
   }
 

@@ -31,17 +31,16 @@ namespace attn {
 // the K half of issue_kv_tile: a 64-key K tile, every wave its share of the
 // HD / 2 DMA instructions (rows past the run arrive as zeros)
 template <int HD, int KT>
-__device__ __forceinline__ void issue_k_tile(int hk, int wave, int lane, const TileCursor& tc, bf16* sk) {
+__device__ __forceinline__ void issue_k_tile(int wave, int lane, const TileCursor& tc, bf16* sk) {
   constexpr int CH = HD / 8, RPI = 64 / CH, NI = KT / RPI;
   const int nvalid = min(KT, tc.len - tc.kt0);
-  const bf16* kb = (const bf16*)tc.k + (int64_t)tc.kt0 * tc.k_row_stride + (int64_t)hk * tc.k_head_stride;
-  const u32x4 rk = raw_descriptor(kb, (uint32_t)(nvalid * tc.k_row_stride * 2));
+  const u32x4 rk = raw_descriptor(tc.kt, (uint32_t)(nvalid * tc.k_rs * 2));
 #pragma unroll
   for (int u = 0; u < NI / 4; ++u) {
     const int t = wave + 4 * u;
     const int row = RPI * t + lane / CH;
     const int chunk = ((lane % CH) ^ tile_swizzle(row & 15)) << 3;
-    buffer_dma16_untracked(rk, sk + t * 512, (int)((row * tc.k_row_stride + chunk) * 2));
+    buffer_dma16_untracked(rk, sk + t * 512, (row * tc.k_rs + chunk) * 2);
   }
 }
 
@@ -123,7 +122,7 @@ __global__ __launch_bounds__(kThreads, dq_ds_occupancy<HD>()) void dq_ds_kernel(
   };
   auto issue = [&](const TileCursor& tc, int st) {
     bf16* buf = s_buf + st * STAGE;
-    issue_k_tile<HD, KT>(hk, wave, lane, tc, buf);
+    issue_k_tile<HD, KT>(wave, lane, tc, buf);
     if (tc.sp != ds_sp) ds_enter(tc);
     const int kb0 = tc.kt0 >> 4;
     const int nb = max(0, min(NKB, ds_n - kb0));
@@ -172,13 +171,13 @@ __global__ __launch_bounds__(kThreads, dq_ds_occupancy<HD>()) void dq_ds_kernel(
   };
 
   // tiles i .. i + NST - 2 are in flight at the top of step i
-  TileCursor nx = first_kv_tile<KT>(P, seg, last);
+  TileCursor nx = first_kv_tile<KT>(P, seg, hk, last);
   int issued = 0;
 #pragma unroll
   for (int p = 0; p < NST - 1; ++p) {
     if (nx.sp < seg.nspan) {
       issue(nx, p);
-      nx = next_kv_tile<KT>(P, seg, last, nx);
+      nx = next_kv_tile<KT>(P, seg, hk, last, nx);
       ++issued;
     }
   }
@@ -195,7 +194,7 @@ __global__ __launch_bounds__(kThreads, dq_ds_occupancy<HD>()) void dq_ds_kernel(
     __syncthreads();  // tile i is in every stage; stage (i - 1) % NST is free
     if (nx.sp < seg.nspan) {
       issue(nx, (i + NST - 1) % NST);
-      nx = next_kv_tile<KT>(P, seg, last, nx);
+      nx = next_kv_tile<KT>(P, seg, hk, last, nx);
       ++issued;
     }
     compute(i % NST);

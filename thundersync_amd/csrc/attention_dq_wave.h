@@ -243,13 +243,13 @@ __global__ __launch_bounds__(64 * 8 / (NQB * NP), 1) void dq_wave_kernel(ts_attn
   auto step = [&](auto bsel, TileCursor& cur) {
     const int kpos = cur.kpos;
     const int kt0 = cur.kt0;
-    const TileCursor nxt = next_kv_tile(P, seg, last, cur);
+    const TileCursor nxt = next_kv_tile(P, seg, hk, last, cur);
     __builtin_amdgcn_s_waitcnt(0);  // this wave's part of the tile has landed
     __syncthreads();                // every part has, and the other stage is free
     const bf16* tk = bsel.value == 0 ? s_k0 : s_k1;
     const bf16* tv = bsel.value == 0 ? s_v0 : s_v1;
     if (nxt.sp < seg.nspan)
-      issue_kv_tile<kWaves, HD>(hk, wave, lane, nxt, bsel.value == 0 ? s_k1 : s_k0, bsel.value == 0 ? s_v1 : s_v0);
+      issue_kv_tile<kWaves, HD>(wave, lane, nxt, bsel.value == 0 ? s_k1 : s_k0, bsel.value == 0 ? s_v1 : s_v0);
 
     if (kpos + kt0 + BK - 1 > off + qw)
       tile_body(std::true_type{}, tk, tv, kpos, kt0);
@@ -258,8 +258,8 @@ __global__ __launch_bounds__(64 * 8 / (NQB * NP), 1) void dq_wave_kernel(ts_attn
     cur = nxt;
   };
 
-  TileCursor cur = first_kv_tile(P, seg, last);
-  if (cur.sp < seg.nspan) issue_kv_tile<kWaves, HD>(hk, wave, lane, cur, s_k0, s_v0);
+  TileCursor cur = first_kv_tile(P, seg, hk, last);
+  if (cur.sp < seg.nspan) issue_kv_tile<kWaves, HD>(wave, lane, cur, s_k0, s_v0);
   while (cur.sp < seg.nspan) {
     step(std::integral_constant<int, 0>{}, cur);
     if (cur.sp >= seg.nspan) break;

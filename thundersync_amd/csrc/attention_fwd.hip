@@ -232,13 +232,13 @@ __global__ __launch_bounds__(64 * 8 / NQB, (fwd_occupancy<NQB, HD, KT>())) void 
   auto step = [&](auto bsel, TileCursor& cur) {
     const int kpos = cur.kpos, run_len = cur.len;
     const int kt0 = cur.kt0;
-    const TileCursor nxt = next_kv_tile<KT>(P, seg, last, cur);
+    const TileCursor nxt = next_kv_tile<KT>(P, seg, hk, last, cur);
     __builtin_amdgcn_s_waitcnt(0);  // this wave's part of the tile has landed
     __syncthreads();                // every part has, and the other stage is free
     const bf16* tk = bsel.value == 0 ? s_k0 : s_k1;
     const bf16* tv = bsel.value == 0 ? s_v0 : s_v1;
     if (nxt.sp < seg.nspan)
-      issue_kv_tile<kWaves, HD, KT>(hk, wave, lane, nxt, bsel.value == 0 ? s_k1 : s_k0, bsel.value == 0 ? s_v1 : s_v0);
+      issue_kv_tile<kWaves, HD, KT>(wave, lane, nxt, bsel.value == 0 ? s_k1 : s_k0, bsel.value == 0 ? s_v1 : s_v0);
 
     const bool masked = (kpos + kt0 + KT - 1 > off + qw) | (kt0 + KT > run_len);
     // two halves of 32 keys, each one online-softmax update:
@@ -361,8 +361,8 @@ __global__ __launch_bounds__(64 * 8 / NQB, (fwd_occupancy<NQB, HD, KT>())) void 
     cur = nxt;
   };
 
-  TileCursor cur = first_kv_tile<KT>(P, seg, last);
-  if (cur.sp < seg.nspan) issue_kv_tile<kWaves, HD, KT>(hk, wave, lane, cur, s_k0, s_v0);
+  TileCursor cur = first_kv_tile<KT>(P, seg, hk, last);
+  if (cur.sp < seg.nspan) issue_kv_tile<kWaves, HD, KT>(wave, lane, cur, s_k0, s_v0);
   while (cur.sp < seg.nspan) {
     step(std::integral_constant<int, 0>{}, cur);
     if (cur.sp >= seg.nspan) break;

@@ -322,40 +322,40 @@ __device__ __forceinline__ int ds_store_offset(int lane) {
 constexpr int kKV64 = BK * D;  // elements of one 64-key tile
 
 struct TileCursor {
-  int sp;    // span index; == nspan at the end
-  int kt0;   // first run-local key of the tile
-  int kpos;  // position of the span's first key in the segment's key order
-  int len;   // keys of the span's run
-  uint64_t k, v;
-  int64_t k_row_stride, k_head_stride, v_row_stride, v_head_stride;
+  int sp;          // span index; == nspan at the end
+  int kt0;         // first run-local key of the tile
+  int kpos;        // position of the span's first key in the segment's key order
+  int len;         // keys of the span's run
+  const bf16* kt;  // K row kt0 of the KV head (advanced with kt0 within a span)
+  const bf16* vt;  // V row kt0 likewise
+  int k_rs, v_rs;  // the run's row strides (elements, below 2^24)
 };
 
-// cache span tc.sp's reference and run fields (tc.sp < nspan)
-__device__ __forceinline__ void enter_span(const ts_attn_problem& P, const ts_attn_segment& seg, TileCursor& tc) {
+// cache span tc.sp's reference and run fields, at the span's first key of KV
+// head hk (tc.sp < nspan)
+__device__ __forceinline__ void enter_span(const ts_attn_problem& P, const ts_attn_segment& seg, int hk,
+                                           TileCursor& tc) {
   const ts_attn_ref ref = load_uniform(P.seg_spans, seg.span0 + tc.sp);
   const ts_attn_run run = load_uniform(P.runs, ref.index);
   tc.kpos = ref.kpos;
   tc.len = run.len;
-  tc.k = run.k;
-  tc.v = run.v;
-  tc.k_row_stride = run.k_row_stride;
-  tc.k_head_stride = run.k_head_stride;
-  tc.v_row_stride = run.v_row_stride;
-  tc.v_head_stride = run.v_head_stride;
+  tc.k_rs = (int)run.k_row_stride;
+  tc.v_rs = (int)run.v_row_stride;
+  tc.kt = (const bf16*)run.k + (int64_t)hk * run.k_head_stride;
+  tc.vt = (const bf16*)run.v + (int64_t)hk * run.v_head_stride;
 }
 
-// Next 64-key tile after `tc` in a segment's key order that some row up to
-// `last` (segment-local) can see; sp == nspan when none is left.  Spans are in
-// key order, so once a tile starts past the last visible key so do all later
-// ones.  Tables are read only on entering a span.
+// `tc` itself if some row up to `last` (segment-local) can see its tile, else
+// the next such tile in the segment's key order; sp == nspan when none is
+// left.  Spans are in key order, so once a tile starts past the last visible
+// key so do all later ones.  Tables are read only on entering a span.
 template <int KT = BK>
-__device__ __forceinline__ TileCursor next_kv_tile(const ts_attn_problem& P, const ts_attn_segment& seg,
-                                                   int last, TileCursor tc) {
+__device__ __forceinline__ TileCursor settle_kv_tile(const ts_attn_problem& P, const ts_attn_segment& seg, int hk,
+                                                     int last, TileCursor tc) {
   const int off = seg.kv_len - seg.q_len;
-  tc.kt0 += KT;
   while (tc.sp < seg.nspan) {
     if (tc.kt0 >= tc.len) {
-      if (++tc.sp < seg.nspan) enter_span(P, seg, tc);
+      if (++tc.sp < seg.nspan) enter_span(P, seg, hk, tc);
       tc.kt0 = 0;
       continue;
     }
@@ -365,13 +365,24 @@ __device__ __forceinline__ TileCursor next_kv_tile(const ts_attn_problem& P, con
   return tc;
 }
 
+// the visible tile after `tc`: the K / V pointers advance by KT rows within a
+// span (no table reads, no 64-bit products)
+template <int KT = BK>
+__device__ __forceinline__ TileCursor next_kv_tile(const ts_attn_problem& P, const ts_attn_segment& seg, int hk,
+                                                   int last, TileCursor tc) {
+  tc.kt0 += KT;
+  tc.kt += KT * tc.k_rs;
+  tc.vt += KT * tc.v_rs;
+  return settle_kv_tile<KT>(P, seg, hk, last, tc);
+}
+
 // the first visible tile of a segment
 template <int KT = BK>
-__device__ __forceinline__ TileCursor first_kv_tile(const ts_attn_problem& P, const ts_attn_segment& seg,
+__device__ __forceinline__ TileCursor first_kv_tile(const ts_attn_problem& P, const ts_attn_segment& seg, int hk,
                                                     int last) {
-  TileCursor tc{0, -KT, 0, 0, 0, 0, 0, 0, 0, 0};
-  if (seg.nspan > 0) enter_span(P, seg, tc);
-  return next_kv_tile<KT>(P, seg, last, tc);
+  TileCursor tc{0, 0, 0, 0, nullptr, nullptr, 0, 0};
+  if (seg.nspan > 0) enter_span(P, seg, hk, tc);
+  return settle_kv_tile<KT>(P, seg, hk, last, tc);
 }
 
 // Row swizzle of the 256-byte-row LDS tiles: 16-byte chunk c of row r sits at
@@ -386,7 +397,7 @@ __device__ __forceinline__ TileCursor first_kv_tile(const ts_attn_problem& P, co
 // 2.2 clk per transposed read per CU, against 4.2 and 4.1 for s(r) = r).
 __device__ __forceinline__ int tile_swizzle(int r) { return r ^ ((r & 1) ? 12 : 0); }
 
-// DMA of one 64-key K/V tile of KV head hk into swizzled LDS tiles (rows of
+// DMA of the cursor's K/V tile of KT keys into swizzled LDS tiles (rows of
 // HD elements, chunk c of row r at slot c ^ tile_swizzle(r & 15)).  The WAVES
 // waves of a work-group (4 or 8) each issue instructions t = wave + WAVES u;
 // instruction t fills rows RPI t .. RPI t + RPI - 1 (RPI = 4 at HD 128, 2 at
@@ -394,25 +405,22 @@ __device__ __forceinline__ int tile_swizzle(int r) { return r ^ ((r & 1) ? 12 : 
 // chunk (l % (HD / 8)) ^ tile_swizzle(row).  Rows past the run arrive as
 // zeros.
 template <int WAVES = 4, int HD = D, int KT = BK>
-__device__ __forceinline__ void issue_kv_tile(int hk, int wave, int lane, const TileCursor& tc, bf16* sk,
-                                              bf16* sv) {
+__device__ __forceinline__ void issue_kv_tile(int wave, int lane, const TileCursor& tc, bf16* sk, bf16* sv) {
   static_assert(WAVES == 4 || WAVES == 8, "a tile is 16 or 32 instructions");
   static_assert(HD == 128 || HD == 256, "the swizzle needs 16 or 32 chunks per row");
   constexpr int CH = HD / 8, RPI = 64 / CH, NI = KT / RPI;
   static_assert(NI % WAVES == 0, "every wave issues the same number of instructions");
   const int nvalid = min(KT, tc.len - tc.kt0);
-  const bf16* kb = (const bf16*)tc.k + (int64_t)tc.kt0 * tc.k_row_stride + (int64_t)hk * tc.k_head_stride;
-  const bf16* vb = (const bf16*)tc.v + (int64_t)tc.kt0 * tc.v_row_stride + (int64_t)hk * tc.v_head_stride;
-  const rsrc_t rk = make_rsrc(kb, (uint32_t)(nvalid * tc.k_row_stride * 2));
-  const rsrc_t rv = make_rsrc(vb, (uint32_t)(nvalid * tc.v_row_stride * 2));
+  const rsrc_t rk = make_rsrc(tc.kt, (uint32_t)(nvalid * tc.k_rs * 2));
+  const rsrc_t rv = make_rsrc(tc.vt, (uint32_t)(nvalid * tc.v_rs * 2));
   if constexpr (HD == 128) {
     // rows 4 t + g4: the swizzle of row 4 (t + WAVES u) + g4 is that of row 4 t + g4
     const int g4 = lane >> 4, j16 = lane & 15;
     const int dma_row = 4 * wave + g4;
     const int dma_chunk = (j16 ^ tile_swizzle((4 * wave + g4) & 15)) << 3;
-    const int ko = (int)((dma_row * tc.k_row_stride + dma_chunk) * 2);
-    const int vo = (int)((dma_row * tc.v_row_stride + dma_chunk) * 2);
-    const int kstep = (int)(4 * WAVES * tc.k_row_stride * 2), vstep = (int)(4 * WAVES * tc.v_row_stride * 2);
+    const int ko = (dma_row * tc.k_rs + dma_chunk) * 2;
+    const int vo = (dma_row * tc.v_rs + dma_chunk) * 2;
+    const int kstep = 4 * WAVES * tc.k_rs * 2, vstep = 4 * WAVES * tc.v_rs * 2;
 #pragma unroll
     for (int u = 0; u < NI / WAVES; ++u) {
       buffer_dma16(rk, sk + (wave + WAVES * u) * 512, ko + u * kstep);
@@ -424,8 +432,8 @@ __device__ __forceinline__ void issue_kv_tile(int hk, int wave, int lane, const 
       const int t = wave + WAVES * u;
       const int row = RPI * t + lane / CH;
       const int chunk = ((lane % CH) ^ tile_swizzle(row & 15)) << 3;
-      buffer_dma16(rk, sk + t * 512, (int)((row * tc.k_row_stride + chunk) * 2));
-      buffer_dma16(rv, sv + t * 512, (int)((row * tc.v_row_stride + chunk) * 2));
+      buffer_dma16(rk, sk + t * 512, (row * tc.k_rs + chunk) * 2);
+      buffer_dma16(rv, sv + t * 512, (row * tc.v_rs + chunk) * 2);
     }
   }
 }

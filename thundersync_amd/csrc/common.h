@@ -200,6 +200,16 @@ __device__ __forceinline__ void buffer_dma16(rsrc_t r, void* lds, int voffset) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)lds, 16, voffset, 0, 0, 0);
 }
 
+// buffer_dma16 with the immediate instruction offset OFF, which the hardware
+// adds to the LDS address as well as to the global one (pinned by the probe
+// test): lane i writes lds + OFF + 16 i from base + voffset + OFF, so DMA
+// instructions whose LDS and global offsets advance together share one M0.
+template <int OFF>
+__device__ __forceinline__ void buffer_dma16_at(rsrc_t r, void* lds, int voffset) {
+  static_assert(OFF >= 0 && OFF < 4096, "a 12-bit instruction offset");
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)lds, 16, voffset, 0, OFF, 0);
+}
+
 // A raw buffer descriptor as four SGPR words (base[31:0]; base[47:32] with
 // stride 0; num_records; word 3 as above).  `base` and `bytes` must be
 // wave-uniform.
