@@ -111,9 +111,11 @@ def test_fa4_branch_shape_reduced(cuda):
     close(vc.grad, wv, "dv")
 
 
-def test_forest_head_dim_256(cuda):
+@pytest.mark.parametrize("d,hq,hkv", [(256, 24, 4), (80, 8, 2)])
+def test_forest_head_dims(cuda, d, hq, hkv):
     """A two-level forest (shared prompt, four completions, two sharing a first
-    turn) at D 256 with 24/4 heads against the dense-mask oracle."""
+    turn) at D 256 with 24/4 heads, and at D 80 (run zero-padded at 96) with
+    8/2 heads, against the dense-mask oracle."""
     spec = []
     import random
 
@@ -132,7 +134,7 @@ def test_forest_head_dim_256(cuda):
          for g, i, segs in spec]))
     oplan = ofo.compile_plan(ofo.build_forest(
         [ofo.Trajectory([ofo.Segment(tuple(t), k, s) for k, t, s in segs], g, i) for g, i, segs in spec]))
-    p, hq, hkv, d = plan.n_physical, 24, 4, 256
+    p = plan.n_physical
     print(f"forest d{d}: {p} tokens, {plan.n_nodes} nodes, {hq}/{hkv} heads", flush=True)
     mask = torch.tensor(ofo.visibility_mask(oplan))
     g = torch.Generator().manual_seed(9)
@@ -154,8 +156,30 @@ def test_forest_head_dim_256(cuda):
     close(vd.grad, vf.grad, "dv")
 
 
-def test_unsupported_head_dim_refused(cuda):
-    q = torch.randn(8, 4, 80, device=cuda, dtype=torch.bfloat16)
-    k = torch.randn(8, 1, 80, device=cuda, dtype=torch.bfloat16)
+PADDED = [
+    # head dim (runs at the next kernel width), query rows, chunk lengths, hq, hkv, dtype
+    (80, 70, [33, 70], 8, 2, torch.bfloat16),     # -> 96
+    (100, 50, [60, 50], 4, 1, torch.float16),     # -> 128, rows of 100 elements (not 16-byte multiples)
+    (112, 64, [64], 8, 2, torch.bfloat16),        # -> 128, the one-wave-per-head kernels
+    (160, 40, [90, 40], 8, 8, torch.bfloat16),    # -> 192
+    (8, 17, [20, 17], 4, 2, torch.bfloat16),      # -> 32
+    (200, 33, [33], 4, 2, torch.bfloat16),        # -> 256
+]
+
+
+@pytest.mark.parametrize("d,t,chunks,hq,hkv,dtype", PADDED)
+def test_other_head_dims_run_zero_padded(cuda, d, t, chunks, hq, hkv, dtype):
+    """Head dims the kernels are not built for run at the next kernel width
+    over zero-padded Q, K and V; output and gradients against the oracle at
+    the true head dim (scale d^-1/2 of the true head dim)."""
+    print(f"attention chain d={d} (padded to {hip.kernel_head_dim(d)}) t={t} chunks={chunks} hq={hq} hkv={hkv} "
+          f"{dtype}", flush=True)
+    run_chain(cuda, d, t, chunks, hq, hkv, seed=d + t, dtype=dtype)
+
+
+def test_head_dims_above_256_refused(cuda):
+    q = torch.randn(8, 4, 264, device=cuda, dtype=torch.bfloat16)
+    k = torch.randn(8, 1, 264, device=cuda, dtype=torch.bfloat16)
+    assert hip.kernel_head_dim(264) is None and hip.kernel_head_dim(0) is None
     with pytest.raises(ValueError, match="head dims"):
         hip.attention(q, hip.chain_layout(8, [8], 4, 1), [k], [k], 0.1)

@@ -107,15 +107,18 @@ def test_auto_takes_the_kernels_only_after_a_device_trial(unresolved, monkeypatc
     assert dispatch.hip_attention_available(_FakeCuda(torch.bfloat16))
     assert trial_recorder == [("hip_attention", 0, "torch.bfloat16", 128)]
     assert not dispatch.hip_attention_available(_FakeCuda(torch.bfloat16, index=1))
-    # fp16 and every supported head dim take their own trial; fp32 and other
-    # head dims never reach one
+    # fp16 and every head dim take their own trial; fp32 never reaches one
     assert dispatch.hip_attention_available(_FakeCuda(torch.float16))
     assert trial_recorder[-1] == ("hip_attention", 0, "torch.float16", 128)
     assert not dispatch.hip_attention_available(_FakeCuda(torch.float32))
     assert dispatch.hip_attention_available(_FakeCuda(torch.bfloat16, head_dim=256))
     assert trial_recorder[-1] == ("hip_attention", 0, "torch.bfloat16", 256)
-    assert not dispatch.hip_attention_available(_FakeCuda(torch.bfloat16, head_dim=80))
-    assert len(trial_recorder) == 4
+    # a head dim the kernels are not built for runs zero-padded (its own
+    # trial); above 256 none runs
+    assert dispatch.hip_attention_available(_FakeCuda(torch.bfloat16, head_dim=80))
+    assert trial_recorder[-1] == ("hip_attention", 0, "torch.bfloat16", 80)
+    assert not dispatch.hip_attention_available(_FakeCuda(torch.bfloat16, head_dim=320))
+    assert len(trial_recorder) == 5
     assert dispatch.hip_logprob_available(_FakeCuda(torch.bfloat16))
     assert trial_recorder[-1] == ("hip_logprob", 0, "torch.bfloat16", 128)
 

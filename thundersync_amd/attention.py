@@ -37,10 +37,14 @@ Reference entry points mirrored here (same argument meaning):
   (engine/streaming.py:1314-1423).
 
 Element types: bf16 and fp16 (Q, K, V of one call share one).  Head dims D:
-32, 64, 96, 128, 192 and 256 (128 and 256 run the DMA-staged kernels, the
-others the register-staged ones).  At head dim 256 the backward stores dS
-once in a workspace and forms dQ = dS K from it (see ``DS_MAX_BYTES``).
-There is no host path: CPU tensors, other dtypes or head dims raise.
+any from 1 to 256, as the reference's flash paths take
+(engine/streaming.py:532-548, :915-930).  The kernels are built for 32, 64,
+96, 128, 192 and 256 (128 and 256 run the DMA-staged kernels, the others the
+register-staged ones); any other D runs the next larger of them over Q, K
+and V zero-padded to it (see :func:`kernel_head_dim`).  At head dims 128 and
+256 the backward stores dS once in a workspace and forms dQ = dS K from it
+(see ``DS_MAX_BYTES``).  There is no host path: CPU tensors, other dtypes or
+head dims above 256 raise.
 """
 
 from __future__ import annotations
@@ -60,7 +64,8 @@ from ._abi import REF_DTYPE, RUN_DTYPE, SEG_DTYPE, AttnProblem, AttnRows
 from .dispatch import HIP_BACKWARD_PATH, HIP_PATH, count_attention_path
 from .operator_profiling import operator_range
 
-HEAD_DIMS = (32, 64, 96, 128, 192, 256)
+HEAD_DIMS = (32, 64, 96, 128, 192, 256)  # the head dims the kernels are built for
+MAX_HEAD_DIM = 256
 HEAD_DIM = 128  # the head dim the tuned kernels take; also the launch-order estimate's row width
 ELEMENT_DTYPES = (torch.bfloat16, torch.float16)
 
@@ -412,7 +417,8 @@ def _validate_call(layout: AttnLayout, query: torch.Tensor, keys, values) -> Non
         raise TypeError(f"thundersync_amd attention takes bf16 or fp16, got {query.dtype}")
     head_dim = query.shape[-1] if query.dim() == 3 else -1
     if head_dim not in HEAD_DIMS:
-        raise ValueError(f"thundersync_amd attention takes head dims {HEAD_DIMS}, got query {tuple(query.shape)}")
+        raise ValueError(f"thundersync_amd attention takes head dims 1..{MAX_HEAD_DIM} (kernels at {HEAD_DIMS}), "
+                         f"got query {tuple(query.shape)}")
     _check_rows_tensor(query, "query", layout.hq, head_dim)
     if query.shape[0] != layout.q_rows:
         raise ValueError(f"query has {query.shape[0]} rows, layout {layout.q_rows}")
@@ -596,9 +602,36 @@ class _Attention(torch.autograd.Function):
         return (dq, None, None, None, *dkeys, *dvalues)
 
 
+def kernel_head_dim(head_dim: int) -> int | None:
+    """The kernel head dim that runs `head_dim`: itself when the kernels are
+    built for it, else the next larger one (for 1 <= head_dim <= 256), None
+    above 256.  Zero columns appended to Q and K change no score and zero
+    columns of V only add output columns, so the padded call's output and
+    gradients restricted to the first `head_dim` columns are the unpadded
+    ones; the caller's scale is used as given."""
+    if head_dim < 1:
+        return None
+    for d in HEAD_DIMS:
+        if head_dim <= d:
+            return d
+    return None
+
+
 def attention(query: torch.Tensor, layout: AttnLayout, keys: Sequence[torch.Tensor],
               values: Sequence[torch.Tensor], scale: float) -> tuple[torch.Tensor, torch.Tensor]:
-    """Core op: query ``[R, Hq, D]`` bf16 or fp16 -> (out ``[R, Hq, D]``, lse ``[Hq, R]`` fp32)."""
+    """Core op: query ``[R, Hq, D]`` bf16 or fp16 -> (out ``[R, Hq, D]``, lse ``[Hq, R]`` fp32).
+
+    A head dim the kernels are not built for (any other D up to 256) runs at
+    :func:`kernel_head_dim` over zero-padded copies of Q, K and V; autograd
+    takes the gradients back through the padding."""
+    d = query.shape[-1] if query.dim() == 3 else -1
+    dk = kernel_head_dim(d)
+    if dk is not None and dk != d:
+        def pad(t):
+            return torch.nn.functional.pad(t, (0, dk - t.shape[-1]))
+        out, lse = _Attention.apply(pad(query), layout, float(scale), len(keys), *(pad(k) for k in keys),
+                                    *(pad(v) for v in values))
+        return out[..., :d], lse
     return _Attention.apply(query, layout, float(scale), len(keys), *keys, *values)
 
 

@@ -59,11 +59,19 @@ __device__ __forceinline__ void wait_vmcnt() {
 #endif
 // keys per K tile: TS_DQDS_KT256 (64) at head dim 256, TS_DQDS_KT128 (32) at 128
 template <int HD> constexpr int dq_ds_tile_keys() { return HD > 128 ? TS_DQDS_KT256 : TS_DQDS_KT128; }
-// LDS stages: three of 48 KB at head dim 256 with 64-key tiles, else two
-template <int HD> constexpr int dq_ds_stages() { return HD > 128 && dq_ds_tile_keys<HD>() == 64 ? 3 : 2; }
-// work-groups per CU the LDS stages allow
+#ifndef TS_DQDS_ST128
+#define TS_DQDS_ST128 2
+#endif
+// LDS stages: three of 48 KB at head dim 256 with 64-key tiles, else
+// TS_DQDS_ST128 (two) at head dim 128 and two at 256
+template <int HD> constexpr int dq_ds_stages() {
+  return HD > 128 ? (dq_ds_tile_keys<HD>() == 64 ? 3 : 2) : TS_DQDS_ST128;
+}
+// work-groups per CU the LDS stages allow (160 KB per CU, at most four)
 template <int HD> constexpr int dq_ds_occupancy() {
-  return HD > 128 ? (dq_ds_tile_keys<HD>() == 64 ? 1 : 3) : (dq_ds_tile_keys<HD>() == 64 ? 2 : 4);
+  constexpr int stage = (dq_ds_tile_keys<HD>() * HD + 4 * (dq_ds_tile_keys<HD>() / 16) * kDsBlock) * 2;
+  constexpr int n = (160 * 1024) / (dq_ds_stages<HD>() * stage);
+  return n > 4 ? 4 : n;
 }
 
 template <typename E, int HD, int GC>

@@ -97,9 +97,9 @@ def _available(like: torch.Tensor, kernel: str, key: int, trial) -> bool:
 
 def hip_attention_available(query: torch.Tensor) -> bool:
     """Whether this query (any layout with the head dim last) may take the HIP attention."""
-    from .attention import HEAD_DIMS
+    from .attention import kernel_head_dim
 
-    if query.shape[-1] not in HEAD_DIMS:
+    if kernel_head_dim(int(query.shape[-1])) is None:
         return False
     return _available(query, "hip_attention", int(query.shape[-1]), attention_trial)
 
