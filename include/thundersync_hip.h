@@ -36,6 +36,7 @@ extern "C" {
 #define TS_F32 0
 #define TS_F16 1
 #define TS_BF16 2
+#define TS_F64 3
 
 /* Library version string, e.g. "thundersync_hip 0.1.0 gfx950". */
 const char* ts_hip_version(void);
@@ -358,6 +359,52 @@ int ts_logprob_grad_hidden(const void* dlogits, int64_t ld_dlogits, const void* 
 int ts_logprob_grad_weight(const void* dlogits, int64_t ld_dlogits, const void* hidden,
                            int64_t ld_hidden, int64_t rows, int64_t dim, int64_t vocab,
                            float* grad_weight, int64_t ld_grad, int dtype, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Fused logprob / entropy at the inputs' precision (fp32 or fp64)
+ *
+ * The reference keeps FP32/FP64 hidden states and heads at their precision
+ * (accel/fused_logprob.py:27-58: `_accum_dtype` widens only bf16/fp16); these
+ * entry points compute logits, softmax statistics, dlogits and both VJP
+ * products in the input type T (dtype TS_F32 or TS_F64) on the vector ALUs.
+ * hidden [rows, dim] (row stride ld_hidden), weight [vocab, dim]
+ * (ld_weight), target int64 [rows]; every other array is of T.  No
+ * alignment or stride-multiple requirements.  A target outside [0, vocab)
+ * yields a NaN logprob and no one-hot term, as in the bf16/fp16 operators.
+ * ------------------------------------------------------------------------ */
+
+/* Workspace bytes ts_logprob_fwd_exact needs (-1 for a bad argument). */
+int64_t ts_logprob_fwd_exact_workspace(int64_t rows, int64_t vocab, int dtype);
+
+/* logprob[n] = l[n, target[n]] - lse[n], lse[n] (natural log) and, when
+ * `entropy` is not NULL, entropy[n] = lse[n] - sum_v softmax(l[n])_v l[n, v],
+ * with l = hidden . W^T, all in T.  Replaces _FusedLinearLogprob.forward and
+ * _FusedLinearLogprobEntropy.forward for fp32/fp64 inputs
+ * (accel/fused_logprob.py:69-113, :249-267). */
+int ts_logprob_fwd_exact(const void* hidden, int64_t ld_hidden, const void* weight, int64_t ld_weight,
+                         const int64_t* target, int64_t rows, int64_t dim, int64_t vocab, void* logprob,
+                         void* entropy, void* lse, void* workspace, int64_t workspace_bytes, int dtype,
+                         void* stream);
+
+/* dlogits [rows, ld_dlogits] (T) = -p * (g_lp + g_ent * (log p + H)) +
+ * g_lp * onehot(target), p = exp(l - lse), recomputing l; grad_ent (and
+ * then entropy) may be NULL for the logprob-only objective.  Replaces the
+ * coefficient backward of _FusedLinearLogprob.backward and
+ * _FusedLinearLogprobEntropy.backward for fp32/fp64 inputs
+ * (accel/fused_logprob.py:143-165, :285-295). */
+int ts_logprob_dlogits_exact(const void* hidden, int64_t ld_hidden, const void* weight, int64_t ld_weight,
+                             const int64_t* target, const void* lse, const void* entropy, const void* grad_lp,
+                             const void* grad_ent, int64_t rows, int64_t dim, int64_t vocab, void* dlogits,
+                             int64_t ld_dlogits, int dtype, void* stream);
+
+/* c [m, n] (row stride ldc) = a . b, or c += a . b when accumulate != 0,
+ * in T: element (i, j) of the product is sum_k a[i a_m + k a_k] *
+ * b[k b_k + j b_n] (any element strides).  The hidden and weight VJPs
+ * `_matmul_accum(dlogits, weight)` and `_matmul_accum(dlogits.t(), h)` with
+ * the `grad_weight.add_` of _FusedLinearLogprob.backward for fp32/fp64
+ * inputs (accel/fused_logprob.py:167-193, :297-306). */
+int ts_matmul_exact(const void* a, int64_t a_m, int64_t a_k, const void* b, int64_t b_k, int64_t b_n, int64_t m,
+                    int64_t n, int64_t k, void* c, int64_t ldc, int accumulate, int dtype, void* stream);
 
 /* ------------------------------------------------------------------------
  * Merged-weight LoRA linear (bf16 or fp16 operands, fp32 accumulation)

@@ -120,3 +120,56 @@ def test_c1_grpo_update(cuda):
         worst = max(worst, e)
         assert e < 5e-2, (name, e)
     print(f"  SGD update of {len(exp)} parameters: worst relative error {worst:.2e}", flush=True)
+
+
+def test_c1_grpo_update_in_fp32(cuda):
+    """C1 at its stated precision: the fp32 model on the GPU, each
+    trajectory's hidden states from the stock decoder (attention through
+    torch's SDPA, which is where the reference's dispatch sends fp32
+    attention: its flash kernels take bf16 / fp16 only) and every scored
+    token's logprob through the fused logprob's fp32 kernels with the
+    trainable head; against the fp32 model on the CPU.  Bars: loss within
+    1e-5 relative, every gradient within 1e-4 relative Frobenius error (fp32
+    against fp32; only summation orders differ)."""
+    from thundersync_amd.fused_logprob import fused_logprob
+
+    print("C1 in fp32: tiny Qwen3 GRPO update, fused fp32 logprob on the GPU vs the fp32 CPU model", flush=True)
+    ref = c1_model(seed=0)
+    prompt, bodies, adv = c1_rollouts(seed=1)
+    gpu = copy.deepcopy(ref).to(device=cuda)
+    gpu.config._attn_implementation = "sdpa"
+    gpu.train()
+    n_tokens = sum(len(b) for b in bodies)
+    loss = torch.zeros((), device=cuda)
+    for i, body in enumerate(bodies):
+        tokens = torch.tensor(prompt + body, device=cuda)
+        hidden = gpu.model(input_ids=tokens[None]).last_hidden_state[0]
+        rows = hidden[len(prompt) - 1 : -1]
+        lp = fused_logprob(rows, gpu.lm_head.weight, tokens[len(prompt):], chunk=16)
+        assert lp.dtype == torch.float32
+        loss = loss - float(adv[i]) * lp.sum() / n_tokens
+    loss.backward()
+    torch.cuda.synchronize()
+
+    want = torch.zeros(())
+    for i, body in enumerate(bodies):
+        tokens = torch.tensor(prompt + body)
+        logits = ref(input_ids=tokens[None]).logits[0]
+        lp_i = torch.log_softmax(logits, -1)[len(prompt) - 1 : -1].gather(1, tokens[len(prompt):, None])[:, 0]
+        want = want - float(adv[i]) * lp_i.sum() / n_tokens
+    want.backward()
+    err = abs(loss.item() - want.item()) / abs(want.item())
+    print(f"  loss {loss.item():.8f} vs {want.item():.8f} (relative {err:.2e})", flush=True)
+    assert err < 1e-5
+
+    got = {n: p for n, p in gpu.named_parameters()}
+    exp = {n: p for n, p in ref.named_parameters()}
+    worst = 0.0
+    for name in sorted(exp):
+        if exp[name].grad is None:  # the input embedding of unused tokens aside, every parameter learns
+            assert got[name].grad is None, name
+            continue
+        e = rel(got[name].grad, exp[name].grad)
+        worst = max(worst, e)
+        assert e < 1e-4, (name, e)
+    print(f"  parameter gradients: worst relative error {worst:.2e}", flush=True)

@@ -160,8 +160,10 @@ def test_validation_errors(cuda):
         hip.fused_logprob(h, w, t[:3])
     with pytest.raises(ValueError, match="does not match hidden dim"):
         hip.fused_logprob(h, w[:, :4], t)
-    with pytest.raises(TypeError):
-        hip.fused_logprob(h.float(), w.float(), t)
+    with pytest.raises(TypeError):  # one dtype for hidden and head
+        hip.fused_logprob(h.float(), w, t)
+    with pytest.raises(TypeError):  # fp32 / fp64 run at their precision; integer tensors do not
+        hip.fused_logprob(h.to(torch.int32), w.to(torch.int32), t)
     with pytest.raises(RuntimeError, match="GPU only"):
         hip.fused_logprob(h.cpu(), w.cpu(), t.cpu())
 

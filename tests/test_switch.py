@@ -121,6 +121,11 @@ def test_auto_takes_the_kernels_only_after_a_device_trial(unresolved, monkeypatc
     assert len(trial_recorder) == 5
     assert dispatch.hip_logprob_available(_FakeCuda(torch.bfloat16))
     assert trial_recorder[-1] == ("hip_logprob", 0, "torch.bfloat16", 128)
+    # the fused logprob also takes fp32 and fp64 (its input-precision kernels)
+    assert dispatch.hip_logprob_available(_FakeCuda(torch.float32))
+    assert trial_recorder[-1] == ("hip_logprob", 0, "torch.float32", 128)
+    assert dispatch.hip_logprob_available(_FakeCuda(torch.float64))
+    assert not dispatch.hip_logprob_available(_FakeCuda(torch.int32))
 
 
 def test_require_skips_the_trial_and_off_never_loads(unresolved, monkeypatch, trial_recorder):

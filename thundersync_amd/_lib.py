@@ -57,6 +57,13 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "ts_logprob_grad_hidden_workspace": (_I64, [_I64, _I64, _I64]),
     "ts_logprob_grad_hidden": (_INT, [_P, _I64, _P, _I64, _I64, _I64, _I64, _P, _I64, _P, _I64, _INT, _P]),
     "ts_logprob_grad_weight": (_INT, [_P, _I64, _P, _I64, _I64, _I64, _I64, _P, _I64, _INT, _P]),
+    "ts_logprob_fwd_exact_workspace": (_I64, [_I64, _I64, _INT]),
+    "ts_logprob_fwd_exact": (_INT, [_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _P, _P, _P, _P, _I64, _INT, _P]),
+    "ts_logprob_dlogits_exact": (
+        _INT,
+        [_P, _I64, _P, _I64, _P, _P, _P, _P, _P, _I64, _I64, _I64, _P, _I64, _INT, _P],
+    ),
+    "ts_matmul_exact": (_INT, [_P, _I64, _I64, _P, _I64, _I64, _I64, _I64, _I64, _P, _I64, _INT, _INT, _P]),
     "ts_lora_fwd": (_INT, [_P, _I64, _P, _I64, _I64, _I64, _I64, _P, _I64, _INT, _P]),
     "ts_lora_bwd_workspace": (_I64, [_I64, _I64, _I64, _I64]),
     "ts_lora_bwd": (
@@ -90,7 +97,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
 }
 
 TS_OK = 0
-TS_F32, TS_F16, TS_BF16 = 0, 1, 2
+TS_F32, TS_F16, TS_BF16, TS_F64 = 0, 1, 2, 3
 
 _LOCK = threading.Lock()
 _LIB: ctypes.CDLL | None = None
@@ -194,7 +201,8 @@ def dtype_code(dtype) -> int:
     if _DTYPE_CODES is None:
         import torch
 
-        _DTYPE_CODES = {torch.float32: TS_F32, torch.float16: TS_F16, torch.bfloat16: TS_BF16}
+        _DTYPE_CODES = {torch.float32: TS_F32, torch.float16: TS_F16, torch.bfloat16: TS_BF16,
+                        torch.float64: TS_F64}
     code = _DTYPE_CODES.get(dtype)
     if code is None:
         raise TypeError(f"unsupported dtype {dtype}")

@@ -85,8 +85,9 @@ def logprob_trial(device: torch.device, dtype: torch.dtype, dim: int) -> None:
         raise RuntimeError("HIP logprob trial produced nonfinite values")
 
 
-def _available(like: torch.Tensor, kernel: str, key: int, trial) -> bool:
-    if not like.is_cuda or like.dtype not in (torch.bfloat16, torch.float16):
+def _available(like: torch.Tensor, kernel: str, key: int, trial,
+               dtypes=(torch.bfloat16, torch.float16)) -> bool:
+    if not like.is_cuda or like.dtype not in dtypes:
         return False
     if _lib.library() is None:  # off, or auto without a library; require raises
         return False
@@ -105,5 +106,7 @@ def hip_attention_available(query: torch.Tensor) -> bool:
 
 
 def hip_logprob_available(hidden: torch.Tensor) -> bool:
-    """Whether these hidden states may take the HIP fused logprob."""
-    return _available(hidden, "hip_logprob", int(hidden.shape[-1]), logprob_trial)
+    """Whether these hidden states may take the HIP fused logprob (bf16 and
+    fp16 on MFMA; fp32 and fp64 at their own precision)."""
+    return _available(hidden, "hip_logprob", int(hidden.shape[-1]), logprob_trial,
+                      (torch.bfloat16, torch.float16, torch.float32, torch.float64))

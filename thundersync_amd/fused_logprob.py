@@ -22,8 +22,12 @@ is the ``[chunk, V]`` bf16 dlogits block plus a workspace of vocabulary-range
 partial sums for grad_hidden when one block's row tiles do not fill the GPU,
 and the fp32 ``[V, D]`` accumulator when the weight gradient is needed.
 
-bf16 or fp16 (one element type per call), GPU only: other dtypes and CPU
-tensors raise.
+bf16 or fp16 (one element type per call) on the MFMA kernels above; fp32
+and fp64 at their own precision, as the reference keeps them (FL:27-58):
+logits, statistics, dlogits and both VJP products in the input type on the
+vector-ALU kernels (``ts_logprob_fwd_exact``, ``ts_logprob_dlogits_exact``,
+``ts_matmul_exact``), with the same O(chunk * V) dlogits block and outputs
+in the input type.  GPU only: other dtypes and CPU tensors raise.
 """
 
 from __future__ import annotations
@@ -34,7 +38,8 @@ from . import _lib
 from .operator_profiling import device_role, operator_range
 
 
-ELEMENT_DTYPES = (torch.bfloat16, torch.float16)
+ELEMENT_DTYPES = (torch.bfloat16, torch.float16)  # the MFMA kernels
+EXACT_DTYPES = (torch.float32, torch.float64)     # the input-precision kernels
 CHECK_TARGETS_ENV = "THUNDERSYNC_CHECK_TARGETS"
 
 
@@ -66,9 +71,9 @@ def _validate(hidden: torch.Tensor, weight: torch.Tensor, target: torch.Tensor) 
         raise ValueError(f"weight {tuple(weight.shape)} does not match hidden dim {hidden.shape[1]}")
     if not hidden.is_cuda or not weight.is_cuda or not target.is_cuda:
         raise RuntimeError("thundersync_amd fused logprob runs on the GPU only; got a CPU tensor")
-    if hidden.dtype not in ELEMENT_DTYPES or weight.dtype != hidden.dtype:
+    if hidden.dtype not in ELEMENT_DTYPES + EXACT_DTYPES or weight.dtype != hidden.dtype:
         raise TypeError(
-            "thundersync_amd fused logprob takes bf16 or fp16 hidden and weight of one dtype, got "
+            "thundersync_amd fused logprob takes bf16, fp16, fp32 or fp64 hidden and weight of one dtype, got "
             f"{hidden.dtype}/{weight.dtype}"
         )
     _check_targets(target, weight.shape[0])
@@ -86,7 +91,86 @@ def _rows_ok(t: torch.Tensor) -> torch.Tensor:
     return t.contiguous()
 
 
+def _unit_stride(t: torch.Tensor) -> torch.Tensor:
+    return t if t.stride(1) == 1 or t.shape[1] <= 1 else t.contiguous()
+
+
+def _forward_exact(hidden, weight, target, with_entropy):
+    """fp32 / fp64: logprob, entropy and lse in the input type."""
+    lib = _lib.require_library()
+    h, w = _unit_stride(hidden), _unit_stride(weight)
+    t = target.to(torch.int64).contiguous()
+    n, d = h.shape
+    v = w.shape[0]
+    code = _lib.dtype_code(h.dtype)
+    lp = torch.empty(n, dtype=h.dtype, device=h.device)
+    lse = torch.empty(n, dtype=h.dtype, device=h.device)
+    ent = torch.empty(n, dtype=h.dtype, device=h.device) if with_entropy else None
+    ws_bytes = int(lib.ts_logprob_fwd_exact_workspace(n, v, code))
+    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=h.device)
+    _lib.check(
+        lib.ts_logprob_fwd_exact(
+            h.data_ptr(), max(h.stride(0), d), w.data_ptr(), max(w.stride(0), d), t.data_ptr(), n, d, v,
+            lp.data_ptr(), _lib.ptr(ent), lse.data_ptr(), ws.data_ptr(), ws_bytes, code, _lib.stream_of(h),
+        ),
+        f"ts_logprob_fwd_exact(rows={n}, dim={d}, vocab={v}, {h.dtype})",
+    )
+    return lp, ent, lse
+
+
+def _backward_exact(hidden, weight, target, lse, ent, grad_lp, grad_ent, chunk, needs_weight_grad):
+    """fp32 / fp64: the reference's chunk loop (FL:137-193) with a [chunk, V]
+    dlogits block in the input type; grad_weight accumulated in it."""
+    lib = _lib.require_library()
+    h, w = _unit_stride(hidden), _unit_stride(weight)
+    t = target.to(torch.int64).contiguous()
+    n, d = h.shape
+    v = w.shape[0]
+    dt, dev = h.dtype, h.device
+    grad_hidden = torch.empty(n, d, dtype=dt, device=dev)
+    grad_weight = torch.zeros(v, d, dtype=dt, device=dev) if needs_weight_grad else None
+    if n == 0:
+        return grad_hidden, grad_weight
+    code, stream = _lib.dtype_code(dt), _lib.stream_of(h)
+    ldh, ldw = max(h.stride(0), d), max(w.stride(0), d)
+    block = min(max(1, int(chunk)), n)
+    dl = torch.empty(block, v, dtype=dt, device=dev)
+    g_lp = grad_lp.to(dt).contiguous()
+    g_ent = grad_ent.to(dt).contiguous() if grad_ent is not None else None
+    esize = h.element_size()
+    for i in range(0, n, block):
+        rows = min(block, n - i)
+        h_i = h.data_ptr() + i * ldh * esize
+        with operator_range("logprob_head_coefficient_backward", role=device_role(dev), rows=rows, vocab=v):
+            _lib.check(
+                lib.ts_logprob_dlogits_exact(
+                    h_i, ldh, w.data_ptr(), ldw, t[i:].data_ptr(), lse[i:].data_ptr(),
+                    ent[i:].data_ptr() if g_ent is not None else None, g_lp[i:].data_ptr(),
+                    g_ent[i:].data_ptr() if g_ent is not None else None, rows, d, v, dl.data_ptr(), v, code, stream,
+                ),
+                f"ts_logprob_dlogits_exact(rows={rows}, dim={d}, vocab={v})",
+            )
+        with operator_range("logprob_head_hidden_vjp", role=device_role(dev), rows=rows, hidden=d, vocab=v):
+            # grad_hidden[i:i+rows] = dl . W
+            _lib.check(
+                lib.ts_matmul_exact(dl.data_ptr(), v, 1, w.data_ptr(), ldw, 1, rows, d, v,
+                                    grad_hidden[i:].data_ptr(), d, 0, code, stream),
+                f"ts_matmul_exact(dlogits . weight, rows={rows}, dim={d}, vocab={v})",
+            )
+        if grad_weight is not None:
+            with operator_range("logprob_head_weight_vjp", role=device_role(dev), rows=rows, hidden=d, vocab=v):
+                # grad_weight += dl^T . h[i:i+rows]
+                _lib.check(
+                    lib.ts_matmul_exact(dl.data_ptr(), 1, v, h_i, ldh, 1, v, d, rows,
+                                        grad_weight.data_ptr(), d, 1, code, stream),
+                    f"ts_matmul_exact(dlogits^T . hidden, rows={rows}, dim={d}, vocab={v})",
+                )
+    return grad_hidden, grad_weight
+
+
 def _forward(hidden, weight, target, with_entropy):
+    if hidden.dtype in EXACT_DTYPES:
+        return _forward_exact(hidden, weight, target, with_entropy)
     lib = _lib.require_library()
     h, w = _rows_ok(_pad_dim(hidden)), _rows_ok(_pad_dim(weight))
     t = target.to(torch.int64).contiguous()
@@ -126,6 +210,8 @@ def backward_block_rows(n: int, chunk: int) -> int:
 
 
 def _backward(hidden, weight, target, lse, ent, grad_lp, grad_ent, chunk, needs_weight_grad):
+    if hidden.dtype in EXACT_DTYPES:
+        return _backward_exact(hidden, weight, target, lse, ent, grad_lp, grad_ent, chunk, needs_weight_grad)
     lib = _lib.require_library()
     d_in = hidden.shape[1]
     h, w = _rows_ok(_pad_dim(hidden)), _rows_ok(_pad_dim(weight))
