@@ -3,10 +3,11 @@
 Every dK/dV work item is one ``kv_block`` of keys of one visited run, and its
 cost is the number of query rows of its visits that see the block's first
 key; every forward/dQ item is one ``q_block`` of rows of one segment, and its
-cost is the number of keys its last row sees.  Both lists run longest first
-with ties in (segment or run, first row or key) order.  Here they are
-recomputed item by item and compared with the layout's tables, on the bench
-layouts and on random retained-chunk packs.
+cost is the number of keys its last row sees.  Both lists run in geometric
+cost bands of width ORDER_BAND, longest band first, and within a band in
+(segment or run, first row or key) order.  Here they are recomputed item by
+item and compared with the layout's tables, on the bench layouts and on
+random retained-chunk packs.
 """
 
 from __future__ import annotations
@@ -43,8 +44,11 @@ def expected_lists(lay):
                 first = max(0, kpos + k0 - (lay.seg_kv[s] - n))
                 cost += max(0, n - first)
             kv_items.append((-cost, run, k0))
-    q_items.sort()
-    kv_items.sort()
+    def band(cost):
+        return int(np.floor(np.log(np.float64(max(cost, 1))) / np.log(1.0 + att.ORDER_BAND)))
+
+    q_items.sort(key=lambda x: (-band(-x[0]), x[1], x[2]))
+    kv_items.sort(key=lambda x: (-band(-x[0]), x[1], x[2]))
     return [(s, q0) for _, s, q0 in q_items], [(r, k0) for _, r, k0 in kv_items]
 
 
