@@ -277,7 +277,14 @@ int ts_attn_bwd(const ts_attn_problem* problem, ts_attn_rows q, ts_attn_rows out
  * of the layout's offsets and `ds` a 16-byte aligned device workspace of at
  * least (hq * ds_head + 512) * 2 bytes: every head's part, then one block
  * that takes the stores of steps that compute no dS (its contents on entry
- * do not matter).
+ * do not matter).  dq_work (device; may be NULL): the dQ pass's own work
+ * list for GQA groups that are a multiple of 4 at head dim 128, pairs
+ * (segment, first row) of 64-row blocks (first row a multiple of 64, below
+ * the segment's rows; every such block of every segment once, longest first
+ * as the other lists, its first n_dq_long items item-major): each dQ
+ * work-group then serves two 32-row blocks, sharing its K tiles between
+ * eight waves instead of four.  NULL: the dQ pass takes the problem's
+ * q_work.
  * No counterpart in the reference, whose flash/FA4 backward kernels own
  * their scratch; it replaces the same calls as ts_attn_bwd. */
 int ts_attn_ds_route(int head_dim, int group);
@@ -288,7 +295,8 @@ int ts_attn_ds_layout(const ts_attn_segment* segs, int32_t n_segs, const ts_attn
 int ts_attn_bwd_ds(const ts_attn_problem* problem, ts_attn_rows q, ts_attn_rows out,
                    ts_attn_rows dout, const float* lse, int64_t lse_ld, float* rowstats,
                    ts_attn_rows dq, const int64_t* span_ds, const int64_t* visit_ds,
-                   int64_t ds_head, void* ds, int64_t ds_bytes, void* stream);
+                   int64_t ds_head, void* ds, int64_t ds_bytes, const int32_t* dq_work,
+                   int32_t n_dq_work, int32_t n_dq_long, void* stream);
 
 /* ------------------------------------------------------------------------
  * Fused chunked-vocab logprob / entropy (bf16 or fp16 operands, fp32 results)

@@ -92,7 +92,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "ts_attn_bwd_ds": (
         _INT,
         [ctypes.POINTER(AttnProblem), AttnRows, AttnRows, AttnRows, _P, _I64, _P, AttnRows, _P, _P, _I64, _P,
-         _I64, _P],
+         _I64, _P, ctypes.c_int32, ctypes.c_int32, _P],
     ),
 }
 

@@ -84,6 +84,10 @@ def q_block_rows(hq: int, hkv: int) -> int:
     return 32 * 4 // heads_per_block(hq // hkv)
 
 
+# rows per item of the dS route's dQ pass at GQA groups that are a multiple of 4
+DQ_BLOCK_ROWS = 64
+
+
 def kv_block_keys(hq: int, hkv: int) -> int:
     """Keys per dK/dV work-group (mirror of ts_attn_kv_block)."""
     return 48 if (hq // hkv) % 4 == 0 else 64
@@ -213,10 +217,24 @@ class AttnLayout:
         q_bytes = self.q_rows * self.hq * HEAD_DIM * 2 * 2
         q_long = _long_items([-c for c, _, _ in q_items], self.hkv * (group // heads_per_block(group)), kv_bytes)
         kv_long = _long_items(kv_costs, self.hkv, q_bytes)
+        # the dS route's dQ pass over 64-row items (GQA groups that are a
+        # multiple of 4): a dQ work-group then shares its K tiles between the
+        # two 32-row blocks of its four heads
+        dq_work, dq_long = np.zeros((0, 2), np.int32), 0
+        if group % 4 == 0:
+            dq_items = []
+            for s_, ((_, length), kv) in enumerate(zip(self.seg_q, self.seg_kv)):
+                for q0 in range(0, length, DQ_BLOCK_ROWS):
+                    dq_items.append((-(kv - length + min(q0 + DQ_BLOCK_ROWS, length)), s_, q0))
+            if dq_items:
+                da = np.array(dq_items, np.int64).reshape(-1, 3)
+                dq_items = [dq_items[i] for i in np.lexsort((da[:, 2], da[:, 1], -_cost_band(-da[:, 0])))]
+                dq_work = np.array([(s_, q0) for _, s_, q0 in dq_items], np.int32).reshape(-1, 2)
+                dq_long = _long_items([-c for c, _, _ in dq_items], self.hkv, kv_bytes)
         seg_spans = np.array(spans, REF_DTYPE) if spans else np.zeros(0, REF_DTYPE)
         run_visits = np.array(visit_rows, REF_DTYPE) if visit_rows else np.zeros(0, REF_DTYPE)
         return (segs, seg_spans, run_visits, q_work, kv_work, visit0, [len(v) for v in visits_of],
-                q_long, kv_long)
+                q_long, kv_long, dq_work, dq_long)
 
     def device_tables(self, device: torch.device):
         """Upload the layout's integer tables once per device (pinned, non-blocking)."""
@@ -227,9 +245,11 @@ class AttnLayout:
         with self._lock:
             hit = self._tables.get(key)
             if hit is None:
-                segs, spans, visits, q_work, kv_work, visit0, nvisit, q_long, kv_long = self._host_tables()
+                (segs, spans, visits, q_work, kv_work, visit0, nvisit, q_long, kv_long, dq_work,
+                 dq_long) = self._host_tables()
                 parts = [segs.view(np.uint8), spans.view(np.uint8), visits.view(np.uint8),
-                         q_work.view(np.uint8).reshape(-1), kv_work.view(np.uint8).reshape(-1)]
+                         q_work.view(np.uint8).reshape(-1), kv_work.view(np.uint8).reshape(-1),
+                         dq_work.view(np.uint8).reshape(-1)]
                 offsets, total = [], 0
                 for p in parts:
                     offsets.append(total)
@@ -249,6 +269,9 @@ class AttnLayout:
                     "run_visits": base + offsets[2],
                     "q_work": base + offsets[3],
                     "kv_work": base + offsets[4],
+                    "dq_work": base + offsets[5] if dq_work.shape[0] else None,
+                    "n_dq_work": int(dq_work.shape[0]),
+                    "n_dq_long": int(dq_long),
                     "n_q_work": int(q_work.shape[0]),
                     "n_kv_work": int(kv_work.shape[0]),
                     "visit0": visit0,
@@ -595,6 +618,10 @@ class _Attention(torch.autograd.Function):
             else:
                 rows = [_rows(t) for t in (query, out, dout, dq)]
                 keep = []
+                # the dQ pass's 64-row list where it applies (head dim 128, groups of 4)
+                dq_list, n_dq, n_dq_long = None, 0, 0
+                if query.shape[2] == HEAD_DIM and visit["dq_work"] is not None:
+                    dq_list, n_dq, n_dq_long = visit["dq_work"], visit["n_dq_work"], visit["n_dq_long"]
                 for hk0 in range(0, layout.hkv, kv_heads):
                     n, h0 = min(kv_heads, layout.hkv - hk0), hk0 * group
                     sub = problem
@@ -609,7 +636,7 @@ class _Attention(torch.autograd.Function):
                         lib.ts_attn_bwd_ds(ctypes.byref(sub), q_r, o_r, do_r, lse.data_ptr() + h0 * lse.shape[1] * 4,
                                            lse.shape[1], rowstats.data_ptr() + h0 * lse.shape[1] * 8, dq_r,
                                            tabs["span"], tabs["visit"], tabs["head"], work.data_ptr(),
-                                           work.numel() * 2, _lib.stream_of(query)),
+                                           work.numel() * 2, dq_list, n_dq, n_dq_long, _lib.stream_of(query)),
                         f"ts_attn_bwd_ds(rows={layout.q_rows}, hq={layout.hq}, hkv={layout.hkv}, heads from {h0})",
                     )
                 ctx.keep_bwd_heads = keep

@@ -176,7 +176,8 @@ int ts_attn_ds_layout(const ts_attn_segment* segs, int32_t n_segs, const ts_attn
 
 int ts_attn_bwd_ds(const ts_attn_problem* problem, ts_attn_rows q, ts_attn_rows out, ts_attn_rows dout,
                    const float* lse, int64_t lse_ld, float* rowstats, ts_attn_rows dq, const int64_t* span_ds,
-                   const int64_t* visit_ds, int64_t ds_head, void* ds, int64_t ds_bytes, void* stream) {
+                   const int64_t* visit_ds, int64_t ds_head, void* ds, int64_t ds_bytes, const int32_t* dq_work,
+                   int32_t n_dq_work, int32_t n_dq_long, void* stream) {
   using namespace ts::attn;
   const char* what = "ts_attn_bwd_ds";
   TS_CHECK_ARG(problem != nullptr, "%s: null problem", what);
@@ -189,7 +190,12 @@ int ts_attn_bwd_ds(const ts_attn_problem* problem, ts_attn_rows q, ts_attn_rows 
   TS_CHECK_ARG((problem->n_q_work == 0 && problem->n_kv_work == 0) ||
                    (ds && (uint64_t)ds % 16 == 0 && span_ds && visit_ds),
                "%s: null or unaligned workspace or tables", what);
-  const DsArgs args{span_ds, visit_ds, ds_head, (uint64_t)ds};
+  TS_CHECK_ARG(!dq_work || (n_dq_work >= 0 && n_dq_long >= 0 && n_dq_long <= n_dq_work &&
+                             (int64_t)n_dq_work * problem->hq < (1ll << 31)),
+               "%s: dQ work list counts", what);
+  TS_CHECK_ARG(!dq_work || (problem->head_dim == 128 && (problem->hq / problem->hkv) % 4 == 0),
+               "%s: a dQ work list is for GQA groups that are a multiple of 4 at head dim 128", what);
+  const DsArgs args{span_ds, visit_ds, ds_head, (uint64_t)ds, dq_work, n_dq_work, n_dq_long};
   return backward(problem, q, out, dout, lse, lse_ld, rowstats, dq, &args, what, stream);
 }
 

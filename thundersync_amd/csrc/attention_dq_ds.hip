@@ -28,16 +28,17 @@
 namespace ts {
 namespace attn {
 
-// the K half of issue_kv_tile: a 64-key K tile, every wave its share of the
-// HD / 2 DMA instructions (rows past the run arrive as zeros)
-template <int HD, int KT>
+// the K half of issue_kv_tile: a KT-key K tile, each of the WV waves its
+// share of the DMA instructions (rows past the run arrive as zeros)
+template <int HD, int KT, int WV>
 __device__ __forceinline__ void issue_k_tile(int wave, int lane, const TileCursor& tc, bf16* sk) {
   constexpr int CH = HD / 8, RPI = 64 / CH, NI = KT / RPI;
+  static_assert(NI % WV == 0, "every wave issues the same number of instructions");
   const int nvalid = min(KT, tc.len - tc.kt0);
   const u32x4 rk = raw_descriptor(tc.kt, (uint32_t)(nvalid * tc.k_rs * 2));
 #pragma unroll
-  for (int u = 0; u < NI / 4; ++u) {
-    const int t = wave + 4 * u;
+  for (int u = 0; u < NI / WV; ++u) {
+    const int t = wave + WV * u;
     const int row = RPI * t + lane / CH;
     const int chunk = ((lane % CH) ^ tile_swizzle(row & 15)) << 3;
     buffer_dma16_untracked(rk, sk + t * 512, (row * tc.k_rs + chunk) * 2);
@@ -67,16 +68,19 @@ template <int HD> constexpr int dq_ds_tile_keys() { return HD > 128 ? TS_DQDS_KT
 template <int HD> constexpr int dq_ds_stages() {
   return HD > 128 ? (dq_ds_tile_keys<HD>() == 64 ? 3 : 2) : TS_DQDS_ST128;
 }
-// work-groups per CU the LDS stages allow (160 KB per CU, at most four)
-template <int HD> constexpr int dq_ds_occupancy() {
-  constexpr int stage = (dq_ds_tile_keys<HD>() * HD + 4 * (dq_ds_tile_keys<HD>() / 16) * kDsBlock) * 2;
+// work-groups per CU the LDS stages of WV-wave work-groups allow (160 KB per
+// CU, at most four, and at most 16 waves)
+template <int HD, int WV> constexpr int dq_ds_occupancy() {
+  constexpr int stage = (dq_ds_tile_keys<HD>() * HD + WV * (dq_ds_tile_keys<HD>() / 16) * kDsBlock) * 2;
   constexpr int n = (160 * 1024) / (dq_ds_stages<HD>() * stage);
-  return n > 4 ? 4 : n;
+  constexpr int cap = 16 / WV;
+  return n > cap ? cap : n;
 }
 
-template <typename E, int HD, int GC>
-__global__ __launch_bounds__(kThreads, dq_ds_occupancy<HD>()) void dq_ds_kernel(ts_attn_problem P, DsArgs S,
-                                                                                ts_attn_rows dQ) {
+// WV waves (4, or 8 at head dim 128 with GC = 4 over 64-row items)
+template <typename E, int HD, int GC, int WV = 4>
+__global__ __launch_bounds__(64 * WV, (dq_ds_occupancy<HD, WV>())) void dq_ds_kernel(ts_attn_problem P, DsArgs S,
+                                                                                     ts_attn_rows dQ) {
   static_assert(HD == 128 || HD == 256, "the K tile swizzle needs 16 or 32 chunks per row");
   constexpr int KT = dq_ds_tile_keys<HD>();      // keys per tile (64 or 32)
   constexpr int NKB = KT / 16;                   // 16-key dS blocks per tile
@@ -84,8 +88,8 @@ __global__ __launch_bounds__(kThreads, dq_ds_occupancy<HD>()) void dq_ds_kernel(
   constexpr int NST = dq_ds_stages<HD>();        // LDS stages
   constexpr int KTILE = KT * HD;                 // elements of a K tile
   constexpr int DTILE = NKB * kDsBlock;          // a wave's dS blocks of the tile
-  constexpr int STAGE = KTILE + 4 * DTILE;
-  constexpr int PER_TILE = KT * HD / 2048 + NKB;  // DMA instructions per wave and tile
+  constexpr int STAGE = KTILE + WV * DTILE;
+  constexpr int PER_TILE = KT * HD / 512 / WV + NKB;  // DMA instructions per wave and tile
   __shared__ __attribute__((aligned(16))) bf16 s_buf[NST * STAGE];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -102,7 +106,7 @@ __global__ __launch_bounds__(kThreads, dq_ds_occupancy<HD>()) void dq_ds_kernel(
   const ts_attn_segment seg = load_uniform(P.segs, seg_id);
   const int T = seg.q_len;
   const int off = seg.kv_len - seg.q_len;
-  const int last = min(q0 + 128 / GC, T) - 1;  // the work-group's last row
+  const int last = min(q0 + 32 * WV / GC, T) - 1;  // the work-group's last row
   const bool rows_valid = 32 * rb < T;
 
   int ro[4], to[8];
@@ -130,7 +134,7 @@ __global__ __launch_bounds__(kThreads, dq_ds_occupancy<HD>()) void dq_ds_kernel(
   };
   auto issue = [&](const TileCursor& tc, int st) {
     bf16* buf = s_buf + st * STAGE;
-    issue_k_tile<HD, KT>(wave, lane, tc, buf);
+    issue_k_tile<HD, KT, WV>(wave, lane, tc, buf);
     if (tc.sp != ds_sp) ds_enter(tc);
     const int kb0 = tc.kt0 >> 4;
     const int nb = max(0, min(NKB, ds_n - kb0));
@@ -240,6 +244,18 @@ template <typename E>
 void launch_dq_ds_t(const ts_attn_problem& P, const DsArgs& S, ts_attn_rows dq, hipStream_t s) {
   const int group = P.hq / P.hkv;
   const int gc = heads_per_block(group);
+  if (S.dq_work && P.head_dim == 128 && gc == 4) {
+    // 64-row items: eight waves, two 32-row blocks per head
+    ts_attn_problem P2 = P;
+    P2.q_work = S.dq_work;
+    P2.n_q_work = S.n_dq_work;
+    P2.n_q_long = S.n_dq_long;
+    if (P2.n_q_work == 0) return;
+    ts::TimedLaunch timed_("attention.dq_kernel", s);
+    hipLaunchKernelGGL((dq_ds_kernel<E, 128, 4, 8>), dim3((unsigned)(P2.n_q_work * P.hkv * (group / 4))),
+                       dim3(512), 0, s, P2, S, dq);
+    return;
+  }
   const dim3 grid((unsigned)(P.n_q_work * P.hkv * (group / gc)));
   if (P.head_dim == 256)
     launch_dq_ds_hd<E, 256>(P, gc, grid, S, dq, s);

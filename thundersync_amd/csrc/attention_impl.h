@@ -261,6 +261,8 @@ struct DsArgs {
   const int64_t* visit;  // per run_visits entry: that of the span it visits
   int64_t head;          // elements per head
   uint64_t ptr;          // device address of the workspace (hq * head elements)
+  const int32_t* dq_work;  // the dQ pass's 64-row work list (groups of 4 at head dim 128), or null
+  int32_t n_dq_work, n_dq_long;
 };
 
 // One (segment, span) rectangle: row r of the segment sees run key j iff
