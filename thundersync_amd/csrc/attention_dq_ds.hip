@@ -63,16 +63,20 @@ template <int HD> constexpr int dq_ds_tile_keys() { return HD > 128 ? TS_DQDS_KT
 #ifndef TS_DQDS_ST128
 #define TS_DQDS_ST128 2
 #endif
+#ifndef TS_DQDS_ST128_8
+#define TS_DQDS_ST128_8 2
+#endif
 // LDS stages: three of 48 KB at head dim 256 with 64-key tiles, else
-// TS_DQDS_ST128 (two) at head dim 128 and two at 256
-template <int HD> constexpr int dq_ds_stages() {
-  return HD > 128 ? (dq_ds_tile_keys<HD>() == 64 ? 3 : 2) : TS_DQDS_ST128;
+// TS_DQDS_ST128 (two) at head dim 128 (TS_DQDS_ST128_8 for eight-wave
+// work-groups) and two at 256
+template <int HD, int WV = 4> constexpr int dq_ds_stages() {
+  return HD > 128 ? (dq_ds_tile_keys<HD>() == 64 ? 3 : 2) : (WV == 8 ? TS_DQDS_ST128_8 : TS_DQDS_ST128);
 }
 // work-groups per CU the LDS stages of WV-wave work-groups allow (160 KB per
 // CU, at most four, and at most 16 waves)
 template <int HD, int WV> constexpr int dq_ds_occupancy() {
   constexpr int stage = (dq_ds_tile_keys<HD>() * HD + WV * (dq_ds_tile_keys<HD>() / 16) * kDsBlock) * 2;
-  constexpr int n = (160 * 1024) / (dq_ds_stages<HD>() * stage);
+  constexpr int n = (160 * 1024) / (dq_ds_stages<HD, WV>() * stage);
   constexpr int cap = 16 / WV;
   return n > cap ? cap : n;
 }
@@ -85,7 +89,7 @@ __global__ __launch_bounds__(64 * WV, (dq_ds_occupancy<HD, WV>())) void dq_ds_ke
   constexpr int KT = dq_ds_tile_keys<HD>();      // keys per tile (64 or 32)
   constexpr int NKB = KT / 16;                   // 16-key dS blocks per tile
   constexpr int NMB = HD / 16;                   // 16-column blocks of dQ
-  constexpr int NST = dq_ds_stages<HD>();        // LDS stages
+  constexpr int NST = dq_ds_stages<HD, WV>();    // LDS stages
   constexpr int KTILE = KT * HD;                 // elements of a K tile
   constexpr int DTILE = NKB * kDsBlock;          // a wave's dS blocks of the tile
   constexpr int STAGE = KTILE + WV * DTILE;
