@@ -230,7 +230,7 @@ class AttnLayout:
                 da = np.array(dq_items, np.int64).reshape(-1, 3)
                 dq_items = [dq_items[i] for i in np.lexsort((da[:, 2], da[:, 1], -_cost_band(-da[:, 0])))]
                 dq_work = np.array([(s_, q0) for _, s_, q0 in dq_items], np.int32).reshape(-1, 2)
-                dq_long = _long_items([-c for c, _, _ in dq_items], self.hkv, kv_bytes)
+                dq_long = _long_items([-c for c, _, _ in dq_items], self.hkv * (group // 4), kv_bytes)
         seg_spans = np.array(spans, REF_DTYPE) if spans else np.zeros(0, REF_DTYPE)
         run_visits = np.array(visit_rows, REF_DTYPE) if visit_rows else np.zeros(0, REF_DTYPE)
         return (segs, seg_spans, run_visits, q_work, kv_work, visit0, [len(v) for v in visits_of],
