@@ -567,6 +567,7 @@ class _Attention(torch.autograd.Function):
         ctx.keep = (runs, host)
         ctx.save_for_backward(query, out, lse, *kv)
         ctx.mark_non_differentiable(lse)
+        ctx.set_materialize_grads(False)  # no zero-filled gradient for lse
         return out, lse
 
     @staticmethod
@@ -576,8 +577,14 @@ class _Attention(torch.autograd.Function):
         layout, n = ctx.layout, ctx.n_sources
         keys, values = kv[:n], kv[n:]
         lib = _lib.require_library()
+        if dout is None:
+            dout = torch.zeros_like(out)
         dout = dout.contiguous() if dout.stride(2) != 1 or dout.stride(0) % 8 or dout.stride(1) % 8 else dout
-        dq = torch.empty(query.shape, dtype=query.dtype, device=query.device)
+        # dQ in the query's own layout where it is dense (a [1, Hq, T, D] query
+        # seen as rows gets its gradient without a copy into that layout)
+        dq = torch.empty_like(query)
+        if dq.stride(2) != 1 or dq.stride(0) % 8 or dq.stride(1) % 8:
+            dq = torch.empty(query.shape, dtype=query.dtype, device=query.device)
         covered = sum(t for _, t in layout.seg_q)
         if covered != layout.q_rows:
             dq.zero_()
@@ -714,7 +721,8 @@ def _query_rows(query: torch.Tensor) -> torch.Tensor:
     """``[1, Hq, T, D]`` (any strides) -> ``[T, Hq, D]`` view."""
     if query.dim() != 4 or query.shape[0] != 1:
         raise ValueError(f"query must be [1, Hq, T, D], got {tuple(query.shape)}")
-    return query[0].transpose(0, 1)
+    # squeeze, not select: the gradient of a select is a zero-filled copy
+    return query.squeeze(0).transpose(0, 1)
 
 
 def _as_rows(t: torch.Tensor) -> torch.Tensor:
@@ -1125,11 +1133,15 @@ def hip_attention_forward(module, query, key, value, attention_mask, scaling=Non
     """
     if dropout:
         raise ValueError("attention dropout is not supported on this path")
+    scale = scaling if scaling is not None else query.shape[-1] ** -0.5
+    if query.shape[0] == 1:
+        # views whose gradients are views too (an indexed batch row's gradient
+        # would be a zero-filled copy of the whole batch)
+        o = causal_attention(query, [key.squeeze(0).transpose(0, 1)], [value.squeeze(0).transpose(0, 1)], scale)
+        return o.transpose(1, 2), None
     outs = []
-    for b in range(query.shape[0]):
-        k = key[b].transpose(0, 1)
-        v = value[b].transpose(0, 1)
-        o = causal_attention(query[b : b + 1], [k], [v], scaling if scaling is not None else query.shape[-1] ** -0.5)
+    for qb, kb, vb in zip(query.unbind(0), key.unbind(0), value.unbind(0)):
+        o = causal_attention(qb.unsqueeze(0), [kb.transpose(0, 1)], [vb.transpose(0, 1)], scale)
         outs.append(o.transpose(1, 2))
     return torch.cat(outs, 0), None
 
@@ -1141,8 +1153,8 @@ def forest_attention_forward(module, query, key, value, attention_mask, dropout=
         raise RuntimeError("forest attention was invoked outside `forest_context`")
     if query.shape[0] != 1:
         raise ValueError(f"the forest is already the batch; expected batch dim 1, got {query.shape[0]}")
-    out = forest_attention(query[0].transpose(0, 1), key[0].transpose(0, 1), value[0].transpose(0, 1),
-                           plan, scale=scaling)
+    out = forest_attention(query.squeeze(0).transpose(0, 1), key.squeeze(0).transpose(0, 1),
+                           value.squeeze(0).transpose(0, 1), plan, scale=scaling)
     return out.unsqueeze(0), None
 
 
