@@ -453,11 +453,14 @@ __global__ __launch_bounds__(kGemmThreads, 1) void grad_weight_kernel(DwArgs p) 
   }
 }
 
-// ksplit (vocabulary ranges) for grad_hidden: one work-group per CU when the
-// row tiles alone do not give them, each range at least 4096 vocabulary rows
+// ksplit (vocabulary ranges) for grad_hidden: as many ranges as keep the
+// launch within one round of 256 work-groups (one per CU) when the row tiles
+// alone do not fill it -- a second, partial round would cost a whole range's
+// time (80 tiles: three ranges of a third, not four of a quarter in two
+// rounds) -- each range at least 4096 vocabulary rows
 inline void grad_hidden_split(int64_t rows, int64_t dim, int64_t vocab, int& ksplit, int& kper) {
   const int64_t tiles = ((rows + TN - 1) / TN) * ((dim + TM - 1) / TM);
-  int64_t k = (256 + tiles - 1) / tiles;
+  int64_t k = 256 / tiles;
   k = std::min<int64_t>(k, std::max<int64_t>(1, vocab / 4096));
   k = std::max<int64_t>(1, std::min<int64_t>(k, 16));
   int64_t per = (vocab + k - 1) / k;
