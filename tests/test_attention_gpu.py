@@ -77,6 +77,35 @@ def test_chain_matches_oracle(cuda, t, chunks, hq, hkv):
         close(v.grad, wvs[i], f"dv[{i}]")
 
 
+@pytest.mark.parametrize("batch", [1, 2])
+def test_head_major_query_and_adapter_layouts(cuda, batch):
+    """A head-major query ([B, Hq, T, D] contiguous, as the reference's
+    callable backend and FA4 adapter receive it) gets its gradient in its own
+    layout, without a copy through a batch index; the HF adapter (B = 1 and
+    B = 2) returns [B, T, Hq, D] and every gradient matches the oracle."""
+    print(f"head-major query layouts, batch {batch}", flush=True)
+    t, s, hq, hkv = 150, 150, 8, 2
+    g = torch.Generator().manual_seed(11 + batch)
+    q = torch.randn(batch, hq, t, D, generator=g).to(torch.bfloat16)
+    k = torch.randn(batch, hkv, s, D, generator=g).to(torch.bfloat16)
+    v = torch.randn(batch, hkv, s, D, generator=g).to(torch.bfloat16)
+    dout = torch.randn(batch, t, hq, D, generator=g).to(torch.bfloat16)
+    scale = D ** -0.5
+    qc, kc, vc = (x.to(cuda).requires_grad_() for x in (q, k, v))
+    out, _ = hip.hip_attention_forward(None, qc, kc, vc, None, scaling=scale)
+    assert out.shape == (batch, t, hq, D)
+    out.backward(dout.to(cuda))
+    torch.cuda.synchronize()
+    assert qc.grad.stride() == qc.stride() and kc.grad.shape == kc.shape
+    for b in range(batch):
+        want, wq, wks, wvs = ref.attention_with_grads(q[b].transpose(0, 1), [k[b].transpose(0, 1)],
+                                                      [v[b].transpose(0, 1)], dout[b], scale)
+        close(out[b], want, f"out[{b}]")
+        close(qc.grad[b].transpose(0, 1), wq, f"dq[{b}]")
+        close(kc.grad[b].transpose(0, 1), wks[0], f"dk[{b}]")
+        close(vc.grad[b].transpose(0, 1), wvs[0], f"dv[{b}]")
+
+
 def test_lse_and_determinism(cuda):
     t, chunks, hq, hkv = 300, [512, 300], 32, 8
     q, ks, vs, dout = make(t, chunks, hq, hkv, seed=3)
