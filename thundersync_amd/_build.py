@@ -52,6 +52,8 @@ FILE_FLAGS = {
     # VGPRs), its dK/dV accumulators in the accumulation registers through
     # inline assembly
     "attention_dkdv_wave.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+    # the head-dim-256 dK/dV kernel with 32 keys per wave: likewise
+    "attention_dkdv256.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
 }
 
 

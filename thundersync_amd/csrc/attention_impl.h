@@ -497,6 +497,11 @@ int launch_dkdv(const ts_attn_problem& P, ts_attn_rows q, ts_attn_rows dout, con
 template <typename E, bool DS>
 void launch_dkdv_wave(dim3 grid, const ts_attn_problem& P, ts_attn_rows q, ts_attn_rows dout,
                       const float* rowstats, int64_t lse_ld, const DsArgs& S, hipStream_t s);
+// the head-dim-256 dK/dV kernel with 32 keys per wave (groups that are not a
+// multiple of 4, 64-key work items; attention_dkdv256.hip), storing dS when DS
+template <typename E, bool DS>
+void launch_dkdv256(dim3 grid, const ts_attn_problem& P, ts_attn_rows q, ts_attn_rows dout,
+                    const float* rowstats, int64_t lse_ld, const DsArgs& S, hipStream_t s);
 // dQ = scale dS K from the workspace the dK/dV launch filled
 int launch_dq_ds(const ts_attn_problem& P, const DsArgs& ds, ts_attn_rows dq, hipStream_t s);
 
