@@ -88,6 +88,13 @@ def test_fp16_head_dim_64(cuda):
     run_chain(cuda, 64, 77, [120, 77], 8, 2, seed=5, dtype=torch.float16)
 
 
+def test_fp16_head_dim_256(cuda):
+    """fp16 at head dim 256 with GQA group 6: the 32-keys-per-wave dK/dV
+    kernel's fp16 products, over runs that end inside a wave's key blocks."""
+    print("attention chain fp16 d=256 t=90 chunks=[130, 90] hq=12 hkv=2", flush=True)
+    run_chain(cuda, 256, 90, [130, 90], 12, 2, seed=6, dtype=torch.float16)
+
+
 def test_fa4_branch_shape_reduced(cuda):
     """The reference's bottom-right branch (tests/test_fa4_bottom_right.py:13-28:
     a query tail over prefix + tail keys, 24/4 heads, D 256) at a reduced size:
