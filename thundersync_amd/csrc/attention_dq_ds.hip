@@ -56,9 +56,11 @@ __device__ __forceinline__ void wait_vmcnt() {
 #define TS_DQDS_KT128 32
 #endif
 #ifndef TS_DQDS_KT256
-#define TS_DQDS_KT256 64
+#define TS_DQDS_KT256 32
 #endif
-// keys per K tile: TS_DQDS_KT256 (64) at head dim 256, TS_DQDS_KT128 (32) at 128
+// keys per K tile: TS_DQDS_KT256 (32: two 24 KB stages, three work-groups per
+// CU; against 64-key tiles in three 48 KB stages at one per CU, branch-shape
+// dQ 1.04 -> 0.90 ms) at head dim 256, TS_DQDS_KT128 (32) at 128
 template <int HD> constexpr int dq_ds_tile_keys() { return HD > 128 ? TS_DQDS_KT256 : TS_DQDS_KT128; }
 #ifndef TS_DQDS_ST128
 #define TS_DQDS_ST128 2
