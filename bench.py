@@ -1115,7 +1115,7 @@ def main():
 
 
 SECONDARY_FIELDS = ["value", "unit", "ms_per_step", "dominant_kernel", "dominant_frac", "peak_mem_GB",
-                    "cpu_baseline"]
+                    "cpu_baseline", "vs_baseline"]
 
 
 def summary(out: dict) -> dict:
@@ -1143,7 +1143,8 @@ def summary(out: dict) -> dict:
         mem = r.get("memory") or {}
         kernel = (roof.get("kernel") or "").split(".")[-1].removesuffix("_kernel") or None
         rows[r["name"]] = [r["value"], r["unit"], round(r["ms_per_step"], 3), kernel, roof.get("frac"),
-                           round(mem["peak_bytes"] / 1e9, 2) if mem else None, cpu.get("value")]
+                           round(mem["peak_bytes"] / 1e9, 2) if mem else None, cpu.get("value"),
+                           r.get("vs_baseline")]
     line["secondary"] = rows
     line["peaks"] = {k: out["peaks"][k] for k in ("bf16_tflops", "hbm_gbs") if k in out.get("peaks", {})}
     return line
