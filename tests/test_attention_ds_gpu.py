@@ -96,6 +96,25 @@ def test_routes_agree_with_the_oracle(monkeypatch, cuda, d, t, chunks, hq, hkv):
         close(dv1[i], wvs[i], f"dv[{i}]")
 
 
+def _random_chain(seed):
+    import random
+
+    rng = random.Random(seed)
+    d = rng.choice((128, 256))
+    hkv = rng.choice((1, 2))
+    hq = hkv * rng.choice((1, 2, 3, 5, 6))
+    chunks = [rng.randint(1, 260) for _ in range(rng.randint(1, 3))]
+    return d, rng.randint(1, chunks[-1]), chunks, hq, hkv
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_random_chains_both_routes(monkeypatch, cuda, seed):
+    """Seeded random chains (head dims 128 and 256, GQA groups 1, 2, 3, 5 and
+    6, one to three chunks of 1 to 260 keys, any query count up to the last
+    chunk): both routes against the oracle, dK/dV identical across routes."""
+    test_routes_agree_with_the_oracle(monkeypatch, cuda, *_random_chain(seed))
+
+
 def test_fp16_route(monkeypatch, cuda):
     print("routes fp16 d=256 t=96 chunks=[50, 96] hq=6 hkv=2", flush=True)
     g = torch.Generator().manual_seed(4)
