@@ -179,7 +179,7 @@ typedef struct ts_attn_problem {
   int32_t head_dim; /* 32, 64, 96, 128, 192 or 256 */
   float scale;
   int32_t q_block;  /* rows per q_work item: ts_attn_q_block(hq / hkv) */
-  int32_t kv_block; /* keys per kv_work item: ts_attn_kv_block(hq / hkv) */
+  int32_t kv_block; /* keys per kv_work item: ts_attn_kv_block(hq / hkv, head_dim) */
   int64_t q_rows;   /* rows of Q/O/dO/dQ */
   /* Launch order.  The work lists are sorted longest first; their first
    * n_q_long / n_kv_long items run first, item by item across all heads (so
@@ -199,9 +199,11 @@ int ts_attn_heads_per_block(int group);
  * 32 * 4 / ts_attn_heads_per_block(group). */
 int ts_attn_q_block(int group);
 
-/* Keys per dK/dV work-group for a GQA group size: 48 when 4 divides the
- * group (one wave per query head), else 64. */
-int ts_attn_kv_block(int group);
+/* Keys per dK/dV work-group for a GQA group size and head dim: 48 when 4
+ * divides the group below head dim 256 (one wave per query head), else 64.
+ * At head dim 256 a problem may also hold 48-key items (the key-split
+ * kernel, for launches with few work items). */
+int ts_attn_kv_block(int group, int head_dim);
 
 /* Host-side consistency check of a problem's tables, given as host copies
  * of the arrays the problem's device pointers name (those pointers are not

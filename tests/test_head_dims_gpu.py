@@ -25,6 +25,14 @@ from thundersync_amd import forest as prod
 pytestmark = pytest.mark.gpu
 
 
+@pytest.fixture(autouse=True, params=["kv64", "kv48"])
+def head_dim_256_items(request, monkeypatch):
+    """Head dim 256 runs both dK/dV work-item sizes: the 64-key items of the
+    two-waves-of-32-keys kernel (forced for these small shapes) and the
+    48-key items of the key-split kernel that launches with few items take."""
+    monkeypatch.setattr(hip, "DKDV256_MIN_ITEMS", 0 if request.param == "kv64" else 1 << 30)
+
+
 def close(got, want, what, bar=2e-2):
     got = got.detach().float().cpu()
     want = want.detach().float().cpu()

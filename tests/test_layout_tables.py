@@ -78,3 +78,21 @@ def test_random_packs(seed, hq, hkv):
     _, chunk_rows, chunks, rows = bench.c4_layout(seed, chunk=rng.choice([64, 100, 512]), groups=2, per_group=3,
                                                   prompt=rng.randint(1, 700), lo=1, hi=900)
     check(att.retained_chunk_layout(rows, chunk_rows, chunks, hq, hkv))
+
+
+def test_head_dim_256_item_size_follows_the_item_count():
+    """At head dim 256 the dK/dV items hold 64 keys (two waves of 32 keys)
+    unless their count over all KV heads is below DKDV256_MIN_ITEMS, then 48
+    (the key-split kernel); other head dims keep ts_attn_kv_block's size, and
+    each size has its own work list."""
+    cpu = torch.device("cpu")
+    big = att.chain_layout(9288, [3000, 9288], 24, 4)  # (47 + 146) x 4 = 772 items of 64 keys
+    small = att.chain_layout(100, [300, 100], 24, 4)  # (5 + 2) x 4 = 28
+    group4 = att.chain_layout(9288, [3000, 9288], 16, 4)
+    assert big.kv_block_for(cpu, 256) == 64 and small.kv_block_for(cpu, 256) == 48
+    assert big.kv_block_for(cpu, 128) == 64 and group4.kv_block_for(cpu, 128) == 48
+    assert group4.kv_block_for(cpu, 256) == 64
+    for kvb in (48, 64):
+        kv_work = big.device_tables(cpu, kvb)["arrays"][4]
+        assert len(kv_work) == sum(-(-n // kvb) for n in (3000, 9288))
+        assert set(kv_work[:, 1].tolist()) <= set(range(0, 9288, kvb))

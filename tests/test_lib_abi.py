@@ -74,3 +74,21 @@ def test_the_operator_library_exports_no_test_probes():
     probe = ctypes.CDLL(str(PROBE_LIB))
     for name in ("ts_probe_layouts", "ts_probe_lds", "ts_probe_lanes", "ts_probe_last_error"):
         assert hasattr(probe, name), name
+
+
+def test_work_item_sizes_match_the_host_mirrors(monkeypatch):
+    """ts_attn_q_block / ts_attn_kv_block agree with the layout's mirrors for
+    every GQA group and head dim the kernels take (the library validates
+    each problem's q_block / kv_block against them)."""
+    from thundersync_amd import attention as att
+
+    monkeypatch.setenv(_lib.HIP_ENV, "auto")
+    _lib.reset()
+    try:
+        lib = _lib.require_library()
+        for group in (1, 2, 3, 4, 5, 6, 8):
+            assert lib.ts_attn_q_block(group) == att.q_block_rows(group, 1)
+            for head_dim in att.HEAD_DIMS:
+                assert lib.ts_attn_kv_block(group, head_dim) == att.kv_block_keys(group, 1, head_dim), (group, head_dim)
+    finally:
+        _lib.reset()

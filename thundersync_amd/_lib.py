@@ -76,7 +76,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "ts_forest_build": (_INT, [_I64, _P, _P, _P, _I64, _P, _P, _P, _P, _P, _P, _P, _P]),
     "ts_plan_compile": (_INT, [_I64, _P, _P, _P, _P, _P, _I64, _P, _P, _I64] + [_P] * 13),
     "ts_attn_heads_per_block": (_INT, [_INT]),
-    "ts_attn_kv_block": (_INT, [_INT]),
+    "ts_attn_kv_block": (_INT, [_INT, _INT]),
     "ts_attn_q_block": (_INT, [_INT]),
     "ts_attn_check_tables": (_INT, [ctypes.POINTER(AttnProblem), _P, _P, _I64, _P, _P, _I64, _P, _P]),
     "ts_attn_fwd": (_INT, [ctypes.POINTER(AttnProblem), AttnRows, AttnRows, _P, _I64, _P]),

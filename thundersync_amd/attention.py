@@ -88,9 +88,18 @@ def q_block_rows(hq: int, hkv: int) -> int:
 DQ_BLOCK_ROWS = 64
 
 
-def kv_block_keys(hq: int, hkv: int) -> int:
-    """Keys per dK/dV work-group (mirror of ts_attn_kv_block)."""
-    return 48 if (hq // hkv) % 4 == 0 else 64
+def kv_block_keys(hq: int, hkv: int, head_dim: int = HEAD_DIM) -> int:
+    """Keys per dK/dV work-group (mirror of ts_attn_kv_block): 64 at head dim
+    256 and for GQA groups that are not a multiple of 4, else 48."""
+    return 48 if (hq // hkv) % 4 == 0 and head_dim != 256 else 64
+
+
+# At head dim 256 the 64-key dK/dV work items run two work-groups per CU
+# (two waves of 32 keys each); a launch with fewer of them than that fills
+# (512) leaves CUs half used, and the 48-key items of the key-split kernel
+# (one work-group per CU, four waves of 16 keys) balance better: the branch
+# shape at 16/2 heads (384 items of 64 keys) 7.06 ms against 6.54.
+DKDV256_MIN_ITEMS = 512
 
 
 # ---------------------------------------------------------------------------
@@ -161,7 +170,7 @@ class AttnLayout:
             raise ValueError("attention problem too large")
 
     # -- work lists ---------------------------------------------------------
-    def _host_tables(self):
+    def _host_tables(self, kvb: int | None = None):
         qb = q_block_rows(self.hq, self.hkv)
         segs = np.zeros(len(self.seg_q), SEG_DTYPE)
         spans, visits_of = [], [[] for _ in self.runs]
@@ -182,7 +191,7 @@ class AttnLayout:
             visit_rows.extend(vis)
         # dK/dV items: every kvb-key block of every visited run; its cost is
         # the number of query rows that see its first key, over its visits
-        kvb = kv_block_keys(self.hq, self.hkv)
+        kvb = kv_block_keys(self.hq, self.hkv) if kvb is None else kvb
         seg_len = np.array([n for _, n in self.seg_q], np.int64)
         seg_off = np.array(self.seg_kv, np.int64) - seg_len
         kv_cost, kv_run, kv_k0 = [], [], []
@@ -236,9 +245,11 @@ class AttnLayout:
         return (segs, seg_spans, run_visits, q_work, kv_work, visit0, [len(v) for v in visits_of],
                 q_long, kv_long, dq_work, dq_long)
 
-    def device_tables(self, device: torch.device):
-        """Upload the layout's integer tables once per device (pinned, non-blocking)."""
-        key = (device.type, device.index)
+    def device_tables(self, device: torch.device, kv_block: int | None = None):
+        """Upload the layout's integer tables once per device and dK/dV item
+        size (pinned, non-blocking); `kv_block` None: the head-dim-128 size."""
+        kvb = kv_block_keys(self.hq, self.hkv) if kv_block is None else int(kv_block)
+        key = (device.type, device.index, kvb)
         hit = self._tables.get(key)
         if hit is not None:
             return hit
@@ -246,7 +257,7 @@ class AttnLayout:
             hit = self._tables.get(key)
             if hit is None:
                 (segs, spans, visits, q_work, kv_work, visit0, nvisit, q_long, kv_long, dq_work,
-                 dq_long) = self._host_tables()
+                 dq_long) = self._host_tables(kvb)
                 parts = [segs.view(np.uint8), spans.view(np.uint8), visits.view(np.uint8),
                          q_work.view(np.uint8).reshape(-1), kv_work.view(np.uint8).reshape(-1),
                          dq_work.view(np.uint8).reshape(-1)]
@@ -326,13 +337,27 @@ class AttnLayout:
                 self._tables[key] = hit
         return hit
 
+    def kv_block_for(self, device, head_dim: int) -> int:
+        """Keys per dK/dV work item at `head_dim`: ts_attn_kv_block's, except
+        at head dim 256 when the 64-key items of the visited runs, over all
+        KV heads, are fewer than DKDV256_MIN_ITEMS: then 48 (the key-split
+        kernel)."""
+        kvb = kv_block_keys(self.hq, self.hkv, head_dim)
+        if head_dim == 256:
+            nvisit = self.device_tables(device)["nvisit"]
+            n64 = sum((run.length + 63) // 64 for run, nv in zip(self.runs, nvisit) if nv)
+            if n64 * self.hkv < DKDV256_MIN_ITEMS:
+                kvb = 48
+        return kvb
+
     def problem(self, device, runs_ptr: int, scale: float, dtype: torch.dtype = torch.bfloat16,
                 head_dim: int = HEAD_DIM) -> AttnProblem:
-        t = self.device_tables(device)
+        kvb = self.kv_block_for(device, int(head_dim))
+        t = self.device_tables(device, kvb)
         return AttnProblem(
             t["segs"], t["seg_spans"], runs_ptr, t["run_visits"], t["q_work"], t["kv_work"],
             t["n_q_work"], t["n_kv_work"], len(self.seg_q), len(self.runs), self.hq, self.hkv,
-            int(head_dim), float(scale), q_block_rows(self.hq, self.hkv), kv_block_keys(self.hq, self.hkv), self.q_rows,
+            int(head_dim), float(scale), q_block_rows(self.hq, self.hkv), kvb, self.q_rows,
             t["n_q_long"], t["n_kv_long"], _lib.dtype_code(dtype),
         )
 
@@ -435,7 +460,7 @@ def check_tables(layout: AttnLayout, problem: AttnProblem, run_table: np.ndarray
     spans tile every segment's keys, every visit is a span of its segment,
     the work lists hold every row and key block once, K/V/dK/dV addresses are
     aligned.  Raises RuntimeError naming the first inconsistency."""
-    segs, spans, visits, q_work, kv_work = layout.device_tables(device)["arrays"]
+    segs, spans, visits, q_work, kv_work = layout.device_tables(device, problem.kv_block)["arrays"]
     runs = run_table.numpy() if isinstance(run_table, torch.Tensor) else run_table
     runs = np.ascontiguousarray(runs).view(np.uint8)
     if runs.size != len(layout.runs) * RUN_DTYPE.itemsize:

@@ -53,8 +53,9 @@ int validate(const ts_attn_problem* p, const char* what) {
   const int gc = heads_per_block(p->hq / p->hkv);
   TS_CHECK_ARG(p->q_block == q_block_rows(p->hq / p->hkv), "%s: q_block %d, expected %d for group %d",
                what, p->q_block, q_block_rows(p->hq / p->hkv), p->hq / p->hkv);
-  TS_CHECK_ARG(p->kv_block == kv_block_keys(p->hq / p->hkv), "%s: kv_block %d, expected %d", what,
-               p->kv_block, kv_block_keys(p->hq / p->hkv));
+  // head dim 256 also takes 48-key items (the key-split kernel: few work items)
+  TS_CHECK_ARG(p->kv_block == kv_block_keys(p->hq / p->hkv, p->head_dim) || (p->head_dim == 256 && p->kv_block == 48),
+               "%s: kv_block %d, expected %d", what, p->kv_block, kv_block_keys(p->hq / p->hkv, p->head_dim));
   TS_CHECK_ARG(p->n_q_work >= 0 && p->n_kv_work >= 0 && p->n_segs >= 0 && p->n_runs >= 0,
                "%s: negative table size", what);
   TS_CHECK_ARG(p->n_q_long >= 0 && p->n_q_long <= p->n_q_work && p->n_kv_long >= 0 &&
@@ -108,7 +109,7 @@ extern "C" {
 
 int ts_attn_heads_per_block(int group) { return group > 0 ? ts::attn::heads_per_block(group) : 0; }
 
-int ts_attn_kv_block(int group) { return group > 0 ? ts::attn::kv_block_keys(group) : 0; }
+int ts_attn_kv_block(int group, int head_dim) { return group > 0 ? ts::attn::kv_block_keys(group, head_dim) : 0; }
 int ts_attn_q_block(int group) { return group > 0 ? ts::attn::q_block_rows(group) : 0; }
 
 int ts_attn_fwd(const ts_attn_problem* problem, ts_attn_rows q, ts_attn_rows out, float* lse,

@@ -151,8 +151,8 @@ __global__ __launch_bounds__(kThreads, HD > 128 ? 1 : 2) void dkdv_kernel(ts_att
 
 // ---------------------------------------------------------------------------
 // backward dK / dV with the keys split over the waves (head dim 128: GQA
-// groups that are not a multiple of 4; head dim 256: groups that are, whose
-// work items hold 48 keys -- the others take dkdv256_kernel's 32 keys per wave)
+// groups that are not a multiple of 4; head dim 256: 48-key work items, which
+// launches with few 64-key items take)
 //
 // A work-group owns P.kv_block keys (48 or 64) of one run and one KV head;
 // wave w owns keys 16 w .. 16 w + 15, their K^T and V^T in registers, and all
@@ -494,7 +494,7 @@ void launch_dkdv_tuned(dim3 grid, const ts_attn_problem& P, ts_attn_rows q, ts_a
                        const float* rowstats, int64_t lse_ld, const DsArgs& S, hipStream_t s) {
   const int group = P.hq / P.hkv;
   ts::TimedLaunch timed_("attention.dkdv_kernel", s);
-  if (P.head_dim == 256 && group % 4 != 0 && P.kv_block == 64)
+  if (P.head_dim == 256 && P.kv_block == 64)
     launch_dkdv256<E, DS>(grid, P, q, dout, rowstats, lse_ld, S, s);
   else if (P.head_dim == 256)
     hipLaunchKernelGGL((dkdv_split_kernel<E, 256, DS>), grid, dim3(kThreads), 0, s, P, q, dout, rowstats, lse_ld, S);

@@ -1,5 +1,5 @@
-// Attention backward: dK / dV at head dim 256 with 32 keys per wave (GQA
-// groups that are not a multiple of 4, whose work items hold 64 keys).  A
+// Attention backward: dK / dV at head dim 256 with 32 keys per wave (every
+// GQA group: at this head dim the work items hold 64 keys).  A
 // translation unit of its own so that it can take its own code-generation
 // flags (MFMA results in VGPRs, the dK/dV accumulators in accumulation
 // registers through inline assembly).

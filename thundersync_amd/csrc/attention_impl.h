@@ -477,9 +477,11 @@ inline int heads_per_block(int group) {
 // query rows per forward / dQ work item: 32 per query head of the work-group
 inline int q_block_rows(int group) { return 32 * 4 / heads_per_block(group); }
 
-// keys per dK/dV work-group: 48 for the one-wave-per-head kernel (its 192
-// dK/dV accumulators and 48 S/dP values fill the 256 AGPRs), else 64
-inline int kv_block_keys(int group) { return group % 4 == 0 ? 48 : BK; }
+// keys per dK/dV work-group: 48 for the one-wave-per-head kernel (GQA groups
+// that are a multiple of 4 below head dim 256: its 192 dK/dV accumulators and
+// 48 S/dP values fill the 256 AGPRs), else 64 (at head dim 256 the two waves
+// of 32 keys of dkdv256_kernel, every group)
+inline int kv_block_keys(int group, int head_dim) { return group % 4 == 0 && head_dim != 256 ? 48 : BK; }
 
 // launchers (one per kernel family); each returns a TS_* status
 int launch_fwd(const ts_attn_problem& P, ts_attn_rows q, ts_attn_rows out, float* lse, int64_t lse_ld,
@@ -497,8 +499,8 @@ int launch_dkdv(const ts_attn_problem& P, ts_attn_rows q, ts_attn_rows dout, con
 template <typename E, bool DS>
 void launch_dkdv_wave(dim3 grid, const ts_attn_problem& P, ts_attn_rows q, ts_attn_rows dout,
                       const float* rowstats, int64_t lse_ld, const DsArgs& S, hipStream_t s);
-// the head-dim-256 dK/dV kernel with 32 keys per wave (groups that are not a
-// multiple of 4, 64-key work items; attention_dkdv256.hip), storing dS when DS
+// the head-dim-256 dK/dV kernel with 32 keys per wave (64-key work items;
+// attention_dkdv256.hip), storing dS when DS
 template <typename E, bool DS>
 void launch_dkdv256(dim3 grid, const ts_attn_problem& P, ts_attn_rows q, ts_attn_rows dout,
                     const float* rowstats, int64_t lse_ld, const DsArgs& S, hipStream_t s);
