@@ -1,6 +1,6 @@
 """HIP attention against the CPU oracle (bottom-right causal GQA, fp32).
 
-Bar: outputs and input gradients within 2e-2 max-abs
+Bar (the north star's): outputs and input gradients within 2e-2 max-abs
 of the fp32 oracle on identical bf16 inputs.  Where a tensor's magnitude
 exceeds 1 (summed key gradients of a long shared prefix), the bar scales with
 max|ref| -- the bf16 rounding of the stored result alone is 2^-9 relative --

@@ -1,6 +1,6 @@
 """HIP fused logprob / entropy against the CPU oracle (the reference's chunk loop).
 
-Bars: per-token logprobs within 1e-3 and entropies
+Bars: per-token logprobs within 1e-3 (the north star's bar) and entropies
 within 1e-3, on identical bf16 inputs; grad wrt hidden within 1e-2 x
 max|ref| (both sides round dlogits to bf16 before the VJP GEMM, as the
 reference does, and round the result to bf16).  The full-size C3 check
