@@ -103,6 +103,40 @@ def test_fp16_head_dim_256(cuda):
     run_chain(cuda, 256, 90, [130, 90], 12, 2, seed=6, dtype=torch.float16)
 
 
+def test_fused_projection_views_head_dim_256(cuda):
+    """Q, K and V at head dim 256 (GQA group 6) as column slices of one fused
+    projection output [rows, (Hq + 2 Hkv) D]: read in place through their
+    strides; gradients land in the slices of the fused gradient."""
+    t, s_len, hq, hkv, d = 150, 400, 12, 2, 256
+    print(f"fused projection views d={d} t={t} keys={s_len} hq={hq} hkv={hkv}", flush=True)
+    g = torch.Generator().manual_seed(23)
+    width = (hq + 2 * hkv) * d
+    qkv_q = torch.randn(t, width, generator=g).to(torch.bfloat16)
+    qkv_k = torch.randn(s_len, width, generator=g).to(torch.bfloat16)
+    dout = torch.randn(t, hq, d, generator=g).to(torch.bfloat16)
+    scale = d ** -0.5
+    split = lambda x: (x[:, : hq * d].view(-1, hq, d), x[:, hq * d : (hq + hkv) * d].view(-1, hkv, d),
+                       x[:, (hq + hkv) * d :].view(-1, hkv, d))
+    q_ref, _, _ = split(qkv_q)
+    _, k_ref, v_ref = split(qkv_k)
+    want, wq, wks, wvs = ref.attention_with_grads(q_ref, [k_ref], [v_ref], dout, scale)
+    a = qkv_q.to(cuda).requires_grad_()
+    b = qkv_k.to(cuda).requires_grad_()
+    q, _, _ = split(a)
+    _, k, v = split(b)
+    out, _ = hip.attention(q, hip.chain_layout(t, [s_len], hq, hkv), [k], [v], scale)
+    out.backward(dout.to(cuda))
+    torch.cuda.synchronize()
+    close(out, want, "out")
+    gq, _, _ = split(a.grad)
+    _, gk, gv = split(b.grad)
+    close(gq, wq, "dq")
+    close(gk, wks[0], "dk")
+    close(gv, wvs[0], "dv")
+    assert a.grad[:, hq * d :].abs().max().item() == 0.0
+    assert b.grad[:, : hq * d].abs().max().item() == 0.0
+
+
 def test_fa4_branch_shape_reduced(cuda):
     """The reference's bottom-right branch (tests/test_fa4_bottom_right.py:13-28:
     a query tail over prefix + tail keys, 24/4 heads, D 256) at a reduced size:
